@@ -1,0 +1,157 @@
+/*
+ * zeromoe.h -- C ABI of libzeromoe_hip.so, the MI355X (gfx950) routed-expert
+ * MUL_MAT_ID path.
+ *
+ * Every entry point takes plain pointers and sizes.  Device pointers are HIP
+ * device memory; `stream` is a hipStream_t (NULL = the legacy default
+ * stream).  Work is stream-ordered; nothing synchronises unless stated.
+ * Return convention: int entry points return 0 on success and a negative
+ * code on a rejected call (zm_last_error() says why); zm_mul_mat_id follows
+ * the ggml hook convention instead (1 = handled / supported, 0 = declined).
+ *
+ * Each declaration cites the reference interface it replaces
+ * (/root/reference/<file>:<line>).
+ */
+#ifndef ZEROMOE_H
+#define ZEROMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml tensor descriptor: type (ggml_type id), ne[] (elements, fastest
+ * first), nb[] (byte strides), data (device pointer).  The subset of
+ * struct ggml_tensor that ggml_cuda_mul_mat_id hands to its quant hook
+ * (patches/ggml/0010-...:9-27). */
+typedef struct zm_tensor {
+  int32_t type;
+  int64_t ne[4];
+  size_t nb[4];
+  void *data;
+} zm_tensor;
+
+/* ggml_type ids used on this path */
+enum {
+  ZM_TYPE_F32 = 0,
+  ZM_TYPE_Q2_K = 10,
+  ZM_TYPE_Q3_K = 11,
+  ZM_TYPE_Q4_K = 12,
+  ZM_TYPE_Q8_K = 15,
+  ZM_TYPE_IQ2_XXS = 16,
+  ZM_TYPE_I32 = 26,
+};
+
+/* ---------------------------------------------------------------- library */
+
+/* Per-device set-up of the current device (IQ2 tables).  Idempotent.
+ * Replaces init_iq2_grids (kernels/quant/iq2_matmul.cu:55-70). */
+int zm_init(void);
+const char *zm_last_error(void);
+const char *zm_version(void);
+
+/* Load the IQ2_XXS grid (256 x u64, ggml's iq2xxs_grid) for the current
+ * device.  Without a call the built-in stand-in grid is used.
+ * Replaces the grid copy of init_iq2_grids (iq2_matmul.cu:60). */
+int zm_set_iq2xxs_grid(const uint64_t grid[256]);
+void zm_iq2xxs_builtin_grid(uint64_t grid[256]);
+
+/* Capability flags the graph builders probe before emitting negative
+ * (inactive) expert ids: both are 1, the HIP path skips id < 0 in decode and
+ * in batched prefill.  Replace ggml_cpu_mul_mat_id_negative_skip and
+ * ggml_cuda_mul_mat_id_negative_skip_batched
+ * (backends/ggml/mmid_route_skip.hpp:22,41). */
+int zm_mul_mat_id_negative_skip(void);
+int zm_mul_mat_id_negative_skip_batched(void);
+
+/* ---------------------------------------------------------------- the op */
+
+/* GGML_OP_MUL_MAT_ID hook: dst[:, id, t] = W[ids[id, t]] . src1[:, id % ne11, t]
+ * with src1 quantized to Q8_K (ggml CPU semantics), id < 0 -> zero row,
+ * id >= n_experts -> NaN row.
+ *   src0: Q2_K / Q3_K / Q4_K / IQ2_XXS [I, O, E] (row-contiguous)
+ *   src1: F32 [I, ne11, S], ne11 == 1 or n_ids;  ids: I32 [n_ids, S]
+ *   dst : F32 [O, n_ids, S]
+ * execute = 0 is a pure capability query; execute = 1 launches on `stream`.
+ * Returns 1 when handled/supported, 0 when declined.
+ * Replaces native_f32_quant_hook / zeromoe_install_f32_quant_graph_hook
+ * (kernels/quant/kquant_matmul.cu:702-761, patches/ggml/0010-...:9-27). */
+int zm_mul_mat_id(const zm_tensor *src0, const zm_tensor *src1, const zm_tensor *ids, zm_tensor *dst, void *stream,
+                  int execute);
+/* Count of executed zm_mul_mat_id launches (kquant_matmul.cu:762-764). */
+uint64_t zm_mul_mat_id_launches(void);
+
+/* ---------------------------------------------------------------- pieces */
+
+/* f32 rows -> ggml block_q8_K rows (292 B per 256), bit-exact to ggml's
+ * quantize_row_q8_K.  Replaces the from_float step of
+ * ggml_compute_forward_mul_mat_id (patches/ggml/0002-...:18-45). */
+int zm_quantize_q8_K(const float *x, int64_t rows, int64_t n, void *y, void *stream);
+
+/* Router: gating (0 softmax, 1 sigmoid, 2 sqrt-softplus), optional grouped
+ * selection, top-k (descending, lowest index on ties), weight norm/scale,
+ * optional slot table.  logits [S][E]; ids/weights [S][K].
+ * Replaces moe_routed::gate_probs/select_ids/route_weights
+ * (models/graph/moe_routed_ggml.hpp:52-141) and make_branch_inputs
+ * (backends/ggml/moe_partial_route_ggml.hpp:21-35). */
+typedef struct zm_router_spec {
+  int32_t gating;
+  int32_t n_experts;
+  int32_t topk;
+  int32_t n_groups;
+  int32_t n_groups_used;
+  int32_t weights_norm;
+  float weights_scale;
+} zm_router_spec;
+int zm_router(const zm_router_spec *spec, const float *logits, const float *logit_bias, const float *sel_bias,
+              const int32_t *route_map, const float *route_mask, int S, int32_t *ids, float *weights, void *stream);
+
+/* Stable bucketing of the S*K (token, slot) pairs by expert: counts[E],
+ * offs[E+1] (exclusive scan), pairs[S*K] (flat s*K+k, token-major within an
+ * expert), active[E] (experts with count > 0, ascending), n_active[1].
+ * Negative ids are not bucketed.  E <= 512.
+ * Replaces the CSR build of core/batched_dispatch_pipeline.cpp:1181-1202. */
+int zm_bucket(const int32_t *ids, int S, int K, int E, int32_t *counts, int32_t *offs, int32_t *pairs,
+              int32_t *active, int32_t *n_active, void *stream);
+
+/* Debug/verification: per-super-block integer parts of one weight row
+ * against f32 activations quantized to Q8_K: isum[b], imin[b] as defined in
+ * oracle/zm_oracle.h (zmo_block_dots).  Not on the hot path. */
+int zm_block_dots(int type, const void *w_row, const float *x, int n, int32_t *isum, int32_t *imin, void *stream);
+
+/* ---------------------------------------------------------------- routed layer */
+
+/* One routed MoE FFN layer (moe_routed::expert_ffn + ggml_mul + sum_topk,
+ * models/graph/moe_routed_ggml.hpp:166-214, models/graph/moe_block.hpp:86-105,
+ * plus the shared-expert add of moe_block.hpp:201-202).
+ * Weights in ggml layout, contiguous: gate/up [H, F, n_slots], down
+ * [F, H, n_slots].  route_map (optional) maps the router's n_experts ids to
+ * weight slots (-1 = not resident: route skipped, weight masked). */
+typedef struct zm_moe_layer {
+  int32_t H, F;
+  int32_t n_slots;          /* experts held by the weight tensors */
+  zm_router_spec router;    /* router.n_experts = E of the router, router.topk = K */
+  int32_t type_gate, type_up, type_down;
+  const void *w_gate, *w_up, *w_down;
+  const float *router_w;    /* optional fp32 router [E][H] (ggml [H, E]); NULL: logits are an input */
+  const float *logit_bias;  /* optional [E] */
+  const float *sel_bias;    /* optional [E] */
+  const int32_t *route_map; /* optional [E] */
+  const float *route_mask;  /* optional [E] */
+  int32_t F_shared, type_shared; /* shared expert (F_shared = 0: none) */
+  const void *ws_gate, *ws_up, *ws_down;
+} zm_moe_layer;
+
+size_t zm_moe_workspace_size(const zm_moe_layer *layer, int S);
+/* x [S][H] f32; logits [S][E] (ignored when router_w is set); out [S][H];
+ * ids_out / weights_out [S][K] (optional): the routes after the slot table.
+ * workspace: device memory of zm_moe_workspace_size() bytes. */
+int zm_moe_forward(const zm_moe_layer *layer, const float *x, const float *logits, int S, float *out,
+                   int32_t *ids_out, float *weights_out, void *workspace, size_t workspace_size, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

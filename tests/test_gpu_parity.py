@@ -1,0 +1,226 @@
+"""HIP path vs the CPU oracle on identical seeded inputs (MI355X).
+
+Bars: integer/index results bit-exact (Q8_K bytes, per-block integer dots,
+expert ids, bucket order); float outputs of the op and the layer within 1e-3
+relative (see moe_cases.assert_close_layer for the exact norm)."""
+import numpy as np
+import pytest
+import torch
+
+import zm_oracle as O
+from moe_cases import CONFIGS, IQ2, Q2, Q3, Q4, Built, assert_close_layer, dev_random_blocks, reduced
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [Q2, Q3, Q4, IQ2]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    import zeromoe_amd as Z
+
+    assert torch.cuda.is_available(), "GPU tests need a device"
+    Z.init()
+    yield
+
+
+def _sync():
+    torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------------ Q8_K activation quantization
+
+def test_quantize_q8_K_bit_exact():
+    import zeromoe_amd as Z
+
+    rng = np.random.default_rng(0)
+    rows = [rng.standard_normal(4096) * 10 ** rng.uniform(-6, 6) for _ in range(20)]
+    special = np.zeros(4096)
+    special[5], special[700] = -2.0, 2.0          # tie: first wins
+    special[1024 + 3], special[1024 + 9] = 3.0, -3.0
+    special[2048:2304] = 0.0                      # an all-zero block
+    special[3072:3328] = np.linspace(-127, 127, 256)  # exact half-way roundings
+    rows.append(special)
+    x = np.stack(rows).astype(np.float32)
+    got = Z.quantize_q8_K(torch.from_numpy(x).cuda()).cpu().numpy()
+    ref = O.quantize_q8_K(x).view(np.uint8).reshape(got.shape)
+    np.testing.assert_array_equal(got, ref)
+
+
+# ------------------------------------------------------------------ per-block integer dots
+
+@pytest.mark.parametrize("t", TYPES)
+def test_block_dots_exact(t):
+    import zeromoe_amd as Z
+
+    n = 16 * 256
+    w = O.random_blocks(t, 3, n, seed=t + 100)
+    rng = np.random.default_rng(t)
+    for r in range(3):
+        x = rng.standard_normal(n).astype(np.float32)
+        gi, gm = Z.block_dots(t, torch.from_numpy(w[r]).cuda(), torch.from_numpy(x).cuda())
+        ri, rm = O.block_dots(t, w[r], O.quantize_q8_K(x))
+        np.testing.assert_array_equal(gi.cpu().numpy(), ri)
+        if t in (Q2, Q4):
+            np.testing.assert_array_equal(gm.cpu().numpy(), rm)
+
+
+# ------------------------------------------------------------------ the op
+
+def _mmid_case(t, I, O_, E, ids, ne11, seed):
+    import zeromoe_amd as Z
+
+    S, n_ids = ids.shape
+    W = O.random_blocks(t, E * O_, I, seed=seed).reshape(E, O_, -1)
+    x = np.random.default_rng(seed).standard_normal((S, ne11, I)).astype(np.float32)
+    ref = O.mul_mat_id(t, W, x, ids, nthreads=8)
+    got = Z.mul_mat_id(torch.from_numpy(W).cuda(), t, I, torch.from_numpy(x).cuda(),
+                       torch.from_numpy(ids).cuda()).cpu().numpy()
+    return got, ref
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("shape", [(512, 8, 3), (4096, 64, 1), (16384, 64, 1), (768, 200, 2)])
+def test_mul_mat_id_vs_oracle(t, shape):
+    """Reference Test 5 shapes (tests/native/tests_basic_cuda.cpp:301-322) as
+    MUL_MAT_ID with 12 experts and 4 routes per token."""
+    I, O_, S = shape
+    E, n_ids = 12, 4
+    rng = np.random.default_rng(I + O_)
+    ids = np.stack([rng.permutation(E)[:n_ids] for _ in range(S)]).astype(np.int32)
+    got, ref = _mmid_case(t, I, O_, E, ids, 1, seed=t * 7 + S)
+    np.testing.assert_allclose(got, ref, rtol=1e-3, atol=1e-3 * np.abs(ref).max())
+    # per-element relative error is the stronger statement for a single dot
+    rel = np.abs(got - ref) / np.maximum(np.abs(ref), 1e-3 * np.abs(ref).max())
+    assert rel.max() <= 1e-3
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_mul_mat_id_negative_and_broadcast(t):
+    """ids {3,-1,17,-1,-1,8,-1,-1,-1,21} (bench/mmid_exact_check.cpp:41): -1 rows
+    are zero; ne11 == n_ids takes one src1 row per slot."""
+    ids = np.array([[3, -1, 17, -1, -1, 8, -1, -1, -1, 21]], np.int32)
+    for ne11 in (1, 10):
+        got, ref = _mmid_case(t, 2560 if t != IQ2 else 2560, 192, 24, ids, ne11, seed=5 + ne11)
+        assert not got[0, 1].any() and not got[0, 3].any()
+        np.testing.assert_allclose(got, ref, rtol=1e-3, atol=1e-3 * np.abs(ref).max())
+
+
+def test_mul_mat_id_skewed_prefill_buckets():
+    """Many tokens, skewed expert loads (bucket chunks of 4 pairs)."""
+    rng = np.random.default_rng(3)
+    S, n_ids, E = 96, 8, 16
+    p = np.exp(rng.standard_normal(E) * 1.5)
+    p /= p.sum()
+    ids = np.stack([rng.choice(E, n_ids, replace=False, p=p) for _ in range(S)]).astype(np.int32)
+    ids[5, 2] = -1
+    got, ref = _mmid_case(Q4, 1024, 96, E, ids, 1, seed=9)
+    np.testing.assert_allclose(got, ref, rtol=1e-3, atol=1e-3 * np.abs(ref).max())
+
+
+def test_mul_mat_id_out_of_range_is_nan():
+    ids = np.array([[2, 99]], np.int32)
+    got, _ = _mmid_case(Q2, 512, 8, 4, np.array([[2, 1]], np.int32), 1, seed=1)
+    import zeromoe_amd as Z
+
+    W = O.random_blocks(Q2, 4 * 8, 512, seed=1).reshape(4, 8, -1)
+    x = np.ones((1, 1, 512), np.float32)
+    y = Z.mul_mat_id(torch.from_numpy(W).cuda(), Q2, 512, torch.from_numpy(x).cuda(),
+                     torch.from_numpy(ids).cuda()).cpu().numpy()
+    assert np.isnan(y[0, 1]).all() and np.isfinite(y[0, 0]).all()
+
+
+# ------------------------------------------------------------------ router / bucketing
+
+@pytest.mark.parametrize("name", ["c1", "c3", "c4", "c5"])
+def test_router_ids_bit_exact(name):
+    import zeromoe_amd as Z
+
+    c = CONFIGS[name]
+    b = Built(reduced(c, H=256, F=256, S=max(c.S, 64)), seed=11)
+    lg = b.logits
+    ids_r, w_r = O.router(lg, c.K, c.gating, b.logit_bias, None, c.groups, c.groups_used, c.norm, c.scale)
+    t = lambda a: None if a is None else torch.from_numpy(a).cuda()
+    ids, w = Z.router(t(lg), c.K, {0: "softmax", 1: "sigmoid"}[c.gating], logit_bias=t(b.logit_bias),
+                      n_groups=c.groups, n_groups_used=c.groups_used, weights_norm=c.norm, weights_scale=c.scale)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_r)
+    np.testing.assert_allclose(w.cpu().numpy(), w_r, rtol=1e-6, atol=0)
+    if b.route_map is not None:
+        ids2, w2 = Z.router(t(lg), c.K, "sigmoid", n_groups=c.groups, n_groups_used=c.groups_used,
+                            weights_norm=c.norm, weights_scale=c.scale, route_map=t(b.route_map))
+        i_r2, w_r2 = O.apply_slot_table(b.route_map, ids_r, w_r)
+        np.testing.assert_array_equal(ids2.cpu().numpy(), i_r2)
+        np.testing.assert_allclose(w2.cpu().numpy(), w_r2, rtol=1e-6, atol=0)
+
+
+def test_router_ties_lowest_index():
+    import zeromoe_amd as Z
+
+    lg = np.round(np.random.default_rng(1).standard_normal((64, 128)) * 1.5).astype(np.float32)
+    ids, _ = Z.router(torch.from_numpy(lg).cuda(), 8)
+    ref, _ = O.router(lg, 8)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("S,K,E", [(1, 8, 128), (512, 8, 128), (4, 8, 160), (64, 8, 96), (3000, 8, 256)])
+def test_bucket_bit_exact(S, K, E):
+    import zeromoe_amd as Z
+
+    rng = np.random.default_rng(S + E)
+    p = np.exp(rng.standard_normal(E) * 1.5)
+    p /= p.sum()
+    ids = np.stack([rng.choice(E, K, replace=False, p=p) for _ in range(S)]).astype(np.int32)
+    ids[rng.random(ids.shape) < 0.05] = -1
+    counts, offs, pairs, active, n_active = Z.bucket(torch.from_numpy(ids).cuda(), E)
+    rc, ro, rp = O.bucket(ids, E)
+    np.testing.assert_array_equal(counts.cpu().numpy(), rc)
+    np.testing.assert_array_equal(offs.cpu().numpy(), ro)
+    np.testing.assert_array_equal(pairs.cpu().numpy()[: len(rp)], rp)
+    act = np.nonzero(rc)[0]
+    assert int(n_active.item()) == len(act)
+    np.testing.assert_array_equal(active.cpu().numpy()[: len(act)], act)
+
+
+# ------------------------------------------------------------------ the routed layer
+
+LAYER_CASES = {
+    "c1_full": (CONFIGS["c1"], {}),
+    "c2_full": (CONFIGS["c2"], {}),
+    "c3_reduced": (CONFIGS["c3"], dict(S=64, H=1024, F=512)),
+    "c4_full": (CONFIGS["c4"], {}),
+    "c5_full_S1": (CONFIGS["c5"], {}),
+    "c5_S64_reduced": (CONFIGS["c5"], dict(S=64, H=1024, F=512, F_shared=512)),
+}
+
+
+@pytest.mark.parametrize("case", list(LAYER_CASES))
+def test_moe_layer_vs_oracle(case):
+    c, kw = LAYER_CASES[case]
+    c = reduced(c, **kw)
+    b = Built(c, seed=3)
+    L = b.layer()
+    x = torch.from_numpy(b.x).cuda()
+    lg = None if c.router_gemv else torch.from_numpy(b.logits).cuda()
+    out, ids, w = L.forward(x, lg)
+    _sync()
+    ids_r, w_r = b.oracle_route()
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_r)
+    np.testing.assert_allclose(w.cpu().numpy(), w_r, rtol=1e-5, atol=1e-7)
+    ref = b.oracle_forward(ids.cpu().numpy(), w.cpu().numpy())
+    assert_close_layer(out.cpu().numpy(), ref)
+
+
+def test_moe_layer_repeatable_and_stream_ordered():
+    """Same inputs, two streams, many calls: identical bits (no atomics, no races)."""
+    c = reduced(CONFIGS["c2"], H=2048, F=768)
+    b = Built(c, seed=4)
+    L = b.layer()
+    x = torch.from_numpy(b.x).cuda()
+    lg = torch.from_numpy(b.logits).cuda()
+    first, _, _ = L.forward(x, lg)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for _ in range(5):
+            o2, _, _ = L.forward(x, lg)
+    s.synchronize()
+    np.testing.assert_array_equal(first.cpu().numpy(), o2.cpu().numpy())

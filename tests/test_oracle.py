@@ -1,0 +1,427 @@
+"""Pins the CPU oracle (oracle/zm_oracle.c) before it is trusted as the checker.
+
+Each test is chosen so a plausible restatement mistake (wrong nibble/plane
+order, wrong sub-block scale index, dropped mins term, wrong sign/parity,
+wrong tie order, wrong rounding) fails it.  CPU only.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import zm_oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "ref_dots.npz")
+
+
+def f32bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+# ------------------------------------------------------------------ golden vectors from the reference's own kernels
+
+@pytest.mark.parametrize("name,t", [("q2_K", O.TYPE_Q2_K), ("q4_K", O.TYPE_Q4_K)])
+def test_dot_bit_exact_vs_reference_golden(name, t):
+    """oracle dot == ggml stock AVX2 Q2_K (bench/q2k_dot_bench.cpp:31-63) and the
+    reference's Q4_K 512-bit dot (bench/q3k_q4k_dot_bench.cpp:73-125), bitwise."""
+    g = np.load(GOLDEN, allow_pickle=False)
+    for i, nb in enumerate(g[name + "_nb"]):
+        w = np.ascontiguousarray(g[name + "_w"][i][: nb * O.BLOCK_BYTES[t]])
+        q = np.ascontiguousarray(g[name + "_q8"][i][: nb * 292])
+        got = O.vec_dot(t, w, q.view(O.Q8K_DTYPE))
+        assert f32bits(got) == f32bits(g[name + "_dot"][i]), (name, i)
+
+
+@pytest.mark.skipif(O.ref_lib() is None, reason="oracle/_ref not built (needs /root/reference)")
+@pytest.mark.parametrize("t", [O.TYPE_Q2_K, O.TYPE_Q4_K])
+def test_dot_bit_exact_vs_reference_live(t):
+    R = O.ref_lib()
+    fn = R.zmref_dot_q2_K if t == O.TYPE_Q2_K else R.zmref_dot_q4_K
+    rng = np.random.default_rng(7)
+    for trial in range(300):
+        n = 256 * int(rng.integers(1, 17))
+        w = O.random_blocks(t, 1, n, seed=trial)[0]
+        x = (rng.standard_normal(n) * rng.uniform(1e-3, 1e3)).astype(np.float32)
+        q = O.quantize_q8_K(x)
+        assert f32bits(O.vec_dot(t, w, q)) == f32bits(fn(n, w.ctypes.data, q.ctypes.data))
+
+
+# ------------------------------------------------------------------ dequant known answers
+
+def _blank(t):
+    return np.zeros(O.BLOCK_BYTES[t], np.uint8)
+
+
+def _put_half(b, off, v):
+    h = np.array([v], np.float16).view(np.uint16)[0]
+    b[off] = h & 0xFF
+    b[off + 1] = h >> 8
+
+
+def test_q2_K_known_answer():
+    """Single non-zero weight: qs byte 32h+l, bit-plane j (shift 2j) -> weight
+    128h + 32j + l, scaled by scales[idx/16] (low nibble), min by the high nibble
+    (kquant_matmul.cu:55-72)."""
+    for h, j, l in [(0, 0, 0), (0, 3, 17), (1, 1, 5), (1, 2, 31)]:
+        b = _blank(O.TYPE_Q2_K)
+        _put_half(b, 80, 0.5)     # d
+        _put_half(b, 82, 0.25)    # dmin
+        idx = 128 * h + 32 * j + l
+        b[16 + 32 * h + l] = 3 << (2 * j)
+        b[idx // 16] = 6 | (2 << 4)  # scale 6, min 2 for the sub-block holding idx
+        y = O.dequantize(O.TYPE_Q2_K, b, 256)[0]
+        exp = np.zeros(256, np.float32)
+        exp[(idx // 16) * 16:(idx // 16) * 16 + 16] = -0.25 * 2
+        exp[idx] = 0.5 * 6 * 3 - 0.25 * 2
+        np.testing.assert_array_equal(y, exp)
+
+
+def test_q3_K_known_answer():
+    """hmask bit set = no -4 offset; the hmask byte is hmask[l] for both halves
+    (the pointer never advances, kquant_matmul.cu:186-200); scale index 8h+2j+(l>=16),
+    6-bit signed (value-32): low nibble in scales[k] (k<8) / high nibble of
+    scales[k-8], top 2 bits in scales[8 + k%4] at shift 2*(k/4)."""
+    for h, j, l in [(0, 0, 3), (0, 2, 20), (1, 1, 9), (1, 3, 30)]:
+        b = _blank(O.TYPE_Q3_K)
+        _put_half(b, 108, 0.5)
+        b[0:32] = 0xFF           # all high bits set: values q2 in 0..3
+        idx = 128 * h + 32 * j + l
+        k = idx // 16            # sub-block -> scale index
+        sc6 = 32 + 5             # value 5
+        lo, hi2 = sc6 & 15, sc6 >> 4
+        sc = np.zeros(12, np.uint8)
+        sc[:8] = 0x00
+        # all other scales -> value -32 (raw 0): set raw 0 already; set k
+        if k < 8:
+            sc[k] |= lo
+        else:
+            sc[k - 8] |= lo << 4
+        sc[8 + k % 4] |= hi2 << (2 * (k // 4))
+        b[96:108] = sc
+        b[32 + 32 * h + l] = 2 << (2 * j)
+        y = O.dequantize(O.TYPE_Q3_K, b, 256)[0]
+        exp = np.zeros(256, np.float32)
+        exp[idx] = 0.5 * 5 * 2
+        np.testing.assert_array_equal(y, exp)
+        # clearing the hmask bit subtracts 4 (for every weight of plane j sharing hmask[l])
+        b[l] &= ~np.uint8(1 << (4 * h + j))
+        y2 = O.dequantize(O.TYPE_Q3_K, b, 256)[0]
+        assert y2[idx] == 0.5 * 5 * (2 - 4)
+
+
+def test_q4_K_known_answer():
+    """qs byte 32c+l: low nibble -> weight 64c+l, high -> 64c+32+l; 6-bit
+    (scale, min) of sub-block j from get_scale_min_k4 (kquant_matmul.cu:41-48)."""
+    b = _blank(O.TYPE_Q4_K)
+    _put_half(b, 0, 0.5)
+    _put_half(b, 2, 0.125)
+    sc = [1, 2, 3, 4, 5, 6, 7, 8]
+    mn = [9, 10, 11, 12, 13, 14, 15, 3]
+    raw = np.zeros(12, np.uint8)
+    for j in range(4):
+        raw[j] = sc[j]
+        raw[j + 4] = mn[j]
+    for j in range(4, 8):  # values < 16: high 2 bits zero
+        raw[j + 4] = sc[j] | (mn[j] << 4)
+    # put a 6-bit value in j=5: scale 5+32 -> high bits (>>4)=2 into raw[1]>>6
+    raw[1] |= 2 << 6  # j-4 = 1 -> scale high bits of j=5
+    sc[5] = 6 | 32
+    b[4:16] = raw
+    b[16 + 32 * 2 + 7] = 0x9 | (0x4 << 4)  # c=2, l=7: low 9 -> w[135] (sub 4), high 4 -> w[167] (sub 5)
+    y = O.dequantize(O.TYPE_Q4_K, b, 256)[0]
+    for i in range(256):
+        j = i // 32
+        q = 9 if i == 135 else (4 if i == 167 else 0)
+        assert y[i] == np.float32(0.5 * sc[j]) * q - np.float32(0.125 * mn[j]), i
+
+
+def test_iq2_xxs_known_answer():
+    """value = d*(0.5+ls)*0.25*grid[idx][j]*sign, signs = ksigns[7-bit index]
+    with the 8th sign = parity (iq2_matmul.cu:73-91, patches/ggml/0009...:69-75)."""
+    grid = O.iq2xxs_grid()
+    b = _blank(O.TYPE_IQ2_XXS)
+    _put_half(b, 0, 1.0)
+    ib, l = 3, 2
+    gidx = 17
+    sidx = 0b0000101  # two negatives -> parity 0
+    aux0 = gidx << (8 * l)
+    aux1 = (sidx << (7 * l)) | (6 << 28)
+    qs = b[2:].view(np.uint16)
+    qs[4 * ib + 0] = aux0 & 0xFFFF
+    qs[4 * ib + 1] = aux0 >> 16
+    qs[4 * ib + 2] = aux1 & 0xFFFF
+    qs[4 * ib + 3] = aux1 >> 16
+    y = O.dequantize(O.TYPE_IQ2_XXS, b, 256)[0]
+    gb = [(int(grid[gidx]) >> (8 * j)) & 0xFF for j in range(8)]
+    g0 = [(int(grid[0]) >> (8 * j)) & 0xFF for j in range(8)]
+    for s in range(8):
+        for ll in range(4):
+            for j in range(8):
+                i = 32 * s + 8 * ll + j
+                if s == ib and ll == l:
+                    sign = -1 if j in (0, 2) else 1
+                    exp = 1.0 * (0.5 + 6) * 0.25 * gb[j] * sign
+                elif s == ib:
+                    exp = 1.0 * (0.5 + 6) * 0.25 * g0[j]
+                else:
+                    exp = 1.0 * 0.5 * 0.25 * g0[j]
+                assert y[i] == np.float32(exp), (s, ll, j)
+    # odd 7-bit pattern -> the 8th element is negative too
+    assert O.ksigns()[1] == 0x81 and O.ksigns()[3] == 0x03 and O.ksigns()[127] == 0xFF
+
+
+def test_iq2_grid_stand_in_properties():
+    g = O.iq2xxs_grid()
+    assert len(set(g.tolist())) == 256
+    vals = {0x08: 0, 0x19: 1, 0x2B: 2}
+    for v in g.tolist():
+        digs = [vals[(v >> (8 * j)) & 0xFF] for j in range(8)]
+        assert sum(digs) % 2 == 0
+    assert int(g[0]) == 0x0808080808080808
+
+
+# ------------------------------------------------------------------ integer block dots == brute force over dequant
+
+@pytest.mark.parametrize("t", [O.TYPE_Q2_K, O.TYPE_Q3_K, O.TYPE_Q4_K, O.TYPE_IQ2_XXS])
+def test_block_dots_equal_dequant_brute_force(t):
+    """sum_j sc*dot - dmin*sum m*bsum per block equals dequant(w).dequant(q8)
+    scaled by the block scales, exactly in float64 (integers < 2^53)."""
+    rng = np.random.default_rng(3)
+    n = 1024
+    w = O.random_blocks(t, 1, n, seed=11)[0]
+    x = rng.standard_normal(n).astype(np.float32)
+    q = O.quantize_q8_K(x)
+    isum, imin = O.block_dots(t, w, q)
+    wd = O.dequantize(t, w, n)[0].astype(np.float64)
+    qv = q["qs"].astype(np.float64).reshape(-1)
+    blk = w.reshape(n // 256, O.BLOCK_BYTES[t])
+    for b in range(n // 256):
+        bb = blk[b]
+        if t == O.TYPE_Q2_K:
+            d = float(np.frombuffer(bb[80:82].tobytes(), np.float16)[0])
+            dm = float(np.frombuffer(bb[82:84].tobytes(), np.float16)[0])
+            exp = d * isum[b] - dm * imin[b]
+        elif t == O.TYPE_Q3_K:
+            exp = float(np.frombuffer(bb[108:110].tobytes(), np.float16)[0]) * isum[b]
+        elif t == O.TYPE_Q4_K:
+            d = float(np.frombuffer(bb[0:2].tobytes(), np.float16)[0])
+            dm = float(np.frombuffer(bb[2:4].tobytes(), np.float16)[0])
+            exp = d * isum[b] - dm * imin[b]
+        else:
+            exp = float(np.frombuffer(bb[0:2].tobytes(), np.float16)[0]) * isum[b] / 8.0
+        got = float(np.dot(wd[256 * b:256 * b + 256], qv[256 * b:256 * b + 256]))
+        assert abs(got - exp) <= 1e-9 * max(1.0, abs(exp)), (b, got, exp)
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q2_K, O.TYPE_Q3_K, O.TYPE_Q4_K, O.TYPE_IQ2_XXS])
+def test_vec_dot_matches_dequant_dot(t):
+    rng = np.random.default_rng(5)
+    n = 2048
+    w = O.random_blocks(t, 4, n, seed=2)
+    for r in range(4):
+        x = rng.standard_normal(n).astype(np.float32)
+        q = O.quantize_q8_K(x)
+        ref = float(np.dot(O.dequantize(t, w[r], n)[0].astype(np.float64),
+                           O.dequantize(O.TYPE_Q8_K, q, n)[0].astype(np.float64)))
+        got = O.vec_dot(t, w[r], q)
+        assert abs(got - ref) <= 1e-5 * max(1e-3, abs(ref)) + 1e-6
+
+
+# ------------------------------------------------------------------ Q8_K quantization closed forms
+
+def test_q8_K_closed_forms():
+    x = np.zeros(256, np.float32)
+    x[:6] = [-127, 0.5, 1.5, 2.5, -0.5, -1.5]   # max=-127 -> iscale = 1: round half even
+    q = O.quantize_q8_K(x)[0]
+    assert q["d"] == 1.0
+    np.testing.assert_array_equal(q["qs"][:6], [-127, 0, 2, 2, 0, -2])
+    assert q["bsums"][0] == -127 + 0 + 2 + 2 + 0 - 2
+    # first maximal |x| wins the sign: [-2, 2] -> max = -2, iscale = 63.5
+    x = np.zeros(256, np.float32)
+    x[10], x[20] = -2.0, 2.0
+    q = O.quantize_q8_K(x)[0]
+    assert q["qs"][10] == -127 and q["qs"][20] == 127
+    assert q["d"] == np.float32(1.0) / np.float32(-127.0 / -2.0)
+    x[10], x[20] = 2.0, -2.0
+    q = O.quantize_q8_K(x)[0]
+    assert q["qs"][10] == -127 and q["qs"][20] == 127  # iscale = -63.5 now
+    # all zero
+    q = O.quantize_q8_K(np.zeros(256, np.float32))[0]
+    assert q["d"] == 0 and not q["qs"].any() and not q["bsums"].any()
+    # 16-sums of a random row
+    x = np.random.default_rng(1).standard_normal(512).astype(np.float32)
+    q = O.quantize_q8_K(x)
+    for b in range(2):
+        np.testing.assert_array_equal(q[b]["bsums"], q[b]["qs"].astype(np.int32).reshape(16, 16).sum(1))
+        assert np.abs(q[b]["qs"]).max() == 127
+
+
+# ------------------------------------------------------------------ float helpers
+
+def test_fp16_conversions_exhaustive():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ref = h.view(np.float16).astype(np.float32)
+    got = np.array([O.fp16_to_fp32(int(v)) for v in h[::97]], np.float32)
+    np.testing.assert_array_equal(f32bits(got)[~np.isnan(ref[::97])], f32bits(ref[::97])[~np.isnan(ref[::97])])
+    rng = np.random.default_rng(0)
+    xs = np.concatenate([rng.standard_normal(3000) * 10.0 ** rng.uniform(-9, 5, 3000),
+                         [65504, 65519.9, 65520, 6e-8, 2.9e-8, 3e-8, 0.0, -0.0]]).astype(np.float32)
+    for v in xs:
+        assert O.fp32_to_fp16(float(v)) == np.float16(v).view(np.uint16), v
+
+
+def test_expf_accuracy():
+    xs = np.linspace(-100, 88, 200001).astype(np.float32)
+    got = np.array([O.expf(float(v)) for v in xs[::13]], np.float64)
+    ref = np.exp(xs[::13].astype(np.float64))
+    ok = ref > 1.2e-38  # normal range
+    ulp = np.abs(got[ok] - ref[ok]) / np.spacing(ref[ok].astype(np.float32)).astype(np.float64)
+    assert ulp.max() <= 2.0, ulp.max()
+    assert O.expf(0.0) == 1.0 and O.expf(-1000.0) == 0.0 and O.expf(1000.0) == np.inf
+
+
+# ------------------------------------------------------------------ router / bucketing (brute force)
+
+def _router_np(logits, K, gating, logit_bias=None, sel_bias=None, G=0, GU=0, norm=False, scale=0.0):
+    S, E = logits.shape
+    ids = np.zeros((S, K), np.int32)
+    w = np.zeros((S, K), np.float32)
+    for s in range(S):
+        l = logits[s].astype(np.float32)
+        if logit_bias is not None:
+            l = (l + logit_bias).astype(np.float32)
+        if gating == O.GATING_SOFTMAX:
+            e = np.array([O.expf(float(v - l.max())) for v in l], np.float32)
+            p = (e * np.float32(1.0 / e.astype(np.float64).sum())).astype(np.float32)
+        else:
+            p = np.array([1.0 / (1.0 + O.expf(float(-v))) for v in l], np.float32)
+        sel = p if sel_bias is None else (p + sel_bias).astype(np.float32)
+        sel = sel.copy()
+        if G > 1 and 0 < GU < G:
+            gs = E // G
+            sc = []
+            for g in range(G):
+                v = sel[g * gs:(g + 1) * gs]
+                o = sorted(range(gs), key=lambda j: (-v[j], j))
+                sc.append(np.float32(v[o[0]] + v[o[1]]))
+            keep = sorted(range(G), key=lambda g: (-sc[g], g))[:GU]
+            for e_ in range(E):
+                if e_ // gs not in keep:
+                    sel[e_] = -np.inf
+        order = sorted(range(E), key=lambda e_: (-sel[e_], e_))[:K]
+        ids[s] = order
+        w[s] = p[order]
+        if norm:
+            sm = np.float32(w[s].astype(np.float64).sum())
+            w[s] = w[s] / max(sm, np.float32(6.103515625e-5))
+        if scale not in (0.0, 1.0):
+            w[s] = w[s] * np.float32(scale)
+    return ids, w
+
+
+@pytest.mark.parametrize("case", ["softmax", "softmax_bias", "sigmoid_groups", "ties"])
+def test_router_brute_force(case):
+    rng = np.random.default_rng(9)
+    if case == "softmax":
+        lg = rng.standard_normal((5, 128)).astype(np.float32)
+        args = dict(K=8, gating=O.GATING_SOFTMAX)
+    elif case == "softmax_bias":
+        lg = rng.standard_normal((5, 128)).astype(np.float32)
+        args = dict(K=8, gating=O.GATING_SOFTMAX, logit_bias=(rng.standard_normal(128) * 1.5).astype(np.float32),
+                    norm=True)
+    elif case == "sigmoid_groups":
+        lg = rng.standard_normal((4, 256)).astype(np.float32)
+        args = dict(K=8, gating=O.GATING_SIGMOID, sel_bias=(rng.standard_normal(256) * 0.1).astype(np.float32),
+                    G=8, GU=4, norm=True, scale=2.5)
+    else:
+        lg = np.round(rng.standard_normal((6, 64)) * 2).astype(np.float32)  # many exact ties
+        args = dict(K=6, gating=O.GATING_SOFTMAX)
+    ids, w = O.router(lg, args["K"], args["gating"], args.get("logit_bias"), args.get("sel_bias"),
+                      args.get("G", 0), args.get("GU", 0), args.get("norm", False), args.get("scale", 0.0))
+    ri, rw = _router_np(lg, **args)
+    np.testing.assert_array_equal(ids, ri)
+    np.testing.assert_allclose(w, rw, rtol=2e-7, atol=0)
+
+
+def test_bucket_is_stable_counting_sort():
+    rng = np.random.default_rng(4)
+    S, K, E = 200, 8, 40
+    ids = rng.integers(-1, E, size=(S, K)).astype(np.int32)
+    counts, offs, pairs = O.bucket(ids, E)
+    flat = ids.reshape(-1)
+    valid = np.nonzero(flat >= 0)[0]
+    order = valid[np.argsort(flat[valid], kind="stable")]
+    np.testing.assert_array_equal(pairs, order)
+    np.testing.assert_array_equal(counts, np.bincount(flat[valid], minlength=E))
+    np.testing.assert_array_equal(offs, np.concatenate([[0], np.cumsum(counts)]))
+
+
+def test_slot_table():
+    rmap = np.array([3, -1, 0, 1, -1, 2], np.int32)
+    ids = np.array([[0, 1, 2], [5, 4, 3]], np.int32)
+    w = np.array([[0.5, 0.25, 0.25], [0.1, 0.2, 0.7]], np.float32)
+    i2, w2 = O.apply_slot_table(rmap, ids, w)
+    np.testing.assert_array_equal(i2, [[3, -1, 0], [2, -1, 1]])
+    np.testing.assert_array_equal(w2, np.array([[0.5, 0.0, 0.25], [0.1, 0.0, 0.7]], np.float32))
+
+
+# ------------------------------------------------------------------ op semantics
+
+@pytest.mark.parametrize("t", [O.TYPE_Q2_K, O.TYPE_Q3_K, O.TYPE_Q4_K, O.TYPE_IQ2_XXS])
+def test_mul_mat_id_semantics(t):
+    """dst[t,id] = vec_dot(W[ids], q8(x[id % ne11])); id < 0 -> zeros
+    (patches/ggml/0002...:46-58); ids like bench/mmid_exact_check.cpp:41."""
+    I, O_, E, n_ids, S = 512, 8, 24, 10, 2
+    W = O.random_blocks(t, E * O_, I, seed=t).reshape(E, O_, -1)
+    rng = np.random.default_rng(11)
+    ids = np.array([[3, -1, 17, -1, -1, 8, -1, -1, -1, 21], [0, 1, 2, 3, 4, 5, 6, 7, 23, -1]], np.int32)
+    for ne11 in (1, n_ids):
+        x = rng.standard_normal((S, ne11, I)).astype(np.float32)
+        y = O.mul_mat_id(t, W, x, ids)
+        for s in range(S):
+            for k in range(n_ids):
+                e = ids[s, k]
+                if e < 0:
+                    assert not y[s, k].any()
+                    continue
+                q = O.quantize_q8_K(x[s, k % ne11])
+                for r in range(O_):
+                    assert f32bits(y[s, k, r]) == f32bits(O.vec_dot(t, W[e, r], q))
+    # multithreaded == single threaded, bitwise
+    x = rng.standard_normal((S, 1, I)).astype(np.float32)
+    np.testing.assert_array_equal(O.mul_mat_id(t, W, x, ids, 1), O.mul_mat_id(t, W, x, ids, 4))
+
+
+def test_moe_forward_composition():
+    """moe_forward == mul_mat_id(gate/up) -> swiglu -> mul_mat_id(down) ->
+    ((w0*y0 + w1*y1) + ...) with float32 rounding at every step."""
+    H, F, E, K, S = 512, 256, 6, 3, 2
+    tg, td = O.TYPE_Q4_K, O.TYPE_Q3_K
+    Wg = O.random_blocks(tg, E * F, H, 1).reshape(E, F, -1)
+    Wu = O.random_blocks(tg, E * F, H, 2).reshape(E, F, -1)
+    Wd = O.random_blocks(td, E * H, F, 3).reshape(E, H, -1)
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((S, H)).astype(np.float32)
+    ids = np.array([[1, 4, -1], [5, 0, 2]], np.int32)
+    w = np.array([[0.5, 0.3, 0.2], [0.6, 0.25, 0.15]], np.float32)
+    out = O.moe_forward(x, ids, w, tg, tg, td, Wg, Wu, Wd)
+    g = O.mul_mat_id(tg, Wg, x[:, None, :], ids)
+    u = O.mul_mat_id(tg, Wu, x[:, None, :], ids)
+    a = O.swiglu(g, u)
+    d = O.mul_mat_id(td, Wd, a, ids)
+    ref = np.zeros((S, H), np.float32)
+    for s in range(S):
+        acc = (w[s, 0] * d[s, 0]).astype(np.float32)
+        for k in range(1, K):
+            acc = (acc + (w[s, k] * d[s, k]).astype(np.float32)).astype(np.float32)
+        ref[s] = acc
+    np.testing.assert_array_equal(out, ref)
+
+
+@pytest.mark.parametrize("t,tol", [(O.TYPE_Q2_K, 0.40), (O.TYPE_Q3_K, 0.20), (O.TYPE_Q4_K, 0.09),
+                                   (O.TYPE_IQ2_XXS, 0.40)])
+def test_quantizer_round_trip(t, tol):
+    x = O.fill_normal(42, 8 * 1024, 0.0, 0.02).reshape(8, 1024)
+    y = O.dequantize(t, O.quantize(t, x), 1024)
+    rel = np.sqrt(((x - y) ** 2).mean() / (x ** 2).mean())
+    assert rel < tol, rel

@@ -1,0 +1,23 @@
+"""zeromoe_amd -- MI355X (gfx950) routed-expert MUL_MAT_ID path.
+
+Host mirror of the reference's operator surface over the C ABI of
+libzeromoe_hip.so (include/zeromoe.h):
+
+* :func:`mul_mat_id` -- ``ggml_mul_mat_id`` semantics on device tensors
+  (/root/reference/models/graph/moe_routed_ggml.hpp:172-193).
+* :func:`router` -- ``moe_routed::gate_probs/select_ids/route_weights``
+  (moe_routed_ggml.hpp:52-141) with the slot table of
+  ``make_branch_inputs`` (backends/ggml/moe_partial_route_ggml.hpp:21-35).
+* :func:`bucket` -- the per-expert CSR of core/batched_dispatch_pipeline.cpp:1181-1202.
+* :class:`MoELayer` -- one routed layer (expert_ffn + weighted sum_topk +
+  shared expert, moe_routed_ggml.hpp:166-214, moe_block.hpp:86-105).
+
+Torch is used only for device memory and the current stream.
+"""
+from __future__ import annotations
+
+from .ops import (GGML_TYPES, MoELayer, block_dots, bucket, init, mul_mat_id, quantize_q8_K, router, row_size,
+                  set_iq2xxs_grid, builtin_iq2xxs_grid)
+
+__all__ = ["GGML_TYPES", "MoELayer", "block_dots", "bucket", "init", "mul_mat_id", "quantize_q8_K", "router",
+           "row_size", "set_iq2xxs_grid", "builtin_iq2xxs_grid"]

@@ -1,0 +1,73 @@
+"""ctypes binding of libzeromoe_hip.so (include/zeromoe.h).
+
+The shared library is built in-tree by ``zeromoe_amd.build.build()``.  Loading
+fails loudly when it is missing: there is no CPU fallback anywhere in the
+product path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "lib", "libzeromoe_hip.so")
+
+P, I, I32, I64, U64, F, SZ = C.c_void_p, C.c_int, C.c_int32, C.c_int64, C.c_uint64, C.c_float, C.c_size_t
+
+
+class ZmTensor(C.Structure):
+    _fields_ = [("type", C.c_int32), ("ne", C.c_int64 * 4), ("nb", C.c_size_t * 4), ("data", C.c_void_p)]
+
+
+class ZmRouterSpec(C.Structure):
+    _fields_ = [("gating", I32), ("n_experts", I32), ("topk", I32), ("n_groups", I32), ("n_groups_used", I32),
+                ("weights_norm", I32), ("weights_scale", F)]
+
+
+class ZmMoeLayer(C.Structure):
+    _fields_ = [("H", I32), ("F", I32), ("n_slots", I32), ("router", ZmRouterSpec),
+                ("type_gate", I32), ("type_up", I32), ("type_down", I32),
+                ("w_gate", P), ("w_up", P), ("w_down", P),
+                ("router_w", P), ("logit_bias", P), ("sel_bias", P), ("route_map", P), ("route_mask", P),
+                ("F_shared", I32), ("type_shared", I32), ("ws_gate", P), ("ws_up", P), ("ws_down", P)]
+
+
+# name -> (restype, argtypes); every function declared in include/zeromoe.h
+SIGNATURES = {
+    "zm_init": (I, []),
+    "zm_last_error": (C.c_char_p, []),
+    "zm_version": (C.c_char_p, []),
+    "zm_set_iq2xxs_grid": (I, [P]),
+    "zm_iq2xxs_builtin_grid": (None, [P]),
+    "zm_mul_mat_id_negative_skip": (I, []),
+    "zm_mul_mat_id_negative_skip_batched": (I, []),
+    "zm_mul_mat_id": (I, [C.POINTER(ZmTensor)] * 3 + [C.POINTER(ZmTensor), P, I]),
+    "zm_mul_mat_id_launches": (U64, []),
+    "zm_quantize_q8_K": (I, [P, I64, I64, P, P]),
+    "zm_router": (I, [C.POINTER(ZmRouterSpec), P, P, P, P, P, I, P, P, P]),
+    "zm_bucket": (I, [P, I, I, I, P, P, P, P, P, P]),
+    "zm_block_dots": (I, [I, P, P, I, P, P, P]),
+    "zm_moe_workspace_size": (SZ, [C.POINTER(ZmMoeLayer), I]),
+    "zm_moe_forward": (I, [C.POINTER(ZmMoeLayer), P, P, I, P, P, P, P, SZ, P]),
+}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: run `python -c 'import __graft_entry__ as g; g.build()'`")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed ({rc}): {lib().zm_last_error().decode()}")

@@ -1,0 +1,618 @@
+// zm_api.hip -- host side of libzeromoe_hip.so: the C ABI declared in
+// include/zeromoe.h, argument validation, template dispatch and the per-device
+// tables.  Everything below launches stream-ordered HIP work.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <atomic>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "../../include/zeromoe.h"
+#include "zm_kernels.hpp"
+
+using namespace zm;
+
+namespace {
+
+thread_local char g_err[512] = "";
+std::atomic<uint64_t> g_mmid_launches{0};
+
+int fail(const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return -1;
+}
+
+#define HIP_OK(call)                                                                  \
+  do {                                                                                \
+    hipError_t e_ = (call);                                                           \
+    if (e_ != hipSuccess) return fail("%s: %s", #call, hipGetErrorString(e_));        \
+  } while (0)
+
+// ------------------------------------------------------------------ per-device state
+
+constexpr int kMaxDevices = 16;
+
+struct DeviceState {
+  bool ready = false;
+  uint64_t *grid = nullptr;   // IQ2_XXS grid, 256 x u64
+  uint64_t *signs = nullptr;  // 128 x u64 byte masks of ksigns_iq2xs
+  void *ws = nullptr;         // zm_mul_mat_id workspace
+  size_t ws_size = 0;
+};
+DeviceState g_dev[kMaxDevices];
+std::mutex g_mu;
+
+void builtin_grid(uint64_t grid[256]) {
+  // the 256 vectors of {1,3,5}^8 with an even digit sum ((v-1)/2 summed) of
+  // smallest norm, lexicographic (coordinate 0 most significant) on ties;
+  // coordinate bytes 1 -> 0x08, 3 -> 0x19, 5 -> 0x2b
+  static const uint8_t bytev[3] = {0x08, 0x19, 0x2b};
+  int count = 0;
+  for (int norm = 0; norm < 200 && count < 256; ++norm)
+    for (int idx = 0; idx < 6561 && count < 256; ++idx) {
+      int t = idx, dig[8], sd = 0, nn = 0;
+      for (int j = 7; j >= 0; --j) {
+        dig[j] = t % 3;
+        t /= 3;
+      }
+      for (int j = 0; j < 8; ++j) {
+        sd += dig[j];
+        nn += (1 + 2 * dig[j]) * (1 + 2 * dig[j]);
+      }
+      if ((sd & 1) || nn != norm) continue;
+      uint64_t g = 0;
+      for (int j = 0; j < 8; ++j) g |= (uint64_t)bytev[dig[j]] << (8 * j);
+      grid[count++] = g;
+    }
+}
+
+int device_state(DeviceState **out) {
+  int dev = 0;
+  HIP_OK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return fail("device %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_mu);
+  DeviceState &d = g_dev[dev];
+  if (!d.ready) {
+    uint64_t grid[256], signs[128];
+    builtin_grid(grid);
+    for (int i = 0; i < 128; ++i) {
+      const int s = i | ((__builtin_popcount(i) & 1) << 7);  // ksigns_iq2xs
+      uint64_t m = 0;
+      for (int j = 0; j < 8; ++j)
+        if ((s >> j) & 1) m |= 0xffull << (8 * j);
+      signs[i] = m;
+    }
+    HIP_OK(hipMalloc(&d.grid, sizeof(grid)));
+    HIP_OK(hipMalloc(&d.signs, sizeof(signs)));
+    HIP_OK(hipMemcpy(d.grid, grid, sizeof(grid), hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(d.signs, signs, sizeof(signs), hipMemcpyHostToDevice));
+    d.ready = true;
+  }
+  *out = &d;
+  return 0;
+}
+
+// ------------------------------------------------------------------ GEMV dispatch
+
+template <int T, int LPR, int ITER, int NP, bool GU>
+void launch_gemv_t(dim3 grid, const GemvArgs &a, hipStream_t st) {
+  hipLaunchKernelGGL((k_gemv<T, LPR, ITER, NP, GU>), grid, dim3(256), 0, st, a);
+}
+
+template <int T, int NP, bool GU>
+int launch_gemv_np(int U, dim3 grid, const GemvArgs &a, hipStream_t st) {
+  if (U <= 16) launch_gemv_t<T, 16, 1, NP, GU>(grid, a, st);
+  else if (U <= 32) launch_gemv_t<T, 32, 1, NP, GU>(grid, a, st);
+  else if (U <= 64) launch_gemv_t<T, 64, 1, NP, GU>(grid, a, st);
+  else if (U <= 128) launch_gemv_t<T, 64, 2, NP, GU>(grid, a, st);
+  else if (U <= 192) launch_gemv_t<T, 64, 3, NP, GU>(grid, a, st);
+  else if (U <= 256) launch_gemv_t<T, 64, 4, NP, GU>(grid, a, st);
+  else return fail("row of %d blocks exceeds the 64-block limit", U / 4);
+  return 0;
+}
+
+template <int T, bool GU>
+int launch_gemv_type(int np, int U, dim3 grid, const GemvArgs &a, hipStream_t st) {
+  if (np >= 4) return launch_gemv_np<T, 4, GU>(U, grid, a, st);
+  if (np >= 2) return launch_gemv_np<T, 2, GU>(U, grid, a, st);
+  return launch_gemv_np<T, 1, GU>(U, grid, a, st);
+}
+
+bool type_supported(int t) { return t == T_Q2_K || t == T_Q3_K || t == T_Q4_K || t == T_IQ2_XXS; }
+
+size_t row_bytes(int t, int64_t n) { return (size_t)(n / QK) * block_bytes(t); }
+
+// pairs per bucket chunk held in registers
+int pick_np(int n_pairs, int n_experts) {
+  const int act = std::max(1, std::min(n_pairs, n_experts));
+  const double avg = (double)n_pairs / act;
+  return avg >= 3.0 ? 4 : (avg >= 1.5 ? 2 : 1);
+}
+
+// rows per workgroup: enough workgroups to cover the chip several times over
+int pick_tile(int nrows, int U, int n_groups) {
+  const int lpr = U <= 16 ? 16 : (U <= 32 ? 32 : 64);
+  const int step = 4 * (64 / lpr);  // rows one workgroup covers per step
+  const int target_wgs = 2048;
+  const int tiles = std::max(1, target_wgs / std::max(1, n_groups));
+  int tile = (nrows + tiles - 1) / tiles;
+  tile = ((tile + step - 1) / step) * step;
+  return std::max(step, tile);
+}
+
+int launch_gemv(int type, bool gateup, int np, const GemvArgs &a0, int n_groups, hipStream_t st) {
+  GemvArgs a = a0;
+  const int U = a.nb * 4;
+  a.tile_rows = pick_tile(a.nrows, U, n_groups);
+  dim3 grid((a.nrows + a.tile_rows - 1) / a.tile_rows, n_groups);
+  int rc;
+  switch (type) {
+  case T_Q2_K: rc = gateup ? launch_gemv_type<T_Q2_K, true>(np, U, grid, a, st) : launch_gemv_type<T_Q2_K, false>(np, U, grid, a, st); break;
+  case T_Q3_K: rc = gateup ? launch_gemv_type<T_Q3_K, true>(np, U, grid, a, st) : launch_gemv_type<T_Q3_K, false>(np, U, grid, a, st); break;
+  case T_Q4_K: rc = gateup ? launch_gemv_type<T_Q4_K, true>(np, U, grid, a, st) : launch_gemv_type<T_Q4_K, false>(np, U, grid, a, st); break;
+  case T_IQ2_XXS: rc = gateup ? launch_gemv_type<T_IQ2_XXS, true>(np, U, grid, a, st) : launch_gemv_type<T_IQ2_XXS, false>(np, U, grid, a, st); break;
+  default: return fail("unsupported weight type %d", type);
+  }
+  if (rc) return rc;
+  HIP_OK(hipGetLastError());
+  return 0;
+}
+
+int launch_quant(const float *x, size_t x_rstride, int nb, int rows, uint8_t *y, size_t y_rstride, int planar,
+                 hipStream_t st) {
+  if (rows <= 0) return 0;
+  const long waves = (long)rows * nb;
+  hipLaunchKernelGGL(k_quant_q8K, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, x, x_rstride, nb, rows, y,
+                     y_rstride, planar);
+  HIP_OK(hipGetLastError());
+  return 0;
+}
+
+// simple bump allocator over a caller workspace
+struct Bump {
+  uint8_t *base;
+  size_t off = 0;
+  template <class P>
+  P *take(size_t bytes) {
+    off = (off + 255) & ~(size_t)255;
+    P *p = reinterpret_cast<P *>(base ? base + off : nullptr);
+    off += bytes;
+    return p;
+  }
+};
+
+}  // namespace
+
+// ====================================================================== C ABI
+
+extern "C" {
+
+const char *zm_last_error(void) { return g_err; }
+const char *zm_version(void) { return "zeromoe_amd 0.1 (gfx950)"; }
+
+int zm_init(void) {
+  DeviceState *d;
+  return device_state(&d);
+}
+
+void zm_iq2xxs_builtin_grid(uint64_t grid[256]) { builtin_grid(grid); }
+
+int zm_set_iq2xxs_grid(const uint64_t grid[256]) {
+  DeviceState *d;
+  if (device_state(&d)) return -1;
+  HIP_OK(hipMemcpy(d->grid, grid, 256 * sizeof(uint64_t), hipMemcpyHostToDevice));
+  return 0;
+}
+
+int zm_mul_mat_id_negative_skip(void) { return 1; }
+int zm_mul_mat_id_negative_skip_batched(void) { return 1; }
+uint64_t zm_mul_mat_id_launches(void) { return g_mmid_launches.load(std::memory_order_relaxed); }
+
+int zm_quantize_q8_K(const float *x, int64_t rows, int64_t n, void *y, void *stream) {
+  if (!x || !y || rows < 0 || n <= 0 || n % QK) return fail("zm_quantize_q8_K: bad arguments");
+  return launch_quant(x, (size_t)n, (int)(n / QK), (int)rows, (uint8_t *)y, (size_t)(n / QK) * 292, 0,
+                      (hipStream_t)stream);
+}
+
+int zm_router(const zm_router_spec *spec, const float *logits, const float *logit_bias, const float *sel_bias,
+              const int32_t *route_map, const float *route_mask, int S, int32_t *ids, float *weights,
+              void *stream) {
+  if (!spec || !logits || !ids || !weights || S < 0) return fail("zm_router: null argument");
+  if (spec->n_experts <= 0 || spec->n_experts > ROUTER_MAX_E) return fail("zm_router: n_experts out of range");
+  if (spec->topk <= 0 || spec->topk > spec->n_experts || spec->topk > 64) return fail("zm_router: bad topk");
+  if (spec->n_groups > 64) return fail("zm_router: n_groups > 64");
+  if (spec->gating < 0 || spec->gating > 2) return fail("zm_router: bad gating");
+  if (S == 0) return 0;
+  RouterArgs a{logits, logit_bias, sel_bias, route_map, route_mask, spec->n_experts, spec->topk, spec->gating,
+               spec->n_groups, spec->n_groups_used, spec->weights_norm, spec->weights_scale, ids, weights};
+  hipLaunchKernelGGL(k_router, dim3(S), dim3(64), 0, (hipStream_t)stream, a);
+  HIP_OK(hipGetLastError());
+  return 0;
+}
+
+int zm_bucket(const int32_t *ids, int S, int K, int E, int32_t *counts, int32_t *offs, int32_t *pairs,
+              int32_t *active, int32_t *n_active, void *stream) {
+  if (!ids || !counts || !offs || !pairs || !active || !n_active) return fail("zm_bucket: null argument");
+  if (E <= 0 || E > BUCKET_MAX_E) return fail("zm_bucket: E out of range (1..%d)", BUCKET_MAX_E);
+  if (S < 0 || K <= 0) return fail("zm_bucket: bad S/K");
+  hipLaunchKernelGGL(k_bucket, dim3(1), dim3(1024), 0, (hipStream_t)stream, ids, S * K, E, counts, offs, pairs,
+                     active, n_active);
+  HIP_OK(hipGetLastError());
+  return 0;
+}
+
+// ---------------------------------------------------------------- mul_mat_id hook
+
+int zm_mul_mat_id(const zm_tensor *w, const zm_tensor *x, const zm_tensor *ids, zm_tensor *y, void *stream,
+                  int execute) {
+  if (!w || !x || !ids || !y) return 0;
+  if (!type_supported(w->type) || x->type != T_F32 || y->type != T_F32 || ids->type != T_I32) return 0;
+  const int64_t I = w->ne[0], O = w->ne[1], E = w->ne[2];
+  if (I <= 0 || I % QK || I / QK > 64 || O <= 0 || O > INT32_MAX || E <= 0 || E > BUCKET_MAX_E || w->ne[3] != 1)
+    return 0;
+  if (w->nb[1] != row_bytes(w->type, I) || w->nb[2] < (size_t)O * w->nb[1]) return 0;
+  const int64_t n_ids = ids->ne[0], S = ids->ne[1];
+  if (ids->nb[0] != 4 || n_ids <= 0 || S <= 0 || ids->ne[2] != 1 || ids->ne[3] != 1) return 0;
+  if (x->nb[0] != 4 || x->ne[0] != I || (x->ne[1] != 1 && x->ne[1] != n_ids) || x->ne[2] != S || x->ne[3] != 1)
+    return 0;
+  if (x->nb[1] % 16 || x->nb[2] % 16 || ((uintptr_t)x->data & 15)) return 0;  // float4 row loads
+  if (y->nb[0] != 4 || y->ne[0] != O || y->ne[1] != n_ids || y->ne[2] != S || y->ne[3] != 1) return 0;
+  if (y->nb[1] % 4 || y->nb[2] % 4 || ids->nb[1] % 4) return 0;
+  const int64_t n_pairs = n_ids * S;
+  if (n_pairs > (1 << 24)) return 0;
+  if (!execute) return 1;
+
+  hipStream_t st = (hipStream_t)stream;
+  DeviceState *d;
+  if (device_state(&d)) return 0;
+  const int nb = (int)(I / QK);
+  const int ne11 = (int)x->ne[1];
+  // workspace: q8 rows, a contiguous copy of ids, bucket arrays
+  const int64_t nq = (int64_t)ne11 * S;
+  Bump sz{nullptr};
+  sz.take<uint8_t>((size_t)nq * q8_row_bytes(nb));
+  sz.take<int32_t>((size_t)n_pairs * 4);
+  sz.take<int32_t>((size_t)E * 4);
+  sz.take<int32_t>((size_t)(E + 1) * 4);
+  sz.take<int32_t>((size_t)n_pairs * 4);
+  sz.take<int32_t>((size_t)E * 4);
+  sz.take<int32_t>(4);
+  const size_t need = sz.off + 256;
+  if (d->ws_size < need) {
+    if (d->ws) (void)hipFree(d->ws);
+    d->ws = nullptr;
+    d->ws_size = 0;
+    if (hipMalloc(&d->ws, need) != hipSuccess) {
+      fail("zm_mul_mat_id: workspace allocation of %zu bytes failed", need);
+      return 0;
+    }
+    d->ws_size = need;
+  }
+  Bump b{(uint8_t *)d->ws};
+  uint8_t *xq = b.take<uint8_t>((size_t)nq * q8_row_bytes(nb));
+  int32_t *idc = b.take<int32_t>((size_t)n_pairs * 4);
+  int32_t *counts = b.take<int32_t>((size_t)E * 4);
+  int32_t *offs = b.take<int32_t>((size_t)(E + 1) * 4);
+  int32_t *pairs = b.take<int32_t>((size_t)n_pairs * 4);
+  int32_t *active = b.take<int32_t>((size_t)E * 4);
+  int32_t *n_active = b.take<int32_t>(4);
+
+  // 1. quantize src1 rows (token t, row i11) -> planar Q8_K row t*ne11 + i11
+  if (x->nb[2] == (size_t)ne11 * x->nb[1]) {
+    if (launch_quant((const float *)x->data, x->nb[1] / 4, nb, (int)nq, xq, q8_row_bytes(nb), 1, st)) return 0;
+  } else {
+    for (int64_t t = 0; t < S; ++t) {
+      const float *xt = (const float *)((const char *)x->data + t * x->nb[2]);
+      if (launch_quant(xt, x->nb[1] / 4, nb, ne11, xq + (size_t)t * ne11 * q8_row_bytes(nb), q8_row_bytes(nb), 1,
+                       st))
+        return 0;
+    }
+  }
+  // 2. ids -> contiguous [S][n_ids] (strided copy), then bucket
+  if (ids->nb[1] == (size_t)n_ids * 4) {
+    if (hipMemcpyAsync(idc, ids->data, (size_t)n_pairs * 4, hipMemcpyDeviceToDevice, st) != hipSuccess) return 0;
+  } else {
+    if (hipMemcpy2DAsync(idc, (size_t)n_ids * 4, ids->data, ids->nb[1], (size_t)n_ids * 4, (size_t)S,
+                         hipMemcpyDeviceToDevice, st) != hipSuccess)
+      return 0;
+  }
+  hipLaunchKernelGGL(k_bucket, dim3(1), dim3(1024), 0, st, idc, (int)n_pairs, (int)E, counts, offs, pairs, active,
+                     n_active);
+  // 3. skipped / invalid routes
+  hipLaunchKernelGGL(k_fill_skipped, dim3((unsigned)std::min<int64_t>((O + 255) / 256, 64), (unsigned)n_pairs),
+                     dim3(256), 0, st, idc, (size_t)n_ids, (size_t)1, (int)n_ids, (int)S, (int)E, (int)O,
+                     (float *)y->data, y->nb[2] / 4, y->nb[1] / 4);
+  // 4. bucketed GEMV
+  GemvArgs a{};
+  a.w0 = (const uint8_t *)w->data;
+  a.w_estride = w->nb[2];
+  a.w_rstride = w->nb[1];
+  a.nrows = (int)O;
+  a.nb = nb;
+  a.xq = xq;
+  a.xq_rstride = q8_row_bytes(nb);
+  a.ne11 = ne11;
+  a.K = (int)n_ids;
+  a.n_active = n_active;
+  a.active = active;
+  a.offs = offs;
+  a.pairs = pairs;
+  a.out = (float *)y->data;
+  a.out_s = y->nb[2] / 4;
+  a.out_k = y->nb[1] / 4;
+  a.grid = d->grid;
+  a.signs = d->signs;
+  const int groups = (int)std::min<int64_t>(E, n_pairs);
+  if (launch_gemv(w->type, false, pick_np((int)n_pairs, (int)E), a, groups, st)) return 0;
+  g_mmid_launches.fetch_add(1, std::memory_order_relaxed);
+  return hipPeekAtLastError() == hipSuccess ? 1 : 0;
+}
+
+// ---------------------------------------------------------------- debug: block dots
+
+}  // extern "C"
+
+namespace {
+template <int T>
+__global__ void k_block_dots(const uint8_t *w, const uint8_t *xq, int nb, int32_t *isum, int32_t *imin) {
+  const int lane = threadIdx.x & 63;
+  const int gq = blockIdx.x * 64 + lane;  // quarter index
+  const int b = gq >> 2, q = gq & 3;
+  QInt r{0, 0};
+  __shared__ uint64_t dummy[1];
+  (void)dummy;
+  if (b < nb) {
+    Q8Slice s;
+    WSlice ws;
+    load_q8_slice<T>(xq, nb, b, q, s);
+    load_w_slice<T>(w + (size_t)b * block_bytes(T), q, ws);
+    r = quarter_int<T>(ws, q, s, nullptr, nullptr);
+  }
+  r.isum = group_sum_i<4>(r.isum);
+  r.imin = group_sum_i<4>(r.imin);
+  if (b < nb && q == 0) {
+    isum[b] = r.isum;
+    imin[b] = r.imin;
+  }
+}
+// IQ2 variant needs the tables (from global memory directly)
+__global__ void k_block_dots_iq2(const uint8_t *w, const uint8_t *xq, int nb, int32_t *isum, int32_t *imin,
+                                 const uint64_t *grid, const uint64_t *signs) {
+  const int lane = threadIdx.x & 63;
+  const int gq = blockIdx.x * 64 + lane;
+  const int b = gq >> 2, q = gq & 3;
+  QInt r{0, 0};
+  if (b < nb) {
+    Q8Slice s;
+    WSlice ws;
+    load_q8_slice<T_IQ2_XXS>(xq, nb, b, q, s);
+    load_w_slice<T_IQ2_XXS>(w + (size_t)b * 66, q, ws);
+    r = quarter_int<T_IQ2_XXS>(ws, q, s, grid, signs);
+  }
+  r.isum = group_sum_i<4>(r.isum);
+  if (b < nb && q == 0) {
+    isum[b] = r.isum;
+    imin[b] = 0;
+  }
+}
+}  // namespace
+
+extern "C" {
+
+int zm_block_dots(int type, const void *w_row, const float *x, int n, int32_t *isum, int32_t *imin, void *stream) {
+  if (!type_supported(type) || n <= 0 || n % QK || !w_row || !x || !isum || !imin)
+    return fail("zm_block_dots: bad arguments");
+  DeviceState *d;
+  if (device_state(&d)) return -1;
+  hipStream_t st = (hipStream_t)stream;
+  const int nb = n / QK;
+  uint8_t *xq = nullptr;
+  HIP_OK(hipMallocAsync((void **)&xq, q8_row_bytes(nb), st));
+  if (launch_quant(x, (size_t)n, nb, 1, xq, q8_row_bytes(nb), 1, st)) return -1;
+  const dim3 g((unsigned)((nb * 4 + 63) / 64));
+  const uint8_t *w = (const uint8_t *)w_row;
+  switch (type) {
+  case T_Q2_K: hipLaunchKernelGGL(k_block_dots<T_Q2_K>, g, dim3(64), 0, st, w, xq, nb, isum, imin); break;
+  case T_Q3_K: hipLaunchKernelGGL(k_block_dots<T_Q3_K>, g, dim3(64), 0, st, w, xq, nb, isum, imin); break;
+  case T_Q4_K: hipLaunchKernelGGL(k_block_dots<T_Q4_K>, g, dim3(64), 0, st, w, xq, nb, isum, imin); break;
+  default: hipLaunchKernelGGL(k_block_dots_iq2, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->grid, d->signs); break;
+  }
+  HIP_OK(hipGetLastError());
+  HIP_OK(hipFreeAsync(xq, st));
+  return 0;
+}
+
+// ---------------------------------------------------------------- routed layer
+
+}  // extern "C"
+
+namespace {
+struct LayerWs {
+  float *logits;
+  int32_t *ids;
+  float *weights;
+  uint8_t *xq;
+  int32_t *counts, *offs, *pairs, *active, *n_active;
+  float *act;
+  uint8_t *aq;
+  float *y;
+  float *act_s;
+  uint8_t *aq_s;
+  float *y_s;
+};
+
+size_t layer_ws(const zm_moe_layer *L, int S, uint8_t *base, LayerWs *w) {
+  const int H = L->H, F = L->F, E = L->router.n_experts, K = L->router.topk, NS = L->n_slots;
+  const int nbH = H / QK, nbF = F / QK;
+  Bump b{base};
+  LayerWs t{};
+  t.logits = b.take<float>((size_t)S * E * 4);
+  t.ids = b.take<int32_t>((size_t)S * K * 4);
+  t.weights = b.take<float>((size_t)S * K * 4);
+  t.xq = b.take<uint8_t>((size_t)S * q8_row_bytes(nbH));
+  t.counts = b.take<int32_t>((size_t)NS * 4);
+  t.offs = b.take<int32_t>((size_t)(NS + 1) * 4);
+  t.pairs = b.take<int32_t>((size_t)S * K * 4);
+  t.active = b.take<int32_t>((size_t)NS * 4);
+  t.n_active = b.take<int32_t>(4);
+  t.act = b.take<float>((size_t)S * K * F * 4);
+  t.aq = b.take<uint8_t>((size_t)S * K * q8_row_bytes(nbF));
+  t.y = b.take<float>((size_t)S * K * H * 4);
+  if (L->F_shared > 0) {
+    t.act_s = b.take<float>((size_t)S * L->F_shared * 4);
+    t.aq_s = b.take<uint8_t>((size_t)S * q8_row_bytes(L->F_shared / QK));
+    t.y_s = b.take<float>((size_t)S * H * 4);
+  }
+  if (w) *w = t;
+  return b.off + 256;
+}
+
+int check_layer(const zm_moe_layer *L) {
+  if (!L) return fail("null layer");
+  if (L->H <= 0 || L->H % QK || L->H / QK > 64) return fail("H must be a multiple of 256, <= 16384");
+  if (L->F <= 0 || L->F % QK || L->F / QK > 64) return fail("F must be a multiple of 256, <= 16384");
+  if (!type_supported(L->type_gate) || L->type_up != L->type_gate || !type_supported(L->type_down))
+    return fail("unsupported expert types (gate and up must share a type)");
+  if (L->n_slots <= 0 || L->n_slots > BUCKET_MAX_E) return fail("n_slots out of range");
+  if (L->router.n_experts <= 0 || L->router.n_experts > ROUTER_MAX_E) return fail("n_experts out of range");
+  if (L->router.topk <= 0 || L->router.topk > 64 || L->router.topk > L->router.n_experts) return fail("bad topk");
+  if (!L->route_map && L->n_slots != L->router.n_experts) return fail("n_slots != n_experts without a slot table");
+  if (!L->w_gate || !L->w_up || !L->w_down) return fail("null expert weights");
+  if (L->F_shared > 0) {
+    if (L->F_shared % QK || L->F_shared / QK > 64 || !type_supported(L->type_shared) || !L->ws_gate || !L->ws_up ||
+        !L->ws_down)
+      return fail("bad shared expert");
+  }
+  if (L->router_w && L->H % 4) return fail("router GEMV needs H % 4 == 0");
+  return 0;
+}
+}  // namespace
+
+extern "C" {
+
+size_t zm_moe_workspace_size(const zm_moe_layer *layer, int S) {
+  if (check_layer(layer) || S <= 0) return 0;
+  return layer_ws(layer, S, nullptr, nullptr);
+}
+
+int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, int S, float *out, int32_t *ids_out,
+                   float *weights_out, void *workspace, size_t workspace_size, void *stream) {
+  if (check_layer(L)) return -1;
+  if (S <= 0 || !x || !out || (!logits && !L->router_w)) return fail("zm_moe_forward: bad arguments");
+  if (S > 65535) return fail("S too large");
+  if (!workspace || workspace_size < layer_ws(L, S, nullptr, nullptr)) return fail("workspace too small");
+  DeviceState *d;
+  if (device_state(&d)) return -1;
+  hipStream_t st = (hipStream_t)stream;
+  LayerWs w;
+  layer_ws(L, S, (uint8_t *)workspace, &w);
+  const int H = L->H, F = L->F, E = L->router.n_experts, K = L->router.topk, NS = L->n_slots;
+  const int nbH = H / QK, nbF = F / QK;
+  int32_t *ids = ids_out ? ids_out : w.ids;
+  float *wts = weights_out ? weights_out : w.weights;
+
+  // router
+  const float *lg = logits;
+  if (L->router_w) {
+    hipLaunchKernelGGL(k_router_gemv, dim3(E), dim3(256), 0, st, L->router_w, x, H, E, S, w.logits);
+    lg = w.logits;
+  }
+  if (zm_router(&L->router, lg, L->logit_bias, L->sel_bias, L->route_map, L->route_mask, S, ids, wts, st))
+    return -1;
+  // activations -> Q8_K, buckets
+  if (launch_quant(x, (size_t)H, nbH, S, w.xq, q8_row_bytes(nbH), 1, st)) return -1;
+  hipLaunchKernelGGL(k_bucket, dim3(1), dim3(1024), 0, st, ids, S * K, NS, w.counts, w.offs, w.pairs, w.active,
+                     w.n_active);
+  // gate/up + SwiGLU
+  const int groups = std::min(NS, S * K);
+  const int np = pick_np(S * K, NS);
+  GemvArgs a{};
+  a.w0 = (const uint8_t *)L->w_gate;
+  a.w1 = (const uint8_t *)L->w_up;
+  a.w_rstride = row_bytes(L->type_gate, H);
+  a.w_estride = a.w_rstride * F;
+  a.nrows = F;
+  a.nb = nbH;
+  a.xq = w.xq;
+  a.xq_rstride = q8_row_bytes(nbH);
+  a.ne11 = 1;
+  a.K = K;
+  a.n_active = w.n_active;
+  a.active = w.active;
+  a.offs = w.offs;
+  a.pairs = w.pairs;
+  a.out = w.act;
+  a.out_s = (size_t)K * F;
+  a.out_k = F;
+  a.grid = d->grid;
+  a.signs = d->signs;
+  if (launch_gemv(L->type_gate, true, np, a, groups, st)) return -1;
+  // act -> Q8_K
+  if (launch_quant(w.act, (size_t)F, nbF, S * K, w.aq, q8_row_bytes(nbF), 1, st)) return -1;
+  // skipped routes read as zero rows
+  hipLaunchKernelGGL(k_fill_skipped, dim3((unsigned)std::min((H + 255) / 256, 64), (unsigned)(S * K)), dim3(256), 0,
+                     st, ids, (size_t)K, (size_t)1, K, S, NS, H, w.y, (size_t)K * H, (size_t)H);
+  // down
+  GemvArgs b = a;
+  b.w0 = (const uint8_t *)L->w_down;
+  b.w1 = nullptr;
+  b.w_rstride = row_bytes(L->type_down, F);
+  b.w_estride = b.w_rstride * H;
+  b.nrows = H;
+  b.nb = nbF;
+  b.xq = w.aq;
+  b.xq_rstride = q8_row_bytes(nbF);
+  b.ne11 = K;
+  b.out = w.y;
+  b.out_s = (size_t)K * H;
+  b.out_k = H;
+  if (launch_gemv(L->type_down, false, np, b, groups, st)) return -1;
+  // shared expert (dense over all tokens)
+  const float *ys = nullptr;
+  if (L->F_shared > 0) {
+    const int Fs = L->F_shared, nbS = Fs / QK;
+    GemvArgs c{};
+    c.w0 = (const uint8_t *)L->ws_gate;
+    c.w1 = (const uint8_t *)L->ws_up;
+    c.w_rstride = row_bytes(L->type_shared, H);
+    c.w_estride = 0;
+    c.nrows = Fs;
+    c.nb = nbH;
+    c.xq = w.xq;
+    c.xq_rstride = q8_row_bytes(nbH);
+    c.ne11 = 1;
+    c.K = 1;
+    c.dense_S = S;
+    c.out = w.act_s;
+    c.out_s = Fs;
+    c.out_k = 0;
+    c.grid = d->grid;
+    c.signs = d->signs;
+    const int nps = S >= 4 ? 4 : (S >= 2 ? 2 : 1);
+    if (launch_gemv(L->type_shared, true, nps, c, 1, st)) return -1;
+    if (launch_quant(w.act_s, (size_t)Fs, nbS, S, w.aq_s, q8_row_bytes(nbS), 1, st)) return -1;
+    GemvArgs e2 = c;
+    e2.w0 = (const uint8_t *)L->ws_down;
+    e2.w1 = nullptr;
+    e2.w_rstride = row_bytes(L->type_shared, Fs);
+    e2.nrows = H;
+    e2.nb = nbS;
+    e2.xq = w.aq_s;
+    e2.xq_rstride = q8_row_bytes(nbS);
+    e2.out = w.y_s;
+    e2.out_s = H;
+    if (launch_gemv(L->type_shared, false, nps, e2, 1, st)) return -1;
+    ys = w.y_s;
+  }
+  hipLaunchKernelGGL(k_combine, dim3((H + 255) / 256, S), dim3(256), 0, st, w.y, wts, ys, H, K, out);
+  HIP_OK(hipGetLastError());
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,316 @@
+// zm_device.hpp -- gfx950 device helpers shared by every zeromoe_amd kernel:
+// GGUF super-block layouts, the per-lane "64-weight slice" integer dots
+// against Q8_K activations, wave64 reductions and the bit-reproducible
+// float helpers (exp, round-half-even) the router and quantizer use.
+//
+// Work unit: a 256-weight super-block is split into 4 quarters of 64
+// weights; one lane owns one quarter.  A quarter is what one lane can dot
+// with a handful of 16-byte loads:
+//   Q2_K / Q3_K quarter q = (h, qq): qs bytes [32h+16qq, +16) hold weights
+//       128h + 32j + 16qq + i (j = 0..3 bit-plane, i < 16), i.e. four
+//       16-weight sub-blocks 8h + 2j + qq.
+//   Q4_K quarter q: qs bytes [32q, +32) hold weights 64q + i (low nibble)
+//       and 64q + 32 + i (high nibble): sub-blocks 2q and 2q+1.
+//   IQ2_XXS quarter q: 32-weight sub-blocks 2q and 2q+1 (16 bytes of qs).
+// Block layouts: /root/reference/kernels/quant/kquant_matmul.cu:35-39,
+// kernels/quant/iq2_matmul.cu:27.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace zm {
+
+constexpr int QK = 256;
+
+enum : int {
+  T_F32 = 0,
+  T_F16 = 1,
+  T_Q2_K = 10,
+  T_Q3_K = 11,
+  T_Q4_K = 12,
+  T_Q8_K = 15,
+  T_IQ2_XXS = 16,
+  T_I32 = 26,
+};
+
+__host__ __device__ constexpr int block_bytes(int t) {
+  return t == T_Q2_K ? 84 : t == T_Q3_K ? 110 : t == T_Q4_K ? 144 : t == T_IQ2_XXS ? 66 : t == T_Q8_K ? 292 : 0;
+}
+
+// ---------------------------------------------------------------- loads
+
+__device__ __forceinline__ uint4 ld16(const uint8_t *p) {
+  uint4 v;
+  __builtin_memcpy(&v, p, 16);
+  return v;
+}
+__device__ __forceinline__ uint2 ld8(const uint8_t *p) {
+  uint2 v;
+  __builtin_memcpy(&v, p, 8);
+  return v;
+}
+__device__ __forceinline__ uint32_t ld4(const uint8_t *p) {
+  uint32_t v;
+  __builtin_memcpy(&v, p, 4);
+  return v;
+}
+__device__ __forceinline__ uint16_t ld2(const uint8_t *p) {
+  uint16_t v;
+  __builtin_memcpy(&v, p, 2);
+  return v;
+}
+__device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// byte k (0..11) of three little-endian dwords
+__device__ __forceinline__ uint32_t byte_of3(uint32_t s0, uint32_t s1, uint32_t s2, int k) {
+  const uint32_t w = k < 4 ? s0 : (k < 8 ? s1 : s2);
+  return (w >> (8 * (k & 3))) & 0xffu;
+}
+
+// ---------------------------------------------------------------- bit-reproducible float helpers
+
+// ggml-quants.c nearest_int (round half to even via the 1.5*2^23 add).
+__device__ __forceinline__ int nearest_int(float f) {
+  const float v = f + 12582912.f;
+  return (__float_as_int(v) & 0x007fffff) - 0x00400000;
+}
+
+// exp(x): Cody-Waite reduction by ln2 and a degree-7 Taylor polynomial; the
+// same IEEE operation sequence as the host checker, so results are bitwise
+// equal on CPU and GPU.  (Compiled with -ffp-contract=off.)
+__device__ __forceinline__ float exp_f32(float x) {
+  if (x != x) return x;
+  if (x > 88.72283935546875f) return __int_as_float(0x7f800000);
+  if (x < -103.972084045410156f) return 0.0f;
+  const float n = __builtin_rintf(x * 1.44269502162933349609375f);
+  float r = __builtin_fmaf(n, -0.693145751953125f, x);
+  r = __builtin_fmaf(n, -1.428606765330187045e-06f, r);
+  float p = 1.98412701138295233249664306640625e-4f;
+  p = __builtin_fmaf(p, r, 1.388888922519981861114501953125e-3f);
+  p = __builtin_fmaf(p, r, 8.33333376795053482055664062500e-3f);
+  p = __builtin_fmaf(p, r, 4.16666679084300994873046875000e-2f);
+  p = __builtin_fmaf(p, r, 1.66666671633720397949218750000e-1f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  return __builtin_ldexpf(p, (int)n);
+}
+
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + exp_f32(-g)); }
+
+// ---------------------------------------------------------------- wave64 reductions
+
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int m = W / 2; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+template <int W>
+__device__ __forceinline__ int group_sum_i(int v) {
+#pragma unroll
+  for (int m = W / 2; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+// ---------------------------------------------------------------- Q8_K activations (planar)
+//
+// Internal activation rows use a planar layout of the same 292 B/256 size as
+// ggml's block_q8_K: qs[nb*256] | d[nb] (f32) | bsums[nb*16] (i16), so one
+// lane's 64 int8 are four aligned 16-byte loads.
+__host__ __device__ constexpr size_t q8_row_bytes(int nb) { return (size_t)nb * 292; }
+__host__ __device__ constexpr size_t q8_d_off(int nb) { return (size_t)nb * 256; }
+__host__ __device__ constexpr size_t q8_bs_off(int nb) { return (size_t)nb * 260; }
+
+struct Q8Slice {
+  uint4 q[4];    // 64 int8, in the order the weight quarter needs them
+  int bs[4];     // sums of 16-weight groups used by the quarter (type dependent)
+  float d;
+};
+
+// positions of the 64 activations matching weight quarter q of block b
+template <int T>
+__device__ __forceinline__ void load_q8_slice(const uint8_t *row, int nb, int b, int q, Q8Slice &s) {
+  const uint8_t *qs = row + (size_t)b * 256;
+  const int16_t *bs = reinterpret_cast<const int16_t *>(row + q8_bs_off(nb)) + b * 16;
+  s.d = reinterpret_cast<const float *>(row + q8_d_off(nb))[b];
+  if constexpr (T == T_Q2_K || T == T_Q3_K) {
+    const int h = q >> 1, qq = q & 1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      s.q[j] = *reinterpret_cast<const uint4 *>(qs + 128 * h + 32 * j + 16 * qq);
+      s.bs[j] = bs[8 * h + 2 * j + qq];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s.q[j] = *reinterpret_cast<const uint4 *>(qs + 64 * q + 16 * j);
+    if constexpr (T == T_Q4_K) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s.bs[j] = bs[4 * q + j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s.bs[j] = 0;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- weight quarters
+
+struct WSlice {
+  uint4 a;     // Q2/Q3: qs16 ; Q4: qs[0..16) ; IQ2: qs 16 B
+  uint4 b;     // Q3: hmask16 ; Q4: qs[16..32)
+  uint4 c;     // Q4: header (d, dmin, scales) ; Q3: scales(12) + d in .w low half
+  uint2 e;     // Q2: scales[8h .. 8h+8)
+  uint32_t f;  // Q2: d|dmin ; IQ2: d
+};
+
+template <int T>
+__device__ __forceinline__ void load_w_slice(const uint8_t *blk, int q, WSlice &w) {
+  if constexpr (T == T_Q2_K) {
+    w.e = ld8(blk + 8 * (q >> 1));
+    w.a = ld16(blk + 16 + 16 * q);
+    w.f = ld4(blk + 80);
+  } else if constexpr (T == T_Q3_K) {
+    w.b = ld16(blk + 16 * (q & 1));
+    w.a = ld16(blk + 32 + 16 * q);
+    w.c.x = ld4(blk + 96);
+    w.c.y = ld4(blk + 100);
+    w.c.z = ld4(blk + 104);
+    w.c.w = ld2(blk + 108);
+  } else if constexpr (T == T_Q4_K) {
+    w.c = ld16(blk);
+    w.a = ld16(blk + 16 + 32 * q);
+    w.b = ld16(blk + 32 + 32 * q);
+  } else {  // IQ2_XXS
+    w.f = ld2(blk);
+    w.a = ld16(blk + 2 + 16 * q);
+  }
+}
+
+__device__ __forceinline__ uint32_t u4_get(const uint4 &v, int i) {
+  return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+
+// Integer parts of one quarter: isum = sum_sub sc*dot (Q3_K: includes the
+// -4*bsum term of missing high bits), imin = sum_sub m*bsum (Q2_K/Q4_K).
+struct QInt {
+  int isum, imin;
+};
+
+template <int T>
+__device__ __forceinline__ QInt quarter_int(const WSlice &w, int q, const Q8Slice &a, const uint64_t *lds_grid,
+                                            const uint64_t *lds_signs) {
+  QInt r{0, 0};
+  if constexpr (T == T_Q2_K) {
+    const int qq = q & 1;
+    const uint32_t lo = w.e.x >> (8 * qq), hi = w.e.y >> (8 * qq);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t scb = ((j < 2 ? lo : hi) >> (16 * (j & 1))) & 0xffu;
+      int dj = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dj = dot4((u4_get(w.a, i) >> (2 * j)) & 0x03030303u, u4_get(a.q[j], i), dj);
+      r.isum += (int)(scb & 15u) * dj;
+      r.imin += (int)(scb >> 4) * a.bs[j];
+    }
+  } else if constexpr (T == T_Q3_K) {
+    const int h = q >> 1, qq = q & 1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = 2 * j + qq;  // scales byte index of the low nibble
+      const uint32_t lo4 = (byte_of3(w.c.x, w.c.y, w.c.z, k) >> (4 * h)) & 15u;
+      const uint32_t hi2 = (byte_of3(w.c.x, w.c.y, w.c.z, 8 + 2 * (j & 1) + qq) >> (2 * (2 * h + (j >> 1)))) & 3u;
+      const int sc = (int)(lo4 | (hi2 << 4)) - 32;
+      int dj = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t q2 = (u4_get(w.a, i) >> (2 * j)) & 0x03030303u;
+        const uint32_t hb = (u4_get(w.b, i) >> (4 * h + j)) & 0x01010101u;
+        dj = dot4(q2 | (hb << 2), u4_get(a.q[j], i), dj);
+      }
+      r.isum += sc * (dj - 4 * a.bs[j]);
+    }
+  } else if constexpr (T == T_Q4_K) {
+    // scales bytes 0..11 live in header dwords y, z, w
+    const int j0 = 2 * q, j1 = 2 * q + 1;
+    uint32_t sc0, m0, sc1, m1;
+    if (q < 2) {
+      sc0 = byte_of3(w.c.y, w.c.z, w.c.w, j0) & 63u;
+      m0 = byte_of3(w.c.y, w.c.z, w.c.w, j0 + 4) & 63u;
+      sc1 = byte_of3(w.c.y, w.c.z, w.c.w, j1) & 63u;
+      m1 = byte_of3(w.c.y, w.c.z, w.c.w, j1 + 4) & 63u;
+    } else {
+      const uint32_t a0 = byte_of3(w.c.y, w.c.z, w.c.w, j0 + 4), b0 = byte_of3(w.c.y, w.c.z, w.c.w, j0 - 4),
+                     c0 = byte_of3(w.c.y, w.c.z, w.c.w, j0);
+      sc0 = (a0 & 15u) | ((b0 >> 6) << 4);
+      m0 = (a0 >> 4) | ((c0 >> 6) << 4);
+      const uint32_t a1 = byte_of3(w.c.y, w.c.z, w.c.w, j1 + 4), b1 = byte_of3(w.c.y, w.c.z, w.c.w, j1 - 4),
+                     c1 = byte_of3(w.c.y, w.c.z, w.c.w, j1);
+      sc1 = (a1 & 15u) | ((b1 >> 6) << 4);
+      m1 = (a1 >> 4) | ((c1 >> 6) << 4);
+    }
+    // qs bytes [0,16) low nibbles pair with activations [0,16), bytes [16,32) with
+    // [16,32); the high nibbles with [32,48) and [48,64).
+    int dl = 0, dh = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dl = dot4(u4_get(w.a, i) & 0x0f0f0f0fu, u4_get(a.q[0], i), dl);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dl = dot4(u4_get(w.b, i) & 0x0f0f0f0fu, u4_get(a.q[1], i), dl);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dh = dot4((u4_get(w.a, i) >> 4) & 0x0f0f0f0fu, u4_get(a.q[2], i), dh);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dh = dot4((u4_get(w.b, i) >> 4) & 0x0f0f0f0fu, u4_get(a.q[3], i), dh);
+    r.isum = (int)sc0 * dl + (int)sc1 * dh;
+    r.imin = (int)m0 * (a.bs[0] + a.bs[1]) + (int)m1 * (a.bs[2] + a.bs[3]);
+  } else {  // IQ2_XXS: sub-blocks 2q, 2q+1; words (aux0, aux1) each
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      const uint32_t aux0 = sb == 0 ? w.a.x : w.a.z;
+      const uint32_t aux1 = sb == 0 ? w.a.y : w.a.w;
+      int dsum = 0;
+#pragma unroll
+      for (int l = 0; l < 4; ++l) {
+        const uint64_t g = lds_grid[(aux0 >> (8 * l)) & 0xffu];
+        const uint64_t m = lds_signs[(aux1 >> (7 * l)) & 127u];
+        const uint32_t glo = (uint32_t)g, ghi = (uint32_t)(g >> 32);
+        const uint32_t mlo = (uint32_t)m, mhi = (uint32_t)(m >> 32);
+        // conditional byte negate: (g ^ m) + (m & 1) per byte (no carries: 8 <= g <= 255)
+        const uint32_t vlo = (glo ^ mlo) + (mlo & 0x01010101u);
+        const uint32_t vhi = (ghi ^ mhi) + (mhi & 0x01010101u);
+        const int qi = 2 * (4 * sb + l);  // dword index inside the 64 activations
+        dsum = dot4(vlo, u4_get(a.q[qi >> 2], qi & 3), dsum);
+        dsum = dot4(vhi, u4_get(a.q[(qi + 1) >> 2], (qi + 1) & 3), dsum);
+      }
+      r.isum += (2 * (int)(aux1 >> 28) + 1) * dsum;
+    }
+  }
+  return r;
+}
+
+// Float value of one quarter's contribution to the dot.
+template <int T>
+__device__ __forceinline__ float quarter_dot(const WSlice &w, int q, const Q8Slice &a, const uint64_t *g,
+                                             const uint64_t *sg) {
+  const QInt r = quarter_int<T>(w, q, a, g, sg);
+  if constexpr (T == T_Q2_K) {
+    const float d = h2f((uint16_t)(w.f & 0xffffu)), dmin = h2f((uint16_t)(w.f >> 16));
+    return (a.d * d) * (float)r.isum - (a.d * dmin) * (float)r.imin;
+  } else if constexpr (T == T_Q3_K) {
+    const float d = h2f((uint16_t)(w.c.w & 0xffffu));
+    return (a.d * d) * (float)r.isum;
+  } else if constexpr (T == T_Q4_K) {
+    const float d = h2f((uint16_t)(w.c.x & 0xffffu)), dmin = h2f((uint16_t)(w.c.x >> 16));
+    return (a.d * d) * (float)r.isum - (a.d * dmin) * (float)r.imin;
+  } else {
+    const float d = h2f((uint16_t)(w.f & 0xffffu));
+    return 0.125f * ((a.d * d) * (float)r.isum);
+  }
+}
+
+}  // namespace zm

@@ -1,0 +1,523 @@
+// zm_kernels.hpp -- the routed-expert kernels for gfx950 (wave64, CDNA4).
+//
+//   k_quant_q8K  : f32 rows -> Q8_K (one wave per 256-value block)
+//   k_router     : gating + (grouped) top-k + weights + slot table, one wave per token
+//   k_bucket     : stable counting sort of (token, slot) pairs by expert
+//   k_gemv       : bucketed MUL_MAT_ID GEMV over Q8_K activations (decode path)
+//   k_combine    : k-ascending weighted sum over the top-k axis (+ shared expert)
+//   k_router_gemv: fp32 router logits
+#pragma once
+
+#include "zm_device.hpp"
+
+namespace zm {
+
+// ============================================================ Q8_K quantization
+//
+// ggml quantize_row_q8_K (restated in oracle/zm_oracle.c): the signed value of
+// largest magnitude (first on ties) gives iscale = -127/max; q = min(127,
+// round_half_even(iscale*x)); d = 1/iscale; bsums = sums of 16.
+// The 256 values of a block sit 4 per lane.
+struct Q8Out {
+  int8_t q[4];
+  float d;
+  int bsum16;  // valid on lanes with (lane & 3) == 0: sum of values 16*(lane/4) .. +16
+};
+
+__device__ __forceinline__ Q8Out quant_block_wave(float4 v, int lane) {
+  float vals[4] = {v.x, v.y, v.z, v.w};
+  float amax = 0.f, mx = 0.f;
+  int idx = 0x7fffffff;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float ax = __builtin_fabsf(vals[j]);
+    if (ax > amax) {
+      amax = ax;
+      mx = vals[j];
+      idx = 4 * lane + j;
+    }
+  }
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) {
+    const float oa = __shfl_xor(amax, m, 64);
+    const float om = __shfl_xor(mx, m, 64);
+    const int oi = __shfl_xor(idx, m, 64);
+    if (oa > amax || (oa == amax && oi < idx)) {
+      amax = oa;
+      mx = om;
+      idx = oi;
+    }
+  }
+  Q8Out o;
+  if (amax == 0.0f) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o.q[j] = 0;
+    o.d = 0.0f;
+    o.bsum16 = 0;
+    return o;
+  }
+  const float iscale = -127.f / mx;
+  int s = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    int q = nearest_int(iscale * vals[j]);
+    q = q < 127 ? q : 127;
+    o.q[j] = (int8_t)q;
+    s += q;
+  }
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  o.bsum16 = s;
+  o.d = 1.0f / iscale;
+  return o;
+}
+
+// rows x nb blocks; planar != 0 writes the internal planar layout, else ggml block_q8_K
+__global__ __launch_bounds__(256) void k_quant_q8K(const float *__restrict__ x, size_t x_rstride, int nb, int rows,
+                                                   uint8_t *__restrict__ y, size_t y_rstride, int planar) {
+  const int lane = threadIdx.x & 63;
+  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = gw / nb, b = gw % nb;
+  if (row >= rows) return;
+  const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)row * x_rstride + (size_t)b * QK + 4 * lane);
+  const Q8Out o = quant_block_wave(v, lane);
+  uint32_t packed = (uint32_t)(uint8_t)o.q[0] | ((uint32_t)(uint8_t)o.q[1] << 8) | ((uint32_t)(uint8_t)o.q[2] << 16) |
+                    ((uint32_t)(uint8_t)o.q[3] << 24);
+  uint8_t *yr = y + (size_t)row * y_rstride;
+  if (planar) {
+    *reinterpret_cast<uint32_t *>(yr + (size_t)b * QK + 4 * lane) = packed;
+    if (lane == 0) reinterpret_cast<float *>(yr + q8_d_off(nb))[b] = o.d;
+    if ((lane & 3) == 0) reinterpret_cast<int16_t *>(yr + q8_bs_off(nb))[b * 16 + (lane >> 2)] = (int16_t)o.bsum16;
+  } else {
+    uint8_t *blk = yr + (size_t)b * 292;
+    __builtin_memcpy(blk + 4 + 4 * lane, &packed, 4);
+    if (lane == 0) __builtin_memcpy(blk, &o.d, 4);
+    if ((lane & 3) == 0) {
+      const int16_t bs = (int16_t)o.bsum16;
+      __builtin_memcpy(blk + 260 + 2 * (lane >> 2), &bs, 2);
+    }
+  }
+}
+
+// ============================================================ router
+//
+// moe_routed::gate_probs / select_ids / route_weights
+// (/root/reference/models/graph/moe_routed_ggml.hpp:52-141), with the grouped
+// selection of core/moe_router_service.cpp:1409-1440 and the device router of
+// kernels/models/glm5next_router.cu:33-93.  Top-k order: descending score,
+// lowest expert index first on ties.
+struct RouterArgs {
+  const float *logits;      // [S][E]
+  const float *logit_bias;  // [E] or null: added to logits before gating
+  const float *sel_bias;    // [E] or null: added to probs for selection only
+  const int32_t *route_map; // [E] or null: global expert -> slot (or -1)
+  const float *route_mask;  // [E] or null
+  int E, K, gating, n_groups, n_groups_used, weights_norm;
+  float weights_scale;
+  int32_t *ids;  // [S][K]
+  float *weights;
+};
+
+__device__ __forceinline__ bool outranks(float sa, int ia, float sb, int ib) {
+  return sa > sb || (sa == sb && ia < ib);
+}
+
+__device__ __forceinline__ void wave_argmax(float &v, int &i) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) {
+    const float ov = __shfl_xor(v, m, 64);
+    const int oi = __shfl_xor(i, m, 64);
+    if (outranks(ov, oi, v, i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+}
+
+constexpr int ROUTER_MAX_E = 1024;
+
+__global__ __launch_bounds__(64) void k_router(RouterArgs a) {
+  __shared__ float p[ROUTER_MAX_E];
+  __shared__ float sel[ROUTER_MAX_E];
+  __shared__ float gscore[64];
+  const int s = blockIdx.x, lane = threadIdx.x;
+  const int E = a.E, K = a.K;
+  const float *l = a.logits + (size_t)s * E;
+  const float NEG_INF = __int_as_float(0xff800000);
+  for (int e = lane; e < E; e += 64) p[e] = a.logit_bias ? l[e] + a.logit_bias[e] : l[e];
+  __syncthreads();
+  if (a.gating == 0) {
+    float mx = NEG_INF;
+    for (int e = lane; e < E; e += 64) mx = p[e] > mx ? p[e] : mx;
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) {
+      const float o = __shfl_xor(mx, m, 64);
+      mx = o > mx ? o : mx;
+    }
+    double sum = 0.0;
+    for (int e = lane; e < E; e += 64) {
+      const float ev = exp_f32(p[e] - mx);
+      p[e] = ev;
+      sum += (double)ev;
+    }
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) sum += __shfl_xor(sum, m, 64);
+    const float inv = (float)(1.0 / sum);
+    for (int e = lane; e < E; e += 64) p[e] = p[e] * inv;
+  } else if (a.gating == 1) {
+    for (int e = lane; e < E; e += 64) p[e] = 1.0f / (1.0f + exp_f32(-p[e]));
+  } else {
+    for (int e = lane; e < E; e += 64) {
+      const float x = p[e];
+      const float sp = x > 0.0f ? x + log1pf(exp_f32(-x)) : log1pf(exp_f32(x));
+      p[e] = sqrtf(sp);
+    }
+  }
+  for (int e = lane; e < E; e += 64) sel[e] = a.sel_bias ? p[e] + a.sel_bias[e] : p[e];
+  __syncthreads();
+  const int G = a.n_groups;
+  if (G > 1 && a.n_groups_used > 0 && a.n_groups_used < G && E % G == 0 && G <= 64) {
+    const int gs = E / G;
+    if (lane < G) {
+      int b1 = -1, b2 = -1;
+      for (int j = 0; j < gs; ++j) {
+        const int e = lane * gs + j;
+        if (b1 < 0 || outranks(sel[e], e, sel[b1], b1)) {
+          b2 = b1;
+          b1 = e;
+        } else if (b2 < 0 || outranks(sel[e], e, sel[b2], b2)) {
+          b2 = e;
+        }
+      }
+      gscore[lane] = gs >= 2 ? sel[b1] + sel[b2] : sel[b1];
+    }
+    __syncthreads();
+    bool keep = false;
+    float gv = lane < G ? gscore[lane] : NEG_INF;
+    int gi = lane < G ? lane : 0x7fffffff;
+    for (int r = 0; r < a.n_groups_used; ++r) {
+      float v = keep ? NEG_INF : gv;
+      int i = keep ? 0x7fffffff : gi;
+      wave_argmax(v, i);
+      if (lane == i) keep = true;
+    }
+    // mask experts of dropped groups
+    for (int e = lane; e < E; e += 64) {
+      const int g = e / gs;
+      const bool kg = __shfl(keep ? 1 : 0, g, 64) != 0;
+      if (!kg) sel[e] = NEG_INF;
+    }
+    __syncthreads();
+  }
+  // top-k: repeated wave argmax; taken[] as a per-lane bitmask (E <= 1024 -> 16 bits)
+  uint32_t taken = 0;
+  float wk = 0.f;
+  int idk = 0;
+  for (int k = 0; k < K; ++k) {
+    float v = NEG_INF;
+    int i = 0x7fffffff;
+    for (int t = 0, e = lane; e < E; ++t, e += 64) {
+      if (taken & (1u << t)) continue;
+      if (i == 0x7fffffff || outranks(sel[e], e, v, i)) {
+        v = sel[e];
+        i = e;
+      }
+    }
+    wave_argmax(v, i);
+    if (i != 0x7fffffff && (i & 63) == lane) taken |= 1u << (i >> 6);
+    if (lane == k) {
+      idk = i;
+      wk = p[i];
+    }
+  }
+  // weights: lane k holds route k; normalise in k order (ggml sum_rows accumulates in double)
+  if (a.weights_norm) {
+    double sum = 0.0;
+    for (int k = 0; k < K; ++k) sum += (double)__shfl(wk, k, 64);
+    float fs = (float)sum;
+    fs = fs < 6.103515625e-5f ? 6.103515625e-5f : fs;
+    wk = wk / fs;
+  }
+  if (a.weights_scale != 0.0f && a.weights_scale != 1.0f) wk = wk * a.weights_scale;
+  if (lane < K) {
+    int id = idk;
+    if (a.route_map) {
+      const float m = a.route_mask ? a.route_mask[idk] : (a.route_map[idk] >= 0 ? 1.0f : 0.0f);
+      id = a.route_map[idk];
+      wk = wk * m;
+    }
+    a.ids[(size_t)s * K + lane] = id;
+    a.weights[(size_t)s * K + lane] = wk;
+  }
+}
+
+// ============================================================ bucketing
+//
+// Stable counting sort of the flat pair ids p = s*K + k by expert, the CSR of
+// /root/reference/core/batched_dispatch_pipeline.cpp:1181-1202 (token-major
+// inside each bucket).  One workgroup of 1024 threads; pairs are ranked in
+// chunks of 1024 with a wave "match" loop (ballot per distinct expert) plus
+// per-wave counts, so the order is exactly the sequential one.
+constexpr int BUCKET_MAX_E = 512;
+
+__global__ __launch_bounds__(1024) void k_bucket(const int32_t *__restrict__ ids, int n_pairs, int E,
+                                                 int32_t *__restrict__ counts, int32_t *__restrict__ offs,
+                                                 int32_t *__restrict__ pairs, int32_t *__restrict__ active,
+                                                 int32_t *__restrict__ n_active) {
+  __shared__ int cnt[BUCKET_MAX_E];
+  __shared__ int base[BUCKET_MAX_E];
+  __shared__ int wcnt[16][BUCKET_MAX_E];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int e = tid; e < E; e += 1024) cnt[e] = 0;
+  __syncthreads();
+  for (int i = tid; i < n_pairs; i += 1024) {
+    const int e = ids[i];
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  if (w == 0) {
+    // exclusive scan over E (<= 512) by one wave: 8 per lane
+    int local[8];
+    int acc = 0, nz = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int e = lane * 8 + j;
+      local[j] = e < E ? cnt[e] : 0;
+      acc += local[j];
+      nz += local[j] > 0;
+    }
+    int incl = acc, inz = nz;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+      const int o = __shfl_up(incl, m, 64);
+      const int oz = __shfl_up(inz, m, 64);
+      if (lane >= m) {
+        incl += o;
+        inz += oz;
+      }
+    }
+    int run = incl - acc, runz = inz - nz;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int e = lane * 8 + j;
+      if (e < E) {
+        offs[e] = run;
+        base[e] = run;
+        counts[e] = local[j];
+        if (local[j] > 0) active[runz++] = e;
+        run += local[j];
+      }
+    }
+    if (lane == 63) {
+      offs[E] = incl;
+      *n_active = inz;
+    }
+  }
+  __syncthreads();
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int c0 = 0; c0 < n_pairs; c0 += 1024) {
+    for (int e = lane; e < E; e += 64) wcnt[w][e] = 0;
+    const int i = c0 + tid;
+    const int e = i < n_pairs ? ids[i] : -1;
+    const bool valid = e >= 0 && e < E;
+    __syncthreads();
+    uint64_t remaining = __ballot(valid);
+    int rank = 0;
+    while (remaining) {
+      const int leader = __builtin_ctzll(remaining);
+      const int v = __builtin_amdgcn_readlane(e, leader);
+      const uint64_t m = __ballot(valid && e == v);
+      if (valid && e == v) rank = __builtin_popcountll(m & lt_mask);
+      if (lane == leader) wcnt[w][v] = __builtin_popcountll(m);
+      remaining &= ~m;
+    }
+    __syncthreads();
+    if (valid) {
+      int r = base[e] + rank;
+      for (int w2 = 0; w2 < w; ++w2) r += wcnt[w2][e];
+      pairs[r] = i;
+    }
+    __syncthreads();
+    for (int e2 = tid; e2 < E; e2 += 1024) {
+      int add = 0;
+      for (int w2 = 0; w2 < 16; ++w2) add += wcnt[w2][e2];
+      base[e2] += add;
+    }
+    __syncthreads();
+  }
+}
+
+// ============================================================ bucketed GEMV
+//
+// dst rows of every (token, slot) pair routed to an expert; one workgroup per
+// (row tile, active expert).  A wave covers 64/LPR rows per step with LPR
+// lanes per row (one 64-weight quarter each, ITER quarters per lane when a
+// row has more than 64 quarters).  Activation slices for NP pairs stay in
+// registers for the whole tile, so each weight byte is read once per bucket
+// chunk of NP pairs.
+struct GemvArgs {
+  const uint8_t *w0;  // expert 0 of the weight tensor (gate, or the only one)
+  const uint8_t *w1;  // up (GATEUP only)
+  size_t w_estride, w_rstride;
+  int nrows, nb;
+  const uint8_t *xq;  // planar Q8_K rows
+  size_t xq_rstride;
+  int ne11, K;
+  const int32_t *n_active, *active, *offs, *pairs;
+  int dense_S;  // > 0: expert 0, pairs 0..dense_S-1 (token = pair)
+  float *out;
+  size_t out_s, out_k;  // in floats
+  int tile_rows;
+  const uint64_t *grid;   // IQ2_XXS tables (global), staged into LDS
+  const uint64_t *signs;
+};
+
+template <int T, int LPR, int ITER, int NP, bool GATEUP>
+__global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
+  __shared__ uint64_t s_grid[T == T_IQ2_XXS ? 256 : 1];
+  __shared__ uint64_t s_signs[T == T_IQ2_XXS ? 128 : 1];
+  if constexpr (T == T_IQ2_XXS) {
+    for (int i = threadIdx.x; i < 256; i += 256) s_grid[i] = a.grid[i];
+    if (threadIdx.x < 128) s_signs[threadIdx.x] = a.signs[threadIdx.x];
+    __syncthreads();
+  }
+  int e, p0, p1;
+  if (a.dense_S > 0) {
+    if (blockIdx.y > 0) return;
+    e = 0;
+    p0 = 0;
+    p1 = a.dense_S;
+  } else {
+    if ((int)blockIdx.y >= *a.n_active) return;
+    e = a.active[blockIdx.y];
+    p0 = a.offs[e];
+    p1 = a.offs[e + 1];
+  }
+  constexpr int RPI = 64 / LPR;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int u0 = lane % LPR, rsub = lane / LPR;
+  const int U = a.nb * 4;
+  const int row_begin = blockIdx.x * a.tile_rows;
+  const int row_end = min(row_begin + a.tile_rows, a.nrows);
+  const uint8_t *W0 = a.w0 + (size_t)e * a.w_estride;
+  const uint8_t *W1 = GATEUP ? a.w1 + (size_t)e * a.w_estride : nullptr;
+  constexpr int BB = block_bytes(T);
+
+  for (int pc = p0; pc < p1; pc += NP) {
+    Q8Slice xs[NP][ITER];
+    int ptok[NP], pk[NP];
+    bool pv[NP];
+#pragma unroll
+    for (int n = 0; n < NP; ++n) {
+      const int p = pc + n;
+      pv[n] = p < p1;
+      const int pair = a.dense_S > 0 ? (pv[n] ? p : p0) : a.pairs[pv[n] ? p : p0];
+      const int Kp = a.dense_S > 0 ? 1 : a.K;
+      ptok[n] = pair / Kp;
+      pk[n] = pair % Kp;
+      const uint8_t *xrow = a.xq + (size_t)(ptok[n] * a.ne11 + pk[n] % a.ne11) * a.xq_rstride;
+#pragma unroll
+      for (int it = 0; it < ITER; ++it) {
+        const int u = u0 + it * LPR;
+        if (u < U) load_q8_slice<T>(xrow, a.nb, u >> 2, u & 3, xs[n][it]);
+      }
+    }
+    for (int r0 = row_begin + wave * RPI; r0 < row_end; r0 += 4 * RPI) {
+      const int r = r0 + rsub;
+      const bool rv = r < row_end;
+      float acc0[NP], acc1[NP];
+#pragma unroll
+      for (int n = 0; n < NP; ++n) acc0[n] = acc1[n] = 0.f;
+#pragma unroll
+      for (int it = 0; it < ITER; ++it) {
+        const int u = u0 + it * LPR;
+        if (rv && u < U) {
+          const int b = u >> 2, q = u & 3;
+          WSlice w0, w1;
+          load_w_slice<T>(W0 + (size_t)r * a.w_rstride + (size_t)b * BB, q, w0);
+          if constexpr (GATEUP) load_w_slice<T>(W1 + (size_t)r * a.w_rstride + (size_t)b * BB, q, w1);
+#pragma unroll
+          for (int n = 0; n < NP; ++n) {
+            acc0[n] += quarter_dot<T>(w0, q, xs[n][it], s_grid, s_signs);
+            if constexpr (GATEUP) acc1[n] += quarter_dot<T>(w1, q, xs[n][it], s_grid, s_signs);
+          }
+        }
+      }
+#pragma unroll
+      for (int n = 0; n < NP; ++n) {
+        acc0[n] = group_sum<LPR>(acc0[n]);
+        if constexpr (GATEUP) acc1[n] = group_sum<LPR>(acc1[n]);
+      }
+      if (rv && u0 == 0) {
+#pragma unroll
+        for (int n = 0; n < NP; ++n) {
+          if (!pv[n]) continue;
+          const float v = GATEUP ? silu_f32(acc0[n]) * acc1[n] : acc0[n];
+          a.out[(size_t)ptok[n] * a.out_s + (size_t)pk[n] * a.out_k + r] = v;
+        }
+      }
+    }
+  }
+}
+
+// ============================================================ combine
+// ggml_mul(down, weights) then sum_topk (moe_routed_ggml.hpp:198-214):
+// out = ((w0*y0 + w1*y1) + w2*y2) + ...   (+ shared, moe_block.hpp:201-202)
+__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, const float *__restrict__ w,
+                                                 const float *__restrict__ shared, int H, int K,
+                                                 float *__restrict__ out) {
+  const int s = blockIdx.y;
+  const int h = blockIdx.x * 256 + threadIdx.x;
+  if (h >= H) return;
+  const float *ys = y + (size_t)s * K * H;
+  float acc = w[(size_t)s * K] * ys[h];
+  for (int k = 1; k < K; ++k) acc = acc + w[(size_t)s * K + k] * ys[(size_t)k * H + h];
+  if (shared) acc = acc + shared[(size_t)s * H + h];
+  out[(size_t)s * H + h] = acc;
+}
+
+// zero (negative id) or NaN (id >= n_experts) rows of routes the GEMV skips
+// (patches/ggml/0002...:50-54; kernels/quant/kquant_matmul.cu:660-663)
+__global__ void k_fill_skipped(const int32_t *__restrict__ ids, size_t id_s, size_t id_k, int n_ids, int S,
+                               int n_experts, int O, float *out, size_t out_s, size_t out_k) {
+  const int pair = blockIdx.y;
+  const int s = pair / n_ids, k = pair % n_ids;
+  const int e = ids[s * id_s + k * id_k];
+  if (e >= 0 && e < n_experts) return;
+  const float v = e < 0 ? 0.0f : __int_as_float(0x7fc00000);
+  for (int r = blockIdx.x * 256 + threadIdx.x; r < O; r += gridDim.x * 256) out[s * out_s + k * out_k + r] = v;
+}
+
+// ============================================================ fp32 router GEMV
+// logits[s][e] = sum_i W[e][i] * x[s][i] (ggml_mul_mat(router, cur), moe_routed_ggml.hpp:55)
+__global__ __launch_bounds__(256) void k_router_gemv(const float *__restrict__ W, const float *__restrict__ x,
+                                                     int H, int E, int S, float *__restrict__ logits) {
+  __shared__ float part[4][64];
+  const int e = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float *wr = W + (size_t)e * H;
+  for (int s0 = 0; s0 < S; s0 += 64) {
+    // each wave covers a quarter of H for up to 64 tokens... tokens looped
+    const int ns = min(64, S - s0);
+    for (int si = 0; si < ns; ++si) {
+      const float *xr = x + (size_t)(s0 + si) * H;
+      float acc = 0.f;
+      for (int i = (wave * 64 + lane) * 4; i < H; i += 1024) {
+        const float4 wv = *reinterpret_cast<const float4 *>(wr + i);
+        const float4 xv = *reinterpret_cast<const float4 *>(xr + i);
+        acc = __builtin_fmaf(wv.x, xv.x, acc);
+        acc = __builtin_fmaf(wv.y, xv.y, acc);
+        acc = __builtin_fmaf(wv.z, xv.z, acc);
+        acc = __builtin_fmaf(wv.w, xv.w, acc);
+      }
+      acc = group_sum<64>(acc);
+      if (lane == 0) part[wave][si] = acc;
+    }
+    __syncthreads();
+    if (wave == 0 && lane < ns) {
+      logits[(size_t)(s0 + lane) * E + e] = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace zm

@@ -1,0 +1,233 @@
+"""Torch-facing wrappers over the C ABI (device tensors in, device tensors out)."""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from typing import Optional
+
+import torch
+
+from ._lib import ZmMoeLayer, ZmRouterSpec, ZmTensor, check, lib
+
+GGML_TYPES = {"f32": 0, "q2_K": 10, "q3_K": 11, "q4_K": 12, "q8_K": 15, "iq2_xxs": 16, "i32": 26}
+BLOCK_BYTES = {10: 84, 11: 110, 12: 144, 15: 292, 16: 66}
+QK_K = 256
+GATING = {"softmax": 0, "sigmoid": 1, "sqrt_softplus": 2}
+
+
+def row_size(t: int, n: int) -> int:
+    return n * 4 if t in (0, 26) else (n // QK_K) * BLOCK_BYTES[t]
+
+
+def _stream(stream=None) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _dev(t: torch.Tensor, name: str):
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+
+
+def init() -> None:
+    check(lib().zm_init(), "zm_init")
+
+
+def set_iq2xxs_grid(grid) -> None:
+    import numpy as np
+
+    g = np.ascontiguousarray(grid, dtype=np.uint64)
+    assert g.shape == (256,)
+    check(lib().zm_set_iq2xxs_grid(g.ctypes.data), "zm_set_iq2xxs_grid")
+
+
+def builtin_iq2xxs_grid():
+    import numpy as np
+
+    g = np.zeros(256, np.uint64)
+    lib().zm_iq2xxs_builtin_grid(g.ctypes.data)
+    return g
+
+
+def _tensor(t: int, x: torch.Tensor, ne_order) -> ZmTensor:
+    """ggml descriptor of a torch tensor whose dims are given slowest-first;
+    ne/nb are written fastest-first.  For quantized rows the last torch dim
+    is bytes and counts as `ne0` weights."""
+    T = ZmTensor()
+    T.type = t
+    shape = list(x.shape)
+    stride = list(x.stride())
+    es = x.element_size()
+    nd = len(shape)
+    ne = [1, 1, 1, 1]
+    nb = [0, 0, 0, 0]
+    for i in range(nd):
+        ne[i] = shape[nd - 1 - i]
+        nb[i] = stride[nd - 1 - i] * es
+    if t in BLOCK_BYTES:  # quantized: ne0 counts weights, nb0 = block bytes
+        ne[0] = ne_order
+        nb[0] = BLOCK_BYTES[t]
+    for i in range(nd, 4):
+        nb[i] = nb[i - 1] * ne[i - 1]
+    for i in range(4):
+        T.ne[i] = ne[i]
+        T.nb[i] = nb[i]
+    T.data = x.data_ptr()
+    return T
+
+
+def mul_mat_id(W: torch.Tensor, wtype: int, n_in: int, x: torch.Tensor, ids: torch.Tensor,
+               out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """ggml_mul_mat_id: W (E, O, row_bytes) uint8 of type `wtype` holding rows of
+    `n_in` weights; x (S, ne11, n_in) f32; ids (S, n_ids) int32 -> (S, n_ids, O)."""
+    for t, n in ((W, "W"), (x, "x"), (ids, "ids")):
+        _dev(t, n)
+    E, O, _ = W.shape
+    S, ne11, I = x.shape
+    n_ids = ids.shape[1]
+    if out is None:
+        out = torch.empty((S, n_ids, O), dtype=torch.float32, device=x.device)
+    tw = _tensor(wtype, W, n_in)
+    tx = _tensor(0, x, None)
+    ti = _tensor(26, ids, None)
+    ty = _tensor(0, out, None)
+    ok = lib().zm_mul_mat_id(C.byref(tw), C.byref(tx), C.byref(ti), C.byref(ty), _stream(stream), 1)
+    if ok != 1:
+        raise RuntimeError(f"zm_mul_mat_id declined: {lib().zm_last_error().decode()}")
+    return out
+
+
+def mul_mat_id_supported(W, wtype, n_in, x, ids, out) -> bool:
+    tw, tx, ti, ty = _tensor(wtype, W, n_in), _tensor(0, x, None), _tensor(26, ids, None), _tensor(0, out, None)
+    return lib().zm_mul_mat_id(C.byref(tw), C.byref(tx), C.byref(ti), C.byref(ty), None, 0) == 1
+
+
+def quantize_q8_K(x: torch.Tensor, stream=None) -> torch.Tensor:
+    _dev(x, "x")
+    x = x.contiguous()
+    rows, n = x.shape
+    y = torch.empty((rows, (n // QK_K) * 292), dtype=torch.uint8, device=x.device)
+    check(lib().zm_quantize_q8_K(x.data_ptr(), rows, n, y.data_ptr(), _stream(stream)), "zm_quantize_q8_K")
+    return y
+
+
+def _spec(E, topk, gating, n_groups, n_groups_used, weights_norm, weights_scale) -> ZmRouterSpec:
+    g = GATING[gating] if isinstance(gating, str) else int(gating)
+    return ZmRouterSpec(g, E, topk, n_groups, n_groups_used, int(weights_norm), float(weights_scale))
+
+
+def router(logits: torch.Tensor, topk: int, gating="softmax", logit_bias=None, sel_bias=None, n_groups: int = 0,
+           n_groups_used: int = 0, weights_norm: bool = False, weights_scale: float = 0.0, route_map=None,
+           route_mask=None, stream=None):
+    _dev(logits, "logits")
+    logits = logits.contiguous()
+    S, E = logits.shape
+    ids = torch.empty((S, topk), dtype=torch.int32, device=logits.device)
+    w = torch.empty((S, topk), dtype=torch.float32, device=logits.device)
+    spec = _spec(E, topk, gating, n_groups, n_groups_used, weights_norm, weights_scale)
+    check(lib().zm_router(C.byref(spec), logits.data_ptr(), _p(logit_bias), _p(sel_bias), _p(route_map),
+                          _p(route_mask), S, ids.data_ptr(), w.data_ptr(), _stream(stream)), "zm_router")
+    return ids, w
+
+
+def bucket(ids: torch.Tensor, E: int, stream=None):
+    _dev(ids, "ids")
+    ids = ids.contiguous()
+    S, K = ids.shape
+    dev = ids.device
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    offs = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    pairs = torch.full((max(1, S * K),), -1, dtype=torch.int32, device=dev)
+    active = torch.full((E,), -1, dtype=torch.int32, device=dev)
+    n_active = torch.empty(1, dtype=torch.int32, device=dev)
+    check(lib().zm_bucket(ids.data_ptr(), S, K, E, counts.data_ptr(), offs.data_ptr(), pairs.data_ptr(),
+                          active.data_ptr(), n_active.data_ptr(), _stream(stream)), "zm_bucket")
+    return counts, offs, pairs, active, n_active
+
+
+def block_dots(wtype: int, w_row: torch.Tensor, x: torch.Tensor, stream=None):
+    n = x.numel()
+    isum = torch.empty(n // QK_K, dtype=torch.int32, device=x.device)
+    imin = torch.empty(n // QK_K, dtype=torch.int32, device=x.device)
+    check(lib().zm_block_dots(wtype, w_row.data_ptr(), x.data_ptr(), n, isum.data_ptr(), imin.data_ptr(),
+                              _stream(stream)), "zm_block_dots")
+    return isum, imin
+
+
+@dataclass
+class MoELayer:
+    """One routed MoE FFN layer on device.
+
+    Weights are uint8 tensors in ggml layout: gate/up (n_slots, F, row_bytes(H)),
+    down (n_slots, H, row_bytes(F)); the shared expert (optional) the same
+    without the expert axis."""
+
+    H: int
+    F: int
+    n_experts: int
+    topk: int
+    type_gate: int
+    type_up: int
+    type_down: int
+    w_gate: torch.Tensor
+    w_up: torch.Tensor
+    w_down: torch.Tensor
+    gating: str = "softmax"
+    n_groups: int = 0
+    n_groups_used: int = 0
+    weights_norm: bool = False
+    weights_scale: float = 0.0
+    router_w: Optional[torch.Tensor] = None
+    logit_bias: Optional[torch.Tensor] = None
+    sel_bias: Optional[torch.Tensor] = None
+    route_map: Optional[torch.Tensor] = None
+    route_mask: Optional[torch.Tensor] = None
+    F_shared: int = 0
+    type_shared: int = 0
+    ws_gate: Optional[torch.Tensor] = None
+    ws_up: Optional[torch.Tensor] = None
+    ws_down: Optional[torch.Tensor] = None
+    _ws: dict = field(default_factory=dict, repr=False)
+
+    def desc(self) -> ZmMoeLayer:
+        d = ZmMoeLayer()
+        d.H, d.F, d.n_slots = self.H, self.F, self.w_gate.shape[0]
+        d.router = _spec(self.n_experts, self.topk, self.gating, self.n_groups, self.n_groups_used,
+                         self.weights_norm, self.weights_scale)
+        d.type_gate, d.type_up, d.type_down = self.type_gate, self.type_up, self.type_down
+        d.w_gate, d.w_up, d.w_down = _p(self.w_gate), _p(self.w_up), _p(self.w_down)
+        d.router_w, d.logit_bias, d.sel_bias = _p(self.router_w), _p(self.logit_bias), _p(self.sel_bias)
+        d.route_map, d.route_mask = _p(self.route_map), _p(self.route_mask)
+        d.F_shared, d.type_shared = self.F_shared, self.type_shared
+        d.ws_gate, d.ws_up, d.ws_down = _p(self.ws_gate), _p(self.ws_up), _p(self.ws_down)
+        return d
+
+    def workspace(self, S: int, device) -> torch.Tensor:
+        if S not in self._ws:
+            d = self.desc()
+            n = lib().zm_moe_workspace_size(C.byref(d), S)
+            if n == 0:
+                raise RuntimeError(f"zm_moe_workspace_size: {lib().zm_last_error().decode()}")
+            self._ws[S] = torch.empty(n, dtype=torch.uint8, device=device)
+        return self._ws[S]
+
+    def forward(self, x: torch.Tensor, logits: Optional[torch.Tensor] = None, out=None, ids=None, weights=None,
+                stream=None):
+        _dev(x, "x")
+        S = x.shape[0]
+        dev = x.device
+        if out is None:
+            out = torch.empty((S, self.H), dtype=torch.float32, device=dev)
+        if ids is None:
+            ids = torch.empty((S, self.topk), dtype=torch.int32, device=dev)
+        if weights is None:
+            weights = torch.empty((S, self.topk), dtype=torch.float32, device=dev)
+        ws = self.workspace(S, dev)
+        d = self.desc()
+        check(lib().zm_moe_forward(C.byref(d), x.data_ptr(), _p(logits), S, out.data_ptr(), ids.data_ptr(),
+                                   weights.data_ptr(), ws.data_ptr(), ws.numel(), _stream(stream)), "zm_moe_forward")
+        return out, ids, weights
