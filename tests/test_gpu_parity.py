@@ -224,3 +224,43 @@ def test_moe_layer_repeatable_and_stream_ordered():
             o2, _, _ = L.forward(x, lg)
     s.synchronize()
     np.testing.assert_array_equal(first.cpu().numpy(), o2.cpu().numpy())
+
+
+# ------------------------------------------------------------------ fused decode kernel vs multi-kernel path
+
+FUSED_CASES = {
+    "c1": (CONFIGS["c1"], {}),
+    "c2": (CONFIGS["c2"], {}),
+    "c2_S8": (CONFIGS["c2"], dict(S=8)),
+    "c4": (CONFIGS["c4"], {}),
+    "c5": (CONFIGS["c5"], {}),
+    "c5_S2": (CONFIGS["c5"], dict(S=2)),
+}
+
+
+@pytest.mark.parametrize("case", list(FUSED_CASES))
+def test_fused_decode_vs_multikernel_and_oracle(case, monkeypatch):
+    """The single persistent decode kernel against the multi-kernel path
+    (same arithmetic, different reduction order) and the oracle; 20 launches
+    back to back must give identical bits (sync words reset every launch)."""
+    c, kw = FUSED_CASES[case]
+    c = reduced(c, **kw)
+    b = Built(c, seed=21)
+    L = b.layer()
+    x = torch.from_numpy(b.x).cuda()
+    lg = None if c.router_gemv else torch.from_numpy(b.logits).cuda()
+    monkeypatch.setenv("ZEROMOE_FUSED_DECODE", "1")
+    out1, ids1, w1 = L.forward(x, lg)
+    first = out1.clone()
+    for _ in range(20):
+        out1, ids1, w1 = L.forward(x, lg)
+    assert L.status(c.S) == 0
+    np.testing.assert_array_equal(first.cpu().numpy(), out1.cpu().numpy())
+    monkeypatch.setenv("ZEROMOE_FUSED_DECODE", "0")
+    out2, ids2, w2 = L.forward(x, lg)
+    _sync()
+    np.testing.assert_array_equal(ids1.cpu().numpy(), ids2.cpu().numpy())
+    np.testing.assert_array_equal(w1.cpu().numpy(), w2.cpu().numpy())
+    assert_close_layer(out1.cpu().numpy(), out2.cpu().numpy(), rtol=1e-4)
+    ref = b.oracle_forward(ids1.cpu().numpy(), w1.cpu().numpy())
+    assert_close_layer(out1.cpu().numpy(), ref)

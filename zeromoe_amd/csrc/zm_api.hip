@@ -7,11 +7,12 @@
 #include <cstdarg>
 #include <atomic>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 
 #include "../../include/zeromoe.h"
-#include "zm_kernels.hpp"
+#include "zm_decode.hpp"
 
 using namespace zm;
 
@@ -445,6 +446,9 @@ struct LayerWs {
   float *act_s;
   uint8_t *aq_s;
   float *y_s;
+  float *f_act;
+  uint8_t *f_aq;
+  uint32_t *f_sync;
 };
 
 size_t layer_ws(const zm_moe_layer *L, int S, uint8_t *base, LayerWs *w) {
@@ -469,6 +473,12 @@ size_t layer_ws(const zm_moe_layer *L, int S, uint8_t *base, LayerWs *w) {
     t.aq_s = b.take<uint8_t>((size_t)S * q8_row_bytes(L->F_shared / QK));
     t.y_s = b.take<float>((size_t)S * H * 4);
   }
+  // fused decode: act rows of every pair then the shared rows, their Q8_K
+  // rows, and the sync words (zero at allocation, left at zero by every launch)
+  const size_t fs = L->F_shared > 0 ? (size_t)L->F_shared : 0;
+  t.f_act = b.take<float>(((size_t)S * K * F + S * fs) * 4);
+  t.f_aq = b.take<uint8_t>((size_t)S * K * q8_row_bytes(nbF) + (fs ? (size_t)S * q8_row_bytes((int)fs / QK) : 0));
+  t.f_sync = b.take<uint32_t>((4 + ((size_t)S * K * F + S * fs) / QK) * 4);
   if (w) *w = t;
   return b.off + 256;
 }
@@ -492,9 +502,134 @@ int check_layer(const zm_moe_layer *L) {
   if (L->router_w && L->H % 4) return fail("router GEMV needs H % 4 == 0");
   return 0;
 }
+using DecFn = void (*)(DecodeArgs);
+
+template <int TG, int TD, int TS>
+DecFn dec_pick(int it1, int it2) {
+  if (it1 <= 1) {
+    if (it2 <= 2) return k_moe_decode<TG, TD, TS, 1, 2>;
+    if (it2 <= 3) return k_moe_decode<TG, TD, TS, 1, 3>;
+    if (it2 <= 5) return k_moe_decode<TG, TD, TS, 1, 5>;
+  } else if (it1 <= 2) {
+    if (it2 <= 2) return k_moe_decode<TG, TD, TS, 2, 2>;
+    if (it2 <= 3) return k_moe_decode<TG, TD, TS, 2, 3>;
+    if (it2 <= 5) return k_moe_decode<TG, TD, TS, 2, 5>;
+  }
+  return nullptr;
+}
+
+DecFn find_decode(int tg, int td, int ts, int it1, int it2) {
+  if (tg == T_Q4_K && td == T_Q4_K && ts == 0) return dec_pick<T_Q4_K, T_Q4_K, 0>(it1, it2);
+  if (tg == T_Q2_K && td == T_Q3_K && ts == 0) return dec_pick<T_Q2_K, T_Q3_K, 0>(it1, it2);
+  if (tg == T_IQ2_XXS && td == T_IQ2_XXS && ts == 0) return dec_pick<T_IQ2_XXS, T_IQ2_XXS, 0>(it1, it2);
+  if (tg == T_Q2_K && td == T_Q2_K && ts == T_Q4_K) return dec_pick<T_Q2_K, T_Q2_K, T_Q4_K>(it1, it2);
+  if (tg == T_Q2_K && td == T_Q2_K && ts == 0) return dec_pick<T_Q2_K, T_Q2_K, 0>(it1, it2);
+  return nullptr;
+}
+
+bool fused_enabled() {
+  const char *e = getenv("ZEROMOE_FUSED_DECODE");
+  return !(e && e[0] == '0');
+}
+
+// grid of co-resident workgroups for a decode kernel (cached per device and kernel)
+int decode_grid(DecFn fn, int *out) {
+  static std::mutex mu;
+  static struct Ent {
+    int dev;
+    DecFn fn;
+    int grid;
+  } cache[64];
+  static int n = 0;
+  int dev = 0;
+  HIP_OK(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(mu);
+  for (int i = 0; i < n; ++i)
+    if (cache[i].dev == dev && cache[i].fn == fn) {
+      *out = cache[i].grid;
+      return 0;
+    }
+  int per_cu = 0, cus = 0;
+  HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(fn), DEC_THREADS, 0));
+  HIP_OK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  const int grid = per_cu * cus;
+  if (grid <= 0) return fail("decode kernel does not fit on a CU");
+  if (n < 64) cache[n++] = Ent{dev, fn, grid};
+  *out = grid;
+  return 0;
+}
+
+// Returns 0 when launched, 1 when this shape takes the multi-kernel path, -1 on error.
+int launch_fused(const zm_moe_layer *L, const float *x, const float *logits, int S, float *out, int32_t *ids,
+                 float *wts, const LayerWs &w, const DeviceState *d, hipStream_t st) {
+  const int H = L->H, F = L->F, E = L->router.n_experts, K = L->router.topk;
+  const int nbH = H / QK, nbF = F / QK;
+  const int Fs = L->F_shared > 0 ? L->F_shared : 0;
+  const int nbFs = Fs / QK;
+  if (!fused_enabled() || S > DEC_MAX_S || S * K > DEC_MAX_PAIRS || S * nbH > DEC_MAX_XQ_BLOCKS || E > ROUTER_MAX_E)
+    return 1;
+  if (L->type_up != L->type_gate) return 1;
+  const int it1 = (4 * nbH + 63) / 64;
+  const int it2 = (K * 4 * nbF + (Fs ? 4 * nbFs : 0) + 63) / 64;
+  DecFn fn = find_decode(L->type_gate, L->type_down, Fs ? L->type_shared : 0, it1, it2);
+  if (!fn) return 1;
+  int G = 0;
+  if (decode_grid(fn, &G)) return -1;
+  const long T1 = (long)S * K * F + (long)S * Fs;
+  if (T1 / G + 2 > (long)(DEC_MAX_TOUCH - 1) * QK) return 1;
+  DecodeArgs a{};
+  a.r = RouterArgs{logits, L->logit_bias, L->sel_bias, L->route_map, L->route_mask, E, K, L->router.gating,
+                   L->router.n_groups, L->router.n_groups_used, L->router.weights_norm, L->router.weights_scale,
+                   ids, wts};
+  a.x = x;
+  a.out = out;
+  a.H = H;
+  a.F = F;
+  a.K = K;
+  a.S = S;
+  a.nbH = nbH;
+  a.nbF = nbF;
+  a.wg = (const uint8_t *)L->w_gate;
+  a.wu = (const uint8_t *)L->w_up;
+  a.wd = (const uint8_t *)L->w_down;
+  a.g_rstride = row_bytes(L->type_gate, H);
+  a.g_estride = a.g_rstride * F;
+  a.d_rstride = row_bytes(L->type_down, F);
+  a.d_estride = a.d_rstride * H;
+  a.Fs = Fs;
+  a.nbFs = nbFs;
+  if (Fs) {
+    a.sg = (const uint8_t *)L->ws_gate;
+    a.su = (const uint8_t *)L->ws_up;
+    a.sd = (const uint8_t *)L->ws_down;
+    a.sg_rstride = row_bytes(L->type_shared, H);
+    a.sd_rstride = row_bytes(L->type_shared, Fs);
+  }
+  a.act = w.f_act;
+  a.aq = w.f_aq;
+  a.sync = w.f_sync;
+  a.grid = d->grid;
+  a.signs = d->signs;
+  a.spin_limit = 1 << 22;
+  void *args[] = {&a};
+  HIP_OK(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(fn), dim3(G), dim3(DEC_THREADS), args, 0, st));
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
+
+int zm_moe_status(const zm_moe_layer *layer, int S, void *workspace, void *stream) {
+  if (check_layer(layer) || S <= 0 || !workspace) return -1;
+  LayerWs w;
+  layer_ws(layer, S, (uint8_t *)workspace, &w);
+  uint32_t err = 0, zero = 0;
+  HIP_OK(hipMemcpyAsync(&err, w.f_sync + 2, 4, hipMemcpyDeviceToHost, (hipStream_t)stream));
+  HIP_OK(hipMemcpyAsync(w.f_sync + 2, &zero, 4, hipMemcpyHostToDevice, (hipStream_t)stream));
+  HIP_OK(hipStreamSynchronize((hipStream_t)stream));
+  return (int)err;
+}
 
 size_t zm_moe_workspace_size(const zm_moe_layer *layer, int S) {
   if (check_layer(layer) || S <= 0) return 0;
@@ -522,6 +657,10 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
   if (L->router_w) {
     hipLaunchKernelGGL(k_router_gemv, dim3(E), dim3(256), 0, st, L->router_w, x, H, E, S, w.logits);
     lg = w.logits;
+  }
+  {
+    const int rc = launch_fused(L, x, lg, S, out, ids, wts, w, d, st);
+    if (rc <= 0) return rc;
   }
   if (zm_router(&L->router, lg, L->logit_bias, L->sel_bias, L->route_map, L->route_mask, S, ids, wts, st))
     return -1;

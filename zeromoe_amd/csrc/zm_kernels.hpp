@@ -136,16 +136,22 @@ __device__ __forceinline__ void wave_argmax(float &v, int &i) {
 
 constexpr int ROUTER_MAX_E = 1024;
 
-__global__ __launch_bounds__(64) void k_router(RouterArgs a) {
-  __shared__ float p[ROUTER_MAX_E];
-  __shared__ float sel[ROUTER_MAX_E];
-  __shared__ float gscore[64];
-  const int s = blockIdx.x, lane = threadIdx.x;
+// LDS visibility between lanes of one wave (no workgroup barrier)
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// One wave routes token s.  p/sel: LDS scratch of E floats each, gscore: 64.
+// Lane k < K ends with (id, weight) of route k after the slot table.
+__device__ __forceinline__ void router_token(const RouterArgs &a, int s, int lane, float *p, float *sel,
+                                             float *gscore, int &id_out, float &w_out) {
   const int E = a.E, K = a.K;
   const float *l = a.logits + (size_t)s * E;
   const float NEG_INF = __int_as_float(0xff800000);
   for (int e = lane; e < E; e += 64) p[e] = a.logit_bias ? l[e] + a.logit_bias[e] : l[e];
-  __syncthreads();
+  wave_sync();
   if (a.gating == 0) {
     float mx = NEG_INF;
     for (int e = lane; e < E; e += 64) mx = p[e] > mx ? p[e] : mx;
@@ -174,7 +180,7 @@ __global__ __launch_bounds__(64) void k_router(RouterArgs a) {
     }
   }
   for (int e = lane; e < E; e += 64) sel[e] = a.sel_bias ? p[e] + a.sel_bias[e] : p[e];
-  __syncthreads();
+  wave_sync();
   const int G = a.n_groups;
   if (G > 1 && a.n_groups_used > 0 && a.n_groups_used < G && E % G == 0 && G <= 64) {
     const int gs = E / G;
@@ -191,46 +197,46 @@ __global__ __launch_bounds__(64) void k_router(RouterArgs a) {
       }
       gscore[lane] = gs >= 2 ? sel[b1] + sel[b2] : sel[b1];
     }
-    __syncthreads();
+    wave_sync();
     bool keep = false;
-    float gv = lane < G ? gscore[lane] : NEG_INF;
-    int gi = lane < G ? lane : 0x7fffffff;
+    const float gv = lane < G ? gscore[lane] : NEG_INF;
+    const int gi = lane < G ? lane : 0x7fffffff;
     for (int r = 0; r < a.n_groups_used; ++r) {
       float v = keep ? NEG_INF : gv;
       int i = keep ? 0x7fffffff : gi;
       wave_argmax(v, i);
       if (lane == i) keep = true;
     }
-    // mask experts of dropped groups
     for (int e = lane; e < E; e += 64) {
-      const int g = e / gs;
-      const bool kg = __shfl(keep ? 1 : 0, g, 64) != 0;
+      const bool kg = __shfl(keep ? 1 : 0, e / gs, 64) != 0;
       if (!kg) sel[e] = NEG_INF;
     }
-    __syncthreads();
+    wave_sync();
   }
-  // top-k: repeated wave argmax; taken[] as a per-lane bitmask (E <= 1024 -> 16 bits)
+  // top-k: repeated wave argmax over register copies (E <= 1024 -> 16 per lane)
+  float sv[ROUTER_MAX_E / 64];
+#pragma unroll
+  for (int t = 0; t < ROUTER_MAX_E / 64; ++t) sv[t] = (lane + 64 * t) < E ? sel[lane + 64 * t] : NEG_INF;
   uint32_t taken = 0;
   float wk = 0.f;
   int idk = 0;
   for (int k = 0; k < K; ++k) {
     float v = NEG_INF;
     int i = 0x7fffffff;
-    for (int t = 0, e = lane; e < E; ++t, e += 64) {
-      if (taken & (1u << t)) continue;
-      if (i == 0x7fffffff || outranks(sel[e], e, v, i)) {
-        v = sel[e];
+#pragma unroll
+    for (int t = 0; t < ROUTER_MAX_E / 64; ++t) {
+      const int e = lane + 64 * t;
+      if (e < E && !(taken & (1u << t)) && (i == 0x7fffffff || outranks(sv[t], e, v, i))) {
+        v = sv[t];
         i = e;
       }
     }
     wave_argmax(v, i);
     if (i != 0x7fffffff && (i & 63) == lane) taken |= 1u << (i >> 6);
-    if (lane == k) {
-      idk = i;
-      wk = p[i];
-    }
+    if (lane == k) idk = i;
   }
-  // weights: lane k holds route k; normalise in k order (ggml sum_rows accumulates in double)
+  if (lane < K) wk = p[idk];
+  // normalise in k order (ggml sum_rows accumulates in double)
   if (a.weights_norm) {
     double sum = 0.0;
     for (int k = 0; k < K; ++k) sum += (double)__shfl(wk, k, 64);
@@ -239,15 +245,27 @@ __global__ __launch_bounds__(64) void k_router(RouterArgs a) {
     wk = wk / fs;
   }
   if (a.weights_scale != 0.0f && a.weights_scale != 1.0f) wk = wk * a.weights_scale;
-  if (lane < K) {
-    int id = idk;
-    if (a.route_map) {
-      const float m = a.route_mask ? a.route_mask[idk] : (a.route_map[idk] >= 0 ? 1.0f : 0.0f);
-      id = a.route_map[idk];
-      wk = wk * m;
-    }
-    a.ids[(size_t)s * K + lane] = id;
-    a.weights[(size_t)s * K + lane] = wk;
+  int id = idk;
+  if (lane < K && a.route_map) {
+    const float m = a.route_mask ? a.route_mask[idk] : (a.route_map[idk] >= 0 ? 1.0f : 0.0f);
+    id = a.route_map[idk];
+    wk = wk * m;
+  }
+  id_out = id;
+  w_out = wk;
+}
+
+__global__ __launch_bounds__(64) void k_router(RouterArgs a) {
+  __shared__ float p[ROUTER_MAX_E];
+  __shared__ float sel[ROUTER_MAX_E];
+  __shared__ float gscore[64];
+  const int s = blockIdx.x, lane = threadIdx.x;
+  int id;
+  float w;
+  router_token(a, s, lane, p, sel, gscore, id, w);
+  if (lane < a.K) {
+    a.ids[(size_t)s * a.K + lane] = id;
+    a.weights[(size_t)s * a.K + lane] = w;
   }
 }
 

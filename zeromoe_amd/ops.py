@@ -212,7 +212,7 @@ class MoELayer:
             n = lib().zm_moe_workspace_size(C.byref(d), S)
             if n == 0:
                 raise RuntimeError(f"zm_moe_workspace_size: {lib().zm_last_error().decode()}")
-            self._ws[S] = torch.empty(n, dtype=torch.uint8, device=device)
+            self._ws[S] = torch.zeros(n, dtype=torch.uint8, device=device)  # sync words start at zero
         return self._ws[S]
 
     def forward(self, x: torch.Tensor, logits: Optional[torch.Tensor] = None, out=None, ids=None, weights=None,
@@ -231,3 +231,8 @@ class MoELayer:
         check(lib().zm_moe_forward(C.byref(d), x.data_ptr(), _p(logits), S, out.data_ptr(), ids.data_ptr(),
                                    weights.data_ptr(), ws.data_ptr(), ws.numel(), _stream(stream)), "zm_moe_forward")
         return out, ids, weights
+
+    def status(self, S: int, stream=None) -> int:
+        """0 when the last decode launches on this workspace completed normally."""
+        d = self.desc()
+        return lib().zm_moe_status(C.byref(d), S, self._ws[S].data_ptr(), _stream(stream))
