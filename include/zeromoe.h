@@ -144,7 +144,13 @@ typedef struct zm_moe_layer {
   const void *ws_gate, *ws_up, *ws_down;
 } zm_moe_layer;
 
+/* Workspace bytes for S tokens.  The workspace must be zero-filled once
+ * before its first use (it holds the decode kernel's sync words, which every
+ * call leaves at zero); calls sharing one workspace must not overlap. */
 size_t zm_moe_workspace_size(const zm_moe_layer *layer, int S);
+/* Synchronises `stream` and returns (then clears) the decode kernel's error
+ * word for this workspace: 0 = ok, 1 = a bounded wait expired. */
+int zm_moe_status(const zm_moe_layer *layer, int S, void *workspace, void *stream);
 /* x [S][H] f32; logits [S][E] (ignored when router_w is set); out [S][H];
  * ids_out / weights_out [S][K] (optional): the routes after the slot table.
  * workspace: device memory of zm_moe_workspace_size() bytes. */
