@@ -157,6 +157,11 @@ int zm_moe_status(const zm_moe_layer *layer, int S, void *workspace, void *strea
 int zm_moe_forward(const zm_moe_layer *layer, const float *x, const float *logits, int S, float *out,
                    int32_t *ids_out, float *weights_out, void *workspace, size_t workspace_size, void *stream);
 
+/* Debug: copy the last decode launch's phase timestamps (8 per workgroup,
+ * wall_clock64 ticks; recorded only when ZEROMOE_TRACE=1) into host[n].
+ * Synchronises the device.  Returns the count copied. */
+int zm_debug_trace(uint64_t *host, int n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -49,6 +49,7 @@ SIGNATURES = {
     "zm_block_dots": (I, [I, P, P, I, P, P, P]),
     "zm_moe_workspace_size": (SZ, [C.POINTER(ZmMoeLayer), I]),
     "zm_moe_status": (I, [C.POINTER(ZmMoeLayer), I, P, P]),
+    "zm_debug_trace": (I, [P, I]),
     "zm_moe_forward": (I, [C.POINTER(ZmMoeLayer), P, P, I, P, P, P, P, SZ, P]),
 }
 

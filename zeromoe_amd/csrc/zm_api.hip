@@ -45,6 +45,8 @@ struct DeviceState {
   uint64_t *signs = nullptr;  // 128 x u64 byte masks of ksigns_iq2xs
   void *ws = nullptr;         // zm_mul_mat_id workspace
   size_t ws_size = 0;
+  uint64_t *trace = nullptr;  // decode-kernel phase timestamps (ZEROMOE_TRACE=1)
+  size_t trace_n = 0;
 };
 DeviceState g_dev[kMaxDevices];
 std::mutex g_mu;
@@ -232,7 +234,7 @@ int zm_router(const zm_router_spec *spec, const float *logits, const float *logi
   if (S == 0) return 0;
   RouterArgs a{logits, logit_bias, sel_bias, route_map, route_mask, spec->n_experts, spec->topk, spec->gating,
                spec->n_groups, spec->n_groups_used, spec->weights_norm, spec->weights_scale, ids, weights};
-  hipLaunchKernelGGL(k_router, dim3(S), dim3(64), 0, (hipStream_t)stream, a);
+  hipLaunchKernelGGL(k_router_wg, dim3(S), dim3(256), 0, (hipStream_t)stream, a);
   HIP_OK(hipGetLastError());
   return 0;
 }
@@ -447,7 +449,6 @@ struct LayerWs {
   uint8_t *aq_s;
   float *y_s;
   float *f_act;
-  uint8_t *f_aq;
   uint32_t *f_sync;
 };
 
@@ -477,8 +478,7 @@ size_t layer_ws(const zm_moe_layer *L, int S, uint8_t *base, LayerWs *w) {
   // rows, and the sync words (zero at allocation, left at zero by every launch)
   const size_t fs = L->F_shared > 0 ? (size_t)L->F_shared : 0;
   t.f_act = b.take<float>(((size_t)S * K * F + S * fs) * 4);
-  t.f_aq = b.take<uint8_t>((size_t)S * K * q8_row_bytes(nbF) + (fs ? (size_t)S * q8_row_bytes((int)fs / QK) : 0));
-  t.f_sync = b.take<uint32_t>((4 + ((size_t)S * K * F + S * fs) / QK) * 4);
+  t.f_sync = b.take<uint32_t>((size_t)DEC_SYNC_WORDS * 4);
   if (w) *w = t;
   return b.off + 256;
 }
@@ -566,7 +566,7 @@ int launch_fused(const zm_moe_layer *L, const float *x, const float *logits, int
   const int nbH = H / QK, nbF = F / QK;
   const int Fs = L->F_shared > 0 ? L->F_shared : 0;
   const int nbFs = Fs / QK;
-  if (!fused_enabled() || S > DEC_MAX_S || S * K > DEC_MAX_PAIRS || S * nbH > DEC_MAX_XQ_BLOCKS || E > ROUTER_MAX_E)
+  if (!fused_enabled() || S > DEC_MAX_S || S * K > DEC_MAX_PAIRS || E > ROUTER_MAX_E)
     return 1;
   if (L->type_up != L->type_gate) return 1;
   const int it1 = (4 * nbH + 63) / 64;
@@ -576,7 +576,9 @@ int launch_fused(const zm_moe_layer *L, const float *x, const float *logits, int
   int G = 0;
   if (decode_grid(fn, &G)) return -1;
   const long T1 = (long)S * K * F + (long)S * Fs;
-  if (T1 / G + 2 > (long)(DEC_MAX_TOUCH - 1) * QK) return 1;
+  const size_t q8F = q8_row_bytes(nbF), q8Fs = Fs ? q8_row_bytes(nbFs) : 0;
+  if ((size_t)S * q8_row_bytes(nbH) > (size_t)DEC_LDS_Q8 || 2 * ((size_t)K * q8F + q8Fs) > (size_t)DEC_LDS_Q8) return 1;
+  if (T1 >= (1l << 24) || (long)S * H >= (1l << 24)) return 1;  // float-reciprocal index math
   DecodeArgs a{};
   a.r = RouterArgs{logits, L->logit_bias, L->sel_bias, L->route_map, L->route_mask, E, K, L->router.gating,
                    L->router.n_groups, L->router.n_groups_used, L->router.weights_norm, L->router.weights_scale,
@@ -605,14 +607,41 @@ int launch_fused(const zm_moe_layer *L, const float *x, const float *logits, int
     a.sg_rstride = row_bytes(L->type_shared, H);
     a.sd_rstride = row_bytes(L->type_shared, Fs);
   }
+  {
+    const size_t NSl = (size_t)L->n_slots;
+    const size_t wgb = NSl * a.g_estride, wdb = NSl * a.d_estride;
+    const size_t sgb = Fs ? (size_t)Fs * a.sg_rstride : 0, sdb = Fs ? (size_t)H * a.sd_rstride : 0;
+    if (wgb >= (1ull << 31) || wdb >= (1ull << 31) || sgb >= (1ull << 31) || sdb >= (1ull << 31)) return 1;
+    a.wg_bytes = (uint32_t)wgb;
+    a.wd_bytes = (uint32_t)wdb;
+    a.sg_bytes = (uint32_t)sgb;
+    a.sd_bytes = (uint32_t)sdb;
+  }
   a.act = w.f_act;
-  a.aq = w.f_aq;
   a.sync = w.f_sync;
   a.grid = d->grid;
   a.signs = d->signs;
-  a.spin_limit = 1 << 22;
+  a.spin_limit = 1 << 23;
+  if (const char *tr = getenv("ZEROMOE_TRACE"); tr && tr[0] == '1') {
+    DeviceState *dm = const_cast<DeviceState *>(d);
+    if (dm->trace_n < (size_t)G * 8) {
+      if (dm->trace) (void)hipFree(dm->trace);
+      HIP_OK(hipMalloc(&dm->trace, (size_t)G * 8 * sizeof(uint64_t)));
+      dm->trace_n = (size_t)G * 8;
+    }
+    HIP_OK(hipMemsetAsync(dm->trace, 0, dm->trace_n * sizeof(uint64_t), st));
+    a.trace = dm->trace;
+  }
   void *args[] = {&a};
-  HIP_OK(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(fn), dim3(G), dim3(DEC_THREADS), args, 0, st));
+  // A plain launch of exactly the co-resident grid: every workgroup is
+  // dispatched at once on an otherwise idle device; the wait in the kernel is
+  // bounded, so a device shared with other work degrades to an error status,
+  // never a hang.  ZEROMOE_COOP=1 uses a cooperative launch instead.
+  const char *coop = getenv("ZEROMOE_COOP");
+  if (coop && coop[0] == '1')
+    HIP_OK(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(fn), dim3(G), dim3(DEC_THREADS), args, 0, st));
+  else
+    HIP_OK(hipLaunchKernel(reinterpret_cast<const void *>(fn), dim3(G), dim3(DEC_THREADS), args, 0, st));
   return 0;
 }
 
@@ -620,13 +649,23 @@ int launch_fused(const zm_moe_layer *L, const float *x, const float *logits, int
 
 extern "C" {
 
+int zm_debug_trace(uint64_t *host, int n) {
+  DeviceState *d;
+  if (device_state(&d)) return -1;
+  if (!d->trace) return 0;
+  const int m = std::min<int>(n, (int)d->trace_n);
+  HIP_OK(hipDeviceSynchronize());
+  HIP_OK(hipMemcpy(host, d->trace, (size_t)m * sizeof(uint64_t), hipMemcpyDeviceToHost));
+  return m;
+}
+
 int zm_moe_status(const zm_moe_layer *layer, int S, void *workspace, void *stream) {
   if (check_layer(layer) || S <= 0 || !workspace) return -1;
   LayerWs w;
   layer_ws(layer, S, (uint8_t *)workspace, &w);
   uint32_t err = 0, zero = 0;
-  HIP_OK(hipMemcpyAsync(&err, w.f_sync + 2, 4, hipMemcpyDeviceToHost, (hipStream_t)stream));
-  HIP_OK(hipMemcpyAsync(w.f_sync + 2, &zero, 4, hipMemcpyHostToDevice, (hipStream_t)stream));
+  HIP_OK(hipMemcpyAsync(&err, w.f_sync + 1, 4, hipMemcpyDeviceToHost, (hipStream_t)stream));
+  HIP_OK(hipMemcpyAsync(w.f_sync + 1, &zero, 4, hipMemcpyHostToDevice, (hipStream_t)stream));
   HIP_OK(hipStreamSynchronize((hipStream_t)stream));
   return (int)err;
 }

@@ -3,22 +3,22 @@
 // Q8_K(act) -> down -> weighted top-k sum (+ shared expert), with no kernel
 // boundary in between.
 //
-// Launch: cooperative (all workgroups co-resident), 512 threads each.
+// Grid: as many 512-thread workgroups as the device holds at once.
 //   P0  every workgroup routes all tokens (one wave) and quantizes x into LDS
-//       (other waves) -- redundant but a few hundred cycles, and it avoids a
-//       grid-wide barrier before the first weight byte is requested.
-//   P1  the (pair, row) space of gate/up rows is cut into one contiguous
-//       range per workgroup; waves stream two rows at a time and write the
-//       SwiGLU output.  Each 256-row act block has a completion counter; the
-//       workgroup whose rows complete a block quantizes it to Q8_K and bumps
-//       `done`.
-//   P2  down rows: each wave first issues the weight loads of its first row,
-//       then waits for `done` to reach the block count, then computes
+//       (the other waves) -- redundant, but it avoids a grid-wide barrier
+//       before the first weight byte is requested.
+//   P1  the (pair, row) space of gate/up rows is cut into one contiguous range
+//       per workgroup; waves stream two rows at a time and store the SwiGLU
+//       output; the workgroup then adds its row count to `rows_done`.
+//   P2  down rows (token s, row h): each wave issues the weight loads of its
+//       first row, then the workgroup waits for rows_done == all rows,
+//       quantizes the act rows of its tokens into LDS (Q8_K) and computes
 //       out[s][h] = sum_k w_k * (W_down[e_k][h] . q8(act_k)) (+ shared).
-//   Exit: the last workgroup to leave resets the counters to zero, so the
-//       sync words are zero again for the next launch on the stream.
-// Waits are bounded (spin limit): on expiry the error word is set and the
-// kernel still drains, so no launch can hang the device.
+//   Exit: the last workgroup to leave zeroes the sync words for the next call.
+// Cross-workgroup data moves through agent-scope relaxed atomic loads/stores
+// (sc1: coherent past the per-XCD L2s) and one counter; no agent-scope fence
+// (an L2 write-back + invalidate on gfx950) is issued.  The wait is bounded:
+// on expiry the error word is set and the kernel still drains.
 #pragma once
 
 #include "zm_kernels.hpp"
@@ -28,9 +28,11 @@ namespace zm {
 constexpr int DEC_THREADS = 512;
 constexpr int DEC_WAVES = DEC_THREADS / 64;
 constexpr int DEC_MAX_S = 8;
-constexpr int DEC_MAX_PAIRS = 128;        // S * K
-constexpr int DEC_MAX_XQ_BLOCKS = 128;    // S * H / 256
-constexpr int DEC_MAX_TOUCH = 16;         // act blocks one workgroup's P1 range may touch
+constexpr int DEC_MAX_PAIRS = 128;  // S * K
+constexpr int DEC_LDS_Q8 = 65536;   // Q8_K staging: x rows in P0/P1, act rows in P2
+constexpr int DEC_NCNT = 16;        // rows-done counters (one 64-byte line each) to spread the atomics
+constexpr int DEC_CNT_STRIDE = 16;  // words between counters
+constexpr int DEC_SYNC_WORDS = DEC_CNT_STRIDE * (1 + DEC_NCNT);
 
 struct DecodeArgs {
   RouterArgs r;  // logits, biases, slot table; r.ids / r.weights: optional global outputs
@@ -42,46 +44,84 @@ struct DecodeArgs {
   int Fs, nbFs;
   const uint8_t *sg, *su, *sd;
   size_t sg_rstride, sd_rstride;
+  uint32_t wg_bytes, wd_bytes, sg_bytes, sd_bytes;  // buffer-resource extents (< 4 GiB)
   float *act;
-  uint8_t *aq;
-  uint32_t *sync;  // [0] done, [1] exit, [2] error, [3] unused, [4..] act block counters
+  uint32_t *sync;  // [0] workgroups exited, [1] error, [DEC_CNT_STRIDE*(1+i)] rows-done counter i
   const uint64_t *grid, *signs;
   int spin_limit;
+  uint64_t *trace;  // optional: 8 timestamps per workgroup
 };
 
-__device__ __forceinline__ uint32_t ld_acq(const uint32_t *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// q = j / d, r = j % d for 0 <= j < 2^24 via a float reciprocal and one
+// correction step (exact in that range); avoids the integer division sequence.
+__device__ __forceinline__ void divmod24(int j, int d, float inv, int &q, int &r) {
+  q = (int)((float)j * inv);
+  r = j - q * d;
+  if (r < 0) {
+    --q;
+    r += d;
+  } else if (r >= d) {
+    ++q;
+    r -= d;
+  }
 }
 
-template <int T>
-__device__ __forceinline__ void load_q8_lds_slice(const uint8_t *row, int nb, int u, Q8Slice &s) {
-  load_q8_slice<T>(row, nb, u >> 2, u & 3, s);
+template <class V>
+__device__ __forceinline__ V ld_co(const V *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+template <class V>
+__device__ __forceinline__ void st_co(V *p, V v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// this wave's coherent stores have completed (vmcnt(0)) before what follows
+__device__ __forceinline__ void stores_done() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt and lgkmcnt left at their maxima
+}
+__device__ __forceinline__ void after_wait() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup"); }
+// LDS writes of this wave visible to its other lanes
+__device__ __forceinline__ void stage_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ void store_q8_lds(uint8_t *row, int nb, int blk, const Q8Out &o, int lane) {
+  const uint32_t packed = (uint32_t)(uint8_t)o.q[0] | ((uint32_t)(uint8_t)o.q[1] << 8) |
+                          ((uint32_t)(uint8_t)o.q[2] << 16) | ((uint32_t)(uint8_t)o.q[3] << 24);
+  *reinterpret_cast<uint32_t *>(row + (size_t)blk * QK + 4 * lane) = packed;
+  if (lane == 0) reinterpret_cast<float *>(row + q8_d_off(nb))[blk] = o.d;
+  if ((lane & 3) == 0) reinterpret_cast<int16_t *>(row + q8_bs_off(nb))[blk * 16 + (lane >> 2)] = (int16_t)o.bsum16;
+}
+
+#define ZM_TRACE(slot)                                                         \
+  do {                                                                         \
+    if (a.trace && tid == 0) a.trace[(size_t)g * 8 + (slot)] = wall_clock64(); \
+  } while (0)
 
 template <int TG, int TD, int TS, int IT1, int IT2>
 __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
-  __shared__ float s_p[ROUTER_MAX_E];
-  __shared__ float s_sel[ROUTER_MAX_E];
-  __shared__ float s_gs[64];
+  __shared__ RouterLds s_rl;
   __shared__ int s_ids[DEC_MAX_PAIRS];
   __shared__ float s_w[DEC_MAX_PAIRS];
-  __shared__ int s_cidx[DEC_MAX_PAIRS];   // pair -> compact routed index (or -1)
-  __shared__ int s_vp[DEC_MAX_PAIRS];     // compact index -> pair
+  __shared__ int s_cidx[DEC_MAX_PAIRS];  // pair -> compact routed index (or -1)
+  __shared__ int s_vp[DEC_MAX_PAIRS];    // compact index -> pair
   __shared__ int s_nvp;
-  __shared__ int s_quant[DEC_MAX_TOUCH];
-  __shared__ int s_nquant;
   __shared__ int s_err;
-  __shared__ __attribute__((aligned(16))) uint8_t s_xq[DEC_MAX_XQ_BLOCKS * 292];
-  __shared__ uint64_t s_grid[(TG == T_IQ2_XXS || TD == T_IQ2_XXS || TS == T_IQ2_XXS) ? 256 : 1];
-  __shared__ uint64_t s_signs[(TG == T_IQ2_XXS || TD == T_IQ2_XXS || TS == T_IQ2_XXS) ? 128 : 1];
+  __shared__ __attribute__((aligned(16))) uint8_t s_q8[DEC_LDS_Q8];
+  __shared__ float4 s_stage[DEC_WAVES][256];  // per-wave transpose of 4 act blocks
   constexpr bool kIQ2 = TG == T_IQ2_XXS || TD == T_IQ2_XXS || TS == T_IQ2_XXS;
+  __shared__ uint64_t s_grid[kIQ2 ? 256 : 1];
+  __shared__ uint64_t s_signs[kIQ2 ? 128 : 1];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
   const int G = gridDim.x, g = blockIdx.x;
   const int S = a.S, K = a.K, H = a.H, F = a.F;
   const size_t q8x = q8_row_bytes(a.nbH);
   const size_t q8F = q8_row_bytes(a.nbF);
   const size_t q8Fs = a.Fs > 0 ? q8_row_bytes(a.nbFs) : 0;
+  ZM_TRACE(0);
 
   // ---------------------------------------------------------------- P0
   if constexpr (kIQ2) {
@@ -89,243 +129,374 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     for (int i = tid; i < 128; i += DEC_THREADS) s_signs[i] = a.signs[i];
   }
   if (tid == 0) s_err = 0;
-  if (wave == 0) {
-    for (int s = 0; s < S; ++s) {
-      int id;
-      float w;
-      router_token(a.r, s, lane, s_p, s_sel, s_gs, id, w);
-      if (lane < K) {
-        s_ids[s * K + lane] = id;
-        s_w[s * K + lane] = w;
-        if (g == 0 && a.r.ids) {
-          a.r.ids[s * K + lane] = id;
-          a.r.weights[s * K + lane] = w;
+  // x loads for the first 32 blocks go out before routing (16 lanes per block)
+  const int nxb = S * a.nbH;
+  const int l16 = lane & 15;
+  float xv[16];
+  {
+    const int bb = wave * 4 + (lane >> 4);
+    if (bb < nxb) {
+      const int s = bb / a.nbH, b = bb % a.nbH;
+      const float4 *src = reinterpret_cast<const float4 *>(a.x + (size_t)s * H + (size_t)b * QK + 16 * l16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 f = src[i];
+        xv[4 * i] = f.x;
+        xv[4 * i + 1] = f.y;
+        xv[4 * i + 2] = f.z;
+        xv[4 * i + 3] = f.w;
+      }
+    }
+  }
+  for (int s = 0; s < S; ++s) {
+    router_wg(a.r, s, s_rl);
+    if (tid < K) {
+      s_ids[s * K + tid] = s_rl.oid[tid];
+      s_w[s * K + tid] = s_rl.ow[tid];
+      if (g == 0 && a.r.ids) {
+        a.r.ids[s * K + tid] = s_rl.oid[tid];
+        a.r.weights[s * K + tid] = s_rl.ow[tid];
+      }
+    }
+  }
+  ZM_TRACE(6);
+  for (int base = wave * 4; base < nxb; base += DEC_WAVES * 4) {
+    const int bb = base + (lane >> 4);
+    if (bb < nxb) {
+      const int s = bb / a.nbH, b = bb % a.nbH;
+      if (base != wave * 4) {
+        const float4 *src = reinterpret_cast<const float4 *>(a.x + (size_t)s * H + (size_t)b * QK + 16 * l16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 f = src[i];
+          xv[4 * i] = f.x;
+          xv[4 * i + 1] = f.y;
+          xv[4 * i + 2] = f.z;
+          xv[4 * i + 3] = f.w;
         }
       }
-      wave_sync();
-    }
-    if (lane == 0) {
-      int n = 0;
-      for (int p = 0; p < S * K; ++p) {
-        if (s_ids[p] >= 0) {
-          s_cidx[p] = n;
-          s_vp[n++] = p;
-        } else {
-          s_cidx[p] = -1;
-        }
-      }
-      s_nvp = n;
-    }
-  } else {
-    const int nblk = S * a.nbH;
-    for (int bi = wave - 1; bi < nblk; bi += DEC_WAVES - 1) {
-      const int s = bi / a.nbH, b = bi % a.nbH;
-      const float4 v = *reinterpret_cast<const float4 *>(a.x + (size_t)s * H + (size_t)b * QK + 4 * lane);
-      const Q8Out o = quant_block_wave(v, lane);
-      uint8_t *row = s_xq + (size_t)s * q8x;
-      const uint32_t packed = (uint32_t)(uint8_t)o.q[0] | ((uint32_t)(uint8_t)o.q[1] << 8) |
-                              ((uint32_t)(uint8_t)o.q[2] << 16) | ((uint32_t)(uint8_t)o.q[3] << 24);
-      *reinterpret_cast<uint32_t *>(row + (size_t)b * QK + 4 * lane) = packed;
-      if (lane == 0) reinterpret_cast<float *>(row + q8_d_off(a.nbH))[b] = o.d;
-      if ((lane & 3) == 0) reinterpret_cast<int16_t *>(row + q8_bs_off(a.nbH))[b * 16 + (lane >> 2)] = (int16_t)o.bsum16;
+      store_q8_16(s_q8 + (size_t)s * q8x, a.nbH, b, quant_block16(xv, l16), l16);
     }
   }
   __syncthreads();
+  if (tid == 0) {
+    int n = 0;
+    for (int p = 0; p < S * K; ++p) {
+      if (s_ids[p] >= 0) {
+        s_cidx[p] = n;
+        s_vp[n++] = p;
+      } else {
+        s_cidx[p] = -1;
+      }
+    }
+    for (int p = n; p < S * K; ++p) s_vp[p] = 0;
+    s_nvp = n;
+  }
+  __syncthreads();
+  ZM_TRACE(1);
   const int nvp = s_nvp;
 
   // ---------------------------------------------------------------- P1: gate/up rows
-  const long T1r = (long)nvp * F;
-  const long T1 = T1r + (long)S * a.Fs;
-  const long t0 = T1 * g / G, t1 = T1 * (g + 1) / G;
+  // Row i of this wave is j = t0 + wave + DEC_WAVES*i.  Rows go in batches of RB
+  // with two register buffers: batch b+1 is in flight while batch b computes.
+  const int T1r = nvp * F;
+  const int T1 = T1r + S * a.Fs;
+  const int t0 = (int)((long)T1 * g / G), t1 = (int)((long)T1 * (g + 1) / G);
   const int U1 = 4 * a.nbH;
+  const float invF = 1.0f / (float)F, invFs = a.Fs > 0 ? 1.0f / (float)a.Fs : 0.f;
   {
     constexpr int BG = block_bytes(TG);
     constexpr int BS = TS ? block_bytes(TS) : 1;
-    for (long j0 = t0 + wave; j0 < t1; j0 += 2 * DEC_WAVES) {
-      WSlice wgs[2][IT1], wus[2][IT1];
-      bool rv[2];
-      bool shared_row[2];
-      int tok[2];
+    constexpr int SLICE_DW = TG == T_Q2_K ? 7 : (TG == T_Q4_K ? 12 : (TG == T_IQ2_XXS ? 5 : 12));
+    constexpr int RB0 = 80 / (2 * 2 * SLICE_DW * IT1);
+    constexpr int RB = RB0 < 1 ? 1 : (RB0 > 4 ? 4 : RB0);
+    const int nrw = t1 - t0 > wave ? (t1 - t0 - wave + DEC_WAVES - 1) / DEC_WAVES : 0;
+
+    const rsrc_t rg = make_rsrc(a.wg, a.wg_bytes), ru = make_rsrc(a.wu, a.wg_bytes);
+    const rsrc_t rsg = make_rsrc(a.sg, a.sg_bytes), rsu = make_rsrc(a.su, a.sg_bytes);
+    auto issue = [&](int i0, WSlice (&bg)[RB][IT1], WSlice (&bu)[RB][IT1]) {
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const long j = j0 + (long)r * DEC_WAVES;
-        rv[r] = j < t1;
-        shared_row[r] = j >= T1r;
-        const uint8_t *gp, *up;
-        if (!shared_row[r]) {
-          const int c = (int)(j / F), n = (int)(j % F);
-          const int p = s_vp[rv[r] ? c : 0];
-          tok[r] = p / K;
-          const size_t off = (size_t)s_ids[p] * a.g_estride + (size_t)n * a.g_rstride;
-          gp = a.wg + off;
-          up = a.wu + off;
-        } else {
-          const long js = j - T1r;
-          tok[r] = (int)(js / a.Fs);
-          const int n = (int)(js % a.Fs);
-          gp = a.sg + (size_t)n * a.sg_rstride;
-          up = a.su + (size_t)n * a.sg_rstride;
-        }
+      for (int r = 0; r < RB; ++r) {
+        const int i = i0 + r;
+        if (i >= nrw) break;
+        const int j = t0 + wave + DEC_WAVES * i;
+        if (j < T1r) {
+          int c, n;
+          divmod24(j, F, invF, c, n);
+          const int e = uniform(s_ids[s_vp[uniform(c)]]);
+          const int so = uniform(e * (int)a.g_estride + uniform(n) * (int)a.g_rstride);
 #pragma unroll
-        for (int it = 0; it < IT1; ++it) {
-          const int u = lane + 64 * it;
-          if (rv[r] && u < U1) {
-            if (!shared_row[r]) {
-              load_w_slice<TG>(gp + (size_t)(u >> 2) * BG, u & 3, wgs[r][it]);
-              load_w_slice<TG>(up + (size_t)(u >> 2) * BG, u & 3, wus[r][it]);
-            } else if constexpr (TS != 0) {
-              load_w_slice<TS>(gp + (size_t)(u >> 2) * BS, u & 3, wgs[r][it]);
-              load_w_slice<TS>(up + (size_t)(u >> 2) * BS, u & 3, wus[r][it]);
+          for (int it = 0; it < IT1; ++it) {
+            const int u = lane + 64 * it;
+            if (u < U1) {
+              load_w_slice_b<TG>(rg, (u >> 2) * BG, so, u & 3, bg[r][it]);
+              load_w_slice_b<TG>(ru, (u >> 2) * BG, so, u & 3, bu[r][it]);
+            }
+          }
+        } else if constexpr (TS != 0) {
+          int ts_, n;
+          divmod24(j - T1r, a.Fs, invFs, ts_, n);
+          const int so = uniform(uniform(n) * (int)a.sg_rstride);
+#pragma unroll
+          for (int it = 0; it < IT1; ++it) {
+            const int u = lane + 64 * it;
+            if (u < U1) {
+              load_w_slice_b<TS>(rsg, (u >> 2) * BS, so, u & 3, bg[r][it]);
+              load_w_slice_b<TS>(rsu, (u >> 2) * BS, so, u & 3, bu[r][it]);
             }
           }
         }
       }
+    };
+    // the token's activation slices stay in registers while the token does not change
+    Q8Slice xsc[IT1];
+    int xs_tok = -1;
+    auto compute = [&](int i0, WSlice (&bg)[RB][IT1], WSlice (&bu)[RB][IT1]) {
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
+      for (int r = 0; r < RB; ++r) {
+        const int i = i0 + r;
+        if (i >= nrw) break;
+        const int j = t0 + wave + DEC_WAVES * i;
+        const bool shared_row = j >= T1r;
+        int q_, r_;
+        if (shared_row)
+          divmod24(j - T1r, a.Fs, invFs, q_, r_);
+        else
+          divmod24(j, F, invF, q_, r_);
+        const int tok = uniform(shared_row ? q_ : s_vp[q_] / K);
+        const int key = shared_row ? tok + DEC_MAX_S : tok;
+        const uint8_t *xrow = s_q8 + (size_t)tok * q8x;
+        if (key != xs_tok) {
+          xs_tok = key;
+#pragma unroll
+          for (int it = 0; it < IT1; ++it) {
+            const int u = lane + 64 * it;
+            if (u < U1) {
+              if (!shared_row)
+                load_q8_slice<TG>(xrow, a.nbH, u >> 2, u & 3, xsc[it]);
+              else if constexpr (TS != 0)
+                load_q8_slice<TS>(xrow, a.nbH, u >> 2, u & 3, xsc[it]);
+            }
+          }
+        }
         float ag = 0.f, au = 0.f;
 #pragma unroll
         for (int it = 0; it < IT1; ++it) {
           const int u = lane + 64 * it;
-          if (rv[r] && u < U1) {
-            Q8Slice xs;
-            const uint8_t *xrow = s_xq + (size_t)tok[r] * q8x;
-            if (!shared_row[r]) {
-              load_q8_lds_slice<TG>(xrow, a.nbH, u, xs);
-              ag += quarter_dot<TG>(wgs[r][it], u & 3, xs, s_grid, s_signs);
-              au += quarter_dot<TG>(wus[r][it], u & 3, xs, s_grid, s_signs);
+          if (u < U1) {
+            if (!shared_row) {
+              ag += quarter_dot<TG>(bg[r][it], u & 3, xsc[it], s_grid, s_signs);
+              au += quarter_dot<TG>(bu[r][it], u & 3, xsc[it], s_grid, s_signs);
             } else if constexpr (TS != 0) {
-              load_q8_lds_slice<TS>(xrow, a.nbH, u, xs);
-              ag += quarter_dot<TS>(wgs[r][it], u & 3, xs, s_grid, s_signs);
-              au += quarter_dot<TS>(wus[r][it], u & 3, xs, s_grid, s_signs);
+              ag += quarter_dot<TS>(bg[r][it], u & 3, xsc[it], s_grid, s_signs);
+              au += quarter_dot<TS>(bu[r][it], u & 3, xsc[it], s_grid, s_signs);
             }
           }
         }
         ag = group_sum<64>(ag);
         au = group_sum<64>(au);
-        if (lane == 0 && rv[r]) a.act[j0 + (long)r * DEC_WAVES] = silu_f32(ag) * au;
+        if (lane == 0) st_co(a.act + j, silu_f32(ag) * au);
+      }
+    };
+    // sched_barrier keeps every load of a batch ahead of the math that waits on
+    // the previous one (vmcnt is in order: an interleaved wait drains the queue)
+    WSlice g0[RB][IT1], v0[RB][IT1], g1[RB][IT1], v1[RB][IT1];
+    if (nrw > 0) issue(0, g0, v0);
+    for (int i0 = 0; i0 < nrw; i0 += 2 * RB) {
+      if (i0 + RB < nrw) issue(i0 + RB, g1, v1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(i0, g0, v0);
+      if (i0 + RB < nrw) {
+        if (i0 + 2 * RB < nrw) issue(i0 + 2 * RB, g0, v0);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(i0 + RB, g1, v1);
       }
     }
   }
-  __threadfence();
+  stores_done();
   __syncthreads();
-  // completion counters of the 256-row act blocks this workgroup touched
-  if (tid == 0) s_nquant = 0;
-  __syncthreads();
-  if (t1 > t0) {
-    const long b0 = t0 / QK, b1 = (t1 - 1) / QK;
-    if (tid <= b1 - b0 && tid < DEC_MAX_TOUCH) {
-      const long b = b0 + tid;
-      const long lo = t0 > b * QK ? t0 : b * QK;
-      const long hi = t1 < (b + 1) * QK ? t1 : (b + 1) * QK;
-      const uint32_t cnt = (uint32_t)(hi - lo);
-      const uint32_t old = atomicAdd(&a.sync[4 + b], cnt);
-      if (old + cnt == QK) s_quant[atomicAdd(&s_nquant, 1)] = (int)b;
-    }
-  }
-  __syncthreads();
-  for (int i = wave; i < s_nquant; i += DEC_WAVES) {
-    __threadfence();
-    const long b = s_quant[i];
-    const float4 v = reinterpret_cast<const float4 *>(a.act + b * QK)[lane];
-    const Q8Out o = quant_block_wave(v, lane);
-    uint8_t *row;
-    int blk, nb;
-    if (b < T1r / QK) {
-      const int c = (int)(b / a.nbF);
-      blk = (int)(b % a.nbF);
-      nb = a.nbF;
-      row = a.aq + (size_t)c * q8F;
-    } else {
-      const long bs = b - T1r / QK;
-      const int s = (int)(bs / a.nbFs);
-      blk = (int)(bs % a.nbFs);
-      nb = a.nbFs;
-      row = a.aq + (size_t)S * K * q8F + (size_t)s * q8Fs;
-    }
-    const uint32_t packed = (uint32_t)(uint8_t)o.q[0] | ((uint32_t)(uint8_t)o.q[1] << 8) |
-                            ((uint32_t)(uint8_t)o.q[2] << 16) | ((uint32_t)(uint8_t)o.q[3] << 24);
-    *reinterpret_cast<uint32_t *>(row + (size_t)blk * QK + 4 * lane) = packed;
-    if (lane == 0) reinterpret_cast<float *>(row + q8_d_off(nb))[blk] = o.d;
-    if ((lane & 3) == 0) reinterpret_cast<int16_t *>(row + q8_bs_off(nb))[blk * 16 + (lane >> 2)] = (int16_t)o.bsum16;
-    __threadfence();
-    if (lane == 0) atomicAdd(&a.sync[0], 1u);
-  }
+  ZM_TRACE(2);
+  if (tid == 0 && t1 > t0) atomicAdd(&a.sync[DEC_CNT_STRIDE * (1 + g % DEC_NCNT)], (uint32_t)(t1 - t0));
 
   // ---------------------------------------------------------------- P2: down rows
-  const long T2 = (long)S * H;
-  const long u0 = T2 * g / G, u1 = T2 * (g + 1) / G;
+  const int T2 = S * H;
+  const int u0 = (int)((long)T2 * g / G), u1 = (int)((long)T2 * (g + 1) / G);
+  const float invH = 1.0f / (float)H;
   const int U2 = 4 * a.nbF, U2s = 4 * a.nbFs;
   const int V = K * U2 + (a.Fs > 0 ? U2s : 0);
   constexpr int BD = block_bytes(TD);
   constexpr int BSD = TS ? block_bytes(TS) : 1;
 
-  auto load_row = [&](long j, WSlice (&ws)[IT2]) {
-    const int s = (int)(j / H), h = (int)(j % H);
+  const rsrc_t rd = make_rsrc(a.wd, a.wd_bytes), rsd = make_rsrc(a.sd, a.sd_bytes);
+  // lane byte offsets (expert slab + block) for token s; -1 = no load (skipped route / idle lane)
+  int vo_tok = -2, vo[IT2];
+  auto lane_offsets = [&](int s) {
 #pragma unroll
     for (int it = 0; it < IT2; ++it) {
       const int v = lane + 64 * it;
+      vo[it] = -1;
       if (v < K * U2) {
         const int k = v / U2, u = v % U2;
         const int e = s_ids[s * K + k];
-        if (e >= 0)
-          load_w_slice<TD>(a.wd + (size_t)e * a.d_estride + (size_t)h * a.d_rstride + (size_t)(u >> 2) * BD, u & 3,
-                           ws[it]);
-      } else if constexpr (TS != 0) {
-        if (v < V) {
-          const int u = v - K * U2;
-          load_w_slice<TS>(a.sd + (size_t)h * a.sd_rstride + (size_t)(u >> 2) * BSD, u & 3, ws[it]);
+        if (e >= 0) vo[it] = e * (int)a.d_estride + (u >> 2) * BD;
+      } else if (v < V) {
+        vo[it] = ((v - K * U2) >> 2) * BSD;
+      }
+    }
+    vo_tok = s;
+  };
+  auto load_row = [&](int j, WSlice (&ws)[IT2]) {
+    int s, h;
+    divmod24(j, H, invH, s, h);
+    s = uniform(s);
+    h = uniform(h);
+    if (s != vo_tok) lane_offsets(s);
+#pragma unroll
+    for (int it = 0; it < IT2; ++it) {
+      const int v = lane + 64 * it;
+      if (vo[it] >= 0) {
+        if (v < K * U2) {
+          load_w_slice_b<TD>(rd, vo[it], uniform(h * (int)a.d_rstride), (v % U2) & 3, ws[it]);
+        } else if constexpr (TS != 0) {
+          load_w_slice_b<TS>(rsd, vo[it], uniform(h * (int)a.sd_rstride), (v - K * U2) & 3, ws[it]);
         }
       }
     }
   };
 
-  WSlice cur[IT2];
-  long j = u0 + wave;
-  if (j < u1) load_row(j, cur);
+  // the first two rows of this wave are requested before the wait
+  WSlice c0[IT2], c1[IT2];
+  const int jw = u0 + wave;
+  if (jw < u1) load_row(jw, c0);
+  if (jw + DEC_WAVES < u1) load_row(jw + DEC_WAVES, c1);
+  __builtin_amdgcn_sched_barrier(0);
 
-  // wait for every act block to be quantized
-  if (tid == 0) {
-    const uint32_t target = (uint32_t)(T1 / QK);
+  // wait until every gate/up row of every workgroup is stored: lanes 0..15 of
+  // wave 0 poll one counter each and sum them
+  if (wave == 0) {
+    const uint32_t target = (uint32_t)T1;
     int spins = 0;
-    while (ld_acq(&a.sync[0]) < target) {
-      __builtin_amdgcn_s_sleep(2);
+    while (true) {
+      const int c = lane < DEC_NCNT ? (int)ld_co(&a.sync[DEC_CNT_STRIDE * (1 + lane)]) : 0;
+      const uint32_t total = (uint32_t)__builtin_amdgcn_readlane(group_sum_i<16>(c), 0);
+      if (total >= target) break;
+      __builtin_amdgcn_s_sleep(1);
       if (++spins > a.spin_limit) {
-        atomicOr(&a.sync[2], 1u);
-        s_err = 1;
+        if (lane == 0) {
+          atomicOr(&a.sync[1], 1u);
+          s_err = 1;
+        }
         break;
       }
     }
-    __threadfence();
   }
   __syncthreads();
-  __threadfence();
+  after_wait();
+  ZM_TRACE(3);
+
+  // quantize the act rows of this workgroup's tokens (at most two) into LDS
+  const int s_lo = u1 > u0 ? u0 / H : 0;
+  const int s_hi = u1 > u0 ? (u1 - 1) / H : -1;
+  const size_t tok_bytes = (size_t)K * q8F + q8Fs;
+  if (!s_err) {
+    const int nb_tok = K * a.nbF + (a.Fs > 0 ? a.nbFs : 0);
+    const int nb_all = (s_hi - s_lo + 1) * nb_tok;
+    // block bi -> (source act block, destination LDS row, blocks per row, block index); false = skipped route
+    auto info = [&](int bi, const float *&src, uint8_t *&row, int &nb, int &blk) -> bool {
+      const int ts = bi / nb_tok, r = bi % nb_tok;
+      const int s = s_lo + ts;
+      if (r < K * a.nbF) {
+        const int k = r / a.nbF;
+        blk = r % a.nbF;
+        nb = a.nbF;
+        const int c = s_cidx[s * K + k];
+        if (c < 0) return false;
+        src = a.act + (size_t)c * F + (size_t)blk * QK;
+        row = s_q8 + (size_t)ts * tok_bytes + (size_t)k * q8F;
+      } else {
+        blk = r - K * a.nbF;
+        nb = a.nbFs;
+        src = a.act + T1r + (size_t)s * a.Fs + (size_t)blk * QK;
+        row = s_q8 + (size_t)ts * tok_bytes + (size_t)K * q8F;
+      }
+      return true;
+    };
+    // Each wave takes 4 act blocks per round: coalesced 16-byte sc1 loads (lane l
+    // holds floats 4l..4l+3 of block k), a transpose through this wave's LDS
+    // stage to 16 lanes per block, then quant_block16.  QR rounds of loads are
+    // in flight together.
+    constexpr int QR = 3;
+    const rsrc_t ract = make_rsrc(a.act, (uint32_t)T1 * 4u);
+    const int l16q = lane & 15, kq = lane >> 4;
+    for (int base = wave * 4; base < nb_all; base += DEC_WAVES * 4 * QR) {
+      float4 ld[QR][4];
+#pragma unroll
+      for (int r = 0; r < QR; ++r) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int bi = base + r * DEC_WAVES * 4 + k;
+          const float *src;
+          uint8_t *row;
+          int nb, blk;
+          if (bi < nb_all && info(bi, src, row, nb, blk)) {
+            const auto v4 = __builtin_amdgcn_raw_buffer_load_b128(ract, (int)((src - a.act) * 4) + 16 * lane, 0, 16);
+            ld[r][k] = make_float4(__uint_as_float(v4[0]), __uint_as_float(v4[1]), __uint_as_float(v4[2]),
+                                   __uint_as_float(v4[3]));
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int r = 0; r < QR; ++r) {
+        if (base + r * DEC_WAVES * 4 >= nb_all) break;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) s_stage[wave][k * 64 + lane] = ld[r][k];
+        stage_sync();
+        float xv16[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 f = s_stage[wave][kq * 64 + 4 * l16q + i];
+          xv16[4 * i] = f.x;
+          xv16[4 * i + 1] = f.y;
+          xv16[4 * i + 2] = f.z;
+          xv16[4 * i + 3] = f.w;
+        }
+        stage_sync();
+        const int bi = base + r * DEC_WAVES * 4 + kq;
+        const float *src;
+        uint8_t *row;
+        int nb, blk;
+        if (bi < nb_all && info(bi, src, row, nb, blk)) store_q8_16(row, nb, blk, quant_block16(xv16, l16q), l16q);
+      }
+    }
+  }
+  __syncthreads();
+  ZM_TRACE(4);
 
   if (!s_err) {
     int cur_s = -1;
     Q8Slice qs[IT2];
     float wr[IT2];
-    for (; j < u1; j += DEC_WAVES) {
-      WSlice nxt[IT2];
-      const long jn = j + DEC_WAVES;
-      if (jn < u1) load_row(jn, nxt);
-      const int s = (int)(j / H), h = (int)(j % H);
+    auto compute_row = [&](int j, WSlice (&cw)[IT2]) {
+      int s, h;
+      divmod24(j, H, invH, s, h);
       if (s != cur_s) {
         cur_s = s;
+        const uint8_t *tb = s_q8 + (size_t)(s - s_lo) * tok_bytes;
 #pragma unroll
         for (int it = 0; it < IT2; ++it) {
           const int v = lane + 64 * it;
           wr[it] = 0.f;
           if (v < K * U2) {
             const int k = v / U2, u = v % U2;
-            const int c = s_cidx[s * K + k];
-            if (c >= 0) {
-              load_q8_slice<TD>(a.aq + (size_t)c * q8F, a.nbF, u >> 2, u & 3, qs[it]);
+            if (s_ids[s * K + k] >= 0) {
+              load_q8_slice<TD>(tb + (size_t)k * q8F, a.nbF, u >> 2, u & 3, qs[it]);
               wr[it] = s_w[s * K + k];
             }
           } else if constexpr (TS != 0) {
             if (v < V) {
               const int u = v - K * U2;
-              load_q8_slice<TS>(a.aq + (size_t)S * K * q8F + (size_t)s * q8Fs, a.nbFs, u >> 2, u & 3, qs[it]);
+              load_q8_slice<TS>(tb + (size_t)K * q8F, a.nbFs, u >> 2, u & 3, qs[it]);
               wr[it] = 1.0f;
             }
           }
@@ -337,34 +508,41 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
         const int v = lane + 64 * it;
         if (v < K * U2) {
           const int k = v / U2, u = v % U2;
-          if (s_ids[s * K + k] >= 0) acc += wr[it] * quarter_dot<TD>(cur[it], u & 3, qs[it], s_grid, s_signs);
+          if (s_ids[s * K + k] >= 0) acc += wr[it] * quarter_dot<TD>(cw[it], u & 3, qs[it], s_grid, s_signs);
         } else if constexpr (TS != 0) {
           if (v < V) {
             const int u = v - K * U2;
-            acc += quarter_dot<TS>(cur[it], u & 3, qs[it], s_grid, s_signs);
+            acc += quarter_dot<TS>(cw[it], u & 3, qs[it], s_grid, s_signs);
           }
         }
       }
       acc = group_sum<64>(acc);
       if (lane == 0) a.out[(size_t)s * H + h] = acc;
-#pragma unroll
-      for (int it = 0; it < IT2; ++it) cur[it] = nxt[it];
+    };
+    for (int j = jw; j < u1; j += 2 * DEC_WAVES) {
+      compute_row(j, c0);
+      if (j + 2 * DEC_WAVES < u1) load_row(j + 2 * DEC_WAVES, c0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (j + DEC_WAVES < u1) {
+        compute_row(j + DEC_WAVES, c1);
+        if (j + 3 * DEC_WAVES < u1) load_row(j + 3 * DEC_WAVES, c1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
+  ZM_TRACE(5);
 
-  // ---------------------------------------------------------------- exit: last workgroup resets the counters
+  // ---------------------------------------------------------------- exit: the last workgroup zeroes the sync words
   __syncthreads();
   if (tid == 0) {
-    __threadfence();
-    const uint32_t old = atomicAdd(&a.sync[1], 1u);
+    const uint32_t old = atomicAdd(&a.sync[0], 1u);
     if (old == (uint32_t)G - 1) {
-      const long nblk = T1 / QK;
-      for (long b = 0; b < nblk; ++b) __hip_atomic_store(&a.sync[4 + b], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&a.sync[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&a.sync[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __threadfence();
+      for (int i = 0; i < DEC_NCNT; ++i) st_co(&a.sync[DEC_CNT_STRIDE * (1 + i)], 0u);
+      st_co(&a.sync[0], 0u);
     }
   }
 }
+
+#undef ZM_TRACE
 
 }  // namespace zm

@@ -20,6 +20,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace zm {
 
 constexpr int QK = 256;
@@ -105,18 +107,76 @@ __device__ __forceinline__ float exp_f32(float x) {
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + exp_f32(-g)); }
 
 // ---------------------------------------------------------------- wave64 reductions
+//
+// Cross-lane steps use DPP (a VALU operand modifier, no LDS round trip):
+// quad_perm(1,0,3,2) = xor 1, quad_perm(2,3,0,1) = xor 2, row_half_mirror and
+// row_mirror combine 4- and 8-lane halves once every lane of the half holds the
+// same partial; the four 16-lane rows are then combined through readlane.
+// Every lane ends with the same result, in a fixed order (deterministic).
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
 
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+__device__ __forceinline__ float readlane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// sum over aligned groups of W lanes (W = 4, 8, 16, 32, 64); all lanes of a group get it
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int m = W / 2; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+  static_assert(W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "group width");
+  v += dpp_f<DPP_XOR1>(v);
+  v += dpp_f<DPP_XOR2>(v);
+  if constexpr (W >= 8) v += dpp_f<DPP_HALF_MIRROR>(v);
+  if constexpr (W >= 16) v += dpp_f<DPP_MIRROR>(v);
+  if constexpr (W == 32) v += __shfl_xor(v, 16, 64);
+  if constexpr (W == 64)
+    v = (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
   return v;
 }
 template <int W>
 __device__ __forceinline__ int group_sum_i(int v) {
-#pragma unroll
-  for (int m = W / 2; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+  static_assert(W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "group width");
+  v += dpp_i<DPP_XOR1>(v);
+  v += dpp_i<DPP_XOR2>(v);
+  if constexpr (W >= 8) v += dpp_i<DPP_HALF_MIRROR>(v);
+  if constexpr (W >= 16) v += dpp_i<DPP_MIRROR>(v);
+  if constexpr (W == 32) v += __shfl_xor(v, 16, 64);
+  if constexpr (W == 64)
+    v = (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+        (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
   return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+  v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+  v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+  v = fmaxf(v, dpp_f<DPP_MIRROR>(v));
+  return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  auto step = [](double x, auto ctrl_tag) -> double {
+    constexpr int C = decltype(ctrl_tag)::value;
+    const long long b = __double_as_longlong(x);
+    const int lo = dpp_i<C>((int)(b & 0xffffffffll)), hi = dpp_i<C>((int)(b >> 32));
+    return x + __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+  };
+  v = step(v, std::integral_constant<int, DPP_XOR1>{});
+  v = step(v, std::integral_constant<int, DPP_XOR2>{});
+  v = step(v, std::integral_constant<int, DPP_HALF_MIRROR>{});
+  v = step(v, std::integral_constant<int, DPP_MIRROR>{});
+  auto rl = [](double x, int l) {
+    const long long b = __double_as_longlong(x);
+    const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffffll), l), hi = __builtin_amdgcn_readlane((int)(b >> 32), l);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+  };
+  return (rl(v, 0) + rl(v, 16)) + (rl(v, 32) + rl(v, 48));
 }
 
 // ---------------------------------------------------------------- Q8_K activations (planar)
@@ -193,6 +253,50 @@ __device__ __forceinline__ void load_w_slice(const uint8_t *blk, int q, WSlice &
   }
 }
 
+// ---- the same slices through buffer loads: `vo` is the lane's byte offset of
+// the block start inside the resource (VGPR), `so` a wave-uniform byte offset
+// (SGPR, e.g. expert * expert_bytes + row * row_bytes).  Out-of-range reads
+// return zero instead of faulting.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 bld16(rsrc_t r, int vo, int so) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint2 bld8(rsrc_t r, int vo, int so) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0);
+  return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ uint32_t bld4(rsrc_t r, int vo, int so) { return __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0); }
+__device__ __forceinline__ uint32_t bld2(rsrc_t r, int vo, int so) { return __builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0); }
+
+template <int T>
+__device__ __forceinline__ void load_w_slice_b(rsrc_t r, int vo, int so, int q, WSlice &w) {
+  if constexpr (T == T_Q2_K) {
+    w.e = bld8(r, vo + 8 * (q >> 1), so);
+    w.a = bld16(r, vo + 16 + 16 * q, so);
+    w.f = bld4(r, vo + 80, so);
+  } else if constexpr (T == T_Q3_K) {
+    w.b = bld16(r, vo + 16 * (q & 1), so);
+    w.a = bld16(r, vo + 32 + 16 * q, so);
+    w.c.x = bld4(r, vo + 96, so);
+    w.c.y = bld4(r, vo + 100, so);
+    w.c.z = bld4(r, vo + 104, so);
+    w.c.w = bld2(r, vo + 108, so);
+  } else if constexpr (T == T_Q4_K) {
+    w.c = bld16(r, vo, so);
+    w.a = bld16(r, vo + 16 + 32 * q, so);
+    w.b = bld16(r, vo + 32 + 32 * q, so);
+  } else {  // IQ2_XXS
+    w.f = bld2(r, vo, so);
+    w.a = bld16(r, vo + 2 + 16 * q, so);
+  }
+}
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
 __device__ __forceinline__ uint32_t u4_get(const uint4 &v, int i) {
   return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
@@ -208,19 +312,31 @@ __device__ __forceinline__ QInt quarter_int(const WSlice &w, int q, const Q8Slic
                                             const uint64_t *lds_signs) {
   QInt r{0, 0};
   if constexpr (T == T_Q2_K) {
+    // Bit-plane j is masked in place (no shift for j < 3): the dot then carries
+    // a factor 4^j that is folded into the scale, so 16*isum is accumulated
+    // exactly and shifted back at the end.
     const int qq = q & 1;
     const uint32_t lo = w.e.x >> (8 * qq), hi = w.e.y >> (8 * qq);
+    int s16 = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t scb = ((j < 2 ? lo : hi) >> (16 * (j & 1))) & 0xffu;
       int dj = 0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dj = dot4((u4_get(w.a, i) >> (2 * j)) & 0x03030303u, u4_get(a.q[j], i), dj);
-      r.isum += (int)(scb & 15u) * dj;
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t x = u4_get(w.a, i);
+        const uint32_t m = j < 3 ? (x & (0x03030303u << (2 * j))) : ((x >> 2) & 0x30303030u);
+        dj = dot4(m, u4_get(a.q[j], i), dj);
+      }
+      s16 += (int)((scb & 15u) << (j == 0 ? 4 : (j == 1 ? 2 : 0))) * dj;
       r.imin += (int)(scb >> 4) * a.bs[j];
     }
+    r.isum = s16 >> 4;
   } else if constexpr (T == T_Q3_K) {
+    // value c + 4*hbit (0..7) is assembled in place at bit 2j (j < 3) or 4 (j = 3),
+    // the 4^j factor folded into the scale as for Q2_K; the -4 offset is -4*bsum.
     const int h = q >> 1, qq = q & 1;
+    int s16 = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int k = 2 * j + qq;  // scales byte index of the low nibble
@@ -230,12 +346,15 @@ __device__ __forceinline__ QInt quarter_int(const WSlice &w, int q, const Q8Slic
       int dj = 0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t q2 = (u4_get(w.a, i) >> (2 * j)) & 0x03030303u;
+        const uint32_t x = u4_get(w.a, i);
         const uint32_t hb = (u4_get(w.b, i) >> (4 * h + j)) & 0x01010101u;
-        dj = dot4(q2 | (hb << 2), u4_get(a.q[j], i), dj);
+        const uint32_t v = j < 3 ? ((x & (0x03030303u << (2 * j))) | (hb << (2 * j + 2)))
+                                 : (((x >> 2) & 0x30303030u) | (hb << 6));
+        dj = dot4(v, u4_get(a.q[j], i), dj);
       }
-      r.isum += sc * (dj - 4 * a.bs[j]);
+      s16 += sc * ((dj << (j == 0 ? 4 : (j == 1 ? 2 : 0))) - 64 * a.bs[j]);
     }
+    r.isum = s16 >> 4;
   } else if constexpr (T == T_Q4_K) {
     // scales bytes 0..11 live in header dwords y, z, w
     const int j0 = 2 * q, j1 = 2 * q + 1;

@@ -1,7 +1,7 @@
 // zm_kernels.hpp -- the routed-expert kernels for gfx950 (wave64, CDNA4).
 //
 //   k_quant_q8K  : f32 rows -> Q8_K (one wave per 256-value block)
-//   k_router     : gating + (grouped) top-k + weights + slot table, one wave per token
+//   k_router_wg  : gating + (grouped) top-k + weights + slot table, one workgroup per token
 //   k_bucket     : stable counting sort of (token, slot) pairs by expert
 //   k_gemv       : bucketed MUL_MAT_ID GEMV over Q8_K activations (decode path)
 //   k_combine    : k-ascending weighted sum over the top-k axis (+ shared expert)
@@ -37,16 +37,32 @@ __device__ __forceinline__ Q8Out quant_block_wave(float4 v, int lane) {
       idx = 4 * lane + j;
     }
   }
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) {
-    const float oa = __shfl_xor(amax, m, 64);
-    const float om = __shfl_xor(mx, m, 64);
-    const int oi = __shfl_xor(idx, m, 64);
+  // (|x|, first index) maximum over the wave; the signed value rides along
+  auto take = [&](float oa, float om, int oi) {
     if (oa > amax || (oa == amax && oi < idx)) {
       amax = oa;
       mx = om;
       idx = oi;
     }
+  };
+  take(dpp_f<DPP_XOR1>(amax), dpp_f<DPP_XOR1>(mx), dpp_i<DPP_XOR1>(idx));
+  take(dpp_f<DPP_XOR2>(amax), dpp_f<DPP_XOR2>(mx), dpp_i<DPP_XOR2>(idx));
+  take(dpp_f<DPP_HALF_MIRROR>(amax), dpp_f<DPP_HALF_MIRROR>(mx), dpp_i<DPP_HALF_MIRROR>(idx));
+  take(dpp_f<DPP_MIRROR>(amax), dpp_f<DPP_MIRROR>(mx), dpp_i<DPP_MIRROR>(idx));
+  {
+    float ra[4], rm[4];
+    int ri[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      ra[r] = readlane_f(amax, 16 * r);
+      rm[r] = readlane_f(mx, 16 * r);
+      ri[r] = __builtin_amdgcn_readlane(idx, 16 * r);
+    }
+    amax = ra[0];
+    mx = rm[0];
+    idx = ri[0];
+#pragma unroll
+    for (int r = 1; r < 4; ++r) take(ra[r], rm[r], ri[r]);
   }
   Q8Out o;
   if (amax == 0.0f) {
@@ -65,9 +81,7 @@ __device__ __forceinline__ Q8Out quant_block_wave(float4 v, int lane) {
     o.q[j] = (int8_t)q;
     s += q;
   }
-  s += __shfl_xor(s, 1, 64);
-  s += __shfl_xor(s, 2, 64);
-  o.bsum16 = s;
+  o.bsum16 = group_sum_i<4>(s);
   o.d = 1.0f / iscale;
   return o;
 }
@@ -122,151 +136,261 @@ __device__ __forceinline__ bool outranks(float sa, int ia, float sb, int ib) {
   return sa > sb || (sa == sb && ia < ib);
 }
 
-__device__ __forceinline__ void wave_argmax(float &v, int &i) {
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) {
-    const float ov = __shfl_xor(v, m, 64);
-    const int oi = __shfl_xor(i, m, 64);
-    if (outranks(ov, oi, v, i)) {
-      v = ov;
-      i = oi;
-    }
-  }
-}
-
 constexpr int ROUTER_MAX_E = 1024;
 
-// LDS visibility between lanes of one wave (no workgroup barrier)
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+// Workgroup-wide router for one token.  Softmax statistics go through
+// per-wave DPP partials in LDS.  The top-k order comes from ranking: with the
+// strict order "higher score, then lower index" packed into a 64-bit key
+// (order-preserving float bits above the complemented index), the rank of an
+// expert is the number of larger keys, which is the position repeated argmax
+// selection would give it.  T threads share one expert's comparisons.
+constexpr int ROUTER_PER = 4;  // experts per thread at most (E <= 4 * blockDim)
+struct RouterLds {
+  float p[ROUTER_MAX_E];
+  float sel[ROUTER_MAX_E];
+  unsigned long long key[ROUTER_MAX_E];
+  double dred[16];
+  float fred[16];
+  float gscore[64];
+  int keep[64];
+  int oid[128];  // top-k ids; also (best, second) per group while grouping
+  float ow[64];
+};
+
+__device__ __forceinline__ unsigned long long rank_key(float v, int e) {
+  const uint32_t u = __float_as_uint(v + 0.0f);  // -0 -> +0: equal scores tie on the index
+  const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)o << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
 }
 
-// One wave routes token s.  p/sel: LDS scratch of E floats each, gscore: 64.
-// Lane k < K ends with (id, weight) of route k after the slot table.
-__device__ __forceinline__ void router_token(const RouterArgs &a, int s, int lane, float *p, float *sel,
-                                             float *gscore, int &id_out, float &w_out) {
+// Results land in L.oid[k] / L.ow[k] (k < K) after the final barrier: ids after
+// the slot table, weights normalised/scaled/masked.
+__device__ void router_wg(const RouterArgs &a, int s, RouterLds &L) {
+  const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63, wave = tid >> 6;
   const int E = a.E, K = a.K;
-  const float *l = a.logits + (size_t)s * E;
+  const int per = (E + nthr - 1) / nthr;             // experts per thread
+  const int nwa = min((E + 63) / 64, nthr / 64);     // waves that own experts
+  const bool owner = wave < nwa;
   const float NEG_INF = __int_as_float(0xff800000);
-  for (int e = lane; e < E; e += 64) p[e] = a.logit_bias ? l[e] + a.logit_bias[e] : l[e];
-  wave_sync();
+  const float *l = a.logits + (size_t)s * E;
+  float v[ROUTER_PER];
+#pragma unroll
+  for (int i = 0; i < ROUTER_PER; ++i) {
+    const int e = tid + i * nthr;
+    v[i] = (i < per && e < E) ? (a.logit_bias ? l[e] + a.logit_bias[e] : l[e]) : NEG_INF;
+  }
   if (a.gating == 0) {
-    float mx = NEG_INF;
-    for (int e = lane; e < E; e += 64) mx = p[e] > mx ? p[e] : mx;
+    if (owner) {
+      float mx = v[0];
 #pragma unroll
-    for (int m = 32; m > 0; m >>= 1) {
-      const float o = __shfl_xor(mx, m, 64);
-      mx = o > mx ? o : mx;
+      for (int i = 1; i < ROUTER_PER; ++i)
+        if (i < per) mx = fmaxf(mx, v[i]);
+      mx = wave_max(mx);
+      if (lane == 0) L.fred[wave] = mx;
     }
-    double sum = 0.0;
-    for (int e = lane; e < E; e += 64) {
-      const float ev = exp_f32(p[e] - mx);
-      p[e] = ev;
-      sum += (double)ev;
-    }
+    __syncthreads();
+    float mx = L.fred[0];
+    for (int w = 1; w < nwa; ++w) mx = fmaxf(mx, L.fred[w]);
+    if (owner) {
+      double sum = 0.0;
 #pragma unroll
-    for (int m = 32; m > 0; m >>= 1) sum += __shfl_xor(sum, m, 64);
-    const float inv = (float)(1.0 / sum);
-    for (int e = lane; e < E; e += 64) p[e] = p[e] * inv;
-  } else if (a.gating == 1) {
-    for (int e = lane; e < E; e += 64) p[e] = 1.0f / (1.0f + exp_f32(-p[e]));
-  } else {
-    for (int e = lane; e < E; e += 64) {
-      const float x = p[e];
-      const float sp = x > 0.0f ? x + log1pf(exp_f32(-x)) : log1pf(exp_f32(x));
-      p[e] = sqrtf(sp);
+      for (int i = 0; i < ROUTER_PER; ++i) {
+        const int e = tid + i * nthr;
+        v[i] = (i < per && e < E) ? exp_f32(v[i] - mx) : 0.0f;
+        sum += (double)v[i];
+      }
+      sum = wave_sum_f64(sum);
+      if (lane == 0) L.dred[wave] = sum;
+    }
+    __syncthreads();
+    if (owner) {
+      double sum = L.dred[0];
+      for (int w = 1; w < nwa; ++w) sum += L.dred[w];
+      const float inv = (float)(1.0 / sum);
+#pragma unroll
+      for (int i = 0; i < ROUTER_PER; ++i) v[i] = v[i] * inv;
+    }
+  } else if (owner) {
+#pragma unroll
+    for (int i = 0; i < ROUTER_PER; ++i) {
+      if (i >= per) break;
+      const float x = v[i];
+      v[i] = a.gating == 1 ? 1.0f / (1.0f + exp_f32(-x)) : sqrtf(x > 0.0f ? x + log1pf(exp_f32(-x)) : log1pf(exp_f32(x)));
     }
   }
-  for (int e = lane; e < E; e += 64) sel[e] = a.sel_bias ? p[e] + a.sel_bias[e] : p[e];
-  wave_sync();
+  if (owner) {
+#pragma unroll
+    for (int i = 0; i < ROUTER_PER; ++i) {
+      const int e = tid + i * nthr;
+      if (i < per && e < E) {
+        L.p[e] = v[i];
+        L.sel[e] = a.sel_bias ? v[i] + a.sel_bias[e] : v[i];
+      }
+    }
+  }
+  __syncthreads();
   const int G = a.n_groups;
   if (G > 1 && a.n_groups_used > 0 && a.n_groups_used < G && E % G == 0 && G <= 64) {
+    // group score = best + second best selection score of the group: each expert
+    // ranks itself inside its group (same key order as the final top-k)
     const int gs = E / G;
-    if (lane < G) {
-      int b1 = -1, b2 = -1;
-      for (int j = 0; j < gs; ++j) {
-        const int e = lane * gs + j;
-        if (b1 < 0 || outranks(sel[e], e, sel[b1], b1)) {
-          b2 = b1;
-          b1 = e;
-        } else if (b2 < 0 || outranks(sel[e], e, sel[b2], b2)) {
-          b2 = e;
-        }
+    for (int e = tid; e < E; e += nthr) L.key[e] = rank_key(L.sel[e], e);
+    __syncthreads();
+    for (int e = tid; e < E; e += nthr) {
+      const int g0 = (e / gs) * gs;
+      const unsigned long long mk = L.key[e];
+      int r = 0;
+      for (int e2 = g0; e2 < g0 + gs; ++e2) r += L.key[e2] > mk;
+      if (r < 2) L.oid[2 * (e / gs) + r] = e;  // oid[] doubles as (best, second) per group
+    }
+    __syncthreads();
+    if (tid < G) L.gscore[tid] = gs >= 2 ? L.sel[L.oid[2 * tid]] + L.sel[L.oid[2 * tid + 1]] : L.sel[L.oid[2 * tid]];
+    __syncthreads();
+    if (tid < G) {
+      int r = 0;
+      for (int g2 = 0; g2 < G; ++g2) r += outranks(L.gscore[g2], g2, L.gscore[tid], tid);
+      L.keep[tid] = r < a.n_groups_used;
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += nthr)
+      if (!L.keep[e / gs]) L.sel[e] = NEG_INF;
+    __syncthreads();
+  }
+  for (int e = tid; e < E; e += nthr) L.key[e] = rank_key(L.sel[e], e);
+  __syncthreads();
+  if (E <= nthr) {
+    // T (power of two, <= 16) adjacent threads per expert, each over E/T keys
+    int T = 1;
+    while (T < 16 && 2 * T * E <= nthr) T *= 2;
+    const int e = tid / T, part = tid % T;
+    const int chunk = (E + T - 1) / T;
+    int r = 0;
+    if (e < E) {
+      const unsigned long long mk = L.key[e];
+      const int lo = part * chunk, hi = min(E, lo + chunk);
+      for (int e2 = lo; e2 < hi; ++e2) r += L.key[e2] > mk;
+    }
+    if (T >= 2) r += dpp_i<DPP_XOR1>(r);
+    if (T >= 4) r += dpp_i<DPP_XOR2>(r);
+    if (T >= 8) r += dpp_i<DPP_HALF_MIRROR>(r);
+    if (T >= 16) r += dpp_i<DPP_MIRROR>(r);
+    if (e < E && part == 0 && r < K) {
+      L.oid[r] = e;
+      L.ow[r] = L.p[e];
+    }
+  } else {
+    for (int e = tid; e < E; e += nthr) {
+      const unsigned long long mk = L.key[e];
+      int r = 0;
+      for (int e2 = 0; e2 < E; ++e2) r += L.key[e2] > mk;
+      if (r < K) {
+        L.oid[r] = e;
+        L.ow[r] = L.p[e];
       }
-      gscore[lane] = gs >= 2 ? sel[b1] + sel[b2] : sel[b1];
     }
-    wave_sync();
-    bool keep = false;
-    const float gv = lane < G ? gscore[lane] : NEG_INF;
-    const int gi = lane < G ? lane : 0x7fffffff;
-    for (int r = 0; r < a.n_groups_used; ++r) {
-      float v = keep ? NEG_INF : gv;
-      int i = keep ? 0x7fffffff : gi;
-      wave_argmax(v, i);
-      if (lane == i) keep = true;
+  }
+  __syncthreads();
+  // lane k < K of wave 0 finishes route k: norm in k order (double, as ggml's
+  // sum_rows), scale, slot table
+  float w = 0.f;
+  int id = 0;
+  if (tid < K) {
+    w = L.ow[tid];
+    id = L.oid[tid];
+    if (a.weights_norm) {
+      double sum = 0.0;
+      for (int k = 0; k < K; ++k) sum += (double)L.ow[k];
+      float fs = (float)sum;
+      fs = fs < 6.103515625e-5f ? 6.103515625e-5f : fs;
+      w = w / fs;
     }
-    for (int e = lane; e < E; e += 64) {
-      const bool kg = __shfl(keep ? 1 : 0, e / gs, 64) != 0;
-      if (!kg) sel[e] = NEG_INF;
+    if (a.weights_scale != 0.0f && a.weights_scale != 1.0f) w = w * a.weights_scale;
+    if (a.route_map) {
+      const float m = a.route_mask ? a.route_mask[id] : (a.route_map[id] >= 0 ? 1.0f : 0.0f);
+      id = a.route_map[id];
+      w = w * m;
     }
-    wave_sync();
   }
-  // top-k: repeated wave argmax over register copies (E <= 1024 -> 16 per lane)
-  float sv[ROUTER_MAX_E / 64];
-#pragma unroll
-  for (int t = 0; t < ROUTER_MAX_E / 64; ++t) sv[t] = (lane + 64 * t) < E ? sel[lane + 64 * t] : NEG_INF;
-  uint32_t taken = 0;
-  float wk = 0.f;
-  int idk = 0;
-  for (int k = 0; k < K; ++k) {
-    float v = NEG_INF;
-    int i = 0x7fffffff;
-#pragma unroll
-    for (int t = 0; t < ROUTER_MAX_E / 64; ++t) {
-      const int e = lane + 64 * t;
-      if (e < E && !(taken & (1u << t)) && (i == 0x7fffffff || outranks(sv[t], e, v, i))) {
-        v = sv[t];
-        i = e;
-      }
-    }
-    wave_argmax(v, i);
-    if (i != 0x7fffffff && (i & 63) == lane) taken |= 1u << (i >> 6);
-    if (lane == k) idk = i;
+  __syncthreads();
+  if (tid < K) {
+    L.oid[tid] = id;
+    L.ow[tid] = w;
   }
-  if (lane < K) wk = p[idk];
-  // normalise in k order (ggml sum_rows accumulates in double)
-  if (a.weights_norm) {
-    double sum = 0.0;
-    for (int k = 0; k < K; ++k) sum += (double)__shfl(wk, k, 64);
-    float fs = (float)sum;
-    fs = fs < 6.103515625e-5f ? 6.103515625e-5f : fs;
-    wk = wk / fs;
-  }
-  if (a.weights_scale != 0.0f && a.weights_scale != 1.0f) wk = wk * a.weights_scale;
-  int id = idk;
-  if (lane < K && a.route_map) {
-    const float m = a.route_mask ? a.route_mask[idk] : (a.route_map[idk] >= 0 ? 1.0f : 0.0f);
-    id = a.route_map[idk];
-    wk = wk * m;
-  }
-  id_out = id;
-  w_out = wk;
+  __syncthreads();
 }
 
-__global__ __launch_bounds__(64) void k_router(RouterArgs a) {
-  __shared__ float p[ROUTER_MAX_E];
-  __shared__ float sel[ROUTER_MAX_E];
-  __shared__ float gscore[64];
-  const int s = blockIdx.x, lane = threadIdx.x;
-  int id;
-  float w;
-  router_token(a, s, lane, p, sel, gscore, id, w);
-  if (lane < a.K) {
-    a.ids[(size_t)s * a.K + lane] = id;
-    a.weights[(size_t)s * a.K + lane] = w;
+__global__ __launch_bounds__(256) void k_router_wg(RouterArgs a) {
+  __shared__ RouterLds L;
+  router_wg(a, blockIdx.x, L);
+  if ((int)threadIdx.x < a.K) {
+    a.ids[(size_t)blockIdx.x * a.K + threadIdx.x] = L.oid[threadIdx.x];
+    a.weights[(size_t)blockIdx.x * a.K + threadIdx.x] = L.ow[threadIdx.x];
   }
+}
+
+// ============================================================ Q8_K with 16 lanes per block
+//
+// Lane l of a 16-lane group holds values [16l, 16l+16) of the block: the
+// (|x|, first index) maximum needs only the four in-row DPP steps, and each
+// lane's 16 values are exactly one of the block's 16-sums.  Same arithmetic as
+// quant_block_wave (bit-identical results).
+struct Q8Out16 {
+  uint4 q;     // 16 int8
+  float d;
+  int bsum;
+};
+
+__device__ __forceinline__ Q8Out16 quant_block16(const float (&x)[16], int l16) {
+  float amax = 0.f, mx = 0.f;
+  int idx = 0x7fffffff;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float ax = __builtin_fabsf(x[j]);
+    if (ax > amax) {
+      amax = ax;
+      mx = x[j];
+      idx = 16 * l16 + j;
+    }
+  }
+  auto take = [&](float oa, float om, int oi) {
+    if (oa > amax || (oa == amax && oi < idx)) {
+      amax = oa;
+      mx = om;
+      idx = oi;
+    }
+  };
+  take(dpp_f<DPP_XOR1>(amax), dpp_f<DPP_XOR1>(mx), dpp_i<DPP_XOR1>(idx));
+  take(dpp_f<DPP_XOR2>(amax), dpp_f<DPP_XOR2>(mx), dpp_i<DPP_XOR2>(idx));
+  take(dpp_f<DPP_HALF_MIRROR>(amax), dpp_f<DPP_HALF_MIRROR>(mx), dpp_i<DPP_HALF_MIRROR>(idx));
+  take(dpp_f<DPP_MIRROR>(amax), dpp_f<DPP_MIRROR>(mx), dpp_i<DPP_MIRROR>(idx));
+  Q8Out16 o;
+  if (amax == 0.0f) {
+    o.q = make_uint4(0, 0, 0, 0);
+    o.d = 0.0f;
+    o.bsum = 0;
+    return o;
+  }
+  const float iscale = -127.f / mx;
+  uint32_t w[4] = {0, 0, 0, 0};
+  int s = 0;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    int q = nearest_int(iscale * x[j]);
+    q = q < 127 ? q : 127;
+    s += q;
+    w[j >> 2] |= (uint32_t)(uint8_t)q << (8 * (j & 3));
+  }
+  o.q = make_uint4(w[0], w[1], w[2], w[3]);
+  o.d = 1.0f / iscale;
+  o.bsum = s;
+  return o;
+}
+
+// one Q8_K block (planar row layout) from the 16 values of this lane
+__device__ __forceinline__ void store_q8_16(uint8_t *row, int nb, int blk, const Q8Out16 &o, int l16) {
+  *reinterpret_cast<uint4 *>(row + (size_t)blk * QK + 16 * l16) = o.q;
+  if (l16 == 0) reinterpret_cast<float *>(row + q8_d_off(nb))[blk] = o.d;
+  reinterpret_cast<int16_t *>(row + q8_bs_off(nb))[blk * 16 + l16] = (int16_t)o.bsum;
 }
 
 // ============================================================ bucketing
