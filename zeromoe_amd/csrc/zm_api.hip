@@ -504,26 +504,37 @@ int check_layer(const zm_moe_layer *L) {
 }
 using DecFn = void (*)(DecodeArgs);
 
-template <int TG, int TD, int TS>
-DecFn dec_pick(int it1, int it2) {
-  if (it1 <= 1) {
-    if (it2 <= 2) return k_moe_decode<TG, TD, TS, 1, 2>;
-    if (it2 <= 3) return k_moe_decode<TG, TD, TS, 1, 3>;
-    if (it2 <= 5) return k_moe_decode<TG, TD, TS, 1, 5>;
-  } else if (it1 <= 2) {
-    if (it2 <= 2) return k_moe_decode<TG, TD, TS, 2, 2>;
-    if (it2 <= 3) return k_moe_decode<TG, TD, TS, 2, 3>;
-    if (it2 <= 5) return k_moe_decode<TG, TD, TS, 2, 5>;
+template <int TG, int TD, int TS, int IT1>
+DecFn dec_pick2(int itr, int its) {
+  if constexpr (TS == 0) {
+    if (its != 0) return nullptr;
+    if (itr <= 2) return k_moe_decode<TG, TD, 0, IT1, 2, 0>;
+    if (itr <= 3) return k_moe_decode<TG, TD, 0, IT1, 3, 0>;
+    if (itr <= 4) return k_moe_decode<TG, TD, 0, IT1, 4, 0>;
+  } else {
+    if (its != 1) return nullptr;
+    if (itr <= 2) return k_moe_decode<TG, TD, TS, IT1, 2, 1>;
+    if (itr <= 3) return k_moe_decode<TG, TD, TS, IT1, 3, 1>;
+    if (itr <= 4) return k_moe_decode<TG, TD, TS, IT1, 4, 1>;
   }
   return nullptr;
 }
 
-DecFn find_decode(int tg, int td, int ts, int it1, int it2) {
-  if (tg == T_Q4_K && td == T_Q4_K && ts == 0) return dec_pick<T_Q4_K, T_Q4_K, 0>(it1, it2);
-  if (tg == T_Q2_K && td == T_Q3_K && ts == 0) return dec_pick<T_Q2_K, T_Q3_K, 0>(it1, it2);
-  if (tg == T_IQ2_XXS && td == T_IQ2_XXS && ts == 0) return dec_pick<T_IQ2_XXS, T_IQ2_XXS, 0>(it1, it2);
-  if (tg == T_Q2_K && td == T_Q2_K && ts == T_Q4_K) return dec_pick<T_Q2_K, T_Q2_K, T_Q4_K>(it1, it2);
-  if (tg == T_Q2_K && td == T_Q2_K && ts == 0) return dec_pick<T_Q2_K, T_Q2_K, 0>(it1, it2);
+// IT1: 64-lane iterations over a gate/up row; ITR / ITS: over the routed /
+// shared part of a down row
+template <int TG, int TD, int TS>
+DecFn dec_pick(int it1, int itr, int its) {
+  if (it1 <= 1) return dec_pick2<TG, TD, TS, 1>(itr, its);
+  if (it1 <= 2) return dec_pick2<TG, TD, TS, 2>(itr, its);
+  return nullptr;
+}
+
+DecFn find_decode(int tg, int td, int ts, int it1, int itr, int its) {
+  if (tg == T_Q4_K && td == T_Q4_K && ts == 0) return dec_pick<T_Q4_K, T_Q4_K, 0>(it1, itr, its);
+  if (tg == T_Q2_K && td == T_Q3_K && ts == 0) return dec_pick<T_Q2_K, T_Q3_K, 0>(it1, itr, its);
+  if (tg == T_IQ2_XXS && td == T_IQ2_XXS && ts == 0) return dec_pick<T_IQ2_XXS, T_IQ2_XXS, 0>(it1, itr, its);
+  if (tg == T_Q2_K && td == T_Q2_K && ts == T_Q4_K) return dec_pick<T_Q2_K, T_Q2_K, T_Q4_K>(it1, itr, its);
+  if (tg == T_Q2_K && td == T_Q2_K && ts == 0) return dec_pick<T_Q2_K, T_Q2_K, 0>(it1, itr, its);
   return nullptr;
 }
 
@@ -570,8 +581,9 @@ int launch_fused(const zm_moe_layer *L, const float *x, const float *logits, int
     return 1;
   if (L->type_up != L->type_gate) return 1;
   const int it1 = (4 * nbH + 63) / 64;
-  const int it2 = (K * 4 * nbF + (Fs ? 4 * nbFs : 0) + 63) / 64;
-  DecFn fn = find_decode(L->type_gate, L->type_down, Fs ? L->type_shared : 0, it1, it2);
+  const int itr = (K * 4 * nbF + 63) / 64;
+  const int its = (4 * nbFs + 63) / 64;
+  DecFn fn = find_decode(L->type_gate, L->type_down, Fs ? L->type_shared : 0, it1, itr, its);
   if (!fn) return 1;
   int G = 0;
   if (decode_grid(fn, &G)) return -1;

@@ -4,17 +4,20 @@
 // boundary in between.
 //
 // Grid: as many 512-thread workgroups as the device holds at once.
-//   P0  every workgroup routes all tokens (one wave) and quantizes x into LDS
-//       (the other waves) -- redundant, but it avoids a grid-wide barrier
-//       before the first weight byte is requested.
+//   P0  every workgroup routes all tokens and quantizes x into LDS --
+//       redundant, but no grid-wide barrier precedes the first weight request.
+//       Each wave then requests the weights of its first down rows (P2), so
+//       they stream while gate/up computes and while the workgroups wait.
 //   P1  the (pair, row) space of gate/up rows is cut into one contiguous range
-//       per workgroup; waves stream two rows at a time and store the SwiGLU
-//       output; the workgroup then adds its row count to `rows_done`.
-//   P2  down rows (token s, row h): each wave issues the weight loads of its
-//       first row, then the workgroup waits for rows_done == all rows,
-//       quantizes the act rows of its tokens into LDS (Q8_K) and computes
-//       out[s][h] = sum_k w_k * (W_down[e_k][h] . q8(act_k)) (+ shared).
+//       per workgroup; waves stream batches of rows (double-buffered) and store
+//       the SwiGLU output; the workgroup then adds its row count to one of 16
+//       rows-done counters.
+//   P2  down rows (token s, row h): the workgroup waits until the counters sum
+//       to all rows, quantizes the act rows of its tokens into LDS (Q8_K) and
+//       computes out[s][h] = sum_k w_k * (W_down[e_k][h] . q8(act_k)) (+ shared).
 //   Exit: the last workgroup to leave zeroes the sync words for the next call.
+// The hot loops carry no lane-divergent branches: a lane without work loads
+// through an out-of-range buffer offset, which returns zeros, so its dot is 0.
 // Cross-workgroup data moves through agent-scope relaxed atomic loads/stores
 // (sc1: coherent past the per-XCD L2s) and one counter; no agent-scope fence
 // (an L2 write-back + invalidate on gfx950) is issued.  The wait is bounded:
@@ -33,6 +36,8 @@ constexpr int DEC_LDS_Q8 = 65536;   // Q8_K staging: x rows in P0/P1, act rows i
 constexpr int DEC_NCNT = 16;        // rows-done counters (one 64-byte line each) to spread the atomics
 constexpr int DEC_CNT_STRIDE = 16;  // words between counters
 constexpr int DEC_SYNC_WORDS = DEC_CNT_STRIDE * (1 + DEC_NCNT);
+// lane offset past every buffer extent (all < 2^31): such a load returns zeros
+constexpr int OOR = (int)0x80000000u;
 
 struct DecodeArgs {
   RouterArgs r;  // logits, biases, slot table; r.ids / r.weights: optional global outputs
@@ -53,17 +58,12 @@ struct DecodeArgs {
 };
 
 // q = j / d, r = j % d for 0 <= j < 2^24 via a float reciprocal and one
-// correction step (exact in that range); avoids the integer division sequence.
+// select-based correction (exact in that range); no division sequence, no branch.
 __device__ __forceinline__ void divmod24(int j, int d, float inv, int &q, int &r) {
   q = (int)((float)j * inv);
   r = j - q * d;
-  if (r < 0) {
-    --q;
-    r += d;
-  } else if (r >= d) {
-    ++q;
-    r -= d;
-  }
+  q += (int)(r >= d) - (int)(r < 0);
+  r = j - q * d;
 }
 
 template <class V>
@@ -87,20 +87,12 @@ __device__ __forceinline__ void stage_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__device__ __forceinline__ void store_q8_lds(uint8_t *row, int nb, int blk, const Q8Out &o, int lane) {
-  const uint32_t packed = (uint32_t)(uint8_t)o.q[0] | ((uint32_t)(uint8_t)o.q[1] << 8) |
-                          ((uint32_t)(uint8_t)o.q[2] << 16) | ((uint32_t)(uint8_t)o.q[3] << 24);
-  *reinterpret_cast<uint32_t *>(row + (size_t)blk * QK + 4 * lane) = packed;
-  if (lane == 0) reinterpret_cast<float *>(row + q8_d_off(nb))[blk] = o.d;
-  if ((lane & 3) == 0) reinterpret_cast<int16_t *>(row + q8_bs_off(nb))[blk * 16 + (lane >> 2)] = (int16_t)o.bsum16;
-}
-
 #define ZM_TRACE(slot)                                                         \
   do {                                                                         \
     if (a.trace && tid == 0) a.trace[(size_t)g * 8 + (slot)] = wall_clock64(); \
   } while (0)
 
-template <int TG, int TD, int TS, int IT1, int IT2>
+template <int TG, int TD, int TS, int IT1, int ITR, int ITS>
 __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   __shared__ RouterLds s_rl;
   __shared__ int s_ids[DEC_MAX_PAIRS];
@@ -114,8 +106,11 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   constexpr bool kIQ2 = TG == T_IQ2_XXS || TD == T_IQ2_XXS || TS == T_IQ2_XXS;
   __shared__ uint64_t s_grid[kIQ2 ? 256 : 1];
   __shared__ uint64_t s_signs[kIQ2 ? 128 : 1];
+  static_assert(ITS == 0 || TS != 0, "shared iterations need a shared type");
+  constexpr int NS = ITS > 0 ? ITS : 1;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
+  const int q4 = lane & 3;  // quarter of a super-block this lane handles (every unit count is a multiple of 4)
   const int G = gridDim.x, g = blockIdx.x;
   const int S = a.S, K = a.K, H = a.H, F = a.F;
   const size_t q8x = q8_row_bytes(a.nbH);
@@ -123,7 +118,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   const size_t q8Fs = a.Fs > 0 ? q8_row_bytes(a.nbFs) : 0;
   ZM_TRACE(0);
 
-  // ---------------------------------------------------------------- P0
+  // ---------------------------------------------------------------- P0: route, quantize x
   if constexpr (kIQ2) {
     for (int i = tid; i < 256; i += DEC_THREADS) s_grid[i] = a.grid[i];
     for (int i = tid; i < 128; i += DEC_THREADS) s_signs[i] = a.signs[i];
@@ -195,12 +190,66 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   __syncthreads();
   ZM_TRACE(1);
   const int nvp = s_nvp;
+  const int T1r = nvp * F;
+  const int T1 = T1r + S * a.Fs;
+
+  // ---------------------------------------------------------------- P2 set-up: down rows
+  // Lane unit v = lane + 64*it of a down row: the ITR routed iterations cover
+  // K*U2 quarters (route v / U2, quarter v % U2), the ITS shared iterations the
+  // shared expert's U2s quarters.  Lane offsets depend on the token only.  The
+  // first rows of every wave are requested now, before any gate/up work.
+  const int T2 = S * H;
+  const int u0 = (int)((long)T2 * g / G), u1 = (int)((long)T2 * (g + 1) / G);
+  const float invH = 1.0f / (float)H;
+  const int U2 = 4 * a.nbF, U2s = 4 * a.nbFs;
+  constexpr int BD = block_bytes(TD);
+  constexpr int BSD = TS ? block_bytes(TS) : 1;
+  const rsrc_t rd = make_rsrc(a.wd, a.wd_bytes), rsd = make_rsrc(a.sd, a.sd_bytes);
+  int vo_r[ITR], vo_s[NS];
+  int vo_tok = -1;
+  auto lane_offsets = [&](int s) {
+#pragma unroll
+    for (int it = 0; it < ITR; ++it) {
+      const int v = lane + 64 * it;
+      const int k = v / U2, u = v - k * U2;
+      const int e = s_ids[s * K + min(k, K - 1)];
+      vo_r[it] = (k < K && e >= 0) ? e * (int)a.d_estride + (u >> 2) * BD : OOR;
+    }
+#pragma unroll
+    for (int it = 0; it < ITS; ++it) {
+      const int u = lane + 64 * it;
+      vo_s[it] = u < U2s ? (u >> 2) * BSD : OOR;
+    }
+    vo_tok = s;
+  };
+  auto load_row = [&](int j, WSlice(&wr)[ITR], WSlice(&ws)[NS]) {
+    int s, h;
+    divmod24(j, H, invH, s, h);
+    s = uniform(s);
+    h = uniform(h);
+    if (s != vo_tok) lane_offsets(s);
+    const int so = uniform(h * (int)a.d_rstride);
+#pragma unroll
+    for (int it = 0; it < ITR; ++it) load_w_slice_b<TD>(rd, vo_r[it], so, q4, wr[it]);
+    if constexpr (ITS > 0) {
+      const int sos = uniform(h * (int)a.sd_rstride);
+#pragma unroll
+      for (int it = 0; it < ITS; ++it) load_w_slice_b<TS>(rsd, vo_s[it], sos, q4, ws[it]);
+    }
+  };
+  // two rows in flight when they fit in registers, else one
+  constexpr bool P2DB = ITR + ITS <= 3;
+  WSlice c0r[ITR], c0s[NS];
+  WSlice c1r[P2DB ? ITR : 1], c1s[P2DB ? NS : 1];
+  const int jw = u0 + wave;
+  if (jw < u1) load_row(jw, c0r, c0s);
+  if constexpr (P2DB)
+    if (jw + DEC_WAVES < u1) load_row(jw + DEC_WAVES, c1r, c1s);
+  __builtin_amdgcn_sched_barrier(0);
 
   // ---------------------------------------------------------------- P1: gate/up rows
   // Row i of this wave is j = t0 + wave + DEC_WAVES*i.  Rows go in batches of RB
   // with two register buffers: batch b+1 is in flight while batch b computes.
-  const int T1r = nvp * F;
-  const int T1 = T1r + S * a.Fs;
   const int t0 = (int)((long)T1 * g / G), t1 = (int)((long)T1 * (g + 1) / G);
   const int U1 = 4 * a.nbH;
   const float invF = 1.0f / (float)F, invFs = a.Fs > 0 ? 1.0f / (float)a.Fs : 0.f;
@@ -211,10 +260,19 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     constexpr int RB0 = 80 / (2 * 2 * SLICE_DW * IT1);
     constexpr int RB = RB0 < 1 ? 1 : (RB0 > 4 ? 4 : RB0);
     const int nrw = t1 - t0 > wave ? (t1 - t0 - wave + DEC_WAVES - 1) / DEC_WAVES : 0;
-
     const rsrc_t rg = make_rsrc(a.wg, a.wg_bytes), ru = make_rsrc(a.wu, a.wg_bytes);
     const rsrc_t rsg = make_rsrc(a.sg, a.sg_bytes), rsu = make_rsrc(a.su, a.sg_bytes);
-    auto issue = [&](int i0, WSlice (&bg)[RB][IT1], WSlice (&bu)[RB][IT1]) {
+    // lane offsets inside a row (routed / shared block sizes; OOR past the row)
+    // and the activation block (clamped: idle lanes read real, finite data)
+    int vo1[IT1], vo1s[IT1], xb1[IT1];
+#pragma unroll
+    for (int it = 0; it < IT1; ++it) {
+      const int u = lane + 64 * it;
+      vo1[it] = u < U1 ? (u >> 2) * BG : OOR;
+      vo1s[it] = u < U1 ? (u >> 2) * BS : OOR;
+      xb1[it] = min(u >> 2, a.nbH - 1);
+    }
+    auto issue = [&](int i0, WSlice(&bg)[RB][IT1], WSlice(&bu)[RB][IT1]) {
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
         const int i = i0 + r;
@@ -227,11 +285,8 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
           const int so = uniform(e * (int)a.g_estride + uniform(n) * (int)a.g_rstride);
 #pragma unroll
           for (int it = 0; it < IT1; ++it) {
-            const int u = lane + 64 * it;
-            if (u < U1) {
-              load_w_slice_b<TG>(rg, (u >> 2) * BG, so, u & 3, bg[r][it]);
-              load_w_slice_b<TG>(ru, (u >> 2) * BG, so, u & 3, bu[r][it]);
-            }
+            load_w_slice_b<TG>(rg, vo1[it], so, q4, bg[r][it]);
+            load_w_slice_b<TG>(ru, vo1[it], so, q4, bu[r][it]);
           }
         } else if constexpr (TS != 0) {
           int ts_, n;
@@ -239,19 +294,16 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
           const int so = uniform(uniform(n) * (int)a.sg_rstride);
 #pragma unroll
           for (int it = 0; it < IT1; ++it) {
-            const int u = lane + 64 * it;
-            if (u < U1) {
-              load_w_slice_b<TS>(rsg, (u >> 2) * BS, so, u & 3, bg[r][it]);
-              load_w_slice_b<TS>(rsu, (u >> 2) * BS, so, u & 3, bu[r][it]);
-            }
+            load_w_slice_b<TS>(rsg, vo1s[it], so, q4, bg[r][it]);
+            load_w_slice_b<TS>(rsu, vo1s[it], so, q4, bu[r][it]);
           }
         }
       }
     };
     // the token's activation slices stay in registers while the token does not change
     Q8Slice xsc[IT1];
-    int xs_tok = -1;
-    auto compute = [&](int i0, WSlice (&bg)[RB][IT1], WSlice (&bu)[RB][IT1]) {
+    int xs_key = -1;
+    auto compute = [&](int i0, WSlice(&bg)[RB][IT1], WSlice(&bu)[RB][IT1]) {
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
         const int i = i0 + r;
@@ -259,38 +311,32 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
         const int j = t0 + wave + DEC_WAVES * i;
         const bool shared_row = j >= T1r;
         int q_, r_;
-        if (shared_row)
-          divmod24(j - T1r, a.Fs, invFs, q_, r_);
-        else
-          divmod24(j, F, invF, q_, r_);
+        divmod24(shared_row ? j - T1r : j, shared_row ? a.Fs : F, shared_row ? invFs : invF, q_, r_);
         const int tok = uniform(shared_row ? q_ : s_vp[q_] / K);
         const int key = shared_row ? tok + DEC_MAX_S : tok;
-        const uint8_t *xrow = s_q8 + (size_t)tok * q8x;
-        if (key != xs_tok) {
-          xs_tok = key;
+        if (key != xs_key) {
+          xs_key = key;
+          const uint8_t *xrow = s_q8 + (size_t)tok * q8x;
 #pragma unroll
           for (int it = 0; it < IT1; ++it) {
-            const int u = lane + 64 * it;
-            if (u < U1) {
-              if (!shared_row)
-                load_q8_slice<TG>(xrow, a.nbH, u >> 2, u & 3, xsc[it]);
-              else if constexpr (TS != 0)
-                load_q8_slice<TS>(xrow, a.nbH, u >> 2, u & 3, xsc[it]);
-            }
+            if (!shared_row)
+              load_q8_slice<TG>(xrow, a.nbH, xb1[it], q4, xsc[it]);
+            else if constexpr (TS != 0)
+              load_q8_slice<TS>(xrow, a.nbH, xb1[it], q4, xsc[it]);
           }
         }
         float ag = 0.f, au = 0.f;
+        if (!shared_row) {
 #pragma unroll
-        for (int it = 0; it < IT1; ++it) {
-          const int u = lane + 64 * it;
-          if (u < U1) {
-            if (!shared_row) {
-              ag += quarter_dot<TG>(bg[r][it], u & 3, xsc[it], s_grid, s_signs);
-              au += quarter_dot<TG>(bu[r][it], u & 3, xsc[it], s_grid, s_signs);
-            } else if constexpr (TS != 0) {
-              ag += quarter_dot<TS>(bg[r][it], u & 3, xsc[it], s_grid, s_signs);
-              au += quarter_dot<TS>(bu[r][it], u & 3, xsc[it], s_grid, s_signs);
-            }
+          for (int it = 0; it < IT1; ++it) {
+            ag += quarter_dot<TG>(bg[r][it], q4, xsc[it], s_grid, s_signs);
+            au += quarter_dot<TG>(bu[r][it], q4, xsc[it], s_grid, s_signs);
+          }
+        } else if constexpr (TS != 0) {
+#pragma unroll
+          for (int it = 0; it < IT1; ++it) {
+            ag += quarter_dot<TS>(bg[r][it], q4, xsc[it], s_grid, s_signs);
+            au += quarter_dot<TS>(bu[r][it], q4, xsc[it], s_grid, s_signs);
           }
         }
         ag = group_sum<64>(ag);
@@ -318,61 +364,8 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   ZM_TRACE(2);
   if (tid == 0 && t1 > t0) atomicAdd(&a.sync[DEC_CNT_STRIDE * (1 + g % DEC_NCNT)], (uint32_t)(t1 - t0));
 
-  // ---------------------------------------------------------------- P2: down rows
-  const int T2 = S * H;
-  const int u0 = (int)((long)T2 * g / G), u1 = (int)((long)T2 * (g + 1) / G);
-  const float invH = 1.0f / (float)H;
-  const int U2 = 4 * a.nbF, U2s = 4 * a.nbFs;
-  const int V = K * U2 + (a.Fs > 0 ? U2s : 0);
-  constexpr int BD = block_bytes(TD);
-  constexpr int BSD = TS ? block_bytes(TS) : 1;
-
-  const rsrc_t rd = make_rsrc(a.wd, a.wd_bytes), rsd = make_rsrc(a.sd, a.sd_bytes);
-  // lane byte offsets (expert slab + block) for token s; -1 = no load (skipped route / idle lane)
-  int vo_tok = -2, vo[IT2];
-  auto lane_offsets = [&](int s) {
-#pragma unroll
-    for (int it = 0; it < IT2; ++it) {
-      const int v = lane + 64 * it;
-      vo[it] = -1;
-      if (v < K * U2) {
-        const int k = v / U2, u = v % U2;
-        const int e = s_ids[s * K + k];
-        if (e >= 0) vo[it] = e * (int)a.d_estride + (u >> 2) * BD;
-      } else if (v < V) {
-        vo[it] = ((v - K * U2) >> 2) * BSD;
-      }
-    }
-    vo_tok = s;
-  };
-  auto load_row = [&](int j, WSlice (&ws)[IT2]) {
-    int s, h;
-    divmod24(j, H, invH, s, h);
-    s = uniform(s);
-    h = uniform(h);
-    if (s != vo_tok) lane_offsets(s);
-#pragma unroll
-    for (int it = 0; it < IT2; ++it) {
-      const int v = lane + 64 * it;
-      if (vo[it] >= 0) {
-        if (v < K * U2) {
-          load_w_slice_b<TD>(rd, vo[it], uniform(h * (int)a.d_rstride), (v % U2) & 3, ws[it]);
-        } else if constexpr (TS != 0) {
-          load_w_slice_b<TS>(rsd, vo[it], uniform(h * (int)a.sd_rstride), (v - K * U2) & 3, ws[it]);
-        }
-      }
-    }
-  };
-
-  // the first two rows of this wave are requested before the wait
-  WSlice c0[IT2], c1[IT2];
-  const int jw = u0 + wave;
-  if (jw < u1) load_row(jw, c0);
-  if (jw + DEC_WAVES < u1) load_row(jw + DEC_WAVES, c1);
-  __builtin_amdgcn_sched_barrier(0);
-
-  // wait until every gate/up row of every workgroup is stored: lanes 0..15 of
-  // wave 0 poll one counter each and sum them
+  // ---------------------------------------------------------------- P2: wait, quantize act, down rows
+  // lanes 0..15 of wave 0 poll one counter each and sum them
   if (wave == 0) {
     const uint32_t target = (uint32_t)T1;
     int spins = 0;
@@ -394,55 +387,54 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   after_wait();
   ZM_TRACE(3);
 
-  // quantize the act rows of this workgroup's tokens (at most two) into LDS
+  // act rows of this workgroup's tokens (at most two) -> Q8_K in LDS; the rows
+  // of skipped routes become zero blocks, so every LDS value read later is finite
   const int s_lo = u1 > u0 ? u0 / H : 0;
   const int s_hi = u1 > u0 ? (u1 - 1) / H : -1;
   const size_t tok_bytes = (size_t)K * q8F + q8Fs;
   if (!s_err) {
     const int nb_tok = K * a.nbF + (a.Fs > 0 ? a.nbFs : 0);
     const int nb_all = (s_hi - s_lo + 1) * nb_tok;
-    // block bi -> (source act block, destination LDS row, blocks per row, block index); false = skipped route
-    auto info = [&](int bi, const float *&src, uint8_t *&row, int &nb, int &blk) -> bool {
-      const int ts = bi / nb_tok, r = bi % nb_tok;
+    // block bi -> act byte offset (OOR: skipped route or past the end), LDS row,
+    // blocks in that row, block index
+    auto info = [&](int bi, int &aoff, uint8_t *&row, int &nb, int &blk) {
+      const int ts = bi / nb_tok, r = bi - ts * nb_tok;
       const int s = s_lo + ts;
       if (r < K * a.nbF) {
         const int k = r / a.nbF;
-        blk = r % a.nbF;
+        blk = r - k * a.nbF;
         nb = a.nbF;
         const int c = s_cidx[s * K + k];
-        if (c < 0) return false;
-        src = a.act + (size_t)c * F + (size_t)blk * QK;
+        aoff = c < 0 ? OOR : (c * F + blk * QK) * 4;
         row = s_q8 + (size_t)ts * tok_bytes + (size_t)k * q8F;
       } else {
         blk = r - K * a.nbF;
         nb = a.nbFs;
-        src = a.act + T1r + (size_t)s * a.Fs + (size_t)blk * QK;
+        aoff = (T1r + s * a.Fs + blk * QK) * 4;
         row = s_q8 + (size_t)ts * tok_bytes + (size_t)K * q8F;
       }
-      return true;
     };
-    // Each wave takes 4 act blocks per round: coalesced 16-byte sc1 loads (lane l
+    // Each wave takes 4 blocks per round: coalesced 16-byte sc1 loads (lane l
     // holds floats 4l..4l+3 of block k), a transpose through this wave's LDS
     // stage to 16 lanes per block, then quant_block16.  QR rounds of loads are
     // in flight together.
     constexpr int QR = 3;
     const rsrc_t ract = make_rsrc(a.act, (uint32_t)T1 * 4u);
-    const int l16q = lane & 15, kq = lane >> 4;
+    const int kq = lane >> 4;
     for (int base = wave * 4; base < nb_all; base += DEC_WAVES * 4 * QR) {
       float4 ld[QR][4];
 #pragma unroll
       for (int r = 0; r < QR; ++r) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          const int bi = base + r * DEC_WAVES * 4 + k;
-          const float *src;
+          int aoff, nb, blk;
           uint8_t *row;
-          int nb, blk;
-          if (bi < nb_all && info(bi, src, row, nb, blk)) {
-            const auto v4 = __builtin_amdgcn_raw_buffer_load_b128(ract, (int)((src - a.act) * 4) + 16 * lane, 0, 16);
-            ld[r][k] = make_float4(__uint_as_float(v4[0]), __uint_as_float(v4[1]), __uint_as_float(v4[2]),
-                                   __uint_as_float(v4[3]));
-          }
+          const int bi = base + r * DEC_WAVES * 4 + k;
+          info(min(bi, nb_all - 1), aoff, row, nb, blk);
+          const int vo = (bi >= nb_all || aoff == OOR) ? OOR : aoff + 16 * lane;
+          const auto v4 = __builtin_amdgcn_raw_buffer_load_b128(ract, vo, 0, 16);
+          ld[r][k] = make_float4(__uint_as_float(v4[0]), __uint_as_float(v4[1]), __uint_as_float(v4[2]),
+                                 __uint_as_float(v4[3]));
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -455,7 +447,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
         float xv16[16];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float4 f = s_stage[wave][kq * 64 + 4 * l16q + i];
+          const float4 f = s_stage[wave][kq * 64 + 4 * l16 + i];
           xv16[4 * i] = f.x;
           xv16[4 * i + 1] = f.y;
           xv16[4 * i + 2] = f.z;
@@ -463,10 +455,12 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
         }
         stage_sync();
         const int bi = base + r * DEC_WAVES * 4 + kq;
-        const float *src;
-        uint8_t *row;
-        int nb, blk;
-        if (bi < nb_all && info(bi, src, row, nb, blk)) store_q8_16(row, nb, blk, quant_block16(xv16, l16q), l16q);
+        if (bi < nb_all) {
+          int aoff, nb, blk;
+          uint8_t *row;
+          info(bi, aoff, row, nb, blk);
+          store_q8_16(row, nb, blk, quant_block16(xv16, l16), l16);  // a zero block for a skipped route
+        }
       }
     }
   }
@@ -475,57 +469,52 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
 
   if (!s_err) {
     int cur_s = -1;
-    Q8Slice qs[IT2];
-    float wr[IT2];
-    auto compute_row = [&](int j, WSlice (&cw)[IT2]) {
+    Q8Slice qr[ITR], qsh[NS];
+    float wgt[ITR];
+    auto compute_row = [&](int j, WSlice(&cr)[ITR], WSlice(&cs)[NS]) {
       int s, h;
       divmod24(j, H, invH, s, h);
+      s = uniform(s);
+      h = uniform(h);
       if (s != cur_s) {
         cur_s = s;
         const uint8_t *tb = s_q8 + (size_t)(s - s_lo) * tok_bytes;
 #pragma unroll
-        for (int it = 0; it < IT2; ++it) {
+        for (int it = 0; it < ITR; ++it) {
           const int v = lane + 64 * it;
-          wr[it] = 0.f;
-          if (v < K * U2) {
-            const int k = v / U2, u = v % U2;
-            if (s_ids[s * K + k] >= 0) {
-              load_q8_slice<TD>(tb + (size_t)k * q8F, a.nbF, u >> 2, u & 3, qs[it]);
-              wr[it] = s_w[s * K + k];
-            }
-          } else if constexpr (TS != 0) {
-            if (v < V) {
-              const int u = v - K * U2;
-              load_q8_slice<TS>(tb + (size_t)K * q8F, a.nbFs, u >> 2, u & 3, qs[it]);
-              wr[it] = 1.0f;
-            }
-          }
+          const int kr = v / U2, u = v - kr * U2, k = min(kr, K - 1);
+          load_q8_slice<TD>(tb + (size_t)k * q8F, a.nbF, u >> 2, q4, qr[it]);
+          wgt[it] = kr < K ? s_w[s * K + k] : 0.0f;
+        }
+#pragma unroll
+        for (int it = 0; it < ITS; ++it) {
+          const int u = lane + 64 * it;
+          load_q8_slice<TS>(tb + (size_t)K * q8F, a.nbFs, min(u >> 2, a.nbFs - 1), q4, qsh[it]);
         }
       }
       float acc = 0.f;
 #pragma unroll
-      for (int it = 0; it < IT2; ++it) {
-        const int v = lane + 64 * it;
-        if (v < K * U2) {
-          const int k = v / U2, u = v % U2;
-          if (s_ids[s * K + k] >= 0) acc += wr[it] * quarter_dot<TD>(cw[it], u & 3, qs[it], s_grid, s_signs);
-        } else if constexpr (TS != 0) {
-          if (v < V) {
-            const int u = v - K * U2;
-            acc += quarter_dot<TS>(cw[it], u & 3, qs[it], s_grid, s_signs);
-          }
-        }
-      }
+      for (int it = 0; it < ITR; ++it) acc += wgt[it] * quarter_dot<TD>(cr[it], q4, qr[it], s_grid, s_signs);
+#pragma unroll
+      for (int it = 0; it < ITS; ++it) acc += quarter_dot<TS>(cs[it], q4, qsh[it], s_grid, s_signs);
       acc = group_sum<64>(acc);
       if (lane == 0) a.out[(size_t)s * H + h] = acc;
     };
-    for (int j = jw; j < u1; j += 2 * DEC_WAVES) {
-      compute_row(j, c0);
-      if (j + 2 * DEC_WAVES < u1) load_row(j + 2 * DEC_WAVES, c0);
-      __builtin_amdgcn_sched_barrier(0);
-      if (j + DEC_WAVES < u1) {
-        compute_row(j + DEC_WAVES, c1);
-        if (j + 3 * DEC_WAVES < u1) load_row(j + 3 * DEC_WAVES, c1);
+    if constexpr (P2DB) {
+      for (int j = jw; j < u1; j += 2 * DEC_WAVES) {
+        compute_row(j, c0r, c0s);
+        if (j + 2 * DEC_WAVES < u1) load_row(j + 2 * DEC_WAVES, c0r, c0s);
+        __builtin_amdgcn_sched_barrier(0);
+        if (j + DEC_WAVES < u1) {
+          compute_row(j + DEC_WAVES, c1r, c1s);
+          if (j + 3 * DEC_WAVES < u1) load_row(j + 3 * DEC_WAVES, c1r, c1s);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    } else {
+      for (int j = jw; j < u1; j += DEC_WAVES) {
+        compute_row(j, c0r, c0s);
+        if (j + DEC_WAVES < u1) load_row(j + DEC_WAVES, c0r, c0s);
         __builtin_amdgcn_sched_barrier(0);
       }
     }

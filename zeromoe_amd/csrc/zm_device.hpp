@@ -356,23 +356,21 @@ __device__ __forceinline__ QInt quarter_int(const WSlice &w, int q, const Q8Slic
     }
     r.isum = s16 >> 4;
   } else if constexpr (T == T_Q4_K) {
-    // scales bytes 0..11 live in header dwords y, z, w
-    const int j0 = 2 * q, j1 = 2 * q + 1;
+    // 6-bit (scale, min) of sub-blocks 2q and 2q+1 without a branch: scales bytes
+    // 0..11 are header dwords y (A), z (B), w (C); sub-block j < 4 keeps them in
+    // A[j] / B[j], j >= 4 splits them over C[j-4] (low bits) and the top bits of
+    // A[j-4] / B[j-4] (get_scale_min_k4).
+    const uint32_t sh = 16u * (uint32_t)(q & 1);
+    const uint32_t hA = w.c.y >> sh, hB = w.c.z >> sh, hC = w.c.w >> sh;
+    const bool lo_half = q < 2;
     uint32_t sc0, m0, sc1, m1;
-    if (q < 2) {
-      sc0 = byte_of3(w.c.y, w.c.z, w.c.w, j0) & 63u;
-      m0 = byte_of3(w.c.y, w.c.z, w.c.w, j0 + 4) & 63u;
-      sc1 = byte_of3(w.c.y, w.c.z, w.c.w, j1) & 63u;
-      m1 = byte_of3(w.c.y, w.c.z, w.c.w, j1 + 4) & 63u;
-    } else {
-      const uint32_t a0 = byte_of3(w.c.y, w.c.z, w.c.w, j0 + 4), b0 = byte_of3(w.c.y, w.c.z, w.c.w, j0 - 4),
-                     c0 = byte_of3(w.c.y, w.c.z, w.c.w, j0);
-      sc0 = (a0 & 15u) | ((b0 >> 6) << 4);
-      m0 = (a0 >> 4) | ((c0 >> 6) << 4);
-      const uint32_t a1 = byte_of3(w.c.y, w.c.z, w.c.w, j1 + 4), b1 = byte_of3(w.c.y, w.c.z, w.c.w, j1 - 4),
-                     c1 = byte_of3(w.c.y, w.c.z, w.c.w, j1);
-      sc1 = (a1 & 15u) | ((b1 >> 6) << 4);
-      m1 = (a1 >> 4) | ((c1 >> 6) << 4);
+    {
+      const uint32_t a0 = hA & 0xffu, b0 = hB & 0xffu, c0 = hC & 0xffu;
+      const uint32_t a1 = (hA >> 8) & 0xffu, b1 = (hB >> 8) & 0xffu, c1 = (hC >> 8) & 0xffu;
+      sc0 = lo_half ? (a0 & 63u) : ((c0 & 15u) | ((a0 >> 6) << 4));
+      m0 = lo_half ? (b0 & 63u) : ((c0 >> 4) | ((b0 >> 6) << 4));
+      sc1 = lo_half ? (a1 & 63u) : ((c1 & 15u) | ((a1 >> 6) << 4));
+      m1 = lo_half ? (b1 & 63u) : ((c1 >> 4) | ((b1 >> 6) << 4));
     }
     // qs bytes [0,16) low nibbles pair with activations [0,16), bytes [16,32) with
     // [16,32); the high nibbles with [32,48) and [48,64).

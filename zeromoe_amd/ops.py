@@ -194,6 +194,9 @@ class MoELayer:
     _ws: dict = field(default_factory=dict, repr=False)
 
     def desc(self) -> ZmMoeLayer:
+        cached = self._ws.get("desc")
+        if cached is not None:
+            return cached
         d = ZmMoeLayer()
         d.H, d.F, d.n_slots = self.H, self.F, self.w_gate.shape[0]
         d.router = _spec(self.n_experts, self.topk, self.gating, self.n_groups, self.n_groups_used,
@@ -204,6 +207,7 @@ class MoELayer:
         d.route_map, d.route_mask = _p(self.route_map), _p(self.route_mask)
         d.F_shared, d.type_shared = self.F_shared, self.type_shared
         d.ws_gate, d.ws_up, d.ws_down = _p(self.ws_gate), _p(self.ws_up), _p(self.ws_down)
+        self._ws["desc"] = d  # tensors are fixed for the layer's lifetime
         return d
 
     def workspace(self, S: int, device) -> torch.Tensor:
