@@ -111,7 +111,7 @@ def build_layers(torch, Z, c, replicas, seed):
     return layers
 
 
-def run_config(torch, Z, name, steps, warmup, replicas, use_graph=True):
+def run_config(torch, Z, name, steps, warmup, replicas, use_graph=True, kernel_launches=0):
     c = CONFIGS[name]
     S, H, E, K = c["S"], c["H"], c["E"], c["K"]
     layers = build_layers(torch, Z, c, replicas, seed=1234)
@@ -171,44 +171,117 @@ def run_config(torch, Z, name, steps, warmup, replicas, use_graph=True):
         extra_bytes += E * H * 4
     bytes_step = mean_uniq * eb + extra_bytes
     gbs = bytes_step / (ms * 1e-3) / 1e9
-    return dict(us_per_layer=ms * 1e3, ms_per_step=ms, GBps=gbs, frac_hbm_peak=gbs / HBM_PEAK_GBS,
-                bytes_per_layer=bytes_step, unique_experts=mean_uniq, tok_per_s=S / (ms * 1e-3),
-                wall_s=wall, replicas=replicas)
+    res = dict(us_per_layer=ms * 1e3, ms_per_step=ms, GBps=gbs, frac_hbm_peak=gbs / HBM_PEAK_GBS,
+               bytes_per_layer=bytes_step, unique_experts=mean_uniq, tok_per_s=S / (ms * 1e-3),
+               wall_s=wall, replicas=replicas)
+    if kernel_launches:
+        res["kernel_us"] = time_launches(torch, step, warmup, min(steps, kernel_launches))
+    return res
 
 
-def cpu_baseline(seconds: float = 10.0):
-    """CPU restatement of ggml's MUL_MAT_ID layer (oracle/zm_oracle.c) on this
-    host's cores at the c2 shape, S=1: ids re-drawn every iteration over a
-    32-expert pool (218 MB of weights, beyond the LLC)."""
-    import numpy as np
+def time_launches(torch, step, first, n):
+    """Mean device time of one layer launch: a HIP event pair on the stream the
+    library launches on (torch's current stream) around n back-to-back
+    launches, queued behind a spin kernel so Python's dispatch never leaves the
+    device idle between them.  For a layer that is one kernel (decode with
+    given logits) this is that kernel's average duration, launch gaps included,
+    as rocprofv3's kernel trace reports it."""
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    torch.cuda._sleep(50_000_000)  # spin ahead of the queue (long enough for n host dispatches)
+    e0.record(stream)
+    for i in range(n):
+        step(first + i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return {"mean": e0.elapsed_time(e1) * 1e3 / n, "launches": n}
 
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import zm_oracle as O
 
-    c = CONFIGS["c2"]
-    H, F, K = c["H"], c["F"], c["K"]
-    pool = 32
-    Wg = O.random_blocks(Q2, pool * F, H, seed=1).reshape(pool, F, -1)
-    Wu = O.random_blocks(Q2, pool * F, H, seed=2).reshape(pool, F, -1)
-    Wd = O.random_blocks(Q3, pool * H, F, seed=3).reshape(pool, H, -1)
-    rng = np.random.default_rng(0)
-    x = rng.standard_normal((1, H)).astype(np.float32)
-    threads = max(1, min(16, os.cpu_count() or 1))
-    w = np.full((1, K), 1.0 / K, np.float32)
-    O.moe_forward(x, rng.permutation(pool)[:K][None].astype(np.int32), w, Q2, Q2, Q3, Wg, Wu, Wd, nthreads=threads)
-    n, t0 = 0, time.perf_counter()
-    while True:
-        ids = rng.permutation(pool)[:K][None].astype(np.int32)
-        O.moe_forward(x, ids, w, Q2, Q2, Q3, Wg, Wu, Wd, nthreads=threads)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and n >= 3:
-            break
-    us = el / n * 1e6
-    gbs = K * expert_bytes(c) / (us * 1e-6) / 1e9
-    return {"value": round(us, 1), "unit": "us/layer", "GBps": round(gbs, 2), "cores": threads, "kind": "port",
-            "sample": f"c2 layer S=1 (8 of a 32-expert pool per iteration), {n} iterations in {el:.1f} s, "
-                      f"OpenMP over output rows"}
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "k_moe_decode_c2_hbm_traffic.txt")
+COPY_PROBE_BYTES = 1 << 30
+
+
+def copy_probe(torch):
+    """A plain device copy of known size (1 GiB read + 1 GiB written): the
+    scale for the FETCH_SIZE / WRITE_SIZE counters."""
+    a = torch.ones(COPY_PROBE_BYTES // 4, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+
+
+def _read_counters(d):
+    """{(kernel name, counter): [value per dispatch]} from a rocprofv3 --pmc csv."""
+    import csv
+    import glob
+
+    out = {}
+    for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                out.setdefault((r["Kernel_Name"], r["Counter_Name"]), []).append(float(r["Counter_Value"]))
+    return out
+
+
+def pmc_summary(fetch_dir, write_dir, out_path, command):
+    """Per-launch HBM traffic of the decode kernel from FETCH_SIZE / WRITE_SIZE
+    (KiB per dispatch), each scaled by what the counter reads for the copy probe."""
+    lines = [f"# HBM traffic per launch: decode kernel, c2 (bench.py --profile c2)", f"# command: {command}"]
+    tot = 0.0
+    for ctr, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        vals = _read_counters(d)
+        dec = [v for (k, c), vs in vals.items() if c == ctr and "k_moe_decode" in k for v in vs]
+        cp = [v for (k, c), vs in vals.items() if c == ctr and "copy" in k.lower() for v in vs]
+        cp = [v for v in cp if v >= 0.9 * max(cp, default=0.0)]  # the 1 GiB probe, not smaller copies
+        if not dec or not cp:
+            raise SystemExit(f"pmc_summary: no {ctr} samples for the decode kernel or the copy probe in {d}")
+        probe = sum(cp) / len(cp)
+        factor = (COPY_PROBE_BYTES / 1024) / probe
+        kib = sum(dec) / len(dec)
+        b = kib * 1024 * factor
+        tot += b
+        lines += [f"{ctr}_kib_per_launch: {kib:.1f}  (dispatches: {len(dec)})",
+                  f"{ctr}_copy_probe_kib: {probe:.1f}  (expected {COPY_PROBE_BYTES // 1024}; factor {factor:.4f})",
+                  f"{ctr}_bytes_per_launch: {b:.0f}"]
+    lines.append(f"traffic_bytes_per_launch: {tot:.0f}")
+    with open(out_path, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+def stats_summary(d, out_path, command, top=8):
+    """Top kernels of a rocprofv3 --kernel-trace --stats run, as text."""
+    import csv
+    import glob
+    import re
+
+    f = glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True)
+    if not f:
+        raise SystemExit(f"stats_summary: no kernel_stats.csv under {d}")
+    with open(f[0]) as fh:
+        rows = list(csv.DictReader(fh))
+    lines = [f"# rocprofv3 kernel stats", f"# command: {command}",
+             f"{'calls':>6} {'avg_us':>9} {'min_us':>9} {'max_us':>9} {'pct':>6}  kernel"]
+    for r in rows[:top]:
+        name = re.sub(r"\(.*", "", r["Name"].replace("void ", ""))[:100]
+        lines.append(f"{int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.2f} {float(r['MinNs']) / 1e3:9.2f} "
+                     f"{float(r['MaxNs']) / 1e3:9.2f} {float(r['Percentage']):6.2f}  {name}")
+    with open(out_path, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+def committed_traffic():
+    try:
+        with open(PMC_SUMMARY) as fh:
+            for l in fh:
+                if l.startswith("traffic_bytes_per_launch:"):
+                    return float(l.split()[1])
+    except OSError:
+        pass
+    return None
 
 
 def main():
@@ -221,7 +294,19 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch every step from Python instead of a HIP graph")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--profile", metavar="CFG", help="profiling run: CFG's layer launched eagerly --steps times, "
+                    "then a 1 GiB copy probe; prints a short summary (for rocprofv3)")
+    ap.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "OUT"),
+                    help="summarize two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of --profile c2")
+    ap.add_argument("--stats-summary", nargs=2, metavar=("DIR", "OUT"), help="summarize a rocprofv3 --stats run")
+    ap.add_argument("--command", default="", help="command line recorded in a summary")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary, args.command)
+        return
+    if args.stats_summary:
+        stats_summary(*args.stats_summary, args.command)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the expert axis would "
               f"shard across GPUs as described in DESIGN.md, but no multi-GPU figure is produced.", file=sys.stderr)
@@ -241,7 +326,17 @@ def main():
         per = NS * expert_bytes(c)
         return max(2, min(16, int(1.2e9 // per) + 2))
 
-    main_res = run_config(torch, Z, "c2", args.steps, args.warmup, reps("c2"), use_graph=not args.eager)
+    if args.profile:
+        r = run_config(torch, Z, args.profile, args.steps, args.warmup, reps(args.profile), use_graph=False)
+        copy_probe(torch)
+        print(json.dumps({"profile": args.profile, "us_per_layer": round(r["us_per_layer"], 2),
+                          "bytes_per_layer": int(r["bytes_per_layer"])}))
+        return
+    main_res = run_config(torch, Z, "c2", args.steps, args.warmup, reps("c2"), use_graph=not args.eager,
+                          kernel_launches=100)
+    kern = main_res["kernel_us"]
+    kern_gbs = main_res["bytes_per_layer"] / (kern["mean"] * 1e-6) / 1e9
+    traffic = committed_traffic()
     extras = {}
     for name in [n for n in args.extras.split(",") if n]:
         st = max(10, args.steps // 4) if name == "c3" else args.steps
@@ -265,10 +360,14 @@ def main():
         "config": {"workload": "c2: " + WORKLOAD["c2"], "H": 4096, "F": 1536, "experts": 128, "topk": 8,
                    "tokens": 1, "replicas": main_res["replicas"]},
         "us_per_layer": round(main_res["us_per_layer"], 2),
-        "roofline": {"bound": "hbm", "kernel": "routed layer (all launches of zm_moe_forward)",
-                     "achieved": round(main_res["GBps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(main_res["frac_hbm_peak"], 4), "traffic": None,
-                     "bytes_per_layer": int(main_res["bytes_per_layer"])},
+        "roofline": {"bound": "hbm", "kernel": "zm::k_moe_decode<Q2_K,Q3_K> (the whole c2 layer is this one launch)",
+                     "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None if traffic is None else int(traffic),
+                     "algorithmic_bytes_per_launch": int(main_res["bytes_per_layer"]),
+                     "kernel_us": {k: (round(v, 2) if isinstance(v, float) else v) for k, v in kern.items()},
+                     "traffic_source": "profiles/k_moe_decode_c2_hbm_traffic.txt (rocprofv3 --pmc FETCH_SIZE, "
+                                       "WRITE_SIZE, scaled by a 1 GiB copy)"},
         "cpu_baseline": cpu,
         "extras": extras,
     }
