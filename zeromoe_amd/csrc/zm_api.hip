@@ -234,7 +234,7 @@ int zm_router(const zm_router_spec *spec, const float *logits, const float *logi
   if (S == 0) return 0;
   RouterArgs a{logits, logit_bias, sel_bias, route_map, route_mask, spec->n_experts, spec->topk, spec->gating,
                spec->n_groups, spec->n_groups_used, spec->weights_norm, spec->weights_scale, ids, weights};
-  hipLaunchKernelGGL(k_router_wg, dim3(S), dim3(256), 0, (hipStream_t)stream, a);
+  hipLaunchKernelGGL(k_router, dim3((S + 3) / 4), dim3(256), 0, (hipStream_t)stream, a, S);
   HIP_OK(hipGetLastError());
   return 0;
 }

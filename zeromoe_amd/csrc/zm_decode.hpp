@@ -80,13 +80,6 @@ __device__ __forceinline__ void stores_done() {
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt and lgkmcnt left at their maxima
 }
 __device__ __forceinline__ void after_wait() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup"); }
-// LDS writes of this wave visible to its other lanes
-__device__ __forceinline__ void stage_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 #define ZM_TRACE(slot)                                                         \
   do {                                                                         \
     if (a.trace && tid == 0) a.trace[(size_t)g * 8 + (slot)] = wall_clock64(); \
@@ -94,7 +87,6 @@ __device__ __forceinline__ void stage_sync() {
 
 template <int TG, int TD, int TS, int IT1, int ITR, int ITS>
 __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
-  __shared__ RouterLds s_rl;
   __shared__ int s_ids[DEC_MAX_PAIRS];
   __shared__ float s_w[DEC_MAX_PAIRS];
   __shared__ int s_cidx[DEC_MAX_PAIRS];  // pair -> compact routed index (or -1)
@@ -119,17 +111,16 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   ZM_TRACE(0);
 
   // ---------------------------------------------------------------- P0: route, quantize x
-  if constexpr (kIQ2) {
-    for (int i = tid; i < 256; i += DEC_THREADS) s_grid[i] = a.grid[i];
-    for (int i = tid; i < 128; i += DEC_THREADS) s_signs[i] = a.signs[i];
-  }
+  // Wave w < S routes token w (its loads go out first); the other waves
+  // quantize x (16 lanes per block, 4 blocks per wave and round), then the
+  // routing waves join them.
   if (tid == 0) s_err = 0;
-  // x loads for the first 32 blocks go out before routing (16 lanes per block)
   const int nxb = S * a.nbH;
   const int l16 = lane & 15;
+  const int wi = wave >= S ? wave - S : wave + DEC_WAVES - S;  // x-quant worker index
   float xv[16];
-  {
-    const int bb = wave * 4 + (lane >> 4);
+  auto load_x = [&](int grp) {
+    const int bb = grp * 4 + (lane >> 4);
     if (bb < nxb) {
       const int s = bb / a.nbH, b = bb % a.nbH;
       const float4 *src = reinterpret_cast<const float4 *>(a.x + (size_t)s * H + (size_t)b * QK + 16 * l16);
@@ -142,50 +133,53 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
         xv[4 * i + 3] = f.w;
       }
     }
-  }
-  for (int s = 0; s < S; ++s) {
-    router_wg(a.r, s, s_rl);
-    if (tid < K) {
-      s_ids[s * K + tid] = s_rl.oid[tid];
-      s_w[s * K + tid] = s_rl.ow[tid];
+  };
+  if (wave < S) {
+    const WaveRoute r = route_token(a.r, wave, reinterpret_cast<float *>(s_stage[wave]));
+    if (lane < K) {
+      s_ids[wave * K + lane] = r.id;
+      s_w[wave * K + lane] = r.w;
       if (g == 0 && a.r.ids) {
-        a.r.ids[s * K + tid] = s_rl.oid[tid];
-        a.r.weights[s * K + tid] = s_rl.ow[tid];
+        a.r.ids[wave * K + lane] = r.id;
+        a.r.weights[wave * K + lane] = r.w;
       }
     }
   }
+  if constexpr (kIQ2) {
+    for (int i = tid; i < 256; i += DEC_THREADS) s_grid[i] = a.grid[i];
+    for (int i = tid; i < 128; i += DEC_THREADS) s_signs[i] = a.signs[i];
+  }
   ZM_TRACE(6);
-  for (int base = wave * 4; base < nxb; base += DEC_WAVES * 4) {
-    const int bb = base + (lane >> 4);
+  for (int grp = wi; grp * 4 < nxb; grp += DEC_WAVES) {
+    load_x(grp);
+    const int bb = grp * 4 + (lane >> 4);
     if (bb < nxb) {
       const int s = bb / a.nbH, b = bb % a.nbH;
-      if (base != wave * 4) {
-        const float4 *src = reinterpret_cast<const float4 *>(a.x + (size_t)s * H + (size_t)b * QK + 16 * l16);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float4 f = src[i];
-          xv[4 * i] = f.x;
-          xv[4 * i + 1] = f.y;
-          xv[4 * i + 2] = f.z;
-          xv[4 * i + 3] = f.w;
-        }
-      }
       store_q8_16(s_q8 + (size_t)s * q8x, a.nbH, b, quant_block16(xv, l16), l16);
     }
   }
+  ZM_TRACE(7);
   __syncthreads();
-  if (tid == 0) {
+  if (wave == 0) {
+    // compact the routed pairs (id >= 0) in pair order: ballot + prefix count
     int n = 0;
-    for (int p = 0; p < S * K; ++p) {
-      if (s_ids[p] >= 0) {
-        s_cidx[p] = n;
-        s_vp[n++] = p;
-      } else {
-        s_cidx[p] = -1;
+    for (int p0 = 0; p0 < S * K; p0 += 64) {
+      const int p = p0 + lane;
+      const bool ok = p < S * K && s_ids[p] >= 0;
+      const unsigned long long m = __ballot(ok);
+      const int c = n + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+      if (p < S * K) {
+        s_cidx[p] = ok ? c : -1;
+        s_vp[p] = 0;
       }
+      n += __popcll(m);
     }
-    for (int p = n; p < S * K; ++p) s_vp[p] = 0;
-    s_nvp = n;
+    stage_sync();
+    for (int p0 = 0; p0 < S * K; p0 += 64) {
+      const int p = p0 + lane;
+      if (p < S * K && s_cidx[p] >= 0) s_vp[s_cidx[p]] = p;
+    }
+    if (lane == 0) s_nvp = n;
   }
   __syncthreads();
   ZM_TRACE(1);

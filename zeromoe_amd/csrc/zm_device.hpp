@@ -153,6 +153,12 @@ __device__ __forceinline__ int group_sum_i(int v) {
         (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
   return v;
 }
+// LDS writes of this wave visible to its other lanes
+__device__ __forceinline__ void stage_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_f<DPP_XOR1>(v));
   v = fmaxf(v, dpp_f<DPP_XOR2>(v));

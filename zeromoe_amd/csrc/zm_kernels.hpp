@@ -1,7 +1,7 @@
 // zm_kernels.hpp -- the routed-expert kernels for gfx950 (wave64, CDNA4).
 //
 //   k_quant_q8K  : f32 rows -> Q8_K (one wave per 256-value block)
-//   k_router_wg  : gating + (grouped) top-k + weights + slot table, one workgroup per token
+//   k_router     : gating + (grouped) top-k + weights + slot table, one wave per token
 //   k_bucket     : stable counting sort of (token, slot) pairs by expert
 //   k_gemv       : bucketed MUL_MAT_ID GEMV over Q8_K activations (decode path)
 //   k_combine    : k-ascending weighted sum over the top-k axis (+ shared expert)
@@ -138,193 +138,198 @@ __device__ __forceinline__ bool outranks(float sa, int ia, float sb, int ib) {
 
 constexpr int ROUTER_MAX_E = 1024;
 
-// Workgroup-wide router for one token.  Softmax statistics go through
-// per-wave DPP partials in LDS.  The top-k order comes from ranking: with the
-// strict order "higher score, then lower index" packed into a 64-bit key
-// (order-preserving float bits above the complemented index), the rank of an
-// expert is the number of larger keys, which is the position repeated argmax
-// selection would give it.  T threads share one expert's comparisons.
-constexpr int ROUTER_PER = 4;  // experts per thread at most (E <= 4 * blockDim)
-struct RouterLds {
-  float p[ROUTER_MAX_E];
-  float sel[ROUTER_MAX_E];
-  unsigned long long key[ROUTER_MAX_E];
-  double dred[16];
-  float fred[16];
-  float gscore[64];
-  int keep[64];
-  int oid[128];  // top-k ids; also (best, second) per group while grouping
-  float ow[64];
-};
-
+// Strict order "higher score, then lower index" as one 64-bit key: the
+// order-preserving bits of the score above the complemented index.  Keys of
+// distinct experts never tie; 0 is below every key.
 __device__ __forceinline__ unsigned long long rank_key(float v, int e) {
   const uint32_t u = __float_as_uint(v + 0.0f);  // -0 -> +0: equal scores tie on the index
   const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
   return ((unsigned long long)o << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
 }
 
-// Results land in L.oid[k] / L.ow[k] (k < K) after the final barrier: ids after
-// the slot table, weights normalised/scaled/masked.
-__device__ void router_wg(const RouterArgs &a, int s, RouterLds &L) {
-  const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63, wave = tid >> 6;
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k) {
+  auto step = [&](auto tag) {
+    constexpr int C = decltype(tag)::value;
+    const uint32_t lo = (uint32_t)dpp_i<C>((int)(uint32_t)k), hi = (uint32_t)dpp_i<C>((int)(uint32_t)(k >> 32));
+    const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+    k = o > k ? o : k;
+  };
+  step(std::integral_constant<int, DPP_XOR1>{});
+  step(std::integral_constant<int, DPP_XOR2>{});
+  step(std::integral_constant<int, DPP_HALF_MIRROR>{});
+  step(std::integral_constant<int, DPP_MIRROR>{});
+  unsigned long long best = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, 16 * r);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), 16 * r);
+    const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+    best = o > best ? o : best;
+  }
+  return best;
+}
+
+// One wave routes one token.  Expert e = lane + 64*i sits in register i of its
+// lane (E <= 64*P).  Results: lane k < K holds route k (id after the slot
+// table, weight normalised / scaled / masked).  `scr` is E floats of LDS
+// private to the wave (used for grouped selection only).
+struct WaveRoute {
+  int id;
+  float w;
+};
+template <int P>
+__device__ __forceinline__ WaveRoute router_wave(const RouterArgs &a, int s, float *scr) {
+  const int lane = threadIdx.x & 63;
   const int E = a.E, K = a.K;
-  const int per = (E + nthr - 1) / nthr;             // experts per thread
-  const int nwa = min((E + 63) / 64, nthr / 64);     // waves that own experts
-  const bool owner = wave < nwa;
   const float NEG_INF = __int_as_float(0xff800000);
   const float *l = a.logits + (size_t)s * E;
-  float v[ROUTER_PER];
+  float v[P], sb[P];
+  int rm[P];
+  float rk[P];
+  // every global load of the router goes out first
 #pragma unroll
-  for (int i = 0; i < ROUTER_PER; ++i) {
-    const int e = tid + i * nthr;
-    v[i] = (i < per && e < E) ? (a.logit_bias ? l[e] + a.logit_bias[e] : l[e]) : NEG_INF;
+  for (int i = 0; i < P; ++i) {
+    const int e = lane + 64 * i;
+    const bool in = e < E;
+    v[i] = in ? l[e] : NEG_INF;
+    if (a.logit_bias) v[i] = in ? v[i] + a.logit_bias[e] : NEG_INF;
+    sb[i] = (a.sel_bias && in) ? a.sel_bias[e] : 0.0f;
+    rm[i] = (a.route_map && in) ? a.route_map[e] : 0;
+    rk[i] = (a.route_map && a.route_mask && in) ? a.route_mask[e] : 1.0f;
   }
   if (a.gating == 0) {
-    if (owner) {
-      float mx = v[0];
+    float mx = v[0];
 #pragma unroll
-      for (int i = 1; i < ROUTER_PER; ++i)
-        if (i < per) mx = fmaxf(mx, v[i]);
-      mx = wave_max(mx);
-      if (lane == 0) L.fred[wave] = mx;
+    for (int i = 1; i < P; ++i) mx = fmaxf(mx, v[i]);
+    mx = wave_max(mx);
+    double sum = 0.0;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      v[i] = lane + 64 * i < E ? exp_f32(v[i] - mx) : 0.0f;
+      sum += (double)v[i];
     }
-    __syncthreads();
-    float mx = L.fred[0];
-    for (int w = 1; w < nwa; ++w) mx = fmaxf(mx, L.fred[w]);
-    if (owner) {
-      double sum = 0.0;
+    sum = wave_sum_f64(sum);
+    const float inv = (float)(1.0 / sum);
 #pragma unroll
-      for (int i = 0; i < ROUTER_PER; ++i) {
-        const int e = tid + i * nthr;
-        v[i] = (i < per && e < E) ? exp_f32(v[i] - mx) : 0.0f;
-        sum += (double)v[i];
-      }
-      sum = wave_sum_f64(sum);
-      if (lane == 0) L.dred[wave] = sum;
-    }
-    __syncthreads();
-    if (owner) {
-      double sum = L.dred[0];
-      for (int w = 1; w < nwa; ++w) sum += L.dred[w];
-      const float inv = (float)(1.0 / sum);
+    for (int i = 0; i < P; ++i) v[i] = v[i] * inv;
+  } else {
 #pragma unroll
-      for (int i = 0; i < ROUTER_PER; ++i) v[i] = v[i] * inv;
-    }
-  } else if (owner) {
-#pragma unroll
-    for (int i = 0; i < ROUTER_PER; ++i) {
-      if (i >= per) break;
+    for (int i = 0; i < P; ++i) {
       const float x = v[i];
       v[i] = a.gating == 1 ? 1.0f / (1.0f + exp_f32(-x)) : sqrtf(x > 0.0f ? x + log1pf(exp_f32(-x)) : log1pf(exp_f32(x)));
     }
   }
-  if (owner) {
+  // v = gate probabilities p; selection scores sel = p + sel_bias
+  float sel[P];
 #pragma unroll
-    for (int i = 0; i < ROUTER_PER; ++i) {
-      const int e = tid + i * nthr;
-      if (i < per && e < E) {
-        L.p[e] = v[i];
-        L.sel[e] = a.sel_bias ? v[i] + a.sel_bias[e] : v[i];
-      }
-    }
-  }
-  __syncthreads();
+  for (int i = 0; i < P; ++i) sel[i] = a.sel_bias ? v[i] + sb[i] : v[i];
   const int G = a.n_groups;
   if (G > 1 && a.n_groups_used > 0 && a.n_groups_used < G && E % G == 0 && G <= 64) {
-    // group score = best + second best selection score of the group: each expert
-    // ranks itself inside its group (same key order as the final top-k)
+    // group score = best + second best selection score of the group (lane g
+    // scans group g); keep the n_groups_used best groups
     const int gs = E / G;
-    for (int e = tid; e < E; e += nthr) L.key[e] = rank_key(L.sel[e], e);
-    __syncthreads();
-    for (int e = tid; e < E; e += nthr) {
-      const int g0 = (e / gs) * gs;
-      const unsigned long long mk = L.key[e];
-      int r = 0;
-      for (int e2 = g0; e2 < g0 + gs; ++e2) r += L.key[e2] > mk;
-      if (r < 2) L.oid[2 * (e / gs) + r] = e;  // oid[] doubles as (best, second) per group
-    }
-    __syncthreads();
-    if (tid < G) L.gscore[tid] = gs >= 2 ? L.sel[L.oid[2 * tid]] + L.sel[L.oid[2 * tid + 1]] : L.sel[L.oid[2 * tid]];
-    __syncthreads();
-    if (tid < G) {
-      int r = 0;
-      for (int g2 = 0; g2 < G; ++g2) r += outranks(L.gscore[g2], g2, L.gscore[tid], tid);
-      L.keep[tid] = r < a.n_groups_used;
-    }
-    __syncthreads();
-    for (int e = tid; e < E; e += nthr)
-      if (!L.keep[e / gs]) L.sel[e] = NEG_INF;
-    __syncthreads();
-  }
-  for (int e = tid; e < E; e += nthr) L.key[e] = rank_key(L.sel[e], e);
-  __syncthreads();
-  if (E <= nthr) {
-    // T (power of two, <= 16) adjacent threads per expert, each over E/T keys
-    int T = 1;
-    while (T < 16 && 2 * T * E <= nthr) T *= 2;
-    const int e = tid / T, part = tid % T;
-    const int chunk = (E + T - 1) / T;
-    int r = 0;
-    if (e < E) {
-      const unsigned long long mk = L.key[e];
-      const int lo = part * chunk, hi = min(E, lo + chunk);
-      for (int e2 = lo; e2 < hi; ++e2) r += L.key[e2] > mk;
-    }
-    if (T >= 2) r += dpp_i<DPP_XOR1>(r);
-    if (T >= 4) r += dpp_i<DPP_XOR2>(r);
-    if (T >= 8) r += dpp_i<DPP_HALF_MIRROR>(r);
-    if (T >= 16) r += dpp_i<DPP_MIRROR>(r);
-    if (e < E && part == 0 && r < K) {
-      L.oid[r] = e;
-      L.ow[r] = L.p[e];
-    }
-  } else {
-    for (int e = tid; e < E; e += nthr) {
-      const unsigned long long mk = L.key[e];
-      int r = 0;
-      for (int e2 = 0; e2 < E; ++e2) r += L.key[e2] > mk;
-      if (r < K) {
-        L.oid[r] = e;
-        L.ow[r] = L.p[e];
+#pragma unroll
+    for (int i = 0; i < P; ++i)
+      if (lane + 64 * i < E) scr[lane + 64 * i] = sel[i];
+    stage_sync();
+    float gsc = NEG_INF;
+    if (lane < G) {
+      int b1 = -1, b2 = -1;
+      float s1 = 0.f, s2 = 0.f;
+      for (int j = 0; j < gs; ++j) {
+        const int e = lane * gs + j;
+        const float x = scr[e];
+        if (b1 < 0 || outranks(x, e, s1, b1)) {
+          b2 = b1;
+          s2 = s1;
+          b1 = e;
+          s1 = x;
+        } else if (b2 < 0 || outranks(x, e, s2, b2)) {
+          b2 = e;
+          s2 = x;
+        }
       }
+      gsc = gs >= 2 ? s1 + s2 : s1;
     }
+    int r = 0;
+    for (int g2 = 0; g2 < G; ++g2) r += outranks(readlane_f(gsc, g2), g2, gsc, lane);
+    const unsigned long long keep = __ballot(lane < G && r < a.n_groups_used);
+#pragma unroll
+    for (int i = 0; i < P; ++i)
+      if (!((keep >> ((lane + 64 * i) / gs)) & 1ull)) sel[i] = NEG_INF;
+    stage_sync();  // scr is reused by the caller
   }
-  __syncthreads();
-  // lane k < K of wave 0 finishes route k: norm in k order (double, as ggml's
-  // sum_rows), scale, slot table
-  float w = 0.f;
-  int id = 0;
-  if (tid < K) {
-    w = L.ow[tid];
-    id = L.oid[tid];
-    if (a.weights_norm) {
-      double sum = 0.0;
-      for (int k = 0; k < K; ++k) sum += (double)L.ow[k];
-      float fs = (float)sum;
-      fs = fs < 6.103515625e-5f ? 6.103515625e-5f : fs;
-      w = w / fs;
+  // top-K: K rounds of a wave-wide 64-bit key maximum
+  unsigned long long key[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) key[i] = lane + 64 * i < E ? rank_key(sel[i], lane + 64 * i) : 0ull;
+  int myid = 0;
+  float myw = 0.f, mymask = 1.0f;
+  for (int k = 0; k < K; ++k) {
+    unsigned long long m = key[0];
+#pragma unroll
+    for (int i = 1; i < P; ++i) m = key[i] > m ? key[i] : m;
+    const unsigned long long best = wave_max_u64(m);
+    const int e = (int)(0xffffffffu - (uint32_t)best);
+    const int owner = e & 63;
+    // the owner lane takes the winner's values out of its registers (selects,
+    // not an indexed register read, so the arrays stay in registers)
+    float pw = 0.f, rkw = 1.0f;
+    int rmw = 0;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      const bool hit = key[i] == best;
+      pw = hit ? v[i] : pw;
+      rmw = hit ? rm[i] : rmw;
+      rkw = hit ? rk[i] : rkw;
+      key[i] = hit ? 0ull : key[i];
     }
-    if (a.weights_scale != 0.0f && a.weights_scale != 1.0f) w = w * a.weights_scale;
+    pw = readlane_f(pw, owner);
+    int id = e;
+    float msk = 1.0f;
     if (a.route_map) {
-      const float m = a.route_mask ? a.route_mask[id] : (a.route_map[id] >= 0 ? 1.0f : 0.0f);
-      id = a.route_map[id];
-      w = w * m;
+      id = __builtin_amdgcn_readlane(rmw, owner);
+      msk = a.route_mask ? readlane_f(rkw, owner) : (id >= 0 ? 1.0f : 0.0f);
+    }
+    if (lane == k) {
+      myid = id;
+      myw = pw;
+      mymask = msk;
     }
   }
-  __syncthreads();
-  if (tid < K) {
-    L.oid[tid] = id;
-    L.ow[tid] = w;
+  // weights: norm in k order (double, as ggml's sum_rows), scale, slot mask
+  float w = myw;
+  if (a.weights_norm) {
+    double sum = 0.0;
+    for (int k = 0; k < K; ++k) sum += (double)readlane_f(myw, k);
+    float fs = (float)sum;
+    fs = fs < 6.103515625e-5f ? 6.103515625e-5f : fs;
+    w = w / fs;
   }
-  __syncthreads();
+  if (a.weights_scale != 0.0f && a.weights_scale != 1.0f) w = w * a.weights_scale;
+  if (a.route_map) w = w * mymask;
+  return WaveRoute{myid, w};
 }
 
-__global__ __launch_bounds__(256) void k_router_wg(RouterArgs a) {
-  __shared__ RouterLds L;
-  router_wg(a, blockIdx.x, L);
-  if ((int)threadIdx.x < a.K) {
-    a.ids[(size_t)blockIdx.x * a.K + threadIdx.x] = L.oid[threadIdx.x];
-    a.weights[(size_t)blockIdx.x * a.K + threadIdx.x] = L.ow[threadIdx.x];
+// E <= 64*P for the smallest P in {1, 2, 4, 8, 16}
+__device__ __forceinline__ WaveRoute route_token(const RouterArgs &a, int s, float *scr) {
+  if (a.E <= 64) return router_wave<1>(a, s, scr);
+  if (a.E <= 128) return router_wave<2>(a, s, scr);
+  if (a.E <= 256) return router_wave<4>(a, s, scr);
+  if (a.E <= 512) return router_wave<8>(a, s, scr);
+  return router_wave<16>(a, s, scr);
+}
+
+// one wave per token, 4 tokens per workgroup
+__global__ __launch_bounds__(256) void k_router(RouterArgs a, int S) {
+  __shared__ float scr[4][ROUTER_MAX_E];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int s = blockIdx.x * 4 + wave;
+  if (s >= S) return;
+  const WaveRoute r = route_token(a, s, scr[wave]);
+  if (lane < a.K) {
+    a.ids[(size_t)s * a.K + lane] = r.id;
+    a.weights[(size_t)s * a.K + lane] = r.w;
   }
 }
 
