@@ -362,46 +362,42 @@ int zm_mul_mat_id(const zm_tensor *w, const zm_tensor *x, const zm_tensor *ids, 
 }  // extern "C"
 
 namespace {
+// Debug kernel: per super-block integer parts of one weight row against one
+// Q8_K row, computed by both decode dot paths -- the 4-lane quarter path of the
+// bucketed GEMV and the whole-block unit path of the fused decode kernel.  The
+// unit result is written; a disagreement writes INT32_MIN into isum instead.
 template <int T>
-__global__ void k_block_dots(const uint8_t *w, const uint8_t *xq, int nb, int32_t *isum, int32_t *imin) {
+__global__ void k_block_dots(const uint8_t *w, const uint8_t *xq, int nb, int32_t *isum, int32_t *imin,
+                             const uint64_t *grid, const uint64_t *signs) {
   const int lane = threadIdx.x & 63;
   const int gq = blockIdx.x * 64 + lane;  // quarter index
   const int b = gq >> 2, q = gq & 3;
   QInt r{0, 0};
-  __shared__ uint64_t dummy[1];
-  (void)dummy;
+  int ui = 0, um = 0;
   if (b < nb) {
     Q8Slice s;
     WSlice ws;
     load_q8_slice<T>(xq, nb, b, q, s);
     load_w_slice<T>(w + (size_t)b * block_bytes(T), q, ws);
-    r = quarter_int<T>(ws, q, s, nullptr, nullptr);
+    r = quarter_int<T>(ws, q, s, grid, signs);
+    if (q < unit_per_block<T>()) {
+      const rsrc_t rw = make_rsrc(w, (uint32_t)(nb * block_bytes(T)));
+      Unit<T> u[1];
+      load_unit<T>(rw, b * block_bytes(T), q, u[0]);
+      int ri[1], rm[1];
+      unit_ints<T, 1>(u, q, xblk_planar(xq, nb, b), grid, signs, ri, rm);
+      ui = ri[0];
+      um = rm[0];
+    }
   }
   r.isum = group_sum_i<4>(r.isum);
   r.imin = group_sum_i<4>(r.imin);
+  ui = group_sum_i<4>(ui);
+  um = group_sum_i<4>(um);
   if (b < nb && q == 0) {
-    isum[b] = r.isum;
-    imin[b] = r.imin;
-  }
-}
-// IQ2 variant needs the tables (from global memory directly)
-__global__ void k_block_dots_iq2(const uint8_t *w, const uint8_t *xq, int nb, int32_t *isum, int32_t *imin,
-                                 const uint64_t *grid, const uint64_t *signs) {
-  const int lane = threadIdx.x & 63;
-  const int gq = blockIdx.x * 64 + lane;
-  const int b = gq >> 2, q = gq & 3;
-  QInt r{0, 0};
-  if (b < nb) {
-    Q8Slice s;
-    WSlice ws;
-    load_q8_slice<T_IQ2_XXS>(xq, nb, b, q, s);
-    load_w_slice<T_IQ2_XXS>(w + (size_t)b * 66, q, ws);
-    r = quarter_int<T_IQ2_XXS>(ws, q, s, grid, signs);
-  }
-  r.isum = group_sum_i<4>(r.isum);
-  if (b < nb && q == 0) {
-    isum[b] = r.isum;
-    imin[b] = 0;
+    const bool agree = ui == r.isum && um == r.imin;
+    isum[b] = agree ? ui : INT32_MIN;
+    imin[b] = um;
   }
 }
 }  // namespace
@@ -421,10 +417,10 @@ int zm_block_dots(int type, const void *w_row, const float *x, int n, int32_t *i
   const dim3 g((unsigned)((nb * 4 + 63) / 64));
   const uint8_t *w = (const uint8_t *)w_row;
   switch (type) {
-  case T_Q2_K: hipLaunchKernelGGL(k_block_dots<T_Q2_K>, g, dim3(64), 0, st, w, xq, nb, isum, imin); break;
-  case T_Q3_K: hipLaunchKernelGGL(k_block_dots<T_Q3_K>, g, dim3(64), 0, st, w, xq, nb, isum, imin); break;
-  case T_Q4_K: hipLaunchKernelGGL(k_block_dots<T_Q4_K>, g, dim3(64), 0, st, w, xq, nb, isum, imin); break;
-  default: hipLaunchKernelGGL(k_block_dots_iq2, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->grid, d->signs); break;
+  case T_Q2_K: hipLaunchKernelGGL(k_block_dots<T_Q2_K>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->grid, d->signs); break;
+  case T_Q3_K: hipLaunchKernelGGL(k_block_dots<T_Q3_K>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->grid, d->signs); break;
+  case T_Q4_K: hipLaunchKernelGGL(k_block_dots<T_Q4_K>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->grid, d->signs); break;
+  default: hipLaunchKernelGGL(k_block_dots<T_IQ2_XXS>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->grid, d->signs); break;
   }
   HIP_OK(hipGetLastError());
   HIP_OK(hipFreeAsync(xq, st));
@@ -503,38 +499,32 @@ int check_layer(const zm_moe_layer *L) {
   return 0;
 }
 using DecFn = void (*)(DecodeArgs);
+int units_per_block(int t) { return t == T_Q4_K ? 2 : 1; }
 
-template <int TG, int TD, int TS, int IT1>
-DecFn dec_pick2(int itr, int its) {
-  if constexpr (TS == 0) {
-    if (its != 0) return nullptr;
-    if (itr <= 2) return k_moe_decode<TG, TD, 0, IT1, 2, 0>;
-    if (itr <= 3) return k_moe_decode<TG, TD, 0, IT1, 3, 0>;
-    if (itr <= 4) return k_moe_decode<TG, TD, 0, IT1, 4, 0>;
-  } else {
-    if (its != 1) return nullptr;
-    if (itr <= 2) return k_moe_decode<TG, TD, TS, IT1, 2, 1>;
-    if (itr <= 3) return k_moe_decode<TG, TD, TS, IT1, 3, 1>;
-    if (itr <= 4) return k_moe_decode<TG, TD, TS, IT1, 4, 1>;
-  }
+template <int TG, int TD, int TS, int L1>
+DecFn dec_pick2(int ir, int is) {
+  if (is != (TS ? 1 : 0)) return nullptr;
+  constexpr int IS = TS ? 1 : 0;
+  if (ir <= 2) return k_moe_decode<TG, TD, TS, L1, 2, IS>;
+  if (ir <= 3) return k_moe_decode<TG, TD, TS, L1, 3, IS>;
   return nullptr;
 }
 
-// IT1: 64-lane iterations over a gate/up row; ITR / ITS: over the routed /
-// shared part of a down row
+// L1: lanes per routed gate/up row (16 or 32, one unit each; shared rows use
+// 64); IR / IS: 32-lane iterations over the routed / shared units of a down row
 template <int TG, int TD, int TS>
-DecFn dec_pick(int it1, int itr, int its) {
-  if (it1 <= 1) return dec_pick2<TG, TD, TS, 1>(itr, its);
-  if (it1 <= 2) return dec_pick2<TG, TD, TS, 2>(itr, its);
+DecFn dec_pick(int l1, int ir, int is) {
+  if (l1 == 16) return dec_pick2<TG, TD, TS, 16>(ir, is);
+  if (l1 == 32) return dec_pick2<TG, TD, TS, 32>(ir, is);
   return nullptr;
 }
 
-DecFn find_decode(int tg, int td, int ts, int it1, int itr, int its) {
-  if (tg == T_Q4_K && td == T_Q4_K && ts == 0) return dec_pick<T_Q4_K, T_Q4_K, 0>(it1, itr, its);
-  if (tg == T_Q2_K && td == T_Q3_K && ts == 0) return dec_pick<T_Q2_K, T_Q3_K, 0>(it1, itr, its);
-  if (tg == T_IQ2_XXS && td == T_IQ2_XXS && ts == 0) return dec_pick<T_IQ2_XXS, T_IQ2_XXS, 0>(it1, itr, its);
-  if (tg == T_Q2_K && td == T_Q2_K && ts == T_Q4_K) return dec_pick<T_Q2_K, T_Q2_K, T_Q4_K>(it1, itr, its);
-  if (tg == T_Q2_K && td == T_Q2_K && ts == 0) return dec_pick<T_Q2_K, T_Q2_K, 0>(it1, itr, its);
+DecFn find_decode(int tg, int td, int ts, int l1, int ir, int is) {
+  if (tg == T_Q4_K && td == T_Q4_K && ts == 0) return dec_pick<T_Q4_K, T_Q4_K, 0>(l1, ir, is);
+  if (tg == T_Q2_K && td == T_Q3_K && ts == 0) return dec_pick<T_Q2_K, T_Q3_K, 0>(l1, ir, is);
+  if (tg == T_IQ2_XXS && td == T_IQ2_XXS && ts == 0) return dec_pick<T_IQ2_XXS, T_IQ2_XXS, 0>(l1, ir, is);
+  if (tg == T_Q2_K && td == T_Q2_K && ts == T_Q4_K) return dec_pick<T_Q2_K, T_Q2_K, T_Q4_K>(l1, ir, is);
+  if (tg == T_Q2_K && td == T_Q2_K && ts == 0) return dec_pick<T_Q2_K, T_Q2_K, 0>(l1, ir, is);
   return nullptr;
 }
 
@@ -577,19 +567,21 @@ int launch_fused(const zm_moe_layer *L, const float *x, const float *logits, int
   const int nbH = H / QK, nbF = F / QK;
   const int Fs = L->F_shared > 0 ? L->F_shared : 0;
   const int nbFs = Fs / QK;
-  if (!fused_enabled() || S > DEC_MAX_S || S * K > DEC_MAX_PAIRS || E > ROUTER_MAX_E)
+  if (!fused_enabled() || S > DEC_MAX_S || S * K > DEC_MAX_PAIRS || E > DEC_MAX_E)
     return 1;
   if (L->type_up != L->type_gate) return 1;
-  const int it1 = (4 * nbH + 63) / 64;
-  const int itr = (K * 4 * nbF + 63) / 64;
-  const int its = (4 * nbFs + 63) / 64;
-  DecFn fn = find_decode(L->type_gate, L->type_down, Fs ? L->type_shared : 0, it1, itr, its);
+  const int u1 = nbH * units_per_block(L->type_gate);
+  const int l1 = u1 <= 16 ? 16 : (u1 <= 32 ? 32 : 0);
+  if (Fs && nbH * units_per_block(L->type_shared) > 64) return 1;
+  const int ir = (K * nbF * units_per_block(L->type_down) + 31) / 32;
+  const int is = Fs ? (nbFs * units_per_block(L->type_shared) + 31) / 32 : 0;
+  DecFn fn = find_decode(L->type_gate, L->type_down, Fs ? L->type_shared : 0, l1, ir, is);
   if (!fn) return 1;
   int G = 0;
   if (decode_grid(fn, &G)) return -1;
   const long T1 = (long)S * K * F + (long)S * Fs;
-  const size_t q8F = q8_row_bytes(nbF), q8Fs = Fs ? q8_row_bytes(nbFs) : 0;
-  if ((size_t)S * q8_row_bytes(nbH) > (size_t)DEC_LDS_Q8 || 2 * ((size_t)K * q8F + q8Fs) > (size_t)DEC_LDS_Q8) return 1;
+  const size_t q8F = q8l_row_bytes(nbF), q8Fs = Fs ? q8l_row_bytes(nbFs) : 0;
+  if ((size_t)S * q8l_row_bytes(nbH) > (size_t)DEC_LDS_Q8 || 2 * ((size_t)K * q8F + q8Fs) > (size_t)DEC_LDS_Q8) return 1;
   if (T1 >= (1l << 24) || (long)S * H >= (1l << 24)) return 1;  // float-reciprocal index math
   DecodeArgs a{};
   a.r = RouterArgs{logits, L->logit_bias, L->sel_bias, L->route_map, L->route_mask, E, K, L->router.gating,
@@ -675,10 +667,13 @@ int zm_moe_status(const zm_moe_layer *layer, int S, void *workspace, void *strea
   if (check_layer(layer) || S <= 0 || !workspace) return -1;
   LayerWs w;
   layer_ws(layer, S, (uint8_t *)workspace, &w);
-  uint32_t err = 0, zero = 0;
+  uint32_t err = 0;
   HIP_OK(hipMemcpyAsync(&err, w.f_sync + 1, 4, hipMemcpyDeviceToHost, (hipStream_t)stream));
-  HIP_OK(hipMemcpyAsync(w.f_sync + 1, &zero, 4, hipMemcpyHostToDevice, (hipStream_t)stream));
   HIP_OK(hipStreamSynchronize((hipStream_t)stream));
+  if (err) {  // an expired wait leaves the arrival counters unknown: start them over
+    HIP_OK(hipMemsetAsync(w.f_sync, 0, (size_t)DEC_SYNC_WORDS * 4, (hipStream_t)stream));
+    HIP_OK(hipStreamSynchronize((hipStream_t)stream));
+  }
   return (int)err;
 }
 

@@ -1,0 +1,334 @@
+// zm_blockdot.hpp -- whole-super-block int8 dots for the fused decode kernel.
+//
+// One lane holds one "unit" of a weight row in registers: a whole super-block
+// (Q2_K, Q3_K, IQ2_XXS) or half of one (Q4_K), and reads the matching Q8_K
+// block of the activation row from LDS (planar layout: qs | bsums | d).  A
+// unit's integer dot is the ggml per-block integer sum (kquant layouts of
+// /root/reference/kernels/quant/kquant_matmul.cu:35-200, iq2_matmul.cu:27-91);
+// the float combine is d_x * (d * isum - dmin * imin) as in ggml's
+// vec_dot_*_q8_K.  Several weight units (gate and up) share one pass over the
+// activation, and per-sub-block scales are applied once per 16 or 32 weights,
+// so the VALU cost is close to one mask and one v_dot4 per 4 weights.
+//
+// Bit-plane trick (Q2_K, Q3_K): the 2-bit value of plane j is masked in place
+// (x & (3 << 2j) per byte), so v_dot4 yields 4^j times the plane's dot; the
+// sums are kept per plane and shifted back exactly at the end.  v_dot4 reads
+// signed bytes, so a field in bit 7 is first moved down one or two bits (plane
+// 3 is used as (x >> 2) & 0x30, scale 16; the Q3_K high bit 7 as bit 6).
+#pragma once
+
+#include "zm_device.hpp"
+
+namespace zm {
+
+template <int T>
+__host__ __device__ constexpr int unit_per_block() {
+  return T == T_Q4_K ? 2 : 1;
+}
+
+template <int T>
+struct Unit;
+template <>
+struct Unit<T_Q2_K> {  // scales[16] | qs[64] | d, dmin
+  uint4 sc;
+  uint4 q[4];
+  uint32_t dd;
+};
+template <>
+struct Unit<T_Q3_K> {  // hmask[32] | qs[64] | scales[12] | d
+  uint4 hm[2];
+  uint4 q[4];
+  uint32_t sc[3];
+  uint32_t d;
+};
+template <>
+struct Unit<T_Q4_K> {  // d, dmin, scales[12] | half of qs[128]
+  uint4 hdr;
+  uint4 q[4];
+};
+template <>
+struct Unit<T_IQ2_XXS> {  // d | qs u16[32]
+  uint32_t d;
+  uint4 q[4];
+};
+
+// vo: byte offset of the super-block in the resource (an out-of-range offset
+// loads zeros); part: which half for Q4_K
+template <int T>
+__device__ __forceinline__ void load_unit(rsrc_t r, int vo, int part, Unit<T> &u) {
+  if constexpr (T == T_Q2_K) {
+    u.sc = bld16(r, vo, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u.q[i] = bld16(r, vo + 16 + 16 * i, 0);
+    u.dd = bld4(r, vo + 80, 0);
+  } else if constexpr (T == T_Q3_K) {
+    u.hm[0] = bld16(r, vo, 0);
+    u.hm[1] = bld16(r, vo + 16, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u.q[i] = bld16(r, vo + 32 + 16 * i, 0);
+    const auto s = __builtin_amdgcn_raw_buffer_load_b96(r, vo + 96, 0, 0);
+    u.sc[0] = s[0];
+    u.sc[1] = s[1];
+    u.sc[2] = s[2];
+    u.d = bld2(r, vo + 108, 0);
+  } else if constexpr (T == T_Q4_K) {
+    u.hdr = bld16(r, vo, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u.q[i] = bld16(r, vo + 16 + 64 * part + 16 * i, 0);
+  } else {
+    u.d = bld2(r, vo, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u.q[i] = bld16(r, vo + 2 + 16 * i, 0);
+  }
+}
+
+__device__ __forceinline__ uint32_t u4c(const uint4 &v, int i) {
+  return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+__device__ __forceinline__ int sdot2(uint32_t a, uint32_t b, int c) {
+  typedef short short2_t __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, a), __builtin_bit_cast(short2_t, b), c, false);
+}
+__device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
+
+// Activation rows in LDS: qs blocks at a 272-byte stride (so the 16 lanes of
+// a row, one block each, read 16 different bank groups instead of one), then
+// bsums (16 int16 per block), then d (f32 per block); rows padded to 16 bytes.
+constexpr int Q8L_BLK = 272;
+__host__ __device__ constexpr size_t q8l_row_bytes(int nb) { return ((size_t)nb * (Q8L_BLK + 36) + 15) & ~(size_t)15; }
+__host__ __device__ constexpr size_t q8l_bs_off(int nb) { return (size_t)nb * Q8L_BLK; }
+__host__ __device__ constexpr size_t q8l_d_off(int nb) { return (size_t)nb * (Q8L_BLK + 32); }
+
+// One activation block: qs (256 int8), bsums (16 int16), d.
+struct XBlk {
+  const uint4 *q;   // 16 x uint4
+  const uint4 *bs;  // 2 x uint4
+  float d;
+};
+// block of an LDS activation row
+__device__ __forceinline__ XBlk xblk(const uint8_t *row, int nb, int blk) {
+  XBlk x;
+  x.q = reinterpret_cast<const uint4 *>(row + (size_t)blk * Q8L_BLK);
+  x.bs = reinterpret_cast<const uint4 *>(row + q8l_bs_off(nb) + (size_t)blk * 32);
+  x.d = reinterpret_cast<const float *>(row + q8l_d_off(nb))[blk];
+  return x;
+}
+// block of a planar row in global memory (q8_row_bytes layout)
+__device__ __forceinline__ XBlk xblk_planar(const uint8_t *row, int nb, int blk) {
+  XBlk x;
+  x.q = reinterpret_cast<const uint4 *>(row + (size_t)blk * QK);
+  x.bs = reinterpret_cast<const uint4 *>(row + q8_bs_off(nb) + (size_t)blk * 32);
+  x.d = reinterpret_cast<const float *>(row + q8_d_off(nb))[blk];
+  return x;
+}
+
+// Integer parts of weight unit w[n] against activation block x, as ggml's
+// per-block sums: Q2_K/Q4_K isum = sum sc*dot, imin = sum m*bsum; Q3_K isum
+// with q3 = q2 - 4*(bit clear), imin = 0; IQ2_XXS isum = sum (2ls+1)*dot.
+template <int T, int NW>
+__device__ __forceinline__ void unit_ints(const Unit<T> (&w)[NW], int part, const XBlk &x, const uint64_t *lds_grid,
+                                          const uint64_t *lds_signs, int (&ri)[NW], int (&rm)[NW]) {
+  if constexpr (T == T_Q2_K) {
+    // qs dword 8h+k holds plane j = weights 128h + 32j + 4k..+3 (sub-block 8h + 2j + k/4)
+    int acc[NW][4];
+#pragma unroll
+    for (int n = 0; n < NW; ++n)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[n][j] = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // plane j of byte b, in place (scale 4^j), plane 3 moved to bits 4-5 (scale 16)
+        auto pl = [&](uint32_t b) { return j < 3 ? (b & (0x03030303u << (2 * j))) : ((b >> 2) & 0x30303030u); };
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const uint4 xv = x.q[8 * h + 2 * j + kk];
+          const int sb = 8 * h + 2 * j + kk;
+#pragma unroll
+          for (int n = 0; n < NW; ++n) {
+            const uint4 q = w[n].q[2 * h + kk];
+            int s = dot4(pl(q.x), xv.x, 0);
+            s = dot4(pl(q.y), xv.y, s);
+            s = dot4(pl(q.z), xv.z, s);
+            s = dot4(pl(q.w), xv.w, s);
+            const int sc = (int)((u4c(w[n].sc, sb >> 2) >> (8 * (sb & 3))) & 15u);
+            acc[n][j] = mad24(sc, s, acc[n][j]);
+          }
+        }
+      }
+    const uint4 b0 = x.bs[0], b1 = x.bs[1];
+    const uint32_t bs[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int n = 0; n < NW; ++n) {
+      const int isum = acc[n][0] + (acc[n][1] >> 2) + ((acc[n][2] + acc[n][3]) >> 4);
+      int imin = 0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t mm = (u4c(w[n].sc, c) >> 4) & 0x0f0f0f0fu;  // mins of sub-blocks 4c..4c+3
+        imin = sdot2(__builtin_amdgcn_perm(0u, mm, 0x0c010c00u), bs[2 * c], imin);
+        imin = sdot2(__builtin_amdgcn_perm(0u, mm, 0x0c030c02u), bs[2 * c + 1], imin);
+      }
+      ri[n] = isum;
+      rm[n] = imin;
+    }
+  } else if constexpr (T == T_Q3_K) {
+    // q3 = q2 - 4 * (hmask bit clear); hmask byte l (l = 4k + i) holds bit 4h + j of
+    // weight 128h + 32j + l.  Plane dots (scale 4^j) and cleared-bit dots (scale
+    // 2^(4h+j)) are kept apart and shifted back at the end.
+    int accq[NW][4], acch[NW][8];
+    uint32_t s4[NW][4];
+#pragma unroll
+    for (int n = 0; n < NW; ++n) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) accq[n][j] = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acch[n][j] = 0;
+      // 6-bit scales as bytes (ggml's aux[] unpacking), xor 32: a 6-bit signed field is sc - 32
+      const uint32_t a0 = w[n].sc[0], a1 = w[n].sc[1], a2 = w[n].sc[2];
+      s4[n][0] = ((a0 & 0x0f0f0f0fu) | ((a2 & 0x03030303u) << 4)) ^ 0x20202020u;
+      s4[n][1] = ((a1 & 0x0f0f0f0fu) | (((a2 >> 2) & 0x03030303u) << 4)) ^ 0x20202020u;
+      s4[n][2] = (((a0 >> 4) & 0x0f0f0f0fu) | (((a2 >> 4) & 0x03030303u) << 4)) ^ 0x20202020u;
+      s4[n][3] = (((a1 >> 4) & 0x0f0f0f0fu) | (((a2 >> 6) & 0x03030303u) << 4)) ^ 0x20202020u;
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // plane j in place (scale 4^j; plane 3 at bits 4-5, scale 16); cleared high
+        // bit 4h+j in place (bit 7 moved to bit 6)
+        auto pl = [&](uint32_t b) { return j < 3 ? (b & (0x03030303u << (2 * j))) : ((b >> 2) & 0x30303030u); };
+        auto hb = [&](uint32_t b) {
+          return 4 * h + j < 7 ? (~b & (0x01010101u << (4 * h + j))) : ((~b >> 1) & 0x40404040u);
+        };
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const uint4 xv = x.q[8 * h + 2 * j + kk];
+          const int sb = 8 * h + 2 * j + kk;
+#pragma unroll
+          for (int n = 0; n < NW; ++n) {
+            const uint4 q = w[n].q[2 * h + kk];
+            const uint4 hm = w[n].hm[kk];
+            int sq = dot4(pl(q.x), xv.x, 0);
+            sq = dot4(pl(q.y), xv.y, sq);
+            sq = dot4(pl(q.z), xv.z, sq);
+            sq = dot4(pl(q.w), xv.w, sq);
+            int sh = dot4(hb(hm.x), xv.x, 0);
+            sh = dot4(hb(hm.y), xv.y, sh);
+            sh = dot4(hb(hm.z), xv.z, sh);
+            sh = dot4(hb(hm.w), xv.w, sh);
+            const int sc = __builtin_amdgcn_sbfe((int)s4[n][sb >> 2], 8 * (sb & 3), 6);
+            accq[n][j] = mad24(sc, sq, accq[n][j]);
+            acch[n][4 * h + j] = mad24(sc, sh, acch[n][4 * h + j]);
+          }
+        }
+      }
+#pragma unroll
+    for (int n = 0; n < NW; ++n) {
+      const int q = accq[n][0] + (accq[n][1] >> 2) + ((accq[n][2] + accq[n][3]) >> 4);
+      int hsum = 0;
+#pragma unroll
+      for (int i = 0; i < 7; ++i) hsum += acch[n][i] >> i;
+      hsum += acch[n][7] >> 6;
+      ri[n] = q - 4 * hsum;
+      rm[n] = 0;
+    }
+  } else if constexpr (T == T_Q4_K) {
+    // part p: sub-blocks 4p..4p+3; qs bytes 32i..32i+31 of group i = 2p + g hold
+    // sub-block 2i in the low nibbles and 2i+1 in the high nibbles
+    const uint4 b = x.bs[part];  // bsums of sub-blocks 4p..4p+3 (two 16-sums each)
+#pragma unroll
+    for (int n = 0; n < NW; ++n) {
+      const uint32_t u0 = w[n].hdr.y, u1 = w[n].hdr.z, u2 = w[n].hdr.w;
+      const uint32_t scv = part == 0 ? (u0 & 0x3f3f3f3fu) : ((u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4));
+      const uint32_t mv =
+          part == 0 ? (u1 & 0x3f3f3f3fu) : (((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4));
+      int isum = 0, imin = 0;
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const int i = 2 * part + g;
+        int slo = 0, shi = 0;
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm) {
+          const uint4 qv = w[n].q[2 * g + mm];
+          const uint4 xl = x.q[4 * i + mm], xh = x.q[4 * i + 2 + mm];
+          slo = dot4(qv.x & 0x0f0f0f0fu, xl.x, slo);
+          slo = dot4(qv.y & 0x0f0f0f0fu, xl.y, slo);
+          slo = dot4(qv.z & 0x0f0f0f0fu, xl.z, slo);
+          slo = dot4(qv.w & 0x0f0f0f0fu, xl.w, slo);
+          shi = dot4((qv.x >> 4) & 0x0f0f0f0fu, xh.x, shi);
+          shi = dot4((qv.y >> 4) & 0x0f0f0f0fu, xh.y, shi);
+          shi = dot4((qv.z >> 4) & 0x0f0f0f0fu, xh.z, shi);
+          shi = dot4((qv.w >> 4) & 0x0f0f0f0fu, xh.w, shi);
+        }
+        isum = mad24((int)((scv >> (16 * g)) & 0xffu), slo, isum);
+        isum = mad24((int)((scv >> (16 * g + 8)) & 0xffu), shi, isum);
+      }
+      // min of local sub-block l times both 16-sums of that sub-block: (m, m) . (bs_lo, bs_hi)
+      imin = sdot2(__builtin_amdgcn_perm(0u, mv, 0x0c000c00u), b.x, imin);
+      imin = sdot2(__builtin_amdgcn_perm(0u, mv, 0x0c010c01u), b.y, imin);
+      imin = sdot2(__builtin_amdgcn_perm(0u, mv, 0x0c020c02u), b.z, imin);
+      imin = sdot2(__builtin_amdgcn_perm(0u, mv, 0x0c030c03u), b.w, imin);
+      ri[n] = isum;
+      rm[n] = imin;
+    }
+  } else {  // IQ2_XXS: sub-block ib uses qs dwords 2ib (4 grid indices), 2ib+1 (4 x 7-bit signs, 4-bit scale)
+    int isum[NW];
+#pragma unroll
+    for (int n = 0; n < NW; ++n) isum[n] = 0;
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) {
+      const uint4 x0 = x.q[2 * ib], x1 = x.q[2 * ib + 1];
+      const uint32_t xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+      for (int n = 0; n < NW; ++n) {
+        const uint32_t aux0 = u4c(w[n].q[ib >> 1], 2 * (ib & 1)), aux1 = u4c(w[n].q[ib >> 1], 2 * (ib & 1) + 1);
+        int s = 0;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+          const uint64_t g = lds_grid[(aux0 >> (8 * l)) & 0xffu];
+          const uint64_t m = lds_signs[(aux1 >> (7 * l)) & 127u];
+          const uint32_t glo = (uint32_t)g, ghi = (uint32_t)(g >> 32);
+          const uint32_t mlo = (uint32_t)m, mhi = (uint32_t)(m >> 32);
+          // conditional byte negate: (g ^ m) + (m & 1) per byte (no carries: 8 <= g <= 255)
+          s = dot4((glo ^ mlo) + (mlo & 0x01010101u), xs[2 * l], s);
+          s = dot4((ghi ^ mhi) + (mhi & 0x01010101u), xs[2 * l + 1], s);
+        }
+        isum[n] = mad24(2 * (int)(aux1 >> 28) + 1, s, isum[n]);
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < NW; ++n) {
+      ri[n] = isum[n];
+      rm[n] = 0;
+    }
+  }
+}
+
+// float contribution of a unit from its integer parts (ggml's vec_dot combine)
+template <int T>
+__device__ __forceinline__ float unit_float(const Unit<T> &w, float xd, int isum, int imin) {
+  if constexpr (T == T_Q2_K) {
+    const float d = h2f((uint16_t)(w.dd & 0xffffu)), dmin = h2f((uint16_t)(w.dd >> 16));
+    return (xd * d) * (float)isum - (xd * dmin) * (float)imin;
+  } else if constexpr (T == T_Q3_K) {
+    return (xd * h2f((uint16_t)(w.d & 0xffffu))) * (float)isum;
+  } else if constexpr (T == T_Q4_K) {
+    const float d = h2f((uint16_t)(w.hdr.x & 0xffffu)), dmin = h2f((uint16_t)(w.hdr.x >> 16));
+    return (xd * d) * (float)isum - (xd * dmin) * (float)imin;
+  } else {
+    return 0.125f * ((xd * h2f((uint16_t)(w.d & 0xffffu))) * (float)isum);
+  }
+}
+
+// out[n] = float contribution of weight unit w[n] against activation block x
+template <int T, int NW>
+__device__ __forceinline__ void unit_dots(const Unit<T> (&w)[NW], int part, const XBlk &x, const uint64_t *lds_grid,
+                                          const uint64_t *lds_signs, float (&out)[NW]) {
+  int ri[NW], rm[NW];
+  unit_ints<T, NW>(w, part, x, lds_grid, lds_signs, ri, rm);
+#pragma unroll
+  for (int n = 0; n < NW; ++n) out[n] = unit_float<T>(w[n], x.d, ri[n], rm[n]);
+}
+
+}  // namespace zm

@@ -10,20 +10,27 @@
 //       they stream while gate/up computes and while the workgroups wait.
 //   P1  the (pair, row) space of gate/up rows is cut into one contiguous range
 //       per workgroup; waves stream batches of rows (double-buffered) and store
-//       the SwiGLU output; the workgroup then adds its row count to one of 16
-//       rows-done counters.
-//   P2  down rows (token s, row h): the workgroup waits until the counters sum
-//       to all rows, quantizes the act rows of its tokens into LDS (Q8_K) and
+//       the SwiGLU output; the workgroup then counts itself in one of 16
+//       arrival counters.
+//   P2  down rows (token s, row h): the workgroup waits until all workgroups
+//       have arrived, quantizes the act rows of its tokens into LDS (Q8_K) and
 //       computes out[s][h] = sum_k w_k * (W_down[e_k][h] . q8(act_k)) (+ shared).
-//   Exit: the last workgroup to leave zeroes the sync words for the next call.
-// The hot loops carry no lane-divergent branches: a lane without work loads
-// through an out-of-range buffer offset, which returns zeros, so its dot is 0.
-// Cross-workgroup data moves through agent-scope relaxed atomic loads/stores
-// (sc1: coherent past the per-XCD L2s) and one counter; no agent-scope fence
-// (an L2 write-back + invalidate on gfx950) is issued.  The wait is bounded:
-// on expiry the error word is set and the kernel still drains.
+// Arrival counters come in two sets used by alternate calls: an epoch word
+// selects the set; workgroup 0 zeroes the other set when it starts and bumps
+// the epoch once every workgroup has arrived (all of them have read it by
+// then), so no workgroup waits on an atomic's return value.
+// The hot loops are straight-line code: a lane or row without work loads and
+// stores through an out-of-range buffer offset (loads return zeros, stores are
+// dropped), so every load of a batch is issued unconditionally and the
+// compiler's wait counts stay exact (a conditionally issued load or store
+// forces waits for everything issued after it).
+// Cross-workgroup data moves through agent-scope relaxed atomics and sc1
+// loads/stores (coherent past the per-XCD L2s); no agent-scope fence (an L2
+// write-back + invalidate on gfx950) is issued.  The wait is bounded: on
+// expiry the error word is set and the kernel still drains.
 #pragma once
 
+#include "zm_blockdot.hpp"
 #include "zm_kernels.hpp"
 
 namespace zm {
@@ -33,9 +40,10 @@ constexpr int DEC_WAVES = DEC_THREADS / 64;
 constexpr int DEC_MAX_S = 8;
 constexpr int DEC_MAX_PAIRS = 128;  // S * K
 constexpr int DEC_LDS_Q8 = 65536;   // Q8_K staging: x rows in P0/P1, act rows in P2
-constexpr int DEC_NCNT = 16;        // rows-done counters (one 64-byte line each) to spread the atomics
+constexpr int DEC_NCNT = 16;        // arrival counters per set (one 64-byte line each) to spread the atomics
 constexpr int DEC_CNT_STRIDE = 16;  // words between counters
-constexpr int DEC_SYNC_WORDS = DEC_CNT_STRIDE * (1 + DEC_NCNT);
+constexpr int DEC_SYNC_WORDS = DEC_CNT_STRIDE * (1 + 2 * DEC_NCNT);
+constexpr int DEC_MAX_E = 512;      // router experts handled in the fused kernel
 // lane offset past every buffer extent (all < 2^31): such a load returns zeros
 constexpr int OOR = (int)0x80000000u;
 
@@ -49,9 +57,9 @@ struct DecodeArgs {
   int Fs, nbFs;
   const uint8_t *sg, *su, *sd;
   size_t sg_rstride, sd_rstride;
-  uint32_t wg_bytes, wd_bytes, sg_bytes, sd_bytes;  // buffer-resource extents (< 4 GiB)
+  uint32_t wg_bytes, wd_bytes, sg_bytes, sd_bytes;  // buffer-resource extents (< 2 GiB)
   float *act;
-  uint32_t *sync;  // [0] workgroups exited, [1] error, [DEC_CNT_STRIDE*(1+i)] rows-done counter i
+  uint32_t *sync;  // [0] epoch, [1] error, [DEC_CNT_STRIDE*(1+NCNT*set+i)] arrival counter i of set 0/1
   const uint64_t *grid, *signs;
   int spin_limit;
   uint64_t *trace;  // optional: 8 timestamps per workgroup
@@ -80,12 +88,35 @@ __device__ __forceinline__ void stores_done() {
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt and lgkmcnt left at their maxima
 }
 __device__ __forceinline__ void after_wait() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup"); }
+// one f32 through a buffer resource with sc1 (coherent past the L2); an
+// out-of-range offset drops the store
+__device__ __forceinline__ void bst_co(rsrc_t r, int vo, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, vo, 0, 16);
+}
+__device__ __forceinline__ void bst(rsrc_t r, int vo, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, vo, 0, 0);
+}
 #define ZM_TRACE(slot)                                                         \
   do {                                                                         \
     if (a.trace && tid == 0) a.trace[(size_t)g * 8 + (slot)] = wall_clock64(); \
   } while (0)
 
-template <int TG, int TD, int TS, int IT1, int ITR, int ITS>
+// Q8_K block (16 lanes) into an LDS activation row (q8l layout)
+__device__ __forceinline__ void store_q8_16l(uint8_t *row, int nb, int blk, const Q8Out16 &o, int l16) {
+  *reinterpret_cast<uint4 *>(row + (size_t)blk * Q8L_BLK + 16 * l16) = o.q;
+  if (l16 == 0) reinterpret_cast<float *>(row + q8l_d_off(nb))[blk] = o.d;
+  reinterpret_cast<int16_t *>(row + q8l_bs_off(nb))[blk * 16 + l16] = (int16_t)o.bsum;
+}
+
+// gate/up row kind for the P1 streaming loop: weight type and routed/shared
+template <int T, bool SHARED, int L>
+struct RowsTag {
+  static constexpr int value = T;
+  static constexpr bool shared = SHARED;
+  static constexpr int lanes = L;  // lanes per row (one unit each)
+};
+
+template <int TG, int TD, int TS, int L1, int IR, int IS>
 __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   __shared__ int s_ids[DEC_MAX_PAIRS];
   __shared__ float s_w[DEC_MAX_PAIRS];
@@ -94,21 +125,26 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   __shared__ int s_nvp;
   __shared__ int s_err;
   __shared__ __attribute__((aligned(16))) uint8_t s_q8[DEC_LDS_Q8];
-  __shared__ float4 s_stage[DEC_WAVES][256];  // per-wave transpose of 4 act blocks
+  __shared__ float4 s_stage[DEC_WAVES][256];  // per wave: router scratch, then the act transpose
   constexpr bool kIQ2 = TG == T_IQ2_XXS || TD == T_IQ2_XXS || TS == T_IQ2_XXS;
   __shared__ uint64_t s_grid[kIQ2 ? 256 : 1];
   __shared__ uint64_t s_signs[kIQ2 ? 128 : 1];
-  static_assert(ITS == 0 || TS != 0, "shared iterations need a shared type");
-  constexpr int NS = ITS > 0 ? ITS : 1;
+  static_assert(IS == 0 || TS != 0, "shared iterations need a shared type");
+  static_assert(L1 == 16 || L1 == 32, "lanes per routed gate/up row");
+  constexpr int L2 = 32;  // lanes per down row (2 rows per wave step)
+  constexpr int NS = IS > 0 ? IS : 1;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
-  const int q4 = lane & 3;  // quarter of a super-block this lane handles (every unit count is a multiple of 4)
   const int G = gridDim.x, g = blockIdx.x;
   const int S = a.S, K = a.K, H = a.H, F = a.F;
-  const size_t q8x = q8_row_bytes(a.nbH);
-  const size_t q8F = q8_row_bytes(a.nbF);
-  const size_t q8Fs = a.Fs > 0 ? q8_row_bytes(a.nbFs) : 0;
+  const size_t q8x = q8l_row_bytes(a.nbH);
+  const size_t q8F = q8l_row_bytes(a.nbF);
+  const size_t q8Fs = a.Fs > 0 ? q8l_row_bytes(a.nbFs) : 0;
   ZM_TRACE(0);
+  // arrival-counter set of this call; workgroup 0 clears the other set
+  const uint32_t epoch = __builtin_amdgcn_readfirstlane(ld_co(&a.sync[0]));
+  uint32_t *const cnt = a.sync + DEC_CNT_STRIDE * (1 + DEC_NCNT * (int)(epoch & 1u));
+  if (g == 0 && tid < DEC_NCNT) st_co(a.sync + DEC_CNT_STRIDE * (1 + DEC_NCNT * (int)((epoch + 1u) & 1u) + tid), 0u);
 
   // ---------------------------------------------------------------- P0: route, quantize x
   // Wave w < S routes token w (its loads go out first); the other waves
@@ -118,24 +154,8 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   const int nxb = S * a.nbH;
   const int l16 = lane & 15;
   const int wi = wave >= S ? wave - S : wave + DEC_WAVES - S;  // x-quant worker index
-  float xv[16];
-  auto load_x = [&](int grp) {
-    const int bb = grp * 4 + (lane >> 4);
-    if (bb < nxb) {
-      const int s = bb / a.nbH, b = bb % a.nbH;
-      const float4 *src = reinterpret_cast<const float4 *>(a.x + (size_t)s * H + (size_t)b * QK + 16 * l16);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float4 f = src[i];
-        xv[4 * i] = f.x;
-        xv[4 * i + 1] = f.y;
-        xv[4 * i + 2] = f.z;
-        xv[4 * i + 3] = f.w;
-      }
-    }
-  };
   if (wave < S) {
-    const WaveRoute r = route_token(a.r, wave, reinterpret_cast<float *>(s_stage[wave]));
+    const WaveRoute r = route_token<8>(a.r, wave, reinterpret_cast<float *>(s_stage[wave]));
     if (lane < K) {
       s_ids[wave * K + lane] = r.id;
       s_w[wave * K + lane] = r.w;
@@ -151,11 +171,20 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   }
   ZM_TRACE(6);
   for (int grp = wi; grp * 4 < nxb; grp += DEC_WAVES) {
-    load_x(grp);
     const int bb = grp * 4 + (lane >> 4);
     if (bb < nxb) {
       const int s = bb / a.nbH, b = bb % a.nbH;
-      store_q8_16(s_q8 + (size_t)s * q8x, a.nbH, b, quant_block16(xv, l16), l16);
+      const float4 *src = reinterpret_cast<const float4 *>(a.x + (size_t)s * H + (size_t)b * QK + 16 * l16);
+      float xv[16];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 f = src[i];
+        xv[4 * i] = f.x;
+        xv[4 * i + 1] = f.y;
+        xv[4 * i + 2] = f.z;
+        xv[4 * i + 3] = f.w;
+      }
+      store_q8_16l(s_q8 + (size_t)s * q8x, a.nbH, b, quant_block16(xv, l16), l16);
     }
   }
   ZM_TRACE(7);
@@ -188,185 +217,162 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   const int T1 = T1r + S * a.Fs;
 
   // ---------------------------------------------------------------- P2 set-up: down rows
-  // Lane unit v = lane + 64*it of a down row: the ITR routed iterations cover
-  // K*U2 quarters (route v / U2, quarter v % U2), the ITS shared iterations the
-  // shared expert's U2s quarters.  Lane offsets depend on the token only.  The
-  // first rows of every wave are requested now, before any gate/up work.
+  // 16 lanes per down row, 4 rows per wave step; step st of this wave covers
+  // rows u0 + 4*(wave + DEC_WAVES*st) + (lane >> 4).  Lane li = lane & 15 takes
+  // units li + 16*it of the row: IR routed iterations over K*nbF*upb(TD) units
+  // (route, block, part), IS shared iterations over nbFs*upb(TS) units.  The
+  // first step of every wave is requested now, before any gate/up work.
+  const int li2 = lane % L2, rg2 = lane / L2;
   const int T2 = S * H;
   const int u0 = (int)((long)T2 * g / G), u1 = (int)((long)T2 * (g + 1) / G);
+  const int nst2_all = (u1 - u0 + (64 / L2) - 1) / (64 / L2);
+  const int nst2 = nst2_all > wave ? (nst2_all - wave + DEC_WAVES - 1) / DEC_WAVES : 0;
   const float invH = 1.0f / (float)H;
-  const int U2 = 4 * a.nbF, U2s = 4 * a.nbFs;
+  constexpr int UPD = unit_per_block<TD>();
+  constexpr int UPS = TS ? unit_per_block<TS>() : 1;
   constexpr int BD = block_bytes(TD);
   constexpr int BSD = TS ? block_bytes(TS) : 1;
+  const int URd = K * a.nbF * UPD, URb = a.nbF * UPD, USd = a.nbFs * UPS;
   const rsrc_t rd = make_rsrc(a.wd, a.wd_bytes), rsd = make_rsrc(a.sd, a.sd_bytes);
-  int vo_r[ITR], vo_s[NS];
-  int vo_tok = -1;
-  auto lane_offsets = [&](int s) {
-#pragma unroll
-    for (int it = 0; it < ITR; ++it) {
-      const int v = lane + 64 * it;
-      const int k = v / U2, u = v - k * U2;
-      const int e = s_ids[s * K + min(k, K - 1)];
-      vo_r[it] = (k < K && e >= 0) ? e * (int)a.d_estride + (u >> 2) * BD : OOR;
-    }
-#pragma unroll
-    for (int it = 0; it < ITS; ++it) {
-      const int u = lane + 64 * it;
-      vo_s[it] = u < U2s ? (u >> 2) * BSD : OOR;
-    }
-    vo_tok = s;
+  const rsrc_t rout = make_rsrc(a.out, (uint32_t)T2 * 4u);
+  // row of step st for this lane -> (valid, token, row h); invalid rows map to a valid one
+  auto row2 = [&](int st, bool &valid, int &s, int &h) {
+    const int j = u0 + (64 / L2) * (wave + DEC_WAVES * st) + rg2;
+    valid = st < nst2 && j < u1;
+    divmod24(valid ? j : min(u0, T2 - 1), H, invH, s, h);
   };
-  auto load_row = [&](int j, WSlice(&wr)[ITR], WSlice(&ws)[NS]) {
+  auto load_step2 = [&](int st, Unit<TD> (&wr)[IR], Unit<TS ? TS : TD> (&ws)[NS]) {
+    bool valid;
     int s, h;
-    divmod24(j, H, invH, s, h);
-    s = uniform(s);
-    h = uniform(h);
-    if (s != vo_tok) lane_offsets(s);
-    const int so = uniform(h * (int)a.d_rstride);
+    row2(st, valid, s, h);
 #pragma unroll
-    for (int it = 0; it < ITR; ++it) load_w_slice_b<TD>(rd, vo_r[it], so, q4, wr[it]);
-    if constexpr (ITS > 0) {
-      const int sos = uniform(h * (int)a.sd_rstride);
+    for (int it = 0; it < IR; ++it) {
+      const int u = li2 + L2 * it;
+      const int k = u / URb, rem = u - k * URb;
+      const int e = s_ids[s * K + min(k, K - 1)];
+      const bool ok = valid && u < URd && e >= 0;
+      load_unit<TD>(rd, ok ? e * (int)a.d_estride + h * (int)a.d_rstride + (rem / UPD) * BD : OOR, rem % UPD, wr[it]);
+    }
+    if constexpr (IS > 0) {
 #pragma unroll
-      for (int it = 0; it < ITS; ++it) load_w_slice_b<TS>(rsd, vo_s[it], sos, q4, ws[it]);
+      for (int it = 0; it < IS; ++it) {
+        const int u = li2 + L2 * it;
+        const bool ok = valid && u < USd;
+        load_unit<TS>(rsd, ok ? h * (int)a.sd_rstride + (u / UPS) * BSD : OOR, u % UPS, ws[it]);
+      }
     }
   };
-  // two rows in flight when they fit in registers, else one
-  constexpr bool P2DB = ITR + ITS <= 3;
-  WSlice c0r[ITR], c0s[NS];
-  WSlice c1r[P2DB ? ITR : 1], c1s[P2DB ? NS : 1];
-  const int jw = u0 + wave;
-  if (jw < u1) load_row(jw, c0r, c0s);
-  if constexpr (P2DB)
-    if (jw + DEC_WAVES < u1) load_row(jw + DEC_WAVES, c1r, c1s);
+  Unit<TD> c2r[IR];
+  Unit<TS ? TS : TD> c2s[NS];
+  load_step2(0, c2r, c2s);
   __builtin_amdgcn_sched_barrier(0);
 
   // ---------------------------------------------------------------- P1: gate/up rows
-  // Row i of this wave is j = t0 + wave + DEC_WAVES*i.  Rows go in batches of RB
-  // with two register buffers: batch b+1 is in flight while batch b computes.
+  // Rows [t0, t1) of this workgroup: routed rows (route c, row n) first, then
+  // the shared expert's rows (token, row n).  L lanes per row (L1 for routed
+  // rows, 64 for shared rows), 64/L rows per wave step; lane li = lane % L
+  // takes unit li of the row (one super-block,
+  // or half of one for Q4_K).  Steps go through two register buffers: step
+  // st+1 is in flight while step st computes.
   const int t0 = (int)((long)T1 * g / G), t1 = (int)((long)T1 * (g + 1) / G);
-  const int U1 = 4 * a.nbH;
-  const float invF = 1.0f / (float)F, invFs = a.Fs > 0 ? 1.0f / (float)a.Fs : 0.f;
+  const rsrc_t ract = make_rsrc(a.act, (uint32_t)T1 * 4u);
   {
-    constexpr int BG = block_bytes(TG);
-    constexpr int BS = TS ? block_bytes(TS) : 1;
-    constexpr int SLICE_DW = TG == T_Q2_K ? 7 : (TG == T_Q4_K ? 12 : (TG == T_IQ2_XXS ? 5 : 12));
-    constexpr int RB0 = 80 / (2 * 2 * SLICE_DW * IT1);
-    constexpr int RB = RB0 < 1 ? 1 : (RB0 > 4 ? 4 : RB0);
-    const int nrw = t1 - t0 > wave ? (t1 - t0 - wave + DEC_WAVES - 1) / DEC_WAVES : 0;
-    const rsrc_t rg = make_rsrc(a.wg, a.wg_bytes), ru = make_rsrc(a.wu, a.wg_bytes);
-    const rsrc_t rsg = make_rsrc(a.sg, a.sg_bytes), rsu = make_rsrc(a.su, a.sg_bytes);
-    // lane offsets inside a row (routed / shared block sizes; OOR past the row)
-    // and the activation block (clamped: idle lanes read real, finite data)
-    int vo1[IT1], vo1s[IT1], xb1[IT1];
-#pragma unroll
-    for (int it = 0; it < IT1; ++it) {
-      const int u = lane + 64 * it;
-      vo1[it] = u < U1 ? (u >> 2) * BG : OOR;
-      vo1s[it] = u < U1 ? (u >> 2) * BS : OOR;
-      xb1[it] = min(u >> 2, a.nbH - 1);
-    }
-    auto issue = [&](int i0, WSlice(&bg)[RB][IT1], WSlice(&bu)[RB][IT1]) {
-#pragma unroll
-      for (int r = 0; r < RB; ++r) {
-        const int i = i0 + r;
-        if (i >= nrw) break;
-        const int j = t0 + wave + DEC_WAVES * i;
-        if (j < T1r) {
-          int c, n;
-          divmod24(j, F, invF, c, n);
-          const int e = uniform(s_ids[s_vp[uniform(c)]]);
-          const int so = uniform(e * (int)a.g_estride + uniform(n) * (int)a.g_rstride);
-#pragma unroll
-          for (int it = 0; it < IT1; ++it) {
-            load_w_slice_b<TG>(rg, vo1[it], so, q4, bg[r][it]);
-            load_w_slice_b<TG>(ru, vo1[it], so, q4, bu[r][it]);
-          }
-        } else if constexpr (TS != 0) {
-          int ts_, n;
-          divmod24(j - T1r, a.Fs, invFs, ts_, n);
-          const int so = uniform(uniform(n) * (int)a.sg_rstride);
-#pragma unroll
-          for (int it = 0; it < IT1; ++it) {
-            load_w_slice_b<TS>(rsg, vo1s[it], so, q4, bg[r][it]);
-            load_w_slice_b<TS>(rsu, vo1s[it], so, q4, bu[r][it]);
-          }
+    const float invF = 1.0f / (float)F, invFs = a.Fs > 0 ? 1.0f / (float)a.Fs : 0.f;
+    auto stream_rows = [&](auto ttag, int r0, int r1) {
+      constexpr int TT = decltype(ttag)::value;
+      constexpr bool SH = decltype(ttag)::shared;
+      constexpr int LL = decltype(ttag)::lanes;
+      constexpr int R1 = 64 / LL;
+      const int li1 = lane % LL, rg1 = lane / LL;
+      constexpr int UP = unit_per_block<TT>();
+      constexpr int BT = block_bytes(TT);
+      const int U1 = a.nbH * UP;
+      const rsrc_t rgt = SH ? make_rsrc(a.sg, a.sg_bytes) : make_rsrc(a.wg, a.wg_bytes);
+      const rsrc_t rut = SH ? make_rsrc(a.su, a.sg_bytes) : make_rsrc(a.wu, a.wg_bytes);
+      const bool uok = li1 < U1;
+      const int blk = min(li1 / UP, a.nbH - 1), part = li1 % UP;
+      const int nst_all = (r1 - r0 + R1 - 1) / R1;
+      const int nst = nst_all > wave ? (nst_all - wave + DEC_WAVES - 1) / DEC_WAVES : 0;
+      // step st -> this lane's (valid, row j, token, weight-row byte offset)
+      auto row1 = [&](int st, bool &valid, int &j, int &tok, int &roff) {
+        j = r0 + R1 * (wave + DEC_WAVES * st) + rg1;
+        valid = st < nst && j < r1;
+        j = valid ? j : r0;
+        int q, n;
+        if constexpr (SH) {
+          divmod24(j - T1r, a.Fs, invFs, q, n);
+          tok = q;
+          roff = n * (int)a.sg_rstride;
+        } else {
+          divmod24(j, F, invF, q, n);
+          const int p = s_vp[q];
+          tok = p / K;
+          roff = s_ids[p] * (int)a.g_estride + n * (int)a.g_rstride;
         }
-      }
-    };
-    // the token's activation slices stay in registers while the token does not change
-    Q8Slice xsc[IT1];
-    int xs_key = -1;
-    auto compute = [&](int i0, WSlice(&bg)[RB][IT1], WSlice(&bu)[RB][IT1]) {
-#pragma unroll
-      for (int r = 0; r < RB; ++r) {
-        const int i = i0 + r;
-        if (i >= nrw) break;
-        const int j = t0 + wave + DEC_WAVES * i;
-        const bool shared_row = j >= T1r;
-        int q_, r_;
-        divmod24(shared_row ? j - T1r : j, shared_row ? a.Fs : F, shared_row ? invFs : invF, q_, r_);
-        const int tok = uniform(shared_row ? q_ : s_vp[q_] / K);
-        const int key = shared_row ? tok + DEC_MAX_S : tok;
-        if (key != xs_key) {
-          xs_key = key;
-          const uint8_t *xrow = s_q8 + (size_t)tok * q8x;
-#pragma unroll
-          for (int it = 0; it < IT1; ++it) {
-            if (!shared_row)
-              load_q8_slice<TG>(xrow, a.nbH, xb1[it], q4, xsc[it]);
-            else if constexpr (TS != 0)
-              load_q8_slice<TS>(xrow, a.nbH, xb1[it], q4, xsc[it]);
-          }
+      };
+      // a step's row (valid, j, token) is worked out once, when its loads are issued
+      struct RowInfo {
+        bool valid;
+        int j, tok;
+      };
+      auto issue = [&](int st, Unit<TT> (&bw)[2], RowInfo &ri) {
+        int roff;
+        row1(st, ri.valid, ri.j, ri.tok, roff);
+        const int vo = (ri.valid && uok) ? roff + blk * BT : OOR;
+        load_unit<TT>(rgt, vo, part, bw[0]);
+        load_unit<TT>(rut, vo, part, bw[1]);
+      };
+      auto compute = [&](const Unit<TT> (&bw)[2], const RowInfo &ri) {
+        const bool valid = ri.valid;
+        const int j = ri.j, tok = ri.tok;
+        float o[2];
+#ifdef ZM_EXP_NOCOMPUTE_P1
+        {
+          const uint32_t* p0 = reinterpret_cast<const uint32_t*>(&bw[0]);
+          const uint32_t* p1 = reinterpret_cast<const uint32_t*>(&bw[1]);
+          uint32_t h0 = 0, h1 = 0;
+          for (int i = 0; i < (int)(sizeof(Unit<TT>) / 4); ++i) { h0 ^= p0[i]; h1 ^= p1[i]; }
+          o[0] = (float)(h0 & 0xff) * 1e-9f; o[1] = (float)(h1 & 0xff) * 1e-9f;
         }
-        float ag = 0.f, au = 0.f;
-        if (!shared_row) {
-#pragma unroll
-          for (int it = 0; it < IT1; ++it) {
-            ag += quarter_dot<TG>(bg[r][it], q4, xsc[it], s_grid, s_signs);
-            au += quarter_dot<TG>(bu[r][it], q4, xsc[it], s_grid, s_signs);
-          }
-        } else if constexpr (TS != 0) {
-#pragma unroll
-          for (int it = 0; it < IT1; ++it) {
-            ag += quarter_dot<TS>(bg[r][it], q4, xsc[it], s_grid, s_signs);
-            au += quarter_dot<TS>(bu[r][it], q4, xsc[it], s_grid, s_signs);
-          }
-        }
-        ag = group_sum<64>(ag);
-        au = group_sum<64>(au);
-        if (lane == 0) st_co(a.act + j, silu_f32(ag) * au);
-      }
-    };
-    // sched_barrier keeps every load of a batch ahead of the math that waits on
-    // the previous one (vmcnt is in order: an interleaved wait drains the queue)
-    WSlice g0[RB][IT1], v0[RB][IT1], g1[RB][IT1], v1[RB][IT1];
-    if (nrw > 0) issue(0, g0, v0);
-    for (int i0 = 0; i0 < nrw; i0 += 2 * RB) {
-      if (i0 + RB < nrw) issue(i0 + RB, g1, v1);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(i0, g0, v0);
-      if (i0 + RB < nrw) {
-        if (i0 + 2 * RB < nrw) issue(i0 + 2 * RB, g0, v0);
+#else
+        unit_dots<TT, 2>(bw, part, xblk(s_q8 + (size_t)tok * q8x, a.nbH, blk), s_grid, s_signs, o);
+#endif
+        const float ag = group_sum<LL>(o[0]), au = group_sum<LL>(o[1]);
+        bst_co(ract, (li1 == 0 && valid) ? 4 * j : OOR, silu_f32(ag) * au);
+      };
+      // sched_barrier keeps every load of a step ahead of the math that waits
+      // on the previous one (vmcnt is in order: an interleaved wait drains the
+      // queue); steps past the end load and store nothing
+      Unit<TT> A[2], B[2];
+      RowInfo ra, rb;
+      if (nst > 0) issue(0, A, ra);
+      for (int st = 0; st < nst; st += 2) {
+        issue(st + 1, B, rb);
         __builtin_amdgcn_sched_barrier(0);
-        compute(i0 + RB, g1, v1);
+        compute(A, ra);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(st + 2, A, ra);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(B, rb);
+        __builtin_amdgcn_sched_barrier(0);
       }
-    }
+    };
+    stream_rows(RowsTag<TG, false, L1>{}, t0, min(t1, T1r));
+    if constexpr (TS != 0) stream_rows(RowsTag<TS, true, 64>{}, max(t0, T1r), t1);
   }
   stores_done();
   __syncthreads();
   ZM_TRACE(2);
-  if (tid == 0 && t1 > t0) atomicAdd(&a.sync[DEC_CNT_STRIDE * (1 + g % DEC_NCNT)], (uint32_t)(t1 - t0));
+  if (tid == 0) atomicAdd(&cnt[DEC_CNT_STRIDE * (g % DEC_NCNT)], 1u);
 
   // ---------------------------------------------------------------- P2: wait, quantize act, down rows
   // lanes 0..15 of wave 0 poll one counter each and sum them
   if (wave == 0) {
-    const uint32_t target = (uint32_t)T1;
     int spins = 0;
     while (true) {
-      const int c = lane < DEC_NCNT ? (int)ld_co(&a.sync[DEC_CNT_STRIDE * (1 + lane)]) : 0;
-      const uint32_t total = (uint32_t)__builtin_amdgcn_readlane(group_sum_i<16>(c), 0);
-      if (total >= target) break;
+      const int c = lane < DEC_NCNT ? (int)ld_co(&cnt[DEC_CNT_STRIDE * lane]) : 0;
+      const int total = __builtin_amdgcn_readlane(group_sum_i<16>(c), 0);
+      if (total >= G) break;
       __builtin_amdgcn_s_sleep(1);
       if (++spins > a.spin_limit) {
         if (lane == 0) {
@@ -376,6 +382,9 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
         break;
       }
     }
+    // every workgroup has read the epoch once all have arrived; after an
+    // expired wait the epoch stays (the host resets the sync words)
+    if (g == 0 && lane == 0 && !s_err) st_co(&a.sync[0], epoch + 1u);
   }
   __syncthreads();
   after_wait();
@@ -389,8 +398,8 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   if (!s_err) {
     const int nb_tok = K * a.nbF + (a.Fs > 0 ? a.nbFs : 0);
     const int nb_all = (s_hi - s_lo + 1) * nb_tok;
-    // block bi -> act byte offset (OOR: skipped route or past the end), LDS row,
-    // blocks in that row, block index
+    // block bi -> act byte offset (OOR for a skipped route), LDS row, blocks in
+    // that row, block index
     auto info = [&](int bi, int &aoff, uint8_t *&row, int &nb, int &blk) {
       const int ts = bi / nb_tok, r = bi - ts * nb_tok;
       const int s = s_lo + ts;
@@ -413,7 +422,6 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     // stage to 16 lanes per block, then quant_block16.  QR rounds of loads are
     // in flight together.
     constexpr int QR = 3;
-    const rsrc_t ract = make_rsrc(a.act, (uint32_t)T1 * 4u);
     const int kq = lane >> 4;
     for (int base = wave * 4; base < nb_all; base += DEC_WAVES * 4 * QR) {
       float4 ld[QR][4];
@@ -453,7 +461,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
           int aoff, nb, blk;
           uint8_t *row;
           info(bi, aoff, row, nb, blk);
-          store_q8_16(row, nb, blk, quant_block16(xv16, l16), l16);  // a zero block for a skipped route
+          store_q8_16l(row, nb, blk, quant_block16(xv16, l16), l16);  // a zero block for a skipped route
         }
       }
     }
@@ -462,68 +470,42 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   ZM_TRACE(4);
 
   if (!s_err) {
-    int cur_s = -1;
-    Q8Slice qr[ITR], qsh[NS];
-    float wgt[ITR];
-    auto compute_row = [&](int j, WSlice(&cr)[ITR], WSlice(&cs)[NS]) {
+    for (int st = 0; st < nst2; ++st) {
+      bool valid;
       int s, h;
-      divmod24(j, H, invH, s, h);
-      s = uniform(s);
-      h = uniform(h);
-      if (s != cur_s) {
-        cur_s = s;
-        const uint8_t *tb = s_q8 + (size_t)(s - s_lo) * tok_bytes;
-#pragma unroll
-        for (int it = 0; it < ITR; ++it) {
-          const int v = lane + 64 * it;
-          const int kr = v / U2, u = v - kr * U2, k = min(kr, K - 1);
-          load_q8_slice<TD>(tb + (size_t)k * q8F, a.nbF, u >> 2, q4, qr[it]);
-          wgt[it] = kr < K ? s_w[s * K + k] : 0.0f;
-        }
-#pragma unroll
-        for (int it = 0; it < ITS; ++it) {
-          const int u = lane + 64 * it;
-          load_q8_slice<TS>(tb + (size_t)K * q8F, a.nbFs, min(u >> 2, a.nbFs - 1), q4, qsh[it]);
-        }
-      }
+      row2(st, valid, s, h);
+      const uint8_t *tb = s_q8 + (size_t)(s - s_lo) * tok_bytes;
       float acc = 0.f;
 #pragma unroll
-      for (int it = 0; it < ITR; ++it) acc += wgt[it] * quarter_dot<TD>(cr[it], q4, qr[it], s_grid, s_signs);
+      for (int it = 0; it < IR; ++it) {
+        const int u = li2 + L2 * it;
+        const int k = min(u / URb, K - 1), rem = u - (u / URb) * URb;
+        const float wk = u < URd ? s_w[s * K + k] : 0.0f;
+        float o[1];
+        const Unit<TD> one[1] = {c2r[it]};
+        unit_dots<TD, 1>(one, rem % UPD, xblk(tb + (size_t)k * q8F, a.nbF, min(rem / UPD, a.nbF - 1)), s_grid,
+                         s_signs, o);
+        acc += wk * o[0];
+      }
+      if constexpr (IS > 0) {
 #pragma unroll
-      for (int it = 0; it < ITS; ++it) acc += quarter_dot<TS>(cs[it], q4, qsh[it], s_grid, s_signs);
-      acc = group_sum<64>(acc);
-      if (lane == 0) a.out[(size_t)s * H + h] = acc;
-    };
-    if constexpr (P2DB) {
-      for (int j = jw; j < u1; j += 2 * DEC_WAVES) {
-        compute_row(j, c0r, c0s);
-        if (j + 2 * DEC_WAVES < u1) load_row(j + 2 * DEC_WAVES, c0r, c0s);
-        __builtin_amdgcn_sched_barrier(0);
-        if (j + DEC_WAVES < u1) {
-          compute_row(j + DEC_WAVES, c1r, c1s);
-          if (j + 3 * DEC_WAVES < u1) load_row(j + 3 * DEC_WAVES, c1r, c1s);
-          __builtin_amdgcn_sched_barrier(0);
+        for (int it = 0; it < IS; ++it) {
+          const int u = li2 + L2 * it;
+          float o[1];
+          const Unit<TS ? TS : TD> one[1] = {c2s[it]};
+          unit_dots<TS ? TS : TD, 1>(one, u % UPS, xblk(tb + (size_t)K * q8F, a.nbFs, min(u / UPS, a.nbFs - 1)),
+                                     s_grid, s_signs, o);
+          acc += o[0];
         }
       }
-    } else {
-      for (int j = jw; j < u1; j += DEC_WAVES) {
-        compute_row(j, c0r, c0s);
-        if (j + DEC_WAVES < u1) load_row(j + DEC_WAVES, c0r, c0s);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      acc = group_sum<L2>(acc);
+      bst(rout, (li2 == 0 && valid) ? 4 * (s * H + h) : OOR, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      load_step2(st + 1, c2r, c2s);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   ZM_TRACE(5);
-
-  // ---------------------------------------------------------------- exit: the last workgroup zeroes the sync words
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t old = atomicAdd(&a.sync[0], 1u);
-    if (old == (uint32_t)G - 1) {
-      for (int i = 0; i < DEC_NCNT; ++i) st_co(&a.sync[DEC_CNT_STRIDE * (1 + i)], 0u);
-      st_co(&a.sync[0], 0u);
-    }
-  }
 }
 
 #undef ZM_TRACE

@@ -187,12 +187,12 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 
 // ---------------------------------------------------------------- Q8_K activations (planar)
 //
-// Internal activation rows use a planar layout of the same 292 B/256 size as
-// ggml's block_q8_K: qs[nb*256] | d[nb] (f32) | bsums[nb*16] (i16), so one
-// lane's 64 int8 are four aligned 16-byte loads.
-__host__ __device__ constexpr size_t q8_row_bytes(int nb) { return (size_t)nb * 292; }
-__host__ __device__ constexpr size_t q8_d_off(int nb) { return (size_t)nb * 256; }
-__host__ __device__ constexpr size_t q8_bs_off(int nb) { return (size_t)nb * 260; }
+// Internal activation rows use a planar layout with the content of ggml's
+// block_q8_K (292 B per 256): qs[nb*256] | bsums[nb*16] (i16) | d[nb] (f32),
+// the row padded to 16 bytes, so every 16-byte read of qs or bsums is aligned.
+__host__ __device__ constexpr size_t q8_row_bytes(int nb) { return ((size_t)nb * 292 + 15) & ~(size_t)15; }
+__host__ __device__ constexpr size_t q8_bs_off(int nb) { return (size_t)nb * 256; }
+__host__ __device__ constexpr size_t q8_d_off(int nb) { return (size_t)nb * 288; }
 
 struct Q8Slice {
   uint4 q[4];    // 64 int8, in the order the weight quarter needs them

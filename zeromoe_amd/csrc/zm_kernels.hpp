@@ -311,13 +311,14 @@ __device__ __forceinline__ WaveRoute router_wave(const RouterArgs &a, int s, flo
   return WaveRoute{myid, w};
 }
 
-// E <= 64*P for the smallest P in {1, 2, 4, 8, 16}
+// E <= 64*P for the smallest P in {1, 2, 4, 8, 16}, P <= MAXP
+template <int MAXP>
 __device__ __forceinline__ WaveRoute route_token(const RouterArgs &a, int s, float *scr) {
   if (a.E <= 64) return router_wave<1>(a, s, scr);
   if (a.E <= 128) return router_wave<2>(a, s, scr);
-  if (a.E <= 256) return router_wave<4>(a, s, scr);
-  if (a.E <= 512) return router_wave<8>(a, s, scr);
-  return router_wave<16>(a, s, scr);
+  if (MAXP <= 2 || a.E <= 256) return router_wave<MAXP < 4 ? MAXP : 4>(a, s, scr);
+  if (MAXP <= 4 || a.E <= 512) return router_wave<MAXP < 8 ? MAXP : 8>(a, s, scr);
+  return router_wave<MAXP>(a, s, scr);
 }
 
 // one wave per token, 4 tokens per workgroup
@@ -326,7 +327,7 @@ __global__ __launch_bounds__(256) void k_router(RouterArgs a, int S) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int s = blockIdx.x * 4 + wave;
   if (s >= S) return;
-  const WaveRoute r = route_token(a, s, scr[wave]);
+  const WaveRoute r = route_token<16>(a, s, scr[wave]);
   if (lane < a.K) {
     a.ids[(size_t)s * a.K + lane] = r.id;
     a.weights[(size_t)s * a.K + lane] = r.w;
