@@ -157,13 +157,65 @@ class Built:
         return O.moe_forward(self.x, rid, w, c.tg, c.tg, c.td, Wg, Wu, Wd, shared=shared, nthreads=nthreads)
 
 
-def assert_close_layer(got: np.ndarray, ref: np.ndarray, rtol: float = 1e-3):
+    def requant_slack(self, ids, w, tie: float = 2e-4) -> np.ndarray:
+        """Per token: the largest output change that Q8_K rounding ties of the
+        routed activation (SwiGLU output, re-quantized before the down
+        projection) can cause.  An element whose scaled value x*iscale lies
+        within `tie` of a half-integer rounds either way under another valid
+        float summation order of the gate/up dots (ggml's own backends differ in
+        that order); flipping it moves the output by d_x * |W_down column| *
+        |route weight|.  The bound sums these over every tied element."""
+        c = self.c
+        used = sorted(set(int(v) for v in ids.reshape(-1) if v >= 0))
+        slack = np.zeros(c.S, np.float64)
+        if not used:
+            return slack
+        remap = {e: i for i, e in enumerate(used)}
+        rid = np.array([[remap.get(int(v), -1) for v in row] for row in ids], np.int32)
+        sel = torch.tensor(used, device="cuda")
+        Wg = self.wg.index_select(0, sel).cpu().numpy()
+        Wu = self.wu.index_select(0, sel).cpu().numpy()
+        Wd = self.wd.index_select(0, sel).cpu().numpy()
+        x = self.x[:, None, :]
+        g = O.mul_mat_id(c.tg, Wg, x, rid, nthreads=8)
+        u = O.mul_mat_id(c.tg, Wu, x, rid, nthreads=8)
+        act = O.swiglu(g, u).reshape(c.S, c.K, c.F // O.QK_K, O.QK_K).astype(np.float64)
+        # ggml quantize_row_q8_K: iscale = -127 / (value of largest magnitude)
+        idx = np.abs(act).argmax(-1)
+        mx = np.take_along_axis(act, idx[..., None], -1)
+        iscale = np.where(mx != 0, -127.0 / np.where(mx != 0, mx, 1.0), 0.0)
+        v = act * iscale
+        tied = np.abs(np.abs(v - np.floor(v)) - 0.5) < tie
+        dx = np.where(mx != 0, 1.0 / np.where(iscale != 0, iscale, 1.0), 0.0)  # per block d of the act row
+        wdabs = {}
+        for s, k in zip(*np.nonzero(tied.any(axis=(2, 3)))):
+            e = rid[s, k]
+            if e < 0:
+                continue
+            if e not in wdabs:
+                wdabs[e] = np.abs(O.dequantize(c.td, Wd[e], c.F))  # (H, F)
+            cols = np.nonzero(tied[s, k].reshape(-1))[0]
+            dcol = np.abs(dx[s, k, cols // O.QK_K, 0])
+            slack[s] += abs(float(w[s, k])) * (wdabs[e][:, cols] * dcol[None, :]).sum(1).max()
+        return slack
+
+
+def assert_close_layer(got: np.ndarray, ref: np.ndarray, rtol: float = 1e-3, slack=None):
     """Layer-output tolerance: per token, max |got - ref| <= rtol * max |ref|
     (the 1e-3 max relative error of the north star, taken against the token's
-    output scale so isolated near-zero outputs do not dominate)."""
+    output scale so isolated near-zero outputs do not dominate).  `slack`
+    (a callable returning a per-token bound, see Built.requant_slack) is
+    consulted only for tokens over the tolerance: their excess must be
+    explained by activation re-quantization ties."""
     assert got.shape == ref.shape
     assert np.isfinite(got).all()
+    bound = None
     for s in range(ref.shape[0]):
         scale = float(np.abs(ref[s]).max())
         err = float(np.abs(got[s] - ref[s]).max())
-        assert err <= rtol * max(scale, 1e-30), (s, err, scale)
+        if err <= rtol * max(scale, 1e-30):
+            continue
+        assert slack is not None, (s, err, scale)
+        if bound is None:
+            bound = slack()
+        assert err <= rtol * scale + bound[s], (s, err, scale, float(bound[s]))

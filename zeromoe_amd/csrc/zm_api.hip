@@ -13,6 +13,7 @@
 
 #include "../../include/zeromoe.h"
 #include "zm_decode.hpp"
+#include "zm_mmq.hpp"
 
 using namespace zm;
 
@@ -127,6 +128,12 @@ int launch_gemv_type(int np, int U, dim3 grid, const GemvArgs &a, hipStream_t st
   return launch_gemv_np<T, 1, GU>(U, grid, a, st);
 }
 
+// true when the environment variable is set to "0" (switches a path off for testing)
+bool getenv_flag_off(const char *name) {
+  const char *e = getenv(name);
+  return e && e[0] == '0';
+}
+
 bool type_supported(int t) { return t == T_Q2_K || t == T_Q3_K || t == T_Q4_K || t == T_IQ2_XXS; }
 
 size_t row_bytes(int t, int64_t n) { return (size_t)(n / QK) * block_bytes(t); }
@@ -163,6 +170,21 @@ int launch_gemv(int type, bool gateup, int np, const GemvArgs &a0, int n_groups,
   default: return fail("unsupported weight type %d", type);
   }
   if (rc) return rc;
+  HIP_OK(hipGetLastError());
+  return 0;
+}
+
+// MFMA path for prefill-sized buckets: Q4_K weights and, for routed experts,
+// at least 8 pairs per active expert on average.  Returns 1 when it does not
+// apply (the caller takes the GEMV path).
+int launch_mmq(int type, bool gateup, const GemvArgs &a, int n_groups, double avg_pairs, hipStream_t st) {
+  if (type != T_Q4_K || avg_pairs < 8.0 || getenv_flag_off("ZEROMOE_MMQ")) return 1;
+  if ((size_t)a.nrows * a.w_rstride >= (1ull << 31)) return 1;
+  const dim3 grid((unsigned)((a.nrows + 63) / 64), (unsigned)n_groups);
+  if (gateup)
+    hipLaunchKernelGGL(k_mmq_q4k<true>, grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(k_mmq_q4k<false>, grid, dim3(256), 0, st, a);
   HIP_OK(hipGetLastError());
   return 0;
 }
@@ -352,7 +374,10 @@ int zm_mul_mat_id(const zm_tensor *w, const zm_tensor *x, const zm_tensor *ids, 
   a.grid = d->grid;
   a.signs = d->signs;
   const int groups = (int)std::min<int64_t>(E, n_pairs);
-  if (launch_gemv(w->type, false, pick_np((int)n_pairs, (int)E), a, groups, st)) return 0;
+  {
+    const int rc = launch_mmq(w->type, false, a, groups, (double)n_pairs / groups, st);
+    if (rc < 0 || (rc > 0 && launch_gemv(w->type, false, pick_np((int)n_pairs, (int)E), a, groups, st))) return 0;
+  }
   g_mmid_launches.fetch_add(1, std::memory_order_relaxed);
   return hipPeekAtLastError() == hipSuccess ? 1 : 0;
 }
@@ -737,7 +762,11 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
   a.out_k = F;
   a.grid = d->grid;
   a.signs = d->signs;
-  if (launch_gemv(L->type_gate, true, np, a, groups, st)) return -1;
+  const double avg_pairs = (double)(S * K) / std::max(1, std::min(NS, S * K));
+  {
+    const int rc = launch_mmq(L->type_gate, true, a, groups, avg_pairs, st);
+    if (rc < 0 || (rc > 0 && launch_gemv(L->type_gate, true, np, a, groups, st))) return -1;
+  }
   // act -> Q8_K
   if (launch_quant(w.act, (size_t)F, nbF, S * K, w.aq, q8_row_bytes(nbF), 1, st)) return -1;
   // skipped routes read as zero rows
@@ -757,7 +786,10 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
   b.out = w.y;
   b.out_s = (size_t)K * H;
   b.out_k = H;
-  if (launch_gemv(L->type_down, false, np, b, groups, st)) return -1;
+  {
+    const int rc = launch_mmq(L->type_down, false, b, groups, avg_pairs, st);
+    if (rc < 0 || (rc > 0 && launch_gemv(L->type_down, false, np, b, groups, st))) return -1;
+  }
   // shared expert (dense over all tokens)
   const float *ys = nullptr;
   if (L->F_shared > 0) {
@@ -780,7 +812,10 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
     c.grid = d->grid;
     c.signs = d->signs;
     const int nps = S >= 4 ? 4 : (S >= 2 ? 2 : 1);
-    if (launch_gemv(L->type_shared, true, nps, c, 1, st)) return -1;
+    {
+      const int rc = launch_mmq(L->type_shared, true, c, 1, (double)S, st);
+      if (rc < 0 || (rc > 0 && launch_gemv(L->type_shared, true, nps, c, 1, st))) return -1;
+    }
     if (launch_quant(w.act_s, (size_t)Fs, nbS, S, w.aq_s, q8_row_bytes(nbS), 1, st)) return -1;
     GemvArgs e2 = c;
     e2.w0 = (const uint8_t *)L->ws_down;
@@ -792,7 +827,10 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
     e2.xq_rstride = q8_row_bytes(nbS);
     e2.out = w.y_s;
     e2.out_s = H;
-    if (launch_gemv(L->type_shared, false, nps, e2, 1, st)) return -1;
+    {
+      const int rc = launch_mmq(L->type_shared, false, e2, 1, (double)S, st);
+      if (rc < 0 || (rc > 0 && launch_gemv(L->type_shared, false, nps, e2, 1, st))) return -1;
+    }
     ys = w.y_s;
   }
   hipLaunchKernelGGL(k_combine, dim3((H + 255) / 256, S), dim3(256), 0, st, w.y, wts, ys, H, K, out);

@@ -44,8 +44,6 @@ constexpr int DEC_NCNT = 16;        // arrival counters per set (one 64-byte lin
 constexpr int DEC_CNT_STRIDE = 16;  // words between counters
 constexpr int DEC_SYNC_WORDS = DEC_CNT_STRIDE * (1 + 2 * DEC_NCNT);
 constexpr int DEC_MAX_E = 512;      // router experts handled in the fused kernel
-// lane offset past every buffer extent (all < 2^31): such a load returns zeros
-constexpr int OOR = (int)0x80000000u;
 
 struct DecodeArgs {
   RouterArgs r;  // logits, biases, slot table; r.ids / r.weights: optional global outputs

@@ -264,6 +264,9 @@ __device__ __forceinline__ void load_w_slice(const uint8_t *blk, int q, WSlice &
 // (SGPR, e.g. expert * expert_bytes + row * row_bytes).  Out-of-range reads
 // return zero instead of faulting.
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
+// lane offset past every buffer extent (all < 2^31): a load through it returns
+// zeros, a store through it is dropped
+constexpr int OOR = (int)0x80000000u;
 __device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
 }
