@@ -174,19 +174,26 @@ int launch_gemv(int type, bool gateup, int np, const GemvArgs &a0, int n_groups,
   return 0;
 }
 
-// MFMA path for prefill-sized buckets: Q4_K weights and, for routed experts,
-// at least 8 pairs per active expert on average.  Returns 1 when it does not
-// apply (the caller takes the GEMV path).
-int launch_mmq(int type, bool gateup, const GemvArgs &a, int n_groups, double avg_pairs, hipStream_t st) {
-  if (type != T_Q4_K || avg_pairs < 8.0 || getenv_flag_off("ZEROMOE_MMQ")) return 1;
-  if ((size_t)a.nrows * a.w_rstride >= (1ull << 31)) return 1;
-  const dim3 grid((unsigned)((a.nrows + 63) / 64), (unsigned)n_groups);
+// MFMA path for prefill-sized buckets: Q4_K weights and at least 8 pairs per
+// active expert on average.  a.items / a.n_items (or a.dense_S) must be set;
+// max_items bounds *a.n_items.  Returns 1 when the path does not apply (the
+// caller takes the GEMV path).
+bool mmq_applies(int type, double avg_pairs) {
+  return type == T_Q4_K && avg_pairs >= 8.0 && !getenv_flag_off("ZEROMOE_MMQ");
+}
+int launch_mmq(int type, bool gateup, const GemvArgs &a, int max_items, double avg_pairs, hipStream_t st) {
+  if (!mmq_applies(type, avg_pairs)) return 1;
+  if ((size_t)a.nrows * a.w_rstride >= (1ull << 31) || max_items <= 0) return 1;
+  const dim3 grid((unsigned)((a.nrows + 63) / 64), (unsigned)max_items);
   if (gateup)
     hipLaunchKernelGGL(k_mmq_q4k<true>, grid, dim3(256), 0, st, a);
   else
     hipLaunchKernelGGL(k_mmq_q4k<false>, grid, dim3(256), 0, st, a);
   HIP_OK(hipGetLastError());
   return 0;
+}
+int mmq_max_items(int n_pairs, int n_experts) {
+  return (n_pairs + MMQ_TOK - 1) / MMQ_TOK + std::min(n_pairs, n_experts);
 }
 
 int launch_quant(const float *x, size_t x_rstride, int nb, int rows, uint8_t *y, size_t y_rstride, int planar,
@@ -308,6 +315,8 @@ int zm_mul_mat_id(const zm_tensor *w, const zm_tensor *x, const zm_tensor *ids, 
   sz.take<int32_t>((size_t)n_pairs * 4);
   sz.take<int32_t>((size_t)E * 4);
   sz.take<int32_t>(4);
+  sz.take<int32_t>((size_t)mmq_max_items((int)n_pairs, (int)E) * 4);
+  sz.take<int32_t>(4);
   const size_t need = sz.off + 256;
   if (d->ws_size < need) {
     if (d->ws) (void)hipFree(d->ws);
@@ -327,6 +336,8 @@ int zm_mul_mat_id(const zm_tensor *w, const zm_tensor *x, const zm_tensor *ids, 
   int32_t *pairs = b.take<int32_t>((size_t)n_pairs * 4);
   int32_t *active = b.take<int32_t>((size_t)E * 4);
   int32_t *n_active = b.take<int32_t>(4);
+  int32_t *items = b.take<int32_t>((size_t)mmq_max_items((int)n_pairs, (int)E) * 4);
+  int32_t *n_items = b.take<int32_t>(4);
 
   // 1. quantize src1 rows (token t, row i11) -> planar Q8_K row t*ne11 + i11
   if (x->nb[2] == (size_t)ne11 * x->nb[1]) {
@@ -375,7 +386,14 @@ int zm_mul_mat_id(const zm_tensor *w, const zm_tensor *x, const zm_tensor *ids, 
   a.signs = d->signs;
   const int groups = (int)std::min<int64_t>(E, n_pairs);
   {
-    const int rc = launch_mmq(w->type, false, a, groups, (double)n_pairs / groups, st);
+    // the MFMA path addresses the activations through a 32-bit buffer offset
+    const double avg = (size_t)nq * q8_row_bytes(nb) < (1ull << 31) ? (double)n_pairs / groups : 0.0;
+    if (mmq_applies(w->type, avg))
+      hipLaunchKernelGGL(k_mmq_items, dim3(1), dim3(1024), 0, st, n_active, active, offs, items, n_items);
+    a.items = items;
+    a.n_items = n_items;
+    a.xq_bytes = (uint32_t)((size_t)nq * q8_row_bytes(nb));
+    const int rc = launch_mmq(w->type, false, a, mmq_max_items((int)n_pairs, (int)E), avg, st);
     if (rc < 0 || (rc > 0 && launch_gemv(w->type, false, pick_np((int)n_pairs, (int)E), a, groups, st))) return 0;
   }
   g_mmid_launches.fetch_add(1, std::memory_order_relaxed);
@@ -471,6 +489,7 @@ struct LayerWs {
   float *y_s;
   float *f_act;
   uint32_t *f_sync;
+  int32_t *items, *n_items;
 };
 
 size_t layer_ws(const zm_moe_layer *L, int S, uint8_t *base, LayerWs *w) {
@@ -487,6 +506,8 @@ size_t layer_ws(const zm_moe_layer *L, int S, uint8_t *base, LayerWs *w) {
   t.pairs = b.take<int32_t>((size_t)S * K * 4);
   t.active = b.take<int32_t>((size_t)NS * 4);
   t.n_active = b.take<int32_t>(4);
+  t.items = b.take<int32_t>((size_t)mmq_max_items(S * K, NS) * 4);
+  t.n_items = b.take<int32_t>(4);
   t.act = b.take<float>((size_t)S * K * F * 4);
   t.aq = b.take<uint8_t>((size_t)S * K * q8_row_bytes(nbF));
   t.y = b.take<float>((size_t)S * K * H * 4);
@@ -763,8 +784,14 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
   a.grid = d->grid;
   a.signs = d->signs;
   const double avg_pairs = (double)(S * K) / std::max(1, std::min(NS, S * K));
+  const int max_items = mmq_max_items(S * K, NS);
+  if (mmq_applies(L->type_gate, avg_pairs) || mmq_applies(L->type_down, avg_pairs))
+    hipLaunchKernelGGL(k_mmq_items, dim3(1), dim3(1024), 0, st, w.n_active, w.active, w.offs, w.items, w.n_items);
+  a.items = w.items;
+  a.n_items = w.n_items;
+  a.xq_bytes = (uint32_t)((size_t)S * q8_row_bytes(nbH));
   {
-    const int rc = launch_mmq(L->type_gate, true, a, groups, avg_pairs, st);
+    const int rc = launch_mmq(L->type_gate, true, a, max_items, avg_pairs, st);
     if (rc < 0 || (rc > 0 && launch_gemv(L->type_gate, true, np, a, groups, st))) return -1;
   }
   // act -> Q8_K
@@ -782,12 +809,13 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
   b.nb = nbF;
   b.xq = w.aq;
   b.xq_rstride = q8_row_bytes(nbF);
+  b.xq_bytes = (uint32_t)((size_t)S * K * q8_row_bytes(nbF));
   b.ne11 = K;
   b.out = w.y;
   b.out_s = (size_t)K * H;
   b.out_k = H;
   {
-    const int rc = launch_mmq(L->type_down, false, b, groups, avg_pairs, st);
+    const int rc = launch_mmq(L->type_down, false, b, max_items, avg_pairs, st);
     if (rc < 0 || (rc > 0 && launch_gemv(L->type_down, false, np, b, groups, st))) return -1;
   }
   // shared expert (dense over all tokens)
@@ -803,6 +831,7 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
     c.nb = nbH;
     c.xq = w.xq;
     c.xq_rstride = q8_row_bytes(nbH);
+    c.xq_bytes = (uint32_t)((size_t)S * q8_row_bytes(nbH));
     c.ne11 = 1;
     c.K = 1;
     c.dense_S = S;
@@ -813,7 +842,7 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
     c.signs = d->signs;
     const int nps = S >= 4 ? 4 : (S >= 2 ? 2 : 1);
     {
-      const int rc = launch_mmq(L->type_shared, true, c, 1, (double)S, st);
+      const int rc = launch_mmq(L->type_shared, true, c, (S + MMQ_TOK - 1) / MMQ_TOK, (double)S, st);
       if (rc < 0 || (rc > 0 && launch_gemv(L->type_shared, true, nps, c, 1, st))) return -1;
     }
     if (launch_quant(w.act_s, (size_t)Fs, nbS, S, w.aq_s, q8_row_bytes(nbS), 1, st)) return -1;
@@ -825,10 +854,11 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
     e2.nb = nbS;
     e2.xq = w.aq_s;
     e2.xq_rstride = q8_row_bytes(nbS);
+    e2.xq_bytes = (uint32_t)((size_t)S * q8_row_bytes(nbS));
     e2.out = w.y_s;
     e2.out_s = H;
     {
-      const int rc = launch_mmq(L->type_shared, false, e2, 1, (double)S, st);
+      const int rc = launch_mmq(L->type_shared, false, e2, (S + MMQ_TOK - 1) / MMQ_TOK, (double)S, st);
       if (rc < 0 || (rc > 0 && launch_gemv(L->type_shared, false, nps, e2, 1, st))) return -1;
     }
     ys = w.y_s;

@@ -518,6 +518,9 @@ struct GemvArgs {
   int tile_rows;
   const uint64_t *grid;   // IQ2_XXS tables (global), staged into LDS
   const uint64_t *signs;
+  // int8-MFMA path: (expert, first pair) work items of up to 32 pairs each
+  const int32_t *items, *n_items;
+  uint32_t xq_bytes;  // extent of the xq buffer
 };
 
 template <int T, int LPR, int ITER, int NP, bool GATEUP>

@@ -25,27 +25,69 @@ namespace zm {
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 typedef float v4f_t __attribute__((ext_vector_type(4)));
 
-constexpr int MMQ_TT = 4;  // 16-token tiles per pass over the weights
+constexpr int MMQ_TT = 2;              // 16-token tiles per work item
+constexpr int MMQ_TOK = 16 * MMQ_TT;   // pairs per work item
+constexpr int MMQ_XS = QK + 16;        // LDS stride of one token's qs (bank spread)
 
 __device__ __forceinline__ long u2l(uint2 v) { return (long)(((unsigned long)v.y << 32) | v.x); }
 
+// Work items: every active expert's bucket cut into runs of MMQ_TOK pairs,
+// item = expert | (first pair offset within the bucket) << 12.  One workgroup.
+__global__ __launch_bounds__(1024) void k_mmq_items(const int32_t *__restrict__ n_active,
+                                                    const int32_t *__restrict__ active,
+                                                    const int32_t *__restrict__ offs, int32_t *__restrict__ items,
+                                                    int32_t *__restrict__ n_items) {
+  __shared__ int s_n[1024];
+  const int na = *n_active;
+  int total = 0;
+  for (int base = 0; base < na; base += 1024) {
+    const int i = base + (int)threadIdx.x;
+    const int e = i < na ? active[i] : 0;
+    const int np = i < na ? (offs[e + 1] - offs[e] + MMQ_TOK - 1) / MMQ_TOK : 0;
+    s_n[threadIdx.x] = np;
+    __syncthreads();
+    for (int d = 1; d < 1024; d <<= 1) {  // inclusive scan
+      const int v = threadIdx.x >= (unsigned)d ? s_n[threadIdx.x - d] : 0;
+      __syncthreads();
+      s_n[threadIdx.x] += v;
+      __syncthreads();
+    }
+    const int start = total + s_n[threadIdx.x] - np;
+    for (int q = 0; q < np; ++q) items[start + q] = e | ((q * MMQ_TOK) << 12);
+    total += s_n[1023];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *n_items = total;
+}
+
+// One work item (up to MMQ_TOK pairs of one bucket) against 64 weight rows
+// (4 waves x 16 rows).  The activation block of the item is staged in LDS
+// (double buffered over the K blocks; each thread holds the next block's share
+// in registers while the current block computes); the weights of block b+1
+// are requested while block b computes.
 template <bool GATEUP>
 __global__ __launch_bounds__(256) void k_mmq_q4k(GemvArgs a) {
-  int e, p0, p1;
+  __shared__ __attribute__((aligned(16))) uint8_t s_xq[2][MMQ_TOK][MMQ_XS];
+  __shared__ int s_bs[2][MMQ_TOK][8];  // 32-weight bsums of the block
+  __shared__ float s_xd[2][MMQ_TOK];
+  __shared__ int s_xoff[MMQ_TOK];      // byte offset of each pair's activation row (OOR: none)
+  __shared__ int s_pair[MMQ_TOK];
+  int e, pc, p1;
   if (a.dense_S > 0) {
-    if (blockIdx.y > 0) return;
     e = 0;
-    p0 = 0;
+    pc = blockIdx.y * MMQ_TOK;
     p1 = a.dense_S;
+    if (pc >= p1) return;
   } else {
-    if ((int)blockIdx.y >= *a.n_active) return;
-    e = a.active[blockIdx.y];
-    p0 = a.offs[e];
+    if ((int)blockIdx.y >= *a.n_items) return;
+    const int it = a.items[blockIdx.y];
+    e = it & 0xfff;
+    pc = a.offs[e] + (it >> 12);
     p1 = a.offs[e + 1];
   }
   constexpr int NM = GATEUP ? 2 : 1;
   constexpr int BB = 144;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int row = blockIdx.x * 64 + wave * 16 + n;  // weight row of this lane (B operand, output column)
   const bool rv = row < a.nrows;
@@ -53,121 +95,146 @@ __global__ __launch_bounds__(256) void k_mmq_q4k(GemvArgs a) {
   rsrc_t rw[NM];
   rw[0] = make_rsrc(a.w0 + (size_t)e * a.w_estride, wbytes);
   if constexpr (GATEUP) rw[1] = make_rsrc(a.w1 + (size_t)e * a.w_estride, wbytes);
+  const rsrc_t rx = make_rsrc(a.xq, a.xq_bytes);
   const int vrow = rv ? row * (int)a.w_rstride : OOR;
   const int Kp = a.dense_S > 0 ? 1 : a.K;
+  const int nb = a.nb;
+  const int nt = min(MMQ_TT, (p1 - pc + 15) / 16);
 
-  for (int pc = p0; pc < p1; pc += 16 * MMQ_TT) {
-    const int nt = min(MMQ_TT, (p1 - pc + 15) / 16);
-    // x row of this lane's A token (pair pc + 16t + n) and of its four output
-    // tokens (pairs pc + 16t + 4g + j), per tile
-    const uint8_t *xa[MMQ_TT];
-    bool va[MMQ_TT];
-    const uint8_t *xo[MMQ_TT][4];
-    int po[MMQ_TT][4];
-#pragma unroll
-    for (int t = 0; t < MMQ_TT; ++t) {
-      auto xrow_of = [&](int p, bool &ok) {
-        ok = p < p1;
-        const int pair = a.dense_S > 0 ? (ok ? p : p0) : a.pairs[ok ? p : p0];
-        const int tok = pair / Kp, k = pair % Kp;
-        return a.xq + (size_t)(tok * a.ne11 + k % a.ne11) * a.xq_rstride;
-      };
-      xa[t] = xrow_of(pc + 16 * t + n, va[t]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        bool ok;
-        const int p = pc + 16 * t + 4 * g + j;
-        xo[t][j] = xrow_of(p, ok);
-        po[t][j] = ok ? (a.dense_S > 0 ? p : a.pairs[p]) : -1;
-      }
-    }
-    float f[NM][MMQ_TT][4];
-#pragma unroll
-    for (int m = 0; m < NM; ++m)
-#pragma unroll
-      for (int t = 0; t < MMQ_TT; ++t)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) f[m][t][j] = 0.f;
+  if (tid < MMQ_TOK) {
+    const int p = pc + tid;
+    const bool ok = p < p1;
+    const int pair = ok ? (a.dense_S > 0 ? p : a.pairs[p]) : -1;
+    s_pair[tid] = pair;
+    s_xoff[tid] = ok ? (int)(((pair / Kp) * a.ne11 + (pair % Kp) % a.ne11) * a.xq_rstride) : OOR;
+  }
+  __syncthreads();
 
-    for (int b = 0; b < a.nb; ++b) {
-      // weights of this lane's row, block b: header and the 8-byte qs chunks
-      // 32i + 8g (i = 0..3; low nibbles: sub-block 2i, high: 2i+1)
-      uint4 hdr[NM];
-      uint2 qs[NM][4];
+  struct WBlk {
+    uint4 hdr;
+    uint2 qs[4];
+  };
+  auto load_w = [&](int b, WBlk (&w)[NM]) {
+    const int vo = b < nb ? vrow + b * BB : OOR;
 #pragma unroll
-      for (int m = 0; m < NM; ++m) {
-        hdr[m] = bld16(rw[m], vrow + b * BB, 0);
+    for (int m = 0; m < NM; ++m) {
+      w[m].hdr = bld16(rw[m], vo, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) qs[m][i] = bld8(rw[m], vrow + b * BB + 16 + 32 * i + 8 * g, 0);
-      }
-      // activations of the pass: A fragments (x bytes 64i + 8g and 64i + 32 + 8g),
-      // 32-weight bsums of sub-blocks g and g + 4, d of the output tokens
-      uint2 xl[MMQ_TT][4], xh[MMQ_TT][4];
-      float bs_a[MMQ_TT][2], xd[MMQ_TT][4];
-      const int nb = a.nb;
-#pragma unroll
-      for (int t = 0; t < MMQ_TT; ++t) {
-        if (t < nt) {
-          const uint8_t *xq = xa[t] + (size_t)b * QK;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            xl[t][i] = va[t] ? ld8(xq + 64 * i + 8 * g) : make_uint2(0, 0);
-            xh[t][i] = va[t] ? ld8(xq + 64 * i + 32 + 8 * g) : make_uint2(0, 0);
-          }
-          const int16_t *bs = reinterpret_cast<const int16_t *>(xa[t] + q8_bs_off(nb)) + b * 16;
-          bs_a[t][0] = va[t] ? (float)(bs[2 * g] + bs[2 * g + 1]) : 0.f;
-          bs_a[t][1] = va[t] ? (float)(bs[2 * g + 8] + bs[2 * g + 9]) : 0.f;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) xd[t][j] = reinterpret_cast<const float *>(xo[t][j] + q8_d_off(nb))[b];
-        }
-      }
-#pragma unroll
-      for (int m = 0; m < NM; ++m) {
-        const uint32_t u0 = hdr[m].y, u1 = hdr[m].z, u2 = hdr[m].w;
-        const uint32_t sc_lo = u0 & 0x3f3f3f3fu, mn_lo = u1 & 0x3f3f3f3fu;
-        const uint32_t sc_hi = (u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4);
-        const uint32_t mn_hi = ((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4);
-        const float d = h2f((uint16_t)(hdr[m].x & 0xffffu)), dmin = h2f((uint16_t)(hdr[m].x >> 16));
-        // B operand of the min product: m[row][sb] for sb = g and g + 4
-        const float mb0 = (float)((mn_lo >> (8 * g)) & 0xffu), mb1 = (float)((mn_hi >> (8 * g)) & 0xffu);
-#pragma unroll
-        for (int t = 0; t < MMQ_TT; ++t) {
-          if (t >= nt) continue;
-          int isum[4] = {0, 0, 0, 0};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint2 q = qs[m][i];
-            const long wl = u2l(make_uint2(q.x & 0x0f0f0f0fu, q.y & 0x0f0f0f0fu));
-            const long wh = u2l(make_uint2((q.x >> 4) & 0x0f0f0f0fu, (q.y >> 4) & 0x0f0f0f0fu));
-            const v4i_t z = {0, 0, 0, 0};
-            const v4i_t dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(u2l(xl[t][i]), wl, z, 0, 0, 0);
-            const v4i_t dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(u2l(xh[t][i]), wh, z, 0, 0, 0);
-            const uint32_t scw = i < 2 ? sc_lo : sc_hi;
-            const int s0 = (int)((scw >> (16 * (i & 1))) & 0xffu), s1 = (int)((scw >> (16 * (i & 1) + 8)) & 0xffu);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) isum[j] += __mul24(s0, dl[j]) + __mul24(s1, dh[j]);
-          }
-          v4f_t mn = {0.f, 0.f, 0.f, 0.f};
-          mn = __builtin_amdgcn_mfma_f32_16x16x4f32(bs_a[t][0], mb0, mn, 0, 0, 0);
-          mn = __builtin_amdgcn_mfma_f32_16x16x4f32(bs_a[t][1], mb1, mn, 0, 0, 0);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) f[m][t][j] += xd[t][j] * (d * (float)isum[j] - dmin * mn[j]);
-        }
-      }
+      for (int i = 0; i < 4; ++i) w[m].qs[i] = bld8(rw[m], vo + 16 + 32 * i + 8 * g, 0);
     }
-    // lane holds (token pc + 16t + 4g + j, row): store out[tok][k][row]
-    if (rv) {
+  };
+  // this thread's share of an activation block: qs chunks c = tid, tid + 256
+  // (token c >> 4, 16-byte chunk c & 15), one 32-weight bsum (token tid >> 3,
+  // sub-block tid & 7), and d of token tid (tid < MMQ_TOK)
+  struct XShare {
+    uint4 q[MMQ_TOK * 16 / 256];
+    uint32_t bs;
+    float d;
+  };
+  static_assert(MMQ_TOK * 16 % 256 == 0 && MMQ_TOK * 8 <= 256, "staging shares");
+  auto load_x = [&](int b, XShare &x) {
+    const bool bv = b < nb;
+#pragma unroll
+    for (int r = 0; r < MMQ_TOK * 16 / 256; ++r) {
+      const int c = tid + 256 * r, t = c >> 4, ch = c & 15;
+      const int o = s_xoff[t];
+      x.q[r] = bld16(rx, (bv && o != OOR) ? o + b * QK + 16 * ch : OOR, 0);
+    }
+    {
+      const int t = (tid >> 3) & (MMQ_TOK - 1), sb = tid & 7;
+      const int o = s_xoff[t];
+      x.bs = __builtin_amdgcn_raw_buffer_load_b32(rx, (bv && o != OOR && tid < MMQ_TOK * 8) ? o + (int)q8_bs_off(nb) + b * 32 + 4 * sb : OOR, 0, 0);
+    }
+    {
+      const int o = s_xoff[tid & (MMQ_TOK - 1)];
+      x.d = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, (bv && o != OOR && tid < MMQ_TOK) ? o + (int)q8_d_off(nb) + 4 * b : OOR, 0, 0));
+    }
+  };
+  auto store_x = [&](const XShare &x, int buf) {
+#pragma unroll
+    for (int r = 0; r < MMQ_TOK * 16 / 256; ++r) {
+      const int c = tid + 256 * r, t = c >> 4, ch = c & 15;
+      *reinterpret_cast<uint4 *>(&s_xq[buf][t][16 * ch]) = x.q[r];
+    }
+    if (tid < MMQ_TOK * 8) s_bs[buf][tid >> 3][tid & 7] = (int)(int16_t)(x.bs & 0xffffu) + (int)(int16_t)(x.bs >> 16);
+    if (tid < MMQ_TOK) s_xd[buf][tid] = x.d;
+  };
+
+  float f[NM][MMQ_TT][4];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int t = 0; t < MMQ_TT; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) f[m][t][j] = 0.f;
+
+  WBlk wcur[NM], wnxt[NM];
+  XShare xs;
+  load_w(0, wcur);
+  load_x(0, xs);
+  store_x(xs, 0);
+  load_x(1, xs);
+  __syncthreads();
+  for (int b = 0; b < nb; ++b) {
+    const int buf = b & 1;
+    load_w(b + 1, wnxt);
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      const uint32_t u0 = wcur[m].hdr.y, u1 = wcur[m].hdr.z, u2 = wcur[m].hdr.w;
+      const uint32_t sc_lo = u0 & 0x3f3f3f3fu, mn_lo = u1 & 0x3f3f3f3fu;
+      const uint32_t sc_hi = (u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4);
+      const uint32_t mn_hi = ((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4);
+      const float d = h2f((uint16_t)(wcur[m].hdr.x & 0xffffu)), dmin = h2f((uint16_t)(wcur[m].hdr.x >> 16));
+      // B operand of the min product: m[row][sb] for sb = g and g + 4
+      const float mb0 = (float)((mn_lo >> (8 * g)) & 0xffu), mb1 = (float)((mn_hi >> (8 * g)) & 0xffu);
 #pragma unroll
       for (int t = 0; t < MMQ_TT; ++t) {
         if (t >= nt) continue;
+        const uint8_t *xr = &s_xq[buf][16 * t + n][0];
+        int isum[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int pair = po[t][j];
-          if (pair < 0) continue;
-          const int tok = pair / Kp, k = pair % Kp;
-          const float v = GATEUP ? silu_f32(f[0][t][j]) * f[NM - 1][t][j] : f[0][t][j];
-          a.out[(size_t)tok * a.out_s + (size_t)k * a.out_k + row] = v;
+        for (int i = 0; i < 4; ++i) {
+          const uint2 q = wcur[m].qs[i];
+          const long wl = u2l(make_uint2(q.x & 0x0f0f0f0fu, q.y & 0x0f0f0f0fu));
+          const long wh = u2l(make_uint2((q.x >> 4) & 0x0f0f0f0fu, (q.y >> 4) & 0x0f0f0f0fu));
+          const long xl = *reinterpret_cast<const long *>(xr + 64 * i + 8 * g);
+          const long xh = *reinterpret_cast<const long *>(xr + 64 * i + 32 + 8 * g);
+          const v4i_t z = {0, 0, 0, 0};
+          const v4i_t dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(xl, wl, z, 0, 0, 0);
+          const v4i_t dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(xh, wh, z, 0, 0, 0);
+          const uint32_t scw = i < 2 ? sc_lo : sc_hi;
+          const int s0 = (int)((scw >> (16 * (i & 1))) & 0xffu), s1 = (int)((scw >> (16 * (i & 1) + 8)) & 0xffu);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) isum[j] += __mul24(s0, dl[j]) + __mul24(s1, dh[j]);
         }
+        v4f_t mn = {0.f, 0.f, 0.f, 0.f};
+        mn = __builtin_amdgcn_mfma_f32_16x16x4f32((float)s_bs[buf][16 * t + n][g], mb0, mn, 0, 0, 0);
+        mn = __builtin_amdgcn_mfma_f32_16x16x4f32((float)s_bs[buf][16 * t + n][g + 4], mb1, mn, 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          f[m][t][j] += s_xd[buf][16 * t + 4 * g + j] * (d * (float)isum[j] - dmin * mn[j]);
+      }
+    }
+    // block b+1 into the other buffer (its readers finished at the last barrier),
+    // then request block b+2
+    store_x(xs, buf ^ 1);
+    load_x(b + 2, xs);
+#pragma unroll
+    for (int m = 0; m < NM; ++m) wcur[m] = wnxt[m];
+    __syncthreads();
+  }
+  // lane holds (pair pc + 16t + 4g + j, row): store out[tok][k][row]
+  if (rv) {
+#pragma unroll
+    for (int t = 0; t < MMQ_TT; ++t) {
+      if (t >= nt) continue;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int pair = s_pair[16 * t + 4 * g + j];
+        if (pair < 0) continue;
+        const int tok = pair / Kp, k = pair % Kp;
+        const float v = GATEUP ? silu_f32(f[0][t][j]) * f[NM - 1][t][j] : f[0][t][j];
+        a.out[(size_t)tok * a.out_s + (size_t)k * a.out_k + row] = v;
       }
     }
   }
