@@ -198,6 +198,42 @@ def time_launches(torch, step, first, n):
     return {"mean": e0.elapsed_time(e1) * 1e3 / n, "launches": n}
 
 
+def cpu_baseline(seconds: float = 10.0):
+    """CPU restatement of ggml's MUL_MAT_ID layer (oracle/zm_oracle.c) on this
+    host's cores at the c2 shape, S=1: ids re-drawn every iteration over a
+    32-expert pool (218 MB of weights, beyond the LLC)."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import zm_oracle as O
+
+    c = CONFIGS["c2"]
+    H, F, K = c["H"], c["F"], c["K"]
+    pool = 32
+    Wg = O.random_blocks(Q2, pool * F, H, seed=1).reshape(pool, F, -1)
+    Wu = O.random_blocks(Q2, pool * F, H, seed=2).reshape(pool, F, -1)
+    Wd = O.random_blocks(Q3, pool * H, F, seed=3).reshape(pool, H, -1)
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((1, H)).astype(np.float32)
+    threads = max(1, min(16, os.cpu_count() or 1))
+    w = np.full((1, K), 1.0 / K, np.float32)
+    O.moe_forward(x, rng.permutation(pool)[:K][None].astype(np.int32), w, Q2, Q2, Q3, Wg, Wu, Wd, nthreads=threads)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        ids = rng.permutation(pool)[:K][None].astype(np.int32)
+        O.moe_forward(x, ids, w, Q2, Q2, Q3, Wg, Wu, Wd, nthreads=threads)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and n >= 3:
+            break
+    us = el / n * 1e6
+    gbs = K * expert_bytes(c) / (us * 1e-6) / 1e9
+    return {"value": round(us, 1), "unit": "us/layer", "GBps": round(gbs, 2), "cores": threads, "kind": "port",
+            "sample": f"c2 layer S=1 (8 of a 32-expert pool per iteration), {n} iterations in {el:.1f} s, "
+                      f"OpenMP over output rows"}
+
+
+
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "k_moe_decode_c2_hbm_traffic.txt")
 COPY_PROBE_BYTES = 1 << 30
 
