@@ -796,8 +796,9 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
   }
   // act -> Q8_K
   if (launch_quant(w.act, (size_t)F, nbF, S * K, w.aq, q8_row_bytes(nbF), 1, st)) return -1;
-  // skipped routes read as zero rows
-  hipLaunchKernelGGL(k_fill_skipped, dim3((unsigned)std::min((H + 255) / 256, 64), (unsigned)(S * K)), dim3(256), 0,
+  // skipped routes (slot table -1) read as zero rows; router ids are always valid otherwise
+  if (L->route_map)
+    hipLaunchKernelGGL(k_fill_skipped, dim3((unsigned)std::min((H + 255) / 256, 64), (unsigned)(S * K)), dim3(256), 0,
                      st, ids, (size_t)K, (size_t)1, K, S, NS, H, w.y, (size_t)K * H, (size_t)H);
   // down
   GemvArgs b = a;
