@@ -159,6 +159,90 @@ int zm_moe_status(const zm_moe_layer *layer, int S, void *workspace, void *strea
 int zm_moe_forward(const zm_moe_layer *layer, const float *x, const float *logits, int S, float *out,
                    int32_t *ids_out, float *weights_out, void *workspace, size_t workspace_size, void *stream);
 
+/* ---------------------------------------------------------------- FP32-activation path
+ *
+ * Quantized weights times f32 activations, no Q8_K step: the reference's CUDA
+ * executor semantics, not ggml's CPU ones.  Weight rows are I/256 super-blocks
+ * (Q2_K / Q3_K / Q4_K / IQ2_XXS); x must be 16-byte aligned.  Accumulation is
+ * fp32 in a fixed order (deterministic; not the reference's order).  The void
+ * launchers keep the reference's signatures; a rejected call launches nothing
+ * and leaves the reason in zm_last_error(). */
+
+/* y[S][O] = x[S][I] . dequant(W[O][I])^T on the legacy default stream / on
+ * `stream`.  Replace launch_q2_K_matmul ... launch_iq2_xxs_matmul
+ * (backends/cuda/cuda_kernel_dispatcher.cpp:17-28; kernels/quant/kquant_matmul.cu:575-599,
+ * kernels/quant/iq2_matmul.cu:180-183) and the _stream variants. */
+void launch_q2_K_matmul(float *y, const float *x, const void *w, int S, int I, int O);
+void launch_q2_K_matmul_stream(float *y, const float *x, const void *w, int S, int I, int O, void *stream);
+void launch_q3_K_matmul(float *y, const float *x, const void *w, int S, int I, int O);
+void launch_q3_K_matmul_stream(float *y, const float *x, const void *w, int S, int I, int O, void *stream);
+void launch_q4_K_matmul(float *y, const float *x, const void *w, int S, int I, int O);
+void launch_q4_K_matmul_stream(float *y, const float *x, const void *w, int S, int I, int O, void *stream);
+void launch_iq2_xxs_matmul(float *y, const float *x, const void *w, int S, int I, int O);
+void launch_iq2_xxs_matmul_stream(float *y, const float *x, const void *w, int S, int I, int O, void *stream);
+/* The same by type id, returning 0 / -1.  Replaces CudaKernelDispatcher::matmul
+ * (backends/cuda/cuda_kernel_dispatcher.cpp:109-189) for these four types. */
+int zm_f32_matmul(int type, float *y, const float *x, const void *w, int S, int I, int O, void *stream);
+
+/* FP32 quant-matmul hook with the acceptance rules of native_f32_quant_hook
+ * (kernels/quant/kquant_matmul.cu:702-756), widened from Q2_K/Q3_K to the four
+ * types: MUL_MAT_ID (ids set; id < 0 -> 0 row, id >= ne2 -> NaN row), plain
+ * MUL_MAT (ids NULL, 2-D) and the grouped form (ids NULL, ne2 > 1: matrix g
+ * times x[:, :, g]).  Same conventions as zm_mul_mat_id (1 handled, 0
+ * declined; execute = 0 is a pure query); also counted by
+ * zm_mul_mat_id_launches. */
+int zm_mul_mat_id_f32(const zm_tensor *src0, const zm_tensor *src1, const zm_tensor *ids, zm_tensor *dst,
+                      void *stream, int execute);
+
+/* prod[i] = clamp(silu(gate) * up) (fused = 0) or silu(min(gate, c)) *
+ * clamp(up) (fused = 1), clamps applied when clamp > 0; d_bad (device, 2 x
+ * int, optional) += NaN count, Inf count of (gate, up).
+ * Replaces launch_expert_swiglu (kernels/math/expert_activation.cu:61-70). */
+void launch_expert_swiglu(float *prod, const float *gate, const float *up, int n, float clamp, int fused, int *d_bad,
+                          void *stream);
+/* dst[tok[i]][:] += w[i] * src[i][:] for i < n (w NULL: += src), rows with
+ * tok outside [0, S) skipped; the tok of one call must be distinct.
+ * Replace launch_expert_scatter_accum / launch_expert_scatter_add
+ * (kernels/math/expert_accum.cu:39-60). */
+void launch_expert_scatter_accum(const float *src, const int *tok, const float *w, float *dst, int n, int D, int S,
+                                 void *stream);
+void launch_expert_scatter_add(const float *src, const int *tok, float *dst, int n, int D, int S, void *stream);
+/* Router post-processing for S tokens: logits [S][E] overwritten with the
+ * gated probabilities (softmax 0 / sigmoid 1 / sqrt-softplus 2), the chosen
+ * ones then set to -FLT_MAX; ids/weights [S][K]: top-K of prob + bias (bias
+ * optional), ties to the lower index, weight = unbiased prob, optional
+ * normalisation 1/max(sum, 2^-14) and scale (when != 0).  E <= 4096, K <= 64.
+ * Replaces launch_glm5next_router_topk (kernels/models/glm5next_router.cu:95-105). */
+void launch_glm5next_router_topk(float *logits, const float *bias, int32_t *ids, float *weights, int S, int n_experts,
+                                 int topk, int gating_func, int normalize, float weight_scale, void *stream);
+
+/* Per-expert executor over one device slab laid out [gate | up | down]
+ * (up / down at byte offsets from the gate), f32 activations.
+ * Replaces GpuExpertScratch (memory/scratch_buffers.hpp:14-34) and
+ * expert_ffn_gpu_issue / _finish_stage1 / _finish_stage2
+ * (core/gpu_expert_executor.hpp:42-58, core/gpu_expert_executor.cpp:213-533).
+ * The caller owns the struct (zero-initialised before first use); ensure()
+ * grows its buffers monotonically; release() frees them. */
+typedef struct zm_expert_scratch {
+  int32_t *d_bad;   /* 2 counters: NaN, Inf seen by the SwiGLU */
+  float *d_x, *d_gate, *d_up, *d_prod, *d_down;
+  size_t cap_sd, cap_si; /* capacity in floats: S*D and S*F */
+  int32_t device_id;
+} zm_expert_scratch;
+int zm_expert_scratch_ensure(zm_expert_scratch *s, int S, int D, int F, int device);
+void zm_expert_scratch_release(zm_expert_scratch *s);
+/* x (host [S][D], uploaded on `stream`) or device_x (device [S][D]) ->
+ * d_gate, d_up [S][F] on the current device. */
+int zm_expert_ffn_issue(zm_expert_scratch *s, const void *slab, size_t up_offset, int gate_type, int up_type,
+                        const float *host_x, int S, int D, int F, const float *device_x, void *stream);
+/* d_prod = SwiGLU(d_gate, d_up) (counting non-finite inputs), d_down = d_prod . W_down^T. */
+int zm_expert_ffn_finish_stage1(zm_expert_scratch *s, const void *slab, size_t down_offset, int down_type, int S,
+                                int D, int F, float swiglu_clamp, int fused_clamp, void *stream);
+/* d_down -> host_out [S][D]; synchronises `stream`. */
+int zm_expert_ffn_finish_stage2(zm_expert_scratch *s, float *host_out, int S, int D, void *stream);
+/* Read (and optionally reset) the NaN / Inf counters. */
+int zm_expert_bad_counts(zm_expert_scratch *s, int32_t counts[2], int reset);
+
 /* Debug: copy the last decode launch's phase timestamps (8 per workgroup,
  * wall_clock64 ticks; recorded only when ZEROMOE_TRACE=1) into host[n].
  * Synchronises the device.  Returns the count copied. */

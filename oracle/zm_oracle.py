@@ -317,6 +317,109 @@ def router_gemv(W: np.ndarray, x: np.ndarray) -> np.ndarray:
     return out
 
 
+# ---------------------------------------------------------------- FP32-activation path (numpy)
+#
+# The reference's CUDA executor computes with f32 activations and no Q8_K
+# step.  These restatements define the results; the device kernels sum in a
+# different order, so parity is to a float tolerance.
+
+
+def f32_matmul(t: int, W: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """y[S, O] = x[S, I] . dequant(W[O])^T in float64
+    (kernels/quant/kquant_matmul.cu:575-599 launch_<type>_matmul; dequant per
+    kquant_matmul.cu:55-92,161-200, iq2_matmul.cu:73-91)."""
+    x = np.asarray(x, np.float32)
+    Wd = dequantize(t, np.ascontiguousarray(W, np.uint8), x.shape[-1]).astype(np.float64)
+    return x.astype(np.float64) @ Wd.T
+
+
+def f32_matmul_absbound(t: int, W: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """sum_i |w_oi x_si|: the scale of the float rounding of one output."""
+    Wd = dequantize(t, np.ascontiguousarray(W, np.uint8), x.shape[-1]).astype(np.float64)
+    return np.abs(np.asarray(x, np.float64)) @ np.abs(Wd).T
+
+
+def expert_swiglu(g: np.ndarray, u: np.ndarray, clamp: float = 0.0, fused: bool = False):
+    """launch_expert_swiglu (kernels/math/expert_activation.cu:31-59): returns
+    (prod f32, [n_nan, n_inf]) where a NaN in g or u counts as NaN, else an
+    Inf in either counts as Inf.  silu uses the oracle's exp (zmo_expf)."""
+    g = np.asarray(g, np.float32).ravel()
+    u = np.asarray(u, np.float32).ravel()
+    nan = np.isnan(g) | np.isnan(u)
+    inf = ~nan & (np.isinf(g) | np.isinf(u))
+    out = np.empty_like(g)
+    c = np.float32(clamp)
+    for i in range(g.size):
+        gi, ui = g[i], u[i]
+        with np.errstate(all="ignore"):
+            if fused:
+                if c > 0:
+                    gi = np.fmin(gi, c)
+                    ui = np.fmax(-c, np.fmin(c, ui))
+                out[i] = gi / (np.float32(1.0) + np.float32(expf(float(-gi)))) * ui
+            else:
+                o = gi / (np.float32(1.0) + np.float32(expf(float(-gi)))) * ui
+                if c > 0:
+                    o = np.fmax(-c, np.fmin(c, o))
+                out[i] = o
+    return out, [int(nan.sum()), int(inf.sum())]
+
+
+def scatter_accum(src: np.ndarray, tok: np.ndarray, dst: np.ndarray, w=None) -> np.ndarray:
+    """dst[tok[i]] += w[i] * src[i], tok outside [0, S) skipped
+    (kernels/math/expert_accum.cu:22-37; w None: expert_accum.cu:54-60)."""
+    dst = np.array(dst, np.float32, copy=True)
+    S = dst.shape[0]
+    for i, s in enumerate(np.asarray(tok)):
+        if 0 <= s < S:
+            wt = np.float32(1.0) if w is None else np.float32(w[i])
+            dst[s] = (np.float64(wt) * src[i].astype(np.float64) + dst[s]).astype(np.float32)
+    return dst
+
+
+def glm5next_router_topk(logits: np.ndarray, topk: int, bias=None, gating: int = GATING_SOFTMAX,
+                         normalize: bool = False, scale: float = 0.0):
+    """kernels/models/glm5next_router.cu:33-93, one token at a time: returns
+    (row, ids, weights) where row is what the kernel leaves in `logits` (the
+    gated probabilities, chosen ones replaced by -FLT_MAX)."""
+    L = np.array(logits, np.float32, copy=True)
+    S, E = L.shape
+    NEG = np.float32(-3.402823466e38)
+    ids = np.zeros((S, topk), np.int32)
+    ws = np.zeros((S, topk), np.float32)
+    b = None if bias is None else np.asarray(bias, np.float32)
+    for s in range(S):
+        row = L[s]
+        if gating == GATING_SOFTMAX:
+            mx = np.float32(np.nanmax(row)) if not np.all(np.isnan(row)) else np.float32(np.nan)
+            ex = np.array([expf(float(np.float32(v - mx))) for v in row], np.float32)
+            total_e = np.float32(0.0)
+            for v in ex:
+                total_e = np.float32(total_e + v)
+            row[:] = ex * (np.float32(1.0) / total_e)
+        elif gating == GATING_SIGMOID:
+            row[:] = [np.float32(1.0) / (np.float32(1.0) + np.float32(expf(float(-v)))) for v in row]
+        elif gating == GATING_SQRT_SOFTPLUS:
+            r64 = row.astype(np.float64)
+            row[:] = np.sqrt(np.where(r64 > 0, r64 + np.log1p(np.exp(-r64)), np.log1p(np.exp(r64))))
+        total = np.float32(0.0)
+        for k in range(topk):
+            best, best_score = -1, np.float32(0)
+            for e in range(E):
+                sc = np.float32(row[e] + (b[e] if b is not None else np.float32(0)))
+                if best < 0 or sc > best_score or (sc == best_score and e < best):
+                    best, best_score = e, sc
+            ids[s, k] = best
+            ws[s, k] = row[best]
+            row[best] = NEG
+            total = np.float32(total + ws[s, k])
+        if normalize:
+            ws[s] = ws[s] * (np.float32(1.0) / np.fmax(total, np.float32(6.103515625e-5)))
+        if scale != 0.0:
+            ws[s] = ws[s] * np.float32(scale)
+    return L, ids, ws
+
+
 # ---------------------------------------------------------------- reference build (oracle/_ref)
 
 _ref = None

@@ -12,7 +12,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 def header_symbols():
     txt = open(os.path.join(ROOT, "include", "zeromoe.h")).read()
     txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
-    return sorted(set(re.findall(r"\b(zm_[A-Za-z0-9_]+)\s*\(", txt)))
+    return sorted(set(re.findall(r"\b((?:zm|launch)_[A-Za-z0-9_]+)\s*\(", txt)))
 
 
 def test_library_exports_every_header_symbol():

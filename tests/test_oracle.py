@@ -425,3 +425,118 @@ def test_quantizer_round_trip(t, tol):
     y = O.dequantize(t, O.quantize(t, x), 1024)
     rel = np.sqrt(((x - y) ** 2).mean() / (x ** 2).mean())
     assert rel < tol, rel
+
+
+# ------------------------------------------------------------------ FP32-activation path restatements
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q2_K, O.TYPE_Q3_K, O.TYPE_Q4_K, O.TYPE_IQ2_XXS])
+def test_f32_matmul_equals_integer_dot_on_exact_activations(t):
+    """With x = q * 2^-7 (int8 q, |q| = 127 present in every block) the Q8_K
+    quantization is exact, so ggml's integer block dot (pinned by the
+    reference's golden vectors above) and the f32 dequant dot must agree to
+    float rounding: a wrong dequant plane, scale index or sign fails."""
+    rng = np.random.default_rng(31)
+    I, Orows, S = 1024, 6, 3
+    W = O.random_blocks(t, Orows, I, seed=5)
+    q = rng.integers(-127, 128, size=(S, I)).astype(np.float32)
+    q[:, ::256] = 127.0
+    x = q * np.float32(2.0 ** -7)
+    y = O.f32_matmul(t, W, x)
+    bound = O.f32_matmul_absbound(t, W, x)
+    for s in range(S):
+        xq = O.quantize_q8_K(x[s])
+        for o in range(Orows):
+            ref = O.vec_dot(t, W[o], xq)
+            assert abs(y[s, o] - ref) <= 2e-6 * bound[s, o] + 1e-30, (s, o, y[s, o], ref)
+
+
+def test_f32_matmul_is_linear_in_x():
+    W = O.random_blocks(O.TYPE_Q3_K, 4, 512, seed=2)
+    rng = np.random.default_rng(3)
+    a, b = rng.standard_normal((2, 512)).astype(np.float32)
+    ya, yb, yab = O.f32_matmul(O.TYPE_Q3_K, W, a), O.f32_matmul(O.TYPE_Q3_K, W, b), O.f32_matmul(O.TYPE_Q3_K, W, a + b)
+    np.testing.assert_allclose(yab, ya + yb, rtol=1e-6, atol=1e-6)
+
+
+def test_expert_swiglu_closed_forms():
+    g = np.array([0.0, 1.0, -1.0, 30.0, -30.0, 5.0, 2.0, np.nan, np.inf, 1.0], np.float32)
+    u = np.array([3.0, 0.0, 2.0, 1.0, 1.0, 5.0, -9.0, 1.0, 1.0, -np.inf], np.float32)
+    out, bad = O.expert_swiglu(g, u)
+    assert bad == [1, 2]
+    assert out[0] == 0.0 and out[1] == 0.0
+    np.testing.assert_allclose(out[2], -2.0 / (1.0 + np.e), rtol=1e-6)
+    np.testing.assert_allclose(out[3], 30.0, rtol=1e-6)  # silu(30) = 30 (to f32)
+    assert abs(out[4]) < 1e-11
+    # unclamped default == the layer oracle's SwiGLU, bit for bit
+    fin = np.isfinite(g) & np.isfinite(u)
+    np.testing.assert_array_equal(f32bits(out[fin]), f32bits(O.swiglu(g[fin], u[fin])))
+    # default clamp acts on the product; fused clamp on the inputs
+    oc, _ = O.expert_swiglu(g[:7], u[:7], clamp=7.0)
+    np.testing.assert_allclose(oc[5], 7.0)           # silu(5)*5 = 24.8 -> 7
+    np.testing.assert_allclose(oc[6], -7.0)          # silu(2)*(-9) = -15.9 -> -7
+    of, _ = O.expert_swiglu(g[:7], u[:7], clamp=4.0, fused=True)
+    np.testing.assert_allclose(of[5], 4.0 / (1.0 + np.exp(-4.0)) * 4.0, rtol=1e-6)  # min(g,4), clamp(u,4)
+    np.testing.assert_allclose(of[6], 2.0 / (1.0 + np.exp(-2.0)) * -4.0, rtol=1e-6)
+    # fused without a clamp is the plain SwiGLU
+    o0, _ = O.expert_swiglu(g[:7], u[:7], fused=True)
+    np.testing.assert_array_equal(f32bits(o0), f32bits(out[:7]))
+
+
+def test_scatter_accum_brute_force():
+    rng = np.random.default_rng(4)
+    n, D, S = 9, 33, 6
+    src = rng.standard_normal((n, D)).astype(np.float32)
+    tok = np.array([3, 0, 5, -1, 6, 1, 2, 4, 100], np.int32)  # -1, 6, 100: skipped
+    w = rng.random(n).astype(np.float32)
+    dst0 = rng.standard_normal((S, D)).astype(np.float32)
+    got = O.scatter_accum(src, tok, dst0, w)
+    want = dst0.astype(np.float64).copy()
+    for i in range(n):
+        if 0 <= tok[i] < S:
+            want[tok[i]] += float(w[i]) * src[i].astype(np.float64)
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6)
+    np.testing.assert_array_equal(got[[i for i in range(S) if i not in tok]], dst0[[i for i in range(S) if i not in tok]])
+    plain = O.scatter_accum(src, tok, dst0)
+    np.testing.assert_allclose(plain[3], dst0[3] + src[0], rtol=1e-6)
+
+
+@pytest.mark.parametrize("gating,bias,norm,scale", [(O.GATING_SOFTMAX, False, False, 0.0),
+                                                     (O.GATING_SOFTMAX, True, True, 0.0),
+                                                     (O.GATING_SIGMOID, True, True, 2.5),
+                                                     (O.GATING_SQRT_SOFTPLUS, False, True, 1.0)])
+def test_glm_router_matches_layer_router(gating, bias, norm, scale):
+    """Two independent restatements of the same router (glm5next_router.cu's
+    scan and moe_routed's select/gather, the latter pinned by brute force
+    above) must choose the same ids and weights."""
+    rng = np.random.default_rng(12)
+    S, E, K = 7, 96, 6
+    lg = rng.standard_normal((S, E)).astype(np.float32)
+    b = (rng.standard_normal(E) * 0.5).astype(np.float32) if bias else None
+    row, ids, w = O.glm5next_router_topk(lg, K, b, gating, norm, scale)
+    ri, rw = O.router(lg, K, gating, None, b, 0, 0, norm, scale)
+    np.testing.assert_array_equal(ids, ri)
+    np.testing.assert_allclose(w, rw, rtol=2e-6)
+    # the row left behind: probabilities with the chosen ones at -FLT_MAX
+    for s in range(S):
+        assert np.all(row[s, ids[s]] == np.float32(-3.402823466e38))
+        rest = np.delete(row[s], ids[s])
+        assert np.all((rest >= 0) & (rest <= 1.5 if gating != O.GATING_SOFTMAX else rest <= 1))
+    if gating == O.GATING_SOFTMAX:
+        p = row.copy()
+        for s in range(S):
+            p[s, ids[s]] = w[s] if not norm else 0
+        if not norm:
+            np.testing.assert_allclose(p.sum(1), 1.0, rtol=1e-5)
+
+
+def test_glm_router_ties_and_nan():
+    lg = np.zeros((1, 10), np.float32)
+    _, ids, w = O.glm5next_router_topk(lg, 4)
+    assert list(ids[0]) == [0, 1, 2, 3]  # equal scores: lower index first
+    lg = np.array([[np.nan, 5, 4, 3]], np.float32)
+    _, ids, _ = O.glm5next_router_topk(lg, 2, gating=O.GATING_SIGMOID)
+    assert list(ids[0]) == [0, 1]  # a NaN at expert 0 seeds the scan and is never displaced
+    lg = np.array([[1, np.nan, 4, 3]], np.float32)
+    _, ids, _ = O.glm5next_router_topk(lg, 3, gating=O.GATING_SIGMOID)
+    assert list(ids[0]) == [2, 3, 0]  # a NaN elsewhere is never chosen

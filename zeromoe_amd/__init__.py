@@ -11,13 +11,22 @@ libzeromoe_hip.so (include/zeromoe.h):
 * :func:`bucket` -- the per-expert CSR of core/batched_dispatch_pipeline.cpp:1181-1202.
 * :class:`MoELayer` -- one routed layer (expert_ffn + weighted sum_topk +
   shared expert, moe_routed_ggml.hpp:166-214, moe_block.hpp:86-105).
+* FP32-activation path of the CUDA executor: :func:`f32_matmul`
+  (launch_<type>_matmul, kernels/quant/kquant_matmul.cu:575-599),
+  :func:`mul_mat_id_f32` (native_f32_quant_hook, kquant_matmul.cu:702-756),
+  :func:`swiglu`, :func:`scatter_accum`, :func:`glm5next_router_topk`
+  (kernels/math/expert_activation.cu, expert_accum.cu,
+  kernels/models/glm5next_router.cu) and :class:`ExpertExecutor`
+  (core/gpu_expert_executor.hpp:42-58).
 
 Torch is used only for device memory and the current stream.
 """
 from __future__ import annotations
 
-from .ops import (GGML_TYPES, MoELayer, block_dots, bucket, init, mul_mat_id, quantize_q8_K, router, row_size,
-                  set_iq2xxs_grid, builtin_iq2xxs_grid)
+from .ops import (GGML_TYPES, ExpertExecutor, MoELayer, block_dots, bucket, builtin_iq2xxs_grid, f32_matmul,
+                  glm5next_router_topk, init, mul_mat_id, mul_mat_id_f32, quantize_q8_K, router, row_size,
+                  scatter_accum, set_iq2xxs_grid, swiglu)
 
-__all__ = ["GGML_TYPES", "MoELayer", "block_dots", "bucket", "init", "mul_mat_id", "quantize_q8_K", "router",
-           "row_size", "set_iq2xxs_grid", "builtin_iq2xxs_grid"]
+__all__ = ["GGML_TYPES", "ExpertExecutor", "MoELayer", "block_dots", "bucket", "builtin_iq2xxs_grid", "f32_matmul",
+           "glm5next_router_topk", "init", "mul_mat_id", "mul_mat_id_f32", "quantize_q8_K", "router", "row_size",
+           "scatter_accum", "set_iq2xxs_grid", "swiglu"]

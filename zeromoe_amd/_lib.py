@@ -32,6 +32,15 @@ class ZmMoeLayer(C.Structure):
                 ("F_shared", I32), ("type_shared", I32), ("ws_gate", P), ("ws_up", P), ("ws_down", P)]
 
 
+class ZmExpertScratch(C.Structure):
+    _fields_ = [("d_bad", P), ("d_x", P), ("d_gate", P), ("d_up", P), ("d_prod", P), ("d_down", P),
+                ("cap_sd", SZ), ("cap_si", SZ), ("device_id", I32)]
+
+
+_MM = (None, [P, P, P, I, I, I])
+_MMS = (None, [P, P, P, I, I, I, P])
+_XS = C.POINTER(ZmExpertScratch)
+
 # name -> (restype, argtypes); every function declared in include/zeromoe.h
 SIGNATURES = {
     "zm_init": (I, []),
@@ -50,6 +59,22 @@ SIGNATURES = {
     "zm_moe_workspace_size": (SZ, [C.POINTER(ZmMoeLayer), I]),
     "zm_moe_status": (I, [C.POINTER(ZmMoeLayer), I, P, P]),
     "zm_debug_trace": (I, [P, I]),
+    "launch_q2_K_matmul": _MM, "launch_q2_K_matmul_stream": _MMS,
+    "launch_q3_K_matmul": _MM, "launch_q3_K_matmul_stream": _MMS,
+    "launch_q4_K_matmul": _MM, "launch_q4_K_matmul_stream": _MMS,
+    "launch_iq2_xxs_matmul": _MM, "launch_iq2_xxs_matmul_stream": _MMS,
+    "zm_f32_matmul": (I, [I, P, P, P, I, I, I, P]),
+    "zm_mul_mat_id_f32": (I, [C.POINTER(ZmTensor)] * 3 + [C.POINTER(ZmTensor), P, I]),
+    "launch_expert_swiglu": (None, [P, P, P, I, F, I, P, P]),
+    "launch_expert_scatter_accum": (None, [P, P, P, P, I, I, I, P]),
+    "launch_expert_scatter_add": (None, [P, P, P, I, I, I, P]),
+    "launch_glm5next_router_topk": (None, [P, P, P, P, I, I, I, I, I, F, P]),
+    "zm_expert_scratch_ensure": (I, [_XS, I, I, I, I]),
+    "zm_expert_scratch_release": (None, [_XS]),
+    "zm_expert_ffn_issue": (I, [_XS, P, SZ, I, I, P, I, I, I, P, P]),
+    "zm_expert_ffn_finish_stage1": (I, [_XS, P, SZ, I, I, I, I, F, I, P]),
+    "zm_expert_ffn_finish_stage2": (I, [_XS, P, I, I, P]),
+    "zm_expert_bad_counts": (I, [_XS, P, I]),
     "zm_moe_forward": (I, [C.POINTER(ZmMoeLayer), P, P, I, P, P, P, P, SZ, P]),
 }
 

@@ -12,6 +12,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG_DIR)
 SRC = os.path.join(PKG_DIR, "csrc")
 OUT = os.path.join(PKG_DIR, "lib", "libzeromoe_hip.so")
+SOURCES = ("zm_api.hip", "zm_exec.hip")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # -ffp-contract=off: the quantizer, router and SwiGLU are bit-reproducible
@@ -23,7 +24,7 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-shared", "-std=c++17", "-ffp
 
 def build(verbose: bool = False) -> str:
     os.makedirs(os.path.dirname(OUT), exist_ok=True)
-    cmd = [HIPCC, *FLAGS, "-o", OUT, os.path.join(SRC, "zm_api.hip")]
+    cmd = [HIPCC, *FLAGS, "-o", OUT, *[os.path.join(SRC, f) for f in SOURCES]]
     r = subprocess.run(cmd, capture_output=True, text=True)
     msgs = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in l)
     if r.returncode != 0:

@@ -13,28 +13,26 @@
 
 #include "../../include/zeromoe.h"
 #include "zm_decode.hpp"
+#include "zm_host.hpp"
 #include "zm_mmq.hpp"
 
 using namespace zm;
 
 namespace {
-
 thread_local char g_err[512] = "";
 std::atomic<uint64_t> g_mmid_launches{0};
+}  // namespace
 
-int fail(const char *fmt, ...) {
+int zm::fail(const char *fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
   vsnprintf(g_err, sizeof(g_err), fmt, ap);
   va_end(ap);
   return -1;
 }
+void zm::count_mmid_launch() { g_mmid_launches.fetch_add(1, std::memory_order_relaxed); }
 
-#define HIP_OK(call)                                                                  \
-  do {                                                                                \
-    hipError_t e_ = (call);                                                           \
-    if (e_ != hipSuccess) return fail("%s: %s", #call, hipGetErrorString(e_));        \
-  } while (0)
+namespace {
 
 // ------------------------------------------------------------------ per-device state
 
@@ -101,6 +99,17 @@ int device_state(DeviceState **out) {
   *out = &d;
   return 0;
 }
+
+}  // namespace
+
+int zm::device_grid(const uint64_t **grid) {
+  DeviceState *d;
+  if (device_state(&d)) return -1;
+  *grid = d->grid;
+  return 0;
+}
+
+namespace {
 
 // ------------------------------------------------------------------ GEMV dispatch
 
@@ -541,7 +550,7 @@ int check_layer(const zm_moe_layer *L) {
         !L->ws_down)
       return fail("bad shared expert");
   }
-  if (L->router_w && L->H % 4) return fail("router GEMV needs H % 4 == 0");
+  if (L->router_w && L->H % 4) return fail("router GEMV needs H %% 4 == 0");
   return 0;
 }
 using DecFn = void (*)(DecodeArgs);

@@ -185,6 +185,37 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
   return (rl(v, 0) + rl(v, 16)) + (rl(v, 32) + rl(v, 48));
 }
 
+// Strict order "higher score, then lower index" as one 64-bit key: the
+// order-preserving bits of the score above the complemented index.  Keys of
+// distinct experts never tie; 0 is below every key.
+__device__ __forceinline__ unsigned long long rank_key(float v, int e) {
+  const uint32_t u = __float_as_uint(v + 0.0f);  // -0 -> +0: equal scores tie on the index
+  const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)o << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
+}
+
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k) {
+  auto step = [&](auto tag) {
+    constexpr int C = decltype(tag)::value;
+    const uint32_t lo = (uint32_t)dpp_i<C>((int)(uint32_t)k), hi = (uint32_t)dpp_i<C>((int)(uint32_t)(k >> 32));
+    const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+    k = o > k ? o : k;
+  };
+  step(std::integral_constant<int, DPP_XOR1>{});
+  step(std::integral_constant<int, DPP_XOR2>{});
+  step(std::integral_constant<int, DPP_HALF_MIRROR>{});
+  step(std::integral_constant<int, DPP_MIRROR>{});
+  unsigned long long best = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, 16 * r);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), 16 * r);
+    const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+    best = o > best ? o : best;
+  }
+  return best;
+}
+
 // ---------------------------------------------------------------- Q8_K activations (planar)
 //
 // Internal activation rows use a planar layout with the content of ggml's

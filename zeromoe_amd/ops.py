@@ -7,7 +7,7 @@ from typing import Optional
 
 import torch
 
-from ._lib import ZmMoeLayer, ZmRouterSpec, ZmTensor, check, lib
+from ._lib import ZmExpertScratch, ZmMoeLayer, ZmRouterSpec, ZmTensor, check, lib
 
 GGML_TYPES = {"f32": 0, "q2_K": 10, "q3_K": 11, "q4_K": 12, "q8_K": 15, "iq2_xxs": 16, "i32": 26}
 BLOCK_BYTES = {10: 84, 11: 110, 12: 144, 15: 292, 16: 66}
@@ -240,3 +240,110 @@ class MoELayer:
         """0 when the last decode launches on this workspace completed normally."""
         d = self.desc()
         return lib().zm_moe_status(C.byref(d), S, self._ws[S].data_ptr(), _stream(stream))
+
+
+# ---------------------------------------------------------------- FP32-activation path
+
+
+def f32_matmul(W: torch.Tensor, wtype: int, n_in: int, x: torch.Tensor, out=None, stream=None) -> torch.Tensor:
+    """y[S, O] = x[S, n_in] . dequant(W)^T with f32 activations (no Q8_K step);
+    W (O, row_bytes) uint8 holding rows of type `wtype`."""
+    _dev(W, "W")
+    _dev(x, "x")
+    x = x.contiguous()
+    S = x.shape[0]
+    O = W.shape[0]
+    if out is None:
+        out = torch.empty((S, O), dtype=torch.float32, device=x.device)
+    check(lib().zm_f32_matmul(wtype, out.data_ptr(), x.data_ptr(), W.data_ptr(), S, n_in, O, _stream(stream)),
+          "zm_f32_matmul")
+    return out
+
+
+def mul_mat_id_f32(W: torch.Tensor, wtype: int, n_in: int, x: torch.Tensor, ids: torch.Tensor,
+                   out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """The FP32 MUL_MAT_ID hook: W (E, O, row_bytes), x (S, ne11, n_in), ids (S, n_ids) -> (S, n_ids, O)."""
+    for t, n in ((W, "W"), (x, "x"), (ids, "ids")):
+        _dev(t, n)
+    O = W.shape[1]
+    S, n_ids = ids.shape
+    if out is None:
+        out = torch.empty((S, n_ids, O), dtype=torch.float32, device=x.device)
+    tw, tx, ti, ty = _tensor(wtype, W, n_in), _tensor(0, x, None), _tensor(26, ids, None), _tensor(0, out, None)
+    if lib().zm_mul_mat_id_f32(C.byref(tw), C.byref(tx), C.byref(ti), C.byref(ty), _stream(stream), 1) != 1:
+        raise RuntimeError(f"zm_mul_mat_id_f32 declined: {lib().zm_last_error().decode()}")
+    return out
+
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor, clamp: float = 0.0, fused: bool = False, bad=None, stream=None):
+    """launch_expert_swiglu; `bad` (2 x int32 device tensor) accumulates NaN / Inf counts."""
+    _dev(gate, "gate")
+    _dev(up, "up")
+    gate, up = gate.contiguous(), up.contiguous()
+    prod = torch.empty_like(gate)
+    lib().launch_expert_swiglu(prod.data_ptr(), gate.data_ptr(), up.data_ptr(), gate.numel(), float(clamp),
+                               int(fused), _p(bad), _stream(stream))
+    return prod
+
+
+def scatter_accum(src: torch.Tensor, tok: torch.Tensor, dst: torch.Tensor, w: Optional[torch.Tensor] = None,
+                  stream=None) -> torch.Tensor:
+    """dst[tok[i]] += w[i] * src[i] (in place; w None: unweighted add)."""
+    n, D = src.shape
+    S = dst.shape[0]
+    if w is None:
+        lib().launch_expert_scatter_add(src.data_ptr(), tok.data_ptr(), dst.data_ptr(), n, D, S, _stream(stream))
+    else:
+        lib().launch_expert_scatter_accum(src.data_ptr(), tok.data_ptr(), w.data_ptr(), dst.data_ptr(), n, D, S,
+                                          _stream(stream))
+    return dst
+
+
+def glm5next_router_topk(logits: torch.Tensor, topk: int, bias=None, gating="softmax", normalize: bool = False,
+                         scale: float = 0.0, stream=None):
+    """launch_glm5next_router_topk; `logits` (S, E) is overwritten (probs, chosen ones -FLT_MAX)."""
+    _dev(logits, "logits")
+    assert logits.is_contiguous()
+    S, E = logits.shape
+    ids = torch.empty((S, topk), dtype=torch.int32, device=logits.device)
+    w = torch.empty((S, topk), dtype=torch.float32, device=logits.device)
+    g = GATING[gating] if isinstance(gating, str) else int(gating)
+    lib().launch_glm5next_router_topk(logits.data_ptr(), _p(bias), ids.data_ptr(), w.data_ptr(), S, E, topk, g,
+                                      int(normalize), float(scale), _stream(stream))
+    return ids, w
+
+
+class ExpertExecutor:
+    """The per-expert issue / finish_stage1 / finish_stage2 pipeline over one
+    device slab [gate | up | down] (uint8 tensor), host activations in and out."""
+
+    def __init__(self):
+        self.s = ZmExpertScratch()
+        self.s.device_id = -1
+
+    def run(self, slab: torch.Tensor, up_offset: int, down_offset: int, types, x_host, D: int, F: int,
+            clamp: float = 0.0, fused: bool = False, stream=None):
+        import numpy as np
+
+        x_host = np.ascontiguousarray(x_host, dtype=np.float32)
+        S = x_host.shape[0]
+        st = _stream(stream)
+        L = lib()
+        check(L.zm_expert_ffn_issue(C.byref(self.s), slab.data_ptr(), up_offset, types[0], types[1],
+                                    x_host.ctypes.data, S, D, F, None, st), "zm_expert_ffn_issue")
+        check(L.zm_expert_ffn_finish_stage1(C.byref(self.s), slab.data_ptr(), down_offset, types[2], S, D, F,
+                                            float(clamp), int(fused), st), "zm_expert_ffn_finish_stage1")
+        out = np.empty((S, D), np.float32)
+        check(L.zm_expert_ffn_finish_stage2(C.byref(self.s), out.ctypes.data, S, D, st),
+              "zm_expert_ffn_finish_stage2")
+        return out
+
+    def bad_counts(self, reset: bool = False):
+        import numpy as np
+
+        c = np.zeros(2, np.int32)
+        check(lib().zm_expert_bad_counts(C.byref(self.s), c.ctypes.data, int(reset)), "zm_expert_bad_counts")
+        return c
+
+    def release(self):
+        lib().zm_expert_scratch_release(C.byref(self.s))
