@@ -638,6 +638,7 @@ int launch_fused(const zm_moe_layer *L, const float *x, const float *logits, int
   const size_t q8F = q8l_row_bytes(nbF), q8Fs = Fs ? q8l_row_bytes(nbFs) : 0;
   if ((size_t)S * q8l_row_bytes(nbH) > (size_t)DEC_LDS_Q8 || 2 * ((size_t)K * q8F + q8Fs) > (size_t)DEC_LDS_Q8) return 1;
   if (T1 >= (1l << 24) || (long)S * H >= (1l << 24)) return 1;  // float-reciprocal index math
+  if ((T1 + QK - 1) / QK > DEC_MAX_ABLK) return 1;                // act block counters
   DecodeArgs a{};
   a.r = RouterArgs{logits, L->logit_bias, L->sel_bias, L->route_map, L->route_mask, E, K, L->router.gating,
                    L->router.n_groups, L->router.n_groups_used, L->router.weights_norm, L->router.weights_scale,

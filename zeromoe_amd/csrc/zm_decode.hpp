@@ -12,11 +12,16 @@
 //       per workgroup; waves stream batches of rows (double-buffered) and store
 //       the SwiGLU output; the workgroup then counts itself in one of 16
 //       arrival counters.
-//   P2  down rows (token s, row h): the workgroup waits until all workgroups
-//       have arrived, quantizes the act rows of its tokens into LDS (Q8_K) and
+//       and adds its row count to the counter of every 256-row act block its
+//       range touches.
+//   P2  down rows (token s, row h): each wave takes act blocks of the
+//       workgroup's tokens as soon as their counters reach 256 rows,
+//       quantizes them into LDS (Q8_K), and after the last one the workgroup
 //       computes out[s][h] = sum_k w_k * (W_down[e_k][h] . q8(act_k)) (+ shared).
-// Arrival counters come in two sets used by alternate calls: an epoch word
-// selects the set; workgroup 0 zeroes the other set when it starts and bumps
+//       No grid-wide barrier: blocks finished early are quantized while the
+//       last gate/up rows are still being computed elsewhere.
+// Counters come in two sets used by alternate calls: an epoch word selects the
+// set; workgroup 0 zeroes the other set when it starts and, at its end, bumps
 // the epoch once every workgroup has arrived (all of them have read it by
 // then), so no workgroup waits on an atomic's return value.
 // The hot loops are straight-line code: a lane or row without work loads and
@@ -42,7 +47,10 @@ constexpr int DEC_MAX_PAIRS = 128;  // S * K
 constexpr int DEC_LDS_Q8 = 65536;   // Q8_K staging: x rows in P0/P1, act rows in P2
 constexpr int DEC_NCNT = 16;        // arrival counters per set (one 64-byte line each) to spread the atomics
 constexpr int DEC_CNT_STRIDE = 16;  // words between counters
-constexpr int DEC_SYNC_WORDS = DEC_CNT_STRIDE * (1 + 2 * DEC_NCNT);
+constexpr int DEC_MAX_ABLK = 1024;  // act blocks (256 gate/up rows each) tracked per call
+constexpr int DEC_BCNT_STRIDE = 32; // words between block counters (one 128-byte line each)
+constexpr int DEC_BLK_BASE = DEC_CNT_STRIDE * (1 + 2 * DEC_NCNT);
+constexpr int DEC_SYNC_WORDS = DEC_BLK_BASE + 2 * DEC_MAX_ABLK * DEC_BCNT_STRIDE;
 constexpr int DEC_MAX_E = 512;      // router experts handled in the fused kernel
 
 struct DecodeArgs {
@@ -57,7 +65,10 @@ struct DecodeArgs {
   size_t sg_rstride, sd_rstride;
   uint32_t wg_bytes, wd_bytes, sg_bytes, sd_bytes;  // buffer-resource extents (< 2 GiB)
   float *act;
-  uint32_t *sync;  // [0] epoch, [1] error, [DEC_CNT_STRIDE*(1+NCNT*set+i)] arrival counter i of set 0/1
+  // [0] epoch, [1] error, [DEC_CNT_STRIDE*(1+NCNT*set+i)] arrival counter i of
+  // set 0/1, [DEC_BLK_BASE + DEC_BCNT_STRIDE*(DEC_MAX_ABLK*set + b)] rows of act
+  // block b stored
+  uint32_t *sync;
   const uint64_t *grid, *signs;
   int spin_limit;
   uint64_t *trace;  // optional: 8 timestamps per workgroup
@@ -142,7 +153,12 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   // arrival-counter set of this call; workgroup 0 clears the other set
   const uint32_t epoch = __builtin_amdgcn_readfirstlane(ld_co(&a.sync[0]));
   uint32_t *const cnt = a.sync + DEC_CNT_STRIDE * (1 + DEC_NCNT * (int)(epoch & 1u));
-  if (g == 0 && tid < DEC_NCNT) st_co(a.sync + DEC_CNT_STRIDE * (1 + DEC_NCNT * (int)((epoch + 1u) & 1u) + tid), 0u);
+  uint32_t *const bcnt = a.sync + DEC_BLK_BASE + DEC_BCNT_STRIDE * DEC_MAX_ABLK * (int)(epoch & 1u);
+  if (g == 0) {
+    if (tid < DEC_NCNT) st_co(a.sync + DEC_CNT_STRIDE * (1 + DEC_NCNT * (int)((epoch + 1u) & 1u) + tid), 0u);
+    uint32_t *const other = a.sync + DEC_BLK_BASE + DEC_BCNT_STRIDE * DEC_MAX_ABLK * (int)((epoch + 1u) & 1u);
+    for (int i = tid; i < DEC_MAX_ABLK; i += DEC_THREADS) st_co(other + DEC_BCNT_STRIDE * i, 0u);
+  }
 
   // ---------------------------------------------------------------- P0: route, quantize x
   // Wave w < S routes token w (its loads go out first); the other waves
@@ -324,17 +340,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
         const bool valid = ri.valid;
         const int j = ri.j, tok = ri.tok;
         float o[2];
-#ifdef ZM_EXP_NOCOMPUTE_P1
-        {
-          const uint32_t* p0 = reinterpret_cast<const uint32_t*>(&bw[0]);
-          const uint32_t* p1 = reinterpret_cast<const uint32_t*>(&bw[1]);
-          uint32_t h0 = 0, h1 = 0;
-          for (int i = 0; i < (int)(sizeof(Unit<TT>) / 4); ++i) { h0 ^= p0[i]; h1 ^= p1[i]; }
-          o[0] = (float)(h0 & 0xff) * 1e-9f; o[1] = (float)(h1 & 0xff) * 1e-9f;
-        }
-#else
         unit_dots<TT, 2>(bw, part, xblk(s_q8 + (size_t)tok * q8x, a.nbH, blk), s_grid, s_signs, o);
-#endif
         const float ag = group_sum<LL>(o[0]), au = group_sum<LL>(o[1]);
         bst_co(ract, (li1 == 0 && valid) ? 4 * j : OOR, silu_f32(ag) * au);
       };
@@ -361,31 +367,12 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   stores_done();
   __syncthreads();
   ZM_TRACE(2);
+  // arrival (for the epoch) and rows per act block: row j belongs to block j / 256
   if (tid == 0) atomicAdd(&cnt[DEC_CNT_STRIDE * (g % DEC_NCNT)], 1u);
-
-  // ---------------------------------------------------------------- P2: wait, quantize act, down rows
-  // lanes 0..15 of wave 0 poll one counter each and sum them
-  if (wave == 0) {
-    int spins = 0;
-    while (true) {
-      const int c = lane < DEC_NCNT ? (int)ld_co(&cnt[DEC_CNT_STRIDE * lane]) : 0;
-      const int total = __builtin_amdgcn_readlane(group_sum_i<16>(c), 0);
-      if (total >= G) break;
-      __builtin_amdgcn_s_sleep(1);
-      if (++spins > a.spin_limit) {
-        if (lane == 0) {
-          atomicOr(&a.sync[1], 1u);
-          s_err = 1;
-        }
-        break;
-      }
-    }
-    // every workgroup has read the epoch once all have arrived; after an
-    // expired wait the epoch stays (the host resets the sync words)
-    if (g == 0 && lane == 0 && !s_err) st_co(&a.sync[0], epoch + 1u);
+  if (t1 > t0 && tid >= 1 && tid <= ((t1 - 1) >> 8) - (t0 >> 8) + 1) {
+    const int b = (t0 >> 8) + tid - 1;
+    atomicAdd(&bcnt[DEC_BCNT_STRIDE * b], (uint32_t)(min(t1, (b + 1) << 8) - max(t0, b << 8)));
   }
-  __syncthreads();
-  after_wait();
   ZM_TRACE(3);
 
   // act rows of this workgroup's tokens (at most two) -> Q8_K in LDS; the rows
@@ -415,13 +402,45 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
         row = s_q8 + (size_t)ts * tok_bytes + (size_t)K * q8F;
       }
     };
-    // Each wave takes 4 blocks per round: coalesced 16-byte sc1 loads (lane l
-    // holds floats 4l..4l+3 of block k), a transpose through this wave's LDS
-    // stage to 16 lanes per block, then quant_block16.  QR rounds of loads are
-    // in flight together.
+    // Each wave takes 4 blocks per round, QR rounds at a time: it waits until
+    // the counters of those blocks show all 256 rows stored (lane i < 4*QR
+    // polls one), then issues coalesced 16-byte sc1 loads for all of them (lane
+    // l holds floats 4l..4l+3 of block k), transposes each round through this
+    // wave's LDS stage to 16 lanes per block and runs quant_block16.  The wait
+    // is bounded: on expiry the error word is set and the kernel still drains.
     constexpr int QR = 3;
     const int kq = lane >> 4;
+    const int T1b = T1r >> 8;
     for (int base = wave * 4; base < nb_all; base += DEC_WAVES * 4 * QR) {
+      {
+        int bid = -1;
+        const int bi = base + (lane >> 2) * DEC_WAVES * 4 + (lane & 3);
+        if (lane < 4 * QR && bi < nb_all) {
+          const int ts = bi / nb_tok, r = bi - ts * nb_tok;
+          const int s = s_lo + ts;
+          if (r < K * a.nbF) {
+            const int k = r / a.nbF;
+            const int c = s_cidx[s * K + k];
+            bid = c < 0 ? -1 : c * a.nbF + (r - k * a.nbF);
+          } else {
+            bid = T1b + s * a.nbFs + (r - K * a.nbF);
+          }
+        }
+        int spins = 0;
+        while (true) {
+          const bool ready = bid < 0 || ld_co(&bcnt[DEC_BCNT_STRIDE * bid]) >= (uint32_t)QK;
+          if (__ballot(!ready) == 0ull) break;
+          __builtin_amdgcn_s_sleep(1);
+          if (++spins > a.spin_limit) {
+            if (lane == 0) {
+              atomicOr(&a.sync[1], 1u);
+              s_err = 1;
+            }
+            break;
+          }
+        }
+        after_wait();
+      }
       float4 ld[QR][4];
 #pragma unroll
       for (int r = 0; r < QR; ++r) {
@@ -504,6 +523,25 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     }
   }
   ZM_TRACE(5);
+  // workgroup 0 retires the epoch once every workgroup has arrived (each read
+  // the epoch before arriving); after an expired wait the epoch stays (the host
+  // resets the sync words)
+  if (g == 0 && wave == 0) {
+    int spins = 0;
+    bool ok = true;
+    while (true) {
+      const int c = lane < DEC_NCNT ? (int)ld_co(&cnt[DEC_CNT_STRIDE * lane]) : 0;
+      const int total = __builtin_amdgcn_readlane(group_sum_i<16>(c), 0);
+      if (total >= G) break;
+      __builtin_amdgcn_s_sleep(1);
+      if (++spins > a.spin_limit) {
+        ok = false;
+        if (lane == 0) atomicOr(&a.sync[1], 1u);
+        break;
+      }
+    }
+    if (ok && lane == 0 && !s_err) st_co(&a.sync[0], epoch + 1u);
+  }
 }
 
 #undef ZM_TRACE
