@@ -194,6 +194,26 @@ __device__ __forceinline__ unsigned long long rank_key(float v, int e) {
   return ((unsigned long long)o << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
 }
 
+// order-preserving 32-bit image of a score (the upper half of rank_key)
+__device__ __forceinline__ uint32_t score_key(float v) {
+  const uint32_t u = __float_as_uint(v + 0.0f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t k) {
+  auto step = [&](auto tag) {
+    constexpr int C = decltype(tag)::value;
+    const uint32_t o = (uint32_t)dpp_i<C>((int)k);
+    k = o > k ? o : k;
+  };
+  step(std::integral_constant<int, DPP_XOR1>{});
+  step(std::integral_constant<int, DPP_XOR2>{});
+  step(std::integral_constant<int, DPP_HALF_MIRROR>{});
+  step(std::integral_constant<int, DPP_MIRROR>{});
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)k, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)k, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)k, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)k, 48);
+  const uint32_t ab = a > b ? a : b, cd = c > d ? c : d;
+  return ab > cd ? ab : cd;
+}
 __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k) {
   auto step = [&](auto tag) {
     constexpr int C = decltype(tag)::value;

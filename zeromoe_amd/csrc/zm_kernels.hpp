@@ -228,30 +228,40 @@ __device__ __forceinline__ WaveRoute router_wave(const RouterArgs &a, int s, flo
       if (!((keep >> ((lane + 64 * i) / gs)) & 1ull)) sel[i] = NEG_INF;
     stage_sync();  // scr is reused by the caller
   }
-  // top-K: K rounds of a wave-wide 64-bit key maximum
-  unsigned long long key[P];
+  // top-K: K rounds of a wave-wide 32-bit score-key maximum; the winner is the
+  // lowest expert index holding it (register i = 0 first, then the lowest lane
+  // in the ballot), so the order is "higher score, then lower index"
+  uint32_t key[P];
 #pragma unroll
-  for (int i = 0; i < P; ++i) key[i] = lane + 64 * i < E ? rank_key(sel[i], lane + 64 * i) : 0ull;
+  for (int i = 0; i < P; ++i) key[i] = lane + 64 * i < E ? score_key(sel[i]) : 0u;
+  uint32_t valid = 0;
+#pragma unroll
+  for (int i = 0; i < P; ++i) valid |= (lane + 64 * i < E ? 1u : 0u) << i;
   int myid = 0;
   float myw = 0.f, mymask = 1.0f;
   for (int k = 0; k < K; ++k) {
-    unsigned long long m = key[0];
+    uint32_t m = 0;
 #pragma unroll
-    for (int i = 1; i < P; ++i) m = key[i] > m ? key[i] : m;
-    const unsigned long long best = wave_max_u64(m);
-    const int e = (int)(0xffffffffu - (uint32_t)best);
-    const int owner = e & 63;
+    for (int i = 0; i < P; ++i) m = ((valid >> i) & 1u) && key[i] >= m ? key[i] : m;
+    const uint32_t best = wave_max_u32(m);
+    int e = 0;
+#pragma unroll
+    for (int i = P - 1; i >= 0; --i) {
+      const unsigned long long bal = __ballot(((valid >> i) & 1u) && key[i] == best);
+      e = bal ? (int)__builtin_ctzll(bal) + 64 * i : e;
+    }
+    const int owner = e & 63, iw = e >> 6;
     // the owner lane takes the winner's values out of its registers (selects,
     // not an indexed register read, so the arrays stay in registers)
     float pw = 0.f, rkw = 1.0f;
     int rmw = 0;
 #pragma unroll
     for (int i = 0; i < P; ++i) {
-      const bool hit = key[i] == best;
+      const bool hit = i == iw;
       pw = hit ? v[i] : pw;
       rmw = hit ? rm[i] : rmw;
       rkw = hit ? rk[i] : rkw;
-      key[i] = hit ? 0ull : key[i];
+      if (hit && lane == owner) valid &= ~(1u << i);
     }
     pw = readlane_f(pw, owner);
     int id = e;
