@@ -9,7 +9,7 @@ cycling over layer replicas so the working set exceeds the 256 MB
 Infinity Cache; inputs are resident in HBM before the timed region.
 
 Prints ONE JSON line.  The other configurations are reported under
-"extras" (c1, c3 prefill tok/s, c4, c5).  cpu_baseline times the CPU
+"extras" (c1, c3 prefill tok/s, c4, c5 at S=1 and S=64).  cpu_baseline times the CPU
 restatement of ggml's MUL_MAT_ID layer (oracle/) on this host.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
@@ -39,12 +39,14 @@ CONFIGS = {
     "c5": dict(H=7168, F=2048, E=256, K=8, S=1, tg=Q2, td=Q2, gating="sigmoid", n_slots=96, groups=8,
                groups_used=4, norm=True, scale=2.5, F_shared=2048, t_shared=Q4, router_gemv=True),
 }
+CONFIGS["c5_s64"] = dict(CONFIGS["c5"], S=64)
 WORKLOAD = {
     "c1": "decode S=1, H=2048 F=768 E=128 top-8 softmax, Q4_K",
     "c2": "decode S=1, H=4096 F=1536 E=128 top-8 softmax, gate/up Q2_K, down Q3_K",
     "c3": "prefill S=512, H=4096 F=1536 E=128 top-8 softmax + per-expert logit bias N(0,1.5), Q4_K",
     "c4": "small batch S=4, H=5120 F=1536 E=160 top-8 softmax, IQ2_XXS",
     "c5": "full block S=1, H=7168 F=2048, 256 routed Q2_K (96 resident slots) + shared Q4_K, sigmoid 8 groups/top-4",
+    "c5_s64": "full block S=64, H=7168 F=2048, 256 routed Q2_K (96 resident slots) + shared Q4_K, sigmoid 8 groups/top-4",
 }
 
 
@@ -326,7 +328,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--replicas", type=int, default=0, help="layer replicas (0 = enough to exceed the MALL)")
-    ap.add_argument("--extras", default="c1,c3,c4,c5", help="extra configs to report ('' for none)")
+    ap.add_argument("--extras", default="c1,c3,c4,c5,c5_s64", help="extra configs to report ('' for none)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch every step from Python instead of a HIP graph")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -375,7 +377,7 @@ def main():
     traffic = committed_traffic()
     extras = {}
     for name in [n for n in args.extras.split(",") if n]:
-        st = max(10, args.steps // 4) if name == "c3" else args.steps
+        st = max(10, args.steps // 4) if name in ("c3", "c5_s64") else args.steps
         r = run_config(torch, Z, name, st, max(3, args.warmup // 2), reps(name), use_graph=not args.eager)
         extras[name] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}
         extras[name]["workload"] = WORKLOAD[name]

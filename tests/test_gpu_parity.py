@@ -118,14 +118,16 @@ def test_mul_mat_id_skewed_prefill_buckets():
     np.testing.assert_allclose(got, ref, rtol=1e-3, atol=1e-3 * np.abs(ref).max())
 
 
+@pytest.mark.parametrize("t", [Q4, Q2])
 @pytest.mark.parametrize("ne11", [1, 8])
-def test_mul_mat_id_mfma_buckets_per_element(ne11):
-    """Buckets of 64-80 pairs take the int8-MFMA path for Q4_K: every output
-    element within 1e-3 relative of the oracle (the op alone, no re-quantization)."""
+def test_mul_mat_id_mfma_buckets_per_element(ne11, t):
+    """Buckets of 64-80 pairs take the int8-MFMA path for Q4_K and Q2_K: every
+    output element within 1e-3 relative of the oracle (the op alone, no
+    re-quantization)."""
     rng = np.random.default_rng(11 + ne11)
     S, n_ids, E = 72, 8, 8
     ids = np.stack([rng.permutation(E)[:n_ids] for _ in range(S)]).astype(np.int32)
-    got, ref = _mmid_case(Q4, 2048, 160, E, ids, ne11, seed=13 + ne11)
+    got, ref = _mmid_case(t, 2048, 160, E, ids, ne11, seed=13 + ne11)
     rel = np.abs(got - ref) / np.maximum(np.abs(ref), 1e-3 * np.abs(ref).max())
     assert rel.max() <= 1e-3, rel.max()
 
@@ -202,6 +204,7 @@ LAYER_CASES = {
     "c4_full": (CONFIGS["c4"], {}),
     "c5_full_S1": (CONFIGS["c5"], {}),
     "c5_S64_reduced": (CONFIGS["c5"], dict(S=64, H=1024, F=512, F_shared=512)),
+    "c5_S64_full": (CONFIGS["c5"], dict(S=64)),
     # prefill buckets on the MFMA path: 128 pairs per expert on average (two passes of 64)
     "c3_mmq": (CONFIGS["c3"], dict(S=256, H=1024, F=512, E=16)),
 }
@@ -308,16 +311,24 @@ def test_hip_graph_replay_matches_eager(case):
         _sync()
 
 
-@pytest.mark.parametrize("case", ["c3_mmq", "c3_skewed"])
+PREFILL_CASES = {
+    "c3_mmq": (CONFIGS["c3"], dict(S=256, H=1024, F=512, E=16)),
+    "c3_skewed": (CONFIGS["c3"], dict(S=192, H=2048, F=768, E=64)),
+    # Q2_K routed experts (few pairs each) + Q4_K shared expert, slot table
+    "c5_S64": (CONFIGS["c5"], dict(S=64, H=2048, F=1024, F_shared=1024)),
+}
+
+
+@pytest.mark.parametrize("case", list(PREFILL_CASES))
 def test_prefill_mfma_vs_gemv(case, monkeypatch):
     """The int8-MFMA bucketed GEMM (prefill) against the GEMV path on the same
     buckets (same integer sums, different float order) and the oracle."""
-    kw = dict(S=256, H=1024, F=512, E=16) if case == "c3_mmq" else dict(S=192, H=2048, F=768, E=64)
-    c = reduced(CONFIGS["c3"], **kw)
+    c, kw = PREFILL_CASES[case]
+    c = reduced(c, **kw)
     b = Built(c, seed=41)
     L = b.layer()
     x = torch.from_numpy(b.x).cuda()
-    lg = torch.from_numpy(b.logits).cuda()
+    lg = None if c.router_gemv else torch.from_numpy(b.logits).cuda()
     monkeypatch.setenv("ZEROMOE_MMQ", "1")
     out1, ids1, w1 = L.forward(x, lg)
     _sync()
@@ -327,7 +338,11 @@ def test_prefill_mfma_vs_gemv(case, monkeypatch):
     np.testing.assert_array_equal(ids1.cpu().numpy(), ids2.cpu().numpy())
     ids_h, w_h = ids1.cpu().numpy(), w1.cpu().numpy()
     slack = lambda: b.requant_slack(ids_h, w_h)
-    # two device paths may each flip a different tied element: twice the bound
-    assert_close_layer(out1.cpu().numpy(), out2.cpu().numpy(), rtol=1e-4, slack=lambda: 2 * slack())
     ref = b.oracle_forward(ids_h, w_h)
     assert_close_layer(out1.cpu().numpy(), ref, slack=slack)
+    assert_close_layer(out2.cpu().numpy(), ref, slack=slack)
+    # two device paths may each flip a different tied element: twice the bound.
+    # With a shared expert its act re-quantization can flip as well (not in the
+    # slack bound): the layer bar then applies between the paths too.
+    rtol = 1e-3 if c.F_shared else 1e-4
+    assert_close_layer(out1.cpu().numpy(), out2.cpu().numpy(), rtol=rtol, slack=lambda: 2 * slack())

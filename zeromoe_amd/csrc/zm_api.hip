@@ -183,21 +183,29 @@ int launch_gemv(int type, bool gateup, int np, const GemvArgs &a0, int n_groups,
   return 0;
 }
 
-// MFMA path for prefill-sized buckets: Q4_K weights and at least 8 pairs per
-// active expert on average.  a.items / a.n_items (or a.dense_S) must be set;
+// MFMA path for prefill-sized buckets: Q4_K weights with at least 8 pairs per
+// active expert on average, Q2_K weights with at least 2.  a.items / a.n_items (or a.dense_S) must be set;
 // max_items bounds *a.n_items.  Returns 1 when the path does not apply (the
 // caller takes the GEMV path).
 bool mmq_applies(int type, double avg_pairs) {
-  return type == T_Q4_K && avg_pairs >= 8.0 && !getenv_flag_off("ZEROMOE_MMQ");
+  return ((type == T_Q4_K && avg_pairs >= 8.0) || (type == T_Q2_K && avg_pairs >= 2.0)) &&
+         !getenv_flag_off("ZEROMOE_MMQ");
 }
 int launch_mmq(int type, bool gateup, const GemvArgs &a, int max_items, double avg_pairs, hipStream_t st) {
   if (!mmq_applies(type, avg_pairs)) return 1;
   if ((size_t)a.nrows * a.w_rstride >= (1ull << 31) || max_items <= 0) return 1;
   const dim3 grid((unsigned)((a.nrows + 63) / 64), (unsigned)max_items);
-  if (gateup)
-    hipLaunchKernelGGL(k_mmq_q4k<true>, grid, dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL(k_mmq_q4k<false>, grid, dim3(256), 0, st, a);
+  if (type == T_Q4_K) {
+    if (gateup)
+      hipLaunchKernelGGL((k_mmq<T_Q4_K, true>), grid, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((k_mmq<T_Q4_K, false>), grid, dim3(256), 0, st, a);
+  } else {
+    if (gateup)
+      hipLaunchKernelGGL((k_mmq<T_Q2_K, true>), grid, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((k_mmq<T_Q2_K, false>), grid, dim3(256), 0, st, a);
+  }
   HIP_OK(hipGetLastError());
   return 0;
 }
@@ -757,7 +765,11 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
   // router
   const float *lg = logits;
   if (L->router_w) {
-    hipLaunchKernelGGL(k_router_gemv, dim3(E), dim3(256), 0, st, L->router_w, x, H, E, S, w.logits);
+    if (S >= 8 && H % 64 == 0)
+      hipLaunchKernelGGL(k_router_gemm, dim3((E + 15) / 16, (S + 15) / 16), dim3(256), 0, st, L->router_w, x, H, E, S,
+                         w.logits);
+    else
+      hipLaunchKernelGGL(k_router_gemv, dim3(E), dim3(256), 0, st, L->router_w, x, H, E, S, w.logits);
     lg = w.logits;
   }
   {

@@ -650,4 +650,42 @@ __global__ __launch_bounds__(256) void k_router_gemv(const float *__restrict__ W
   }
 }
 
+// Batched form (S >= 8): 16 tokens x 16 experts per workgroup on
+// v_mfma_f32_16x16x4f32, the K range split over the 4 waves and summed in LDS
+// in wave order.  Lane (n = lane % 16, g = lane / 16) feeds token / expert n
+// with the 4 consecutive values k0 + 4g .. 4g+3 of each 16-wide K chunk, one
+// per MFMA.  H % 64 == 0.
+typedef float v4f_rt __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void k_router_gemm(const float *__restrict__ W, const float *__restrict__ x, int H,
+                                                     int E, int S, float *__restrict__ logits) {
+  __shared__ float part[4][64][4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int e0 = blockIdx.x * 16, s0 = blockIdx.y * 16;
+  const int e = min(e0 + n, E - 1), s = min(s0 + n, S - 1);
+  const float4 *wr = reinterpret_cast<const float4 *>(W + (size_t)e * H) + g;
+  const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)s * H) + g;
+  const int kq = H / 64;  // 16-wide chunks per wave
+  const int c0 = wave * kq;
+  v4f_rt acc = {0.f, 0.f, 0.f, 0.f};
+  for (int c = c0; c < c0 + kq; ++c) {
+    const float4 a = xr[4 * c], b = wr[4 * c];
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc, 0, 0, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) part[wave][lane][j] = acc[j];
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ss = s0 + 4 * g + j, ee = e0 + n;  // D lane l, reg j: token 4g + j, expert n
+      const float v = (part[0][lane][j] + part[1][lane][j]) + (part[2][lane][j] + part[3][lane][j]);
+      if (ss < S && ee < E) logits[(size_t)ss * E + ee] = v;
+    }
+  }
+}
+
 }  // namespace zm

@@ -14,7 +14,16 @@
 //                 |terms| < 2^18, sums < 2^24: exact in fp32)
 //   f[t][r]    += d_x[t] * (d[r] * isum - dmin[r] * imin)  (ggml's vec_dot_q4_K_q8_K combine)
 // The weight nibbles feed the MFMA directly (0..15 as int8): no dequantized
-// copy is materialized.  Activations are the planar Q8_K rows of the decode
+// copy is materialized.
+//
+// Q2_K uses v_mfma_i32_16x16x64_i8 with the 4-bit sub-block scale folded into
+// the weights (q * sc <= 45 fits int8): lane (row n, k-group g) of 64-weight
+// chunk c = 2h + jp holds bit-plane j = 2jp + (g >> 1) of qs bytes
+// 32h + 16(g & 1) .. +15, i.e. weights 64c + 16g .. +15 of sub-block
+// 8h + 2j + (g & 1), each byte multiplied by that sub-block's scale; one MFMA
+// chain over the 4 chunks gives isum = sum_sb sc * (q . x)_sb exactly, the
+// mins term sum_sb m * bsum16 goes through four v_mfma_f32_16x16x4f32 (K = 16
+// sub-blocks), and f += d_x * (d * isum - dmin * imin) (ggml's vec_dot_q2_K_q8_K).  Activations are the planar Q8_K rows of the decode
 // path (qs | bsums | d).
 #pragma once
 
@@ -24,6 +33,15 @@ namespace zm {
 
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 typedef float v4f_t __attribute__((ext_vector_type(4)));
+typedef unsigned short v2u16_t __attribute__((ext_vector_type(2)));
+
+// four packed bytes times a small factor, bytewise (every product < 256: no
+// carry crosses a byte): one packed 16-bit multiply
+__device__ __forceinline__ uint32_t mul_bytes(uint32_t packed, uint32_t f) {
+  const v2u16_t p = __builtin_bit_cast(v2u16_t, packed);
+  const v2u16_t m = {(unsigned short)f, (unsigned short)f};
+  return __builtin_bit_cast(uint32_t, p * m);
+}
 
 constexpr int MMQ_TT = 2;              // 16-token tiles per work item
 constexpr int MMQ_TOK = 16 * MMQ_TT;   // pairs per work item
@@ -65,10 +83,26 @@ __global__ __launch_bounds__(1024) void k_mmq_items(const int32_t *__restrict__ 
 // (double buffered over the K blocks; each thread holds the next block's share
 // in registers while the current block computes); the weights of block b+1
 // are requested while block b computes.
-template <bool GATEUP>
-__global__ __launch_bounds__(256) void k_mmq_q4k(GemvArgs a) {
+template <int T>
+struct MmqW;
+template <>
+struct MmqW<T_Q4_K> {  // d, dmin, scales | this lane's 4 x 8 bytes of qs
+  uint4 hdr;
+  uint2 qs[4];
+};
+template <>
+struct MmqW<T_Q2_K> {  // scales | this lane's 2 x 16 bytes of qs | d, dmin
+  uint4 sc;
+  uint4 qs[2];
+  uint32_t dd;
+};
+
+template <int T, bool GATEUP>
+__global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
+  static_assert(T == T_Q4_K || T == T_Q2_K, "MFMA prefill types");
+  constexpr int NBS = T == T_Q4_K ? 8 : 16;  // bsums per block used: 32-sums (Q4_K) or 16-sums (Q2_K)
   __shared__ __attribute__((aligned(16))) uint8_t s_xq[2][MMQ_TOK][MMQ_XS];
-  __shared__ int s_bs[2][MMQ_TOK][8];  // 32-weight bsums of the block
+  __shared__ int s_bs[2][MMQ_TOK][NBS];
   __shared__ float s_xd[2][MMQ_TOK];
   __shared__ int s_xoff[MMQ_TOK];      // byte offset of each pair's activation row (OOR: none)
   __shared__ int s_pair[MMQ_TOK];
@@ -86,7 +120,7 @@ __global__ __launch_bounds__(256) void k_mmq_q4k(GemvArgs a) {
     p1 = a.offs[e + 1];
   }
   constexpr int NM = GATEUP ? 2 : 1;
-  constexpr int BB = 144;
+  constexpr int BB = block_bytes(T);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int row = blockIdx.x * 64 + wave * 16 + n;  // weight row of this lane (B operand, output column)
@@ -110,17 +144,21 @@ __global__ __launch_bounds__(256) void k_mmq_q4k(GemvArgs a) {
   }
   __syncthreads();
 
-  struct WBlk {
-    uint4 hdr;
-    uint2 qs[4];
-  };
+  using WBlk = MmqW<T>;
   auto load_w = [&](int b, WBlk (&w)[NM]) {
     const int vo = b < nb ? vrow + b * BB : OOR;
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
-      w[m].hdr = bld16(rw[m], vo, 0);
+      if constexpr (T == T_Q4_K) {
+        w[m].hdr = bld16(rw[m], vo, 0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) w[m].qs[i] = bld8(rw[m], vo + 16 + 32 * i + 8 * g, 0);
+        for (int i = 0; i < 4; ++i) w[m].qs[i] = bld8(rw[m], vo + 16 + 32 * i + 8 * g, 0);
+      } else {
+        w[m].sc = bld16(rw[m], vo, 0);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) w[m].qs[h] = bld16(rw[m], vo + 16 + 32 * h + 16 * (g & 1), 0);
+        w[m].dd = bld4(rw[m], vo + 80, 0);
+      }
     }
   };
   // this thread's share of an activation block: qs chunks c = tid, tid + 256
@@ -156,7 +194,15 @@ __global__ __launch_bounds__(256) void k_mmq_q4k(GemvArgs a) {
       const int c = tid + 256 * r, t = c >> 4, ch = c & 15;
       *reinterpret_cast<uint4 *>(&s_xq[buf][t][16 * ch]) = x.q[r];
     }
-    if (tid < MMQ_TOK * 8) s_bs[buf][tid >> 3][tid & 7] = (int)(int16_t)(x.bs & 0xffffu) + (int)(int16_t)(x.bs >> 16);
+    if (tid < MMQ_TOK * 8) {
+      const int lo = (int)(int16_t)(x.bs & 0xffffu), hi = (int)(int16_t)(x.bs >> 16);
+      if constexpr (T == T_Q4_K) {
+        s_bs[buf][tid >> 3][tid & 7] = lo + hi;
+      } else {
+        s_bs[buf][tid >> 3][2 * (tid & 7)] = lo;
+        s_bs[buf][tid >> 3][2 * (tid & 7) + 1] = hi;
+      }
+    }
     if (tid < MMQ_TOK) s_xd[buf][tid] = x.d;
   };
 
@@ -178,6 +224,7 @@ __global__ __launch_bounds__(256) void k_mmq_q4k(GemvArgs a) {
   for (int b = 0; b < nb; ++b) {
     const int buf = b & 1;
     load_w(b + 1, wnxt);
+    if constexpr (T == T_Q4_K) {
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
       const uint32_t u0 = wcur[m].hdr.y, u1 = wcur[m].hdr.z, u2 = wcur[m].hdr.w;
@@ -214,6 +261,49 @@ __global__ __launch_bounds__(256) void k_mmq_q4k(GemvArgs a) {
         for (int j = 0; j < 4; ++j)
           f[m][t][j] += s_xd[buf][16 * t + 4 * g + j] * (d * (float)isum[j] - dmin * mn[j]);
       }
+    }
+    } else {
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      const float d = h2f((uint16_t)(wcur[m].dd & 0xffffu)), dmin = h2f((uint16_t)(wcur[m].dd >> 16));
+      const uint32_t scb[4] = {wcur[m].sc.x, wcur[m].sc.y, wcur[m].sc.z, wcur[m].sc.w};
+      // B operand of the min product: m[row][sb] for sb = 4i + g
+      float mb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mb[i] = (float)((scb[i] >> (8 * g + 4)) & 15u);
+      // scale-folded weights of the 4 chunks c = 2h + jp: plane j = 2jp + (g >> 1),
+      // sub-block 8h + 2j + (g & 1)
+      v4i_t bq[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int h = c >> 1, jp = c & 1;
+        const int j = 2 * jp + (g >> 1);
+        const int sb = 8 * h + 2 * j + (g & 1);
+        const uint32_t sc = (scb[sb >> 2] >> (8 * (sb & 3))) & 15u;
+        const uint4 q = wcur[m].qs[h];
+        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) bq[c][k] = (int)mul_bytes((qw[k] >> (2 * j)) & 0x03030303u, sc);
+      }
+#pragma unroll
+      for (int t = 0; t < MMQ_TT; ++t) {
+        if (t >= nt) continue;
+        const uint8_t *xr = &s_xq[buf][16 * t + n][0];
+        v4i_t isum = {0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const v4i_t xa = *reinterpret_cast<const v4i_t *>(xr + 64 * c + 16 * g);
+          isum = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, bq[c], isum, 0, 0, 0);
+        }
+        v4f_t mn = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          mn = __builtin_amdgcn_mfma_f32_16x16x4f32((float)s_bs[buf][16 * t + n][4 * i + g], mb[i], mn, 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          f[m][t][j] += s_xd[buf][16 * t + 4 * g + j] * (d * (float)isum[j] - dmin * mn[j]);
+      }
+    }
     }
     // block b+1 into the other buffer (its readers finished at the last barrier),
     // then request block b+2
