@@ -765,10 +765,17 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
   // router
   const float *lg = logits;
   if (L->router_w) {
-    if (S >= 8 && H % 64 == 0)
-      hipLaunchKernelGGL(k_router_gemm, dim3((E + 15) / 16, (S + 15) / 16), dim3(256), 0, st, L->router_w, x, H, E, S,
-                         w.logits);
-    else
+    // K slices so that ~512 workgroups stream the router weights; the partial
+    // sums go through w.y (S*K*H floats, unused until the down projection)
+    int KS = 1;
+    while (KS < 16 && ((E + 15) / 16) * ((S + 15) / 16) * KS * 2 <= 512 && H % (64 * KS * 2) == 0 &&
+           (size_t)KS * 2 * S * E <= (size_t)S * K * H)
+      KS *= 2;
+    if (S >= 8 && H % 64 == 0) {
+      hipLaunchKernelGGL(k_router_gemm, dim3((E + 15) / 16, (S + 15) / 16, KS), dim3(256), 0, st, L->router_w, x, H,
+                         E, S, w.y);
+      hipLaunchKernelGGL(k_router_sum, dim3((S * E + 255) / 256), dim3(256), 0, st, w.y, S * E, KS, w.logits);
+    } else
       hipLaunchKernelGGL(k_router_gemv, dim3(E), dim3(256), 0, st, L->router_w, x, H, E, S, w.logits);
     lg = w.logits;
   }

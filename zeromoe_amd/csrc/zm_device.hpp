@@ -214,6 +214,31 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t k) {
   const uint32_t ab = a > b ? a : b, cd = c > d ? c : d;
   return ab > cd ? ab : cd;
 }
+// inverse of score_key (-0 comes back as +0)
+__device__ __forceinline__ float score_from_key(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+// maximum over aligned groups of W lanes (W = 16, 32, 64); all lanes of a group get it
+__device__ __forceinline__ uint32_t group_max_u32(uint32_t k, int W) {
+  auto step = [&](auto tag) {
+    constexpr int C = decltype(tag)::value;
+    const uint32_t o = (uint32_t)dpp_i<C>((int)k);
+    k = o > k ? o : k;
+  };
+  step(std::integral_constant<int, DPP_XOR1>{});
+  step(std::integral_constant<int, DPP_XOR2>{});
+  step(std::integral_constant<int, DPP_HALF_MIRROR>{});
+  step(std::integral_constant<int, DPP_MIRROR>{});
+  if (W >= 32) {
+    const uint32_t o = (uint32_t)__shfl_xor((int)k, 16, 64);
+    k = o > k ? o : k;
+  }
+  if (W >= 64) {
+    const uint32_t o = (uint32_t)__shfl_xor((int)k, 32, 64);
+    k = o > k ? o : k;
+  }
+  return k;
+}
 __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k) {
   auto step = [&](auto tag) {
     constexpr int C = decltype(tag)::value;

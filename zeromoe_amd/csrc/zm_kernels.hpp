@@ -194,31 +194,54 @@ __device__ __forceinline__ WaveRoute router_wave(const RouterArgs &a, int s, flo
   for (int i = 0; i < P; ++i) sel[i] = a.sel_bias ? v[i] + sb[i] : v[i];
   const int G = a.n_groups;
   if (G > 1 && a.n_groups_used > 0 && a.n_groups_used < G && E % G == 0 && G <= 64) {
-    // group score = best + second best selection score of the group (lane g
-    // scans group g); keep the n_groups_used best groups
+    // group score = best + second best selection score of the group; keep the
+    // n_groups_used best groups
     const int gs = E / G;
-#pragma unroll
-    for (int i = 0; i < P; ++i)
-      if (lane + 64 * i < E) scr[lane + 64 * i] = sel[i];
-    stage_sync();
     float gsc = NEG_INF;
-    if (lane < G) {
-      int b1 = -1, b2 = -1;
-      float s1 = 0.f, s2 = 0.f;
-      for (int j = 0; j < gs; ++j) {
-        const int e = lane * gs + j;
-        const float x = scr[e];
-        if (b1 < 0 || outranks(x, e, s1, b1)) {
-          b2 = b1;
-          s2 = s1;
-          b1 = e;
-          s1 = x;
-        } else if (b2 < 0 || outranks(x, e, s2, b2)) {
-          b2 = e;
-          s2 = x;
-        }
+    if (gs == 16 || gs == 32 || gs == 64) {
+      // a group is gs consecutive lanes of one register: two group-wide key
+      // maxima, the first one's lowest lane taken out for the second; a score
+      // is recovered from its key (the map is a bijection up to -0 -> +0)
+      const unsigned long long lanes_all = ~0ull;
+#pragma unroll
+      for (int i = 0; i < P; ++i) {
+        const bool ok = lane + 64 * i < E;
+        const uint32_t k0 = ok ? score_key(sel[i]) : 0u;
+        const int base = lane & ~(gs - 1);
+        const unsigned long long gmask = (gs == 64 ? lanes_all : ((1ull << gs) - 1ull)) << base;
+        const uint32_t k1 = group_max_u32(k0, gs);
+        const unsigned long long b1 = __ballot(ok && k0 == k1) & gmask;
+        const bool first = b1 != 0ull && lane == (int)__builtin_ctzll(b1);
+        const uint32_t k2 = group_max_u32(first ? 0u : k0, gs);
+        const float s1 = score_from_key(k1), s2 = score_from_key(k2);
+        if (ok && (lane & (gs - 1)) == 0) scr[(lane + 64 * i) / gs] = gs >= 2 ? s1 + s2 : s1;
       }
-      gsc = gs >= 2 ? s1 + s2 : s1;
+      stage_sync();
+      if (lane < G) gsc = scr[lane];
+    } else {
+      // lane g scans group g
+#pragma unroll
+      for (int i = 0; i < P; ++i)
+        if (lane + 64 * i < E) scr[lane + 64 * i] = sel[i];
+      stage_sync();
+      if (lane < G) {
+        int b1 = -1, b2 = -1;
+        float s1 = 0.f, s2 = 0.f;
+        for (int j = 0; j < gs; ++j) {
+          const int e = lane * gs + j;
+          const float x = scr[e];
+          if (b1 < 0 || outranks(x, e, s1, b1)) {
+            b2 = b1;
+            s2 = s1;
+            b1 = e;
+            s1 = x;
+          } else if (b2 < 0 || outranks(x, e, s2, b2)) {
+            b2 = e;
+            s2 = x;
+          }
+        }
+        gsc = gs >= 2 ? s1 + s2 : s1;
+      }
     }
     int r = 0;
     for (int g2 = 0; g2 < G; ++g2) r += outranks(readlane_f(gsc, g2), g2, gsc, lane);
@@ -651,41 +674,65 @@ __global__ __launch_bounds__(256) void k_router_gemv(const float *__restrict__ W
 }
 
 // Batched form (S >= 8): 16 tokens x 16 experts per workgroup on
-// v_mfma_f32_16x16x4f32, the K range split over the 4 waves and summed in LDS
-// in wave order.  Lane (n = lane % 16, g = lane / 16) feeds token / expert n
-// with the 4 consecutive values k0 + 4g .. 4g+3 of each 16-wide K chunk, one
-// per MFMA.  H % 64 == 0.
+// v_mfma_f32_16x16x4f32.  The K range is cut into KS = gridDim.z slices (one
+// per workgroup, so that enough workgroups stream the router weights) and each
+// slice over the 4 waves, summed in LDS in wave order into part[z][s][e];
+// k_router_sum adds the slices in order.  Lane (n = lane % 16, g = lane / 16)
+// feeds token / expert n with the 4 consecutive values k0 + 4g .. 4g+3 of each
+// 16-wide K chunk, one per MFMA.  H % (64 * KS) == 0.
 typedef float v4f_rt __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(256) void k_router_gemm(const float *__restrict__ W, const float *__restrict__ x, int H,
-                                                     int E, int S, float *__restrict__ logits) {
-  __shared__ float part[4][64][4];
+                                                     int E, int S, float *__restrict__ part) {
+  __shared__ float red[4][64][4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 15, g = lane >> 4;
-  const int e0 = blockIdx.x * 16, s0 = blockIdx.y * 16;
+  const int e0 = blockIdx.x * 16, s0 = blockIdx.y * 16, z = blockIdx.z, KS = gridDim.z;
   const int e = min(e0 + n, E - 1), s = min(s0 + n, S - 1);
   const float4 *wr = reinterpret_cast<const float4 *>(W + (size_t)e * H) + g;
   const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)s * H) + g;
-  const int kq = H / 64;  // 16-wide chunks per wave
-  const int c0 = wave * kq;
-  v4f_rt acc = {0.f, 0.f, 0.f, 0.f};
-  for (int c = c0; c < c0 + kq; ++c) {
-    const float4 a = xr[4 * c], b = wr[4 * c];
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc, 0, 0, 0);
-  }
+  const int kq = H / (64 * KS);  // 16-wide chunks per wave
+  const int c0 = (z * 4 + wave) * kq;
+  // 8 chunks of loads in flight, two accumulator chains
+  v4f_rt acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
+  constexpr int U = 8;
+  for (int cb = c0; cb < c0 + kq; cb += U) {
+    float4 a[U], b[U];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) part[wave][lane][j] = acc[j];
+    for (int u = 0; u < U; ++u) {
+      const int c = min(cb + u, c0 + kq - 1);
+      a[u] = xr[4 * c];
+      b[u] = wr[4 * c];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (cb + u >= c0 + kq) break;
+      v4f_rt &t = (u & 1) ? acc2 : acc;
+      t = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].x, b[u].x, t, 0, 0, 0);
+      t = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].y, b[u].y, t, 0, 0, 0);
+      t = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].z, b[u].z, t, 0, 0, 0);
+      t = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].w, b[u].w, t, 0, 0, 0);
+    }
+  }
+  acc += acc2;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) red[wave][lane][j] = acc[j];
   __syncthreads();
   if (wave == 0) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int ss = s0 + 4 * g + j, ee = e0 + n;  // D lane l, reg j: token 4g + j, expert n
-      const float v = (part[0][lane][j] + part[1][lane][j]) + (part[2][lane][j] + part[3][lane][j]);
-      if (ss < S && ee < E) logits[(size_t)ss * E + ee] = v;
+      const float v = (red[0][lane][j] + red[1][lane][j]) + (red[2][lane][j] + red[3][lane][j]);
+      if (ss < S && ee < E) part[((size_t)z * S + ss) * E + ee] = v;
     }
   }
+}
+__global__ __launch_bounds__(256) void k_router_sum(const float *__restrict__ part, int n, int KS,
+                                                    float *__restrict__ logits) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  float v = part[i];
+  for (int z = 1; z < KS; ++z) v += part[(size_t)z * n + i];
+  logits[i] = v;
 }
 
 }  // namespace zm
