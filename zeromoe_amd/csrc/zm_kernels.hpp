@@ -155,16 +155,30 @@ __device__ __forceinline__ WaveRoute router_wave(const RouterArgs &a, int s, flo
   float v[P], sb[P];
   int rm[P];
   float rk[P];
-  // every global load of the router goes out first
+  // every global load of the router goes out first, unconditionally: an absent
+  // array is a buffer resource of extent 0 (its loads return 0 and touch no memory)
+  const uint32_t ext = (uint32_t)E * 4u;
+  const rsrc_t r_l = make_rsrc(l, ext);
+  const rsrc_t r_lb = make_rsrc(a.logit_bias, a.logit_bias ? ext : 0u);
+  const rsrc_t r_sb = make_rsrc(a.sel_bias, a.sel_bias ? ext : 0u);
+  const rsrc_t r_rm = make_rsrc(a.route_map, a.route_map ? ext : 0u);
+  const rsrc_t r_rk = make_rsrc(a.route_mask, a.route_map && a.route_mask ? ext : 0u);
+  float lb[P];
 #pragma unroll
   for (int i = 0; i < P; ++i) {
     const int e = lane + 64 * i;
-    const bool in = e < E;
-    v[i] = in ? l[e] : NEG_INF;
-    if (a.logit_bias) v[i] = in ? v[i] + a.logit_bias[e] : NEG_INF;
-    sb[i] = (a.sel_bias && in) ? a.sel_bias[e] : 0.0f;
-    rm[i] = (a.route_map && in) ? a.route_map[e] : 0;
-    rk[i] = (a.route_map && a.route_mask && in) ? a.route_mask[e] : 1.0f;
+    const int vo = e < E ? 4 * e : OOR;
+    v[i] = __uint_as_float(bld4(r_l, vo, 0));
+    lb[i] = __uint_as_float(bld4(r_lb, vo, 0));
+    sb[i] = __uint_as_float(bld4(r_sb, vo, 0));
+    rm[i] = (int)bld4(r_rm, vo, 0);
+    rk[i] = __uint_as_float(bld4(r_rk, vo, 0));
+  }
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const bool in = lane + 64 * i < E;
+    v[i] = !in ? NEG_INF : (a.logit_bias ? v[i] + lb[i] : v[i]);
+    rk[i] = a.route_mask ? rk[i] : 1.0f;
   }
   if (a.gating == 0) {
     float mx = v[0];
