@@ -191,20 +191,28 @@ bool mmq_applies(int type, double avg_pairs) {
   return ((type == T_Q4_K && avg_pairs >= 8.0) || (type == T_Q2_K && avg_pairs >= 2.0)) &&
          !getenv_flag_off("ZEROMOE_MMQ");
 }
-int launch_mmq(int type, bool gateup, const GemvArgs &a, int max_items, double avg_pairs, hipStream_t st) {
+// 16-token tiles per work item: routed Q4_K buckets take 4 (the weight
+// unpacking is shared by more tokens), Q2_K and dense (shared expert) rows 2
+int mmq_tt(int type, bool dense) { return type == T_Q4_K && !dense ? 4 : 2; }
+int launch_mmq(int type, bool gateup, const GemvArgs &a, int max_items, double avg_pairs, int tt, hipStream_t st);
+template <int T, int TT>
+void launch_mmq_t(bool gateup, dim3 grid, const GemvArgs &a, hipStream_t st) {
+  if (gateup)
+    hipLaunchKernelGGL((k_mmq<T, true, TT>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((k_mmq<T, false, TT>), grid, dim3(256), 0, st, a);
+}
+// tt: 16-token tiles per work item (the tiling the item list was cut with)
+int launch_mmq(int type, bool gateup, const GemvArgs &a, int max_items, double avg_pairs, int tt, hipStream_t st) {
   if (!mmq_applies(type, avg_pairs)) return 1;
   if ((size_t)a.nrows * a.w_rstride >= (1ull << 31) || max_items <= 0) return 1;
   const dim3 grid((unsigned)((a.nrows + 63) / 64), (unsigned)max_items);
   if (type == T_Q4_K) {
-    if (gateup)
-      hipLaunchKernelGGL((k_mmq<T_Q4_K, true>), grid, dim3(256), 0, st, a);
-    else
-      hipLaunchKernelGGL((k_mmq<T_Q4_K, false>), grid, dim3(256), 0, st, a);
+    if (tt == 4) launch_mmq_t<T_Q4_K, 4>(gateup, grid, a, st);
+    else launch_mmq_t<T_Q4_K, 2>(gateup, grid, a, st);
   } else {
-    if (gateup)
-      hipLaunchKernelGGL((k_mmq<T_Q2_K, true>), grid, dim3(256), 0, st, a);
-    else
-      hipLaunchKernelGGL((k_mmq<T_Q2_K, false>), grid, dim3(256), 0, st, a);
+    if (tt == 4) launch_mmq_t<T_Q2_K, 4>(gateup, grid, a, st);
+    else launch_mmq_t<T_Q2_K, 2>(gateup, grid, a, st);
   }
   HIP_OK(hipGetLastError());
   return 0;
@@ -406,11 +414,12 @@ int zm_mul_mat_id(const zm_tensor *w, const zm_tensor *x, const zm_tensor *ids, 
     // the MFMA path addresses the activations through a 32-bit buffer offset
     const double avg = (size_t)nq * q8_row_bytes(nb) < (1ull << 31) ? (double)n_pairs / groups : 0.0;
     if (mmq_applies(w->type, avg))
-      hipLaunchKernelGGL(k_mmq_items, dim3(1), dim3(1024), 0, st, n_active, active, offs, items, n_items);
+      hipLaunchKernelGGL(k_mmq_items, dim3(1), dim3(1024), 0, st, n_active, active, offs, items, n_items,
+                         16 * mmq_tt(w->type, false));
     a.items = items;
     a.n_items = n_items;
     a.xq_bytes = (uint32_t)((size_t)nq * q8_row_bytes(nb));
-    const int rc = launch_mmq(w->type, false, a, mmq_max_items((int)n_pairs, (int)E), avg, st);
+    const int rc = launch_mmq(w->type, false, a, mmq_max_items((int)n_pairs, (int)E), avg, mmq_tt(w->type, false), st);
     if (rc < 0 || (rc > 0 && launch_gemv(w->type, false, pick_np((int)n_pairs, (int)E), a, groups, st))) return 0;
   }
   g_mmid_launches.fetch_add(1, std::memory_order_relaxed);
@@ -814,13 +823,15 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
   a.signs = d->signs;
   const double avg_pairs = (double)(S * K) / std::max(1, std::min(NS, S * K));
   const int max_items = mmq_max_items(S * K, NS);
+  const int tt = L->type_gate == T_Q4_K && L->type_down == T_Q4_K ? 4 : 2;  // tiles per routed item
   if (mmq_applies(L->type_gate, avg_pairs) || mmq_applies(L->type_down, avg_pairs))
-    hipLaunchKernelGGL(k_mmq_items, dim3(1), dim3(1024), 0, st, w.n_active, w.active, w.offs, w.items, w.n_items);
+    hipLaunchKernelGGL(k_mmq_items, dim3(1), dim3(1024), 0, st, w.n_active, w.active, w.offs, w.items, w.n_items,
+                       16 * tt);
   a.items = w.items;
   a.n_items = w.n_items;
   a.xq_bytes = (uint32_t)((size_t)S * q8_row_bytes(nbH));
   {
-    const int rc = launch_mmq(L->type_gate, true, a, max_items, avg_pairs, st);
+    const int rc = launch_mmq(L->type_gate, true, a, max_items, avg_pairs, tt, st);
     if (rc < 0 || (rc > 0 && launch_gemv(L->type_gate, true, np, a, groups, st))) return -1;
   }
   // act -> Q8_K
@@ -845,7 +856,7 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
   b.out_s = (size_t)K * H;
   b.out_k = H;
   {
-    const int rc = launch_mmq(L->type_down, false, b, max_items, avg_pairs, st);
+    const int rc = launch_mmq(L->type_down, false, b, max_items, avg_pairs, tt, st);
     if (rc < 0 || (rc > 0 && launch_gemv(L->type_down, false, np, b, groups, st))) return -1;
   }
   // shared expert (dense over all tokens)
@@ -872,7 +883,7 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
     c.signs = d->signs;
     const int nps = S >= 4 ? 4 : (S >= 2 ? 2 : 1);
     {
-      const int rc = launch_mmq(L->type_shared, true, c, (S + MMQ_TOK - 1) / MMQ_TOK, (double)S, st);
+      const int rc = launch_mmq(L->type_shared, true, c, (S + 31) / 32, (double)S, 2, st);
       if (rc < 0 || (rc > 0 && launch_gemv(L->type_shared, true, nps, c, 1, st))) return -1;
     }
     if (launch_quant(w.act_s, (size_t)Fs, nbS, S, w.aq_s, q8_row_bytes(nbS), 1, st)) return -1;
@@ -888,7 +899,7 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
     e2.out = w.y_s;
     e2.out_s = H;
     {
-      const int rc = launch_mmq(L->type_shared, false, e2, (S + MMQ_TOK - 1) / MMQ_TOK, (double)S, st);
+      const int rc = launch_mmq(L->type_shared, false, e2, (S + 31) / 32, (double)S, 2, st);
       if (rc < 0 || (rc > 0 && launch_gemv(L->type_shared, false, nps, e2, 1, st))) return -1;
     }
     ys = w.y_s;

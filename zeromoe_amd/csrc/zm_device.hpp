@@ -230,12 +230,12 @@ __device__ __forceinline__ uint32_t group_max_u32(uint32_t k, int W) {
   step(std::integral_constant<int, DPP_HALF_MIRROR>{});
   step(std::integral_constant<int, DPP_MIRROR>{});
   if (W >= 32) {
-    const uint32_t o = (uint32_t)__shfl_xor((int)k, 16, 64);
-    k = o > k ? o : k;
-  }
-  if (W >= 64) {
-    const uint32_t o = (uint32_t)__shfl_xor((int)k, 32, 64);
-    k = o > k ? o : k;
+    // the four 16-lane row maxima through scalar registers
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)k, 0), r1 = (uint32_t)__builtin_amdgcn_readlane((int)k, 16);
+    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)k, 32), r3 = (uint32_t)__builtin_amdgcn_readlane((int)k, 48);
+    const uint32_t lo = r0 > r1 ? r0 : r1, hi = r2 > r3 ? r2 : r3;
+    if (W >= 64) return lo > hi ? lo : hi;
+    k = (threadIdx.x & 32) ? hi : lo;
   }
   return k;
 }

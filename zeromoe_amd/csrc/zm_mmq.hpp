@@ -5,16 +5,22 @@
 // gate/up optionally fused with SwiGLU (moe_routed_ggml.hpp:166-191).
 //
 // Tile: one wave computes 16 tokens x 16 weight rows with
-// v_mfma_i32_16x16x32_i8, tokens as the A operand and weight rows as the B
+// v_mfma_i32_16x16x64_i8, tokens as the A operand and weight rows as the B
 // operand, so every lane's four outputs belong to ONE weight row (lane % 16)
-// whose scales the lane has decoded itself.  A Q4_K sub-block (32 weights,
-// one 6-bit scale and min) is exactly one MFMA K step:
-//   isum[t][r] += sc[r][sb] * (q[r] . x[t])_sb            (int32, exact)
-//   imin[t][r]  = sum_sb bsum[t][sb] * m[r][sb]           (v_mfma_f32_16x16x4f32;
-//                 |terms| < 2^18, sums < 2^24: exact in fp32)
-//   f[t][r]    += d_x[t] * (d[r] * isum - dmin[r] * imin)  (ggml's vec_dot_q4_K_q8_K combine)
-// The weight nibbles feed the MFMA directly (0..15 as int8): no dequantized
-// copy is materialized.
+// and every lane's 16 B-operand bytes to one 32-weight sub-block of that row,
+// whose 6-bit scale sc = 8*hi + lo the lane has decoded itself.  The scale is
+// folded into the weights: the lane multiplies its nibbles by lo and by hi
+// (products <= 105, int8), and two MFMA chains accumulate over the block:
+//   isum[t][r] = D_lo + 8 * D_hi = sum_sb sc[r][sb] * (q[r] . x[t])_sb  (int32, exact)
+//   imin[t][r] = sum_sb bsum[t][sb] * m[r][sb]           (v_mfma_f32_16x16x4f32;
+//                |terms| < 2^18, sums < 2^24: exact in fp32)
+//   f[t][r]   += d_x[t] * (d[r] * isum - dmin[r] * imin)  (ggml's vec_dot_q4_K_q8_K combine)
+// K order of a 64-weight chunk i (qs bytes 32i..32i+31): k-group g holds the
+// low nibbles (g < 2) or high nibbles (g >= 2) of bytes 16*(g & 1)..+15, i.e.
+// weights 64i + 16g .. +15, so the activation operand is the contiguous 16
+// bytes 64i + 16g of the token's row.  The weight unpacking is done once per
+// block for all MMQ_TT token tiles of the work item.
+// No dequantized weight copy is materialized.
 //
 // Q2_K uses v_mfma_i32_16x16x64_i8 with the 4-bit sub-block scale folded into
 // the weights (q * sc <= 45 fits int8): lane (row n, k-group g) of 64-weight
@@ -43,25 +49,23 @@ __device__ __forceinline__ uint32_t mul_bytes(uint32_t packed, uint32_t f) {
   return __builtin_bit_cast(uint32_t, p * m);
 }
 
-constexpr int MMQ_TT = 2;              // 16-token tiles per work item
-constexpr int MMQ_TOK = 16 * MMQ_TT;   // pairs per work item
+constexpr int MMQ_TOK = 32;            // pairs per work item of the 2-tile kernels (item count bound)
 constexpr int MMQ_XS = QK + 16;        // LDS stride of one token's qs (bank spread)
 
-__device__ __forceinline__ long u2l(uint2 v) { return (long)(((unsigned long)v.y << 32) | v.x); }
 
-// Work items: every active expert's bucket cut into runs of MMQ_TOK pairs,
+// Work items: every active expert's bucket cut into runs of `tok` pairs,
 // item = expert | (first pair offset within the bucket) << 12.  One workgroup.
 __global__ __launch_bounds__(1024) void k_mmq_items(const int32_t *__restrict__ n_active,
                                                     const int32_t *__restrict__ active,
                                                     const int32_t *__restrict__ offs, int32_t *__restrict__ items,
-                                                    int32_t *__restrict__ n_items) {
+                                                    int32_t *__restrict__ n_items, int tok) {
   __shared__ int s_n[1024];
   const int na = *n_active;
   int total = 0;
   for (int base = 0; base < na; base += 1024) {
     const int i = base + (int)threadIdx.x;
     const int e = i < na ? active[i] : 0;
-    const int np = i < na ? (offs[e + 1] - offs[e] + MMQ_TOK - 1) / MMQ_TOK : 0;
+    const int np = i < na ? (offs[e + 1] - offs[e] + tok - 1) / tok : 0;
     s_n[threadIdx.x] = np;
     __syncthreads();
     for (int d = 1; d < 1024; d <<= 1) {  // inclusive scan
@@ -71,14 +75,14 @@ __global__ __launch_bounds__(1024) void k_mmq_items(const int32_t *__restrict__ 
       __syncthreads();
     }
     const int start = total + s_n[threadIdx.x] - np;
-    for (int q = 0; q < np; ++q) items[start + q] = e | ((q * MMQ_TOK) << 12);
+    for (int q = 0; q < np; ++q) items[start + q] = e | ((q * tok) << 12);
     total += s_n[1023];
     __syncthreads();
   }
   if (threadIdx.x == 0) *n_items = total;
 }
 
-// One work item (up to MMQ_TOK pairs of one bucket) against 64 weight rows
+// One work item (up to 16*TT pairs of one bucket) against 64 weight rows
 // (4 waves x 16 rows).  The activation block of the item is staged in LDS
 // (double buffered over the K blocks; each thread holds the next block's share
 // in registers while the current block computes); the weights of block b+1
@@ -86,9 +90,9 @@ __global__ __launch_bounds__(1024) void k_mmq_items(const int32_t *__restrict__ 
 template <int T>
 struct MmqW;
 template <>
-struct MmqW<T_Q4_K> {  // d, dmin, scales | this lane's 4 x 8 bytes of qs
+struct MmqW<T_Q4_K> {  // d, dmin, scales | this lane's 4 x 16 bytes of qs
   uint4 hdr;
-  uint2 qs[4];
+  uint4 qs[4];
 };
 template <>
 struct MmqW<T_Q2_K> {  // scales | this lane's 2 x 16 bytes of qs | d, dmin
@@ -97,19 +101,20 @@ struct MmqW<T_Q2_K> {  // scales | this lane's 2 x 16 bytes of qs | d, dmin
   uint32_t dd;
 };
 
-template <int T, bool GATEUP>
+template <int T, bool GATEUP, int TT>
 __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
+  constexpr int TOK = 16 * TT;  // pairs per work item
   static_assert(T == T_Q4_K || T == T_Q2_K, "MFMA prefill types");
   constexpr int NBS = T == T_Q4_K ? 8 : 16;  // bsums per block used: 32-sums (Q4_K) or 16-sums (Q2_K)
-  __shared__ __attribute__((aligned(16))) uint8_t s_xq[2][MMQ_TOK][MMQ_XS];
-  __shared__ int s_bs[2][MMQ_TOK][NBS];
-  __shared__ float s_xd[2][MMQ_TOK];
-  __shared__ int s_xoff[MMQ_TOK];      // byte offset of each pair's activation row (OOR: none)
-  __shared__ int s_pair[MMQ_TOK];
+  __shared__ __attribute__((aligned(16))) uint8_t s_xq[2][TOK][MMQ_XS];
+  __shared__ int s_bs[2][TOK][NBS];
+  __shared__ float s_xd[2][TOK];
+  __shared__ int s_xoff[TOK];      // byte offset of each pair's activation row (OOR: none)
+  __shared__ int s_pair[TOK];
   int e, pc, p1;
   if (a.dense_S > 0) {
     e = 0;
-    pc = blockIdx.y * MMQ_TOK;
+    pc = blockIdx.y * TOK;
     p1 = a.dense_S;
     if (pc >= p1) return;
   } else {
@@ -133,9 +138,9 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
   const int vrow = rv ? row * (int)a.w_rstride : OOR;
   const int Kp = a.dense_S > 0 ? 1 : a.K;
   const int nb = a.nb;
-  const int nt = min(MMQ_TT, (p1 - pc + 15) / 16);
+  const int nt = min(TT, (p1 - pc + 15) / 16);
 
-  if (tid < MMQ_TOK) {
+  if (tid < TOK) {
     const int p = pc + tid;
     const bool ok = p < p1;
     const int pair = ok ? (a.dense_S > 0 ? p : a.pairs[p]) : -1;
@@ -152,7 +157,7 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
       if constexpr (T == T_Q4_K) {
         w[m].hdr = bld16(rw[m], vo, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) w[m].qs[i] = bld8(rw[m], vo + 16 + 32 * i + 8 * g, 0);
+        for (int i = 0; i < 4; ++i) w[m].qs[i] = bld16(rw[m], vo + 16 + 32 * i + 16 * (g & 1), 0);
       } else {
         w[m].sc = bld16(rw[m], vo, 0);
 #pragma unroll
@@ -163,54 +168,61 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
   };
   // this thread's share of an activation block: qs chunks c = tid, tid + 256
   // (token c >> 4, 16-byte chunk c & 15), one 32-weight bsum (token tid >> 3,
-  // sub-block tid & 7), and d of token tid (tid < MMQ_TOK)
+  // sub-block tid & 7), and d of token tid (tid < TOK)
+  constexpr int NBSH = (TOK * 8 + 255) / 256;  // bsum dwords per thread
   struct XShare {
-    uint4 q[MMQ_TOK * 16 / 256];
-    uint32_t bs;
+    uint4 q[TOK * 16 / 256];
+    uint32_t bs[NBSH];
     float d;
   };
-  static_assert(MMQ_TOK * 16 % 256 == 0 && MMQ_TOK * 8 <= 256, "staging shares");
+  static_assert(TOK * 16 % 256 == 0 && TOK <= 256, "staging shares");
   auto load_x = [&](int b, XShare &x) {
     const bool bv = b < nb;
 #pragma unroll
-    for (int r = 0; r < MMQ_TOK * 16 / 256; ++r) {
+    for (int r = 0; r < TOK * 16 / 256; ++r) {
       const int c = tid + 256 * r, t = c >> 4, ch = c & 15;
       const int o = s_xoff[t];
       x.q[r] = bld16(rx, (bv && o != OOR) ? o + b * QK + 16 * ch : OOR, 0);
     }
-    {
-      const int t = (tid >> 3) & (MMQ_TOK - 1), sb = tid & 7;
+#pragma unroll
+    for (int r = 0; r < NBSH; ++r) {
+      const int c = tid + 256 * r;
+      const int t = (c >> 3) & (TOK - 1), sb = c & 7;
       const int o = s_xoff[t];
-      x.bs = __builtin_amdgcn_raw_buffer_load_b32(rx, (bv && o != OOR && tid < MMQ_TOK * 8) ? o + (int)q8_bs_off(nb) + b * 32 + 4 * sb : OOR, 0, 0);
+      x.bs[r] = __builtin_amdgcn_raw_buffer_load_b32(rx, (bv && o != OOR && c < TOK * 8) ? o + (int)q8_bs_off(nb) + b * 32 + 4 * sb : OOR, 0, 0);
     }
     {
-      const int o = s_xoff[tid & (MMQ_TOK - 1)];
-      x.d = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, (bv && o != OOR && tid < MMQ_TOK) ? o + (int)q8_d_off(nb) + 4 * b : OOR, 0, 0));
+      const int o = s_xoff[tid & (TOK - 1)];
+      x.d = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, (bv && o != OOR && tid < TOK) ? o + (int)q8_d_off(nb) + 4 * b : OOR, 0, 0));
     }
   };
   auto store_x = [&](const XShare &x, int buf) {
 #pragma unroll
-    for (int r = 0; r < MMQ_TOK * 16 / 256; ++r) {
+    for (int r = 0; r < TOK * 16 / 256; ++r) {
       const int c = tid + 256 * r, t = c >> 4, ch = c & 15;
       *reinterpret_cast<uint4 *>(&s_xq[buf][t][16 * ch]) = x.q[r];
     }
-    if (tid < MMQ_TOK * 8) {
-      const int lo = (int)(int16_t)(x.bs & 0xffffu), hi = (int)(int16_t)(x.bs >> 16);
-      if constexpr (T == T_Q4_K) {
-        s_bs[buf][tid >> 3][tid & 7] = lo + hi;
-      } else {
-        s_bs[buf][tid >> 3][2 * (tid & 7)] = lo;
-        s_bs[buf][tid >> 3][2 * (tid & 7) + 1] = hi;
+#pragma unroll
+    for (int r = 0; r < NBSH; ++r) {
+      const int c = tid + 256 * r;
+      if (c < TOK * 8) {
+        const int lo = (int)(int16_t)(x.bs[r] & 0xffffu), hi = (int)(int16_t)(x.bs[r] >> 16);
+        if constexpr (T == T_Q4_K) {
+          s_bs[buf][c >> 3][c & 7] = lo + hi;
+        } else {
+          s_bs[buf][c >> 3][2 * (c & 7)] = lo;
+          s_bs[buf][c >> 3][2 * (c & 7) + 1] = hi;
+        }
       }
     }
-    if (tid < MMQ_TOK) s_xd[buf][tid] = x.d;
+    if (tid < TOK) s_xd[buf][tid] = x.d;
   };
 
-  float f[NM][MMQ_TT][4];
+  float f[NM][TT][4];
 #pragma unroll
   for (int m = 0; m < NM; ++m)
 #pragma unroll
-    for (int t = 0; t < MMQ_TT; ++t)
+    for (int t = 0; t < TT; ++t)
 #pragma unroll
       for (int j = 0; j < 4; ++j) f[m][t][j] = 0.f;
 
@@ -234,32 +246,41 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
       const float d = h2f((uint16_t)(wcur[m].hdr.x & 0xffffu)), dmin = h2f((uint16_t)(wcur[m].hdr.x >> 16));
       // B operand of the min product: m[row][sb] for sb = g and g + 4
       const float mb0 = (float)((mn_lo >> (8 * g)) & 0xffu), mb1 = (float)((mn_hi >> (8 * g)) & 0xffu);
+      // scale-folded weights of the 4 chunks: lane's sub-block 2i + (g >> 1),
+      // sc = 8 * hi + lo
+      v4i_t bl[4], bh[4];
+      const int hs = 8 * (g >> 1), ns = 4 * (g >> 1);
 #pragma unroll
-      for (int t = 0; t < MMQ_TT; ++t) {
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t scw = i < 2 ? sc_lo : sc_hi;
+        const uint32_t sc = (scw >> (16 * (i & 1) + hs)) & 0xffu;
+        const uint32_t lo = sc & 7u, hi = sc >> 3;
+        const uint4 q = wcur[m].qs[i];
+        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const uint32_t nib = (qw[c] >> ns) & 0x0f0f0f0fu;
+          bl[i][c] = (int)mul_bytes(nib, lo);
+          bh[i][c] = (int)mul_bytes(nib, hi);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
         if (t >= nt) continue;
         const uint8_t *xr = &s_xq[buf][16 * t + n][0];
-        int isum[4] = {0, 0, 0, 0};
+        v4i_t dlo = {0, 0, 0, 0}, dhi = {0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const uint2 q = wcur[m].qs[i];
-          const long wl = u2l(make_uint2(q.x & 0x0f0f0f0fu, q.y & 0x0f0f0f0fu));
-          const long wh = u2l(make_uint2((q.x >> 4) & 0x0f0f0f0fu, (q.y >> 4) & 0x0f0f0f0fu));
-          const long xl = *reinterpret_cast<const long *>(xr + 64 * i + 8 * g);
-          const long xh = *reinterpret_cast<const long *>(xr + 64 * i + 32 + 8 * g);
-          const v4i_t z = {0, 0, 0, 0};
-          const v4i_t dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(xl, wl, z, 0, 0, 0);
-          const v4i_t dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(xh, wh, z, 0, 0, 0);
-          const uint32_t scw = i < 2 ? sc_lo : sc_hi;
-          const int s0 = (int)((scw >> (16 * (i & 1))) & 0xffu), s1 = (int)((scw >> (16 * (i & 1) + 8)) & 0xffu);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) isum[j] += __mul24(s0, dl[j]) + __mul24(s1, dh[j]);
+          const v4i_t xa = *reinterpret_cast<const v4i_t *>(xr + 64 * i + 16 * g);
+          dlo = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, bl[i], dlo, 0, 0, 0);
+          dhi = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, bh[i], dhi, 0, 0, 0);
         }
         v4f_t mn = {0.f, 0.f, 0.f, 0.f};
         mn = __builtin_amdgcn_mfma_f32_16x16x4f32((float)s_bs[buf][16 * t + n][g], mb0, mn, 0, 0, 0);
         mn = __builtin_amdgcn_mfma_f32_16x16x4f32((float)s_bs[buf][16 * t + n][g + 4], mb1, mn, 0, 0, 0);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          f[m][t][j] += s_xd[buf][16 * t + 4 * g + j] * (d * (float)isum[j] - dmin * mn[j]);
+          f[m][t][j] += s_xd[buf][16 * t + 4 * g + j] * (d * (float)(dlo[j] + 8 * dhi[j]) - dmin * mn[j]);
       }
     }
     } else {
@@ -286,7 +307,7 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
         for (int k = 0; k < 4; ++k) bq[c][k] = (int)mul_bytes((qw[k] >> (2 * j)) & 0x03030303u, sc);
       }
 #pragma unroll
-      for (int t = 0; t < MMQ_TT; ++t) {
+      for (int t = 0; t < TT; ++t) {
         if (t >= nt) continue;
         const uint8_t *xr = &s_xq[buf][16 * t + n][0];
         v4i_t isum = {0, 0, 0, 0};
@@ -316,7 +337,7 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
   // lane holds (pair pc + 16t + 4g + j, row): store out[tok][k][row]
   if (rv) {
 #pragma unroll
-    for (int t = 0; t < MMQ_TT; ++t) {
+    for (int t = 0; t < TT; ++t) {
       if (t >= nt) continue;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
