@@ -9,7 +9,8 @@ cycling over layer replicas so the working set exceeds the 256 MB
 Infinity Cache; inputs are resident in HBM before the timed region.
 
 Prints ONE JSON line.  The other configurations are reported under
-"extras" (c1, c3 prefill tok/s, c4, c5 at S=1 and S=64).  cpu_baseline times the CPU
+"extras" (c1, c3 prefill tok/s, c4, c5 at S=1 and S=64, and the expert-record
+unpack at c2's expert shape).  cpu_baseline times the CPU
 restatement of ggml's MUL_MAT_ID layer (oracle/) on this host.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
@@ -200,6 +201,40 @@ def time_launches(torch, step, first, n):
     return {"mean": e0.elapsed_time(e1) * 1e3 / n, "launches": n}
 
 
+def run_unpack(torch, Z, steps, warmup, records=32):
+    """Expert-record unpack at c2's expert shape: `records` [gate|up|down]
+    records (6.83 MB each) split into the planar expert tensors by one
+    launch_ggml_moe_unpack_scatter call (slots in reverse order).  Bytes moved =
+    2 x record bytes (each read once, written once); a same-size device copy
+    (hipMemcpyAsync via torch) is timed beside it as the practical ceiling."""
+    c = CONFIGS["c2"]
+    H, F = c["H"], c["F"]
+    parts = (F * row_bytes(c["tg"], H), F * row_bytes(c["tg"], H), H * row_bytes(c["td"], F))
+    rec = sum(parts)
+    src = torch.randint(0, 256, (records * rec,), dtype=torch.uint8, device="cuda")
+    dst = [torch.empty(records * p, dtype=torch.uint8, device="cuda") for p in parts]
+    slots = torch.arange(records - 1, -1, -1, dtype=torch.int32, device="cuda")
+    flat = torch.empty_like(src)
+
+    def unpack(_):
+        Z.moe_unpack(src, *dst, records, rec, parts, slots=slots)
+
+    def copy(_):
+        flat.copy_(src)
+
+    for i in range(warmup):
+        unpack(i)
+        copy(i)
+    n = max(20, steps)
+    t_u = time_launches(torch, unpack, 0, n)["mean"]
+    t_c = time_launches(torch, copy, 0, n)["mean"]
+    moved = 2 * records * rec
+    return {"us": t_u, "GBps": moved / (t_u * 1e-6) / 1e9, "frac": moved / (t_u * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "copy_us": t_c, "copy_GBps": moved / (t_c * 1e-6) / 1e9, "bytes_moved": moved, "records": records,
+            "workload": f"unpack {records} c2 expert records (Q2_K gate/up, Q3_K down, {rec} B each) to planar "
+                        f"tensors via the slot table"}
+
+
 def cpu_baseline(seconds: float = 10.0):
     """CPU restatement of ggml's MUL_MAT_ID layer (oracle/zm_oracle.c) on this
     host's cores at the c2 shape, S=1: ids re-drawn every iteration over a
@@ -303,7 +338,7 @@ def stats_summary(d, out_path, command, top=8):
     lines = [f"# rocprofv3 kernel stats", f"# command: {command}",
              f"{'calls':>6} {'avg_us':>9} {'min_us':>9} {'max_us':>9} {'pct':>6}  kernel"]
     for r in rows[:top]:
-        name = re.sub(r"\(.*", "", r["Name"].replace("void ", ""))[:100]
+        name = re.sub(r"\(.*", "", r["Name"].replace("void ", "").replace("(anonymous namespace)::", ""))[:100]
         lines.append(f"{int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.2f} {float(r['MinNs']) / 1e3:9.2f} "
                      f"{float(r['MaxNs']) / 1e3:9.2f} {float(r['Percentage']):6.2f}  {name}")
     with open(out_path, "w") as fh:
@@ -329,6 +364,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--replicas", type=int, default=0, help="layer replicas (0 = enough to exceed the MALL)")
     ap.add_argument("--extras", default="c1,c3,c4,c5,c5_s64", help="extra configs to report ('' for none)")
+    ap.add_argument("--no-unpack", dest="unpack", action="store_false",
+                    help="skip the expert-record unpack extra")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch every step from Python instead of a HIP graph")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -364,6 +401,10 @@ def main():
         per = NS * expert_bytes(c)
         return max(2, min(16, int(1.2e9 // per) + 2))
 
+    if args.profile == "unpack":
+        r = run_unpack(torch, Z, args.steps, args.warmup)
+        print(json.dumps({"profile": "unpack", "us": round(r["us"], 2), "GBps": round(r["GBps"], 1)}))
+        return
     if args.profile:
         r = run_config(torch, Z, args.profile, args.steps, args.warmup, reps(args.profile), use_graph=False)
         copy_probe(torch)
@@ -381,6 +422,9 @@ def main():
         r = run_config(torch, Z, name, st, max(3, args.warmup // 2), reps(name), use_graph=not args.eager)
         extras[name] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}
         extras[name]["workload"] = WORKLOAD[name]
+    if args.unpack:
+        r = run_unpack(torch, Z, args.steps, args.warmup)
+        extras["unpack"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     line = {
         "metric": METRIC,

@@ -243,6 +243,27 @@ int zm_expert_ffn_finish_stage2(zm_expert_scratch *s, float *host_out, int S, in
 /* Read (and optionally reset) the NaN / Inf counters. */
 int zm_expert_bad_counts(zm_expert_scratch *s, int32_t counts[2], int reset);
 
+/* ---------------------------------------------------------------- expert records
+ *
+ * Device-local unpack of expert-major transfer records [gate | up | down]
+ * (record i at src + i*src_stride; gate_bytes, up_bytes, down_bytes each)
+ * into the three planar per-expert tensors: record i's gate bytes go to
+ * gate + e*gate_stride, and likewise for up and down, where e = i
+ * (launch_ggml_moe_unpack) or e = dst_slots[i] (_scatter; a negative slot
+ * skips the record).  Bytes outside each part are not written; two records
+ * with the same slot race.  Stream-ordered; returns a hipError_t value: 0 on
+ * success, hipErrorInvalidValue (1) for a NULL pointer or count <= 0.
+ * Replace launch_ggml_moe_unpack / launch_ggml_moe_unpack_scatter
+ * (kernels/math/ggml_moe_pack.cu:127-179; called from
+ * backends/ggml/ggml_moe_transfer_manager.cpp:395,598,725,859). */
+int launch_ggml_moe_unpack(const void *src, void *gate, void *up, void *down, int count, size_t src_stride,
+                           size_t gate_bytes, size_t up_bytes, size_t down_bytes, size_t gate_stride,
+                           size_t up_stride, size_t down_stride, void *stream);
+int launch_ggml_moe_unpack_scatter(const void *src, void *gate, void *up, void *down, const int32_t *dst_slots,
+                                   int count, size_t src_stride, size_t gate_bytes, size_t up_bytes,
+                                   size_t down_bytes, size_t gate_stride, size_t up_stride, size_t down_stride,
+                                   void *stream);
+
 /* Debug: copy the last decode launch's phase timestamps (8 per workgroup,
  * wall_clock64 ticks; recorded only when ZEROMOE_TRACE=1) into host[n].
  * Synchronises the device.  Returns the count copied. */

@@ -420,6 +420,46 @@ def glm5next_router_topk(logits: np.ndarray, topk: int, bias=None, gating: int =
     return L, ids, ws
 
 
+# ---------------------------------------------------------------- expert records (numpy)
+
+
+def moe_unpack(src: np.ndarray, gate: np.ndarray, up: np.ndarray, down: np.ndarray, count: int, src_stride: int,
+               part_bytes, dst_strides=None, slots=None) -> None:
+    """In place: record i of `src` (bytes [i*src_stride, +gate+up+down)) is
+    split into gate/up/down at expert e*dst_stride, e = i or slots[i]
+    (negative: skipped).  kernels/math/ggml_moe_pack.cu:13-60 (unpack) and
+    :62-113 (scatter): a plain byte copy per part, parts consecutive in the
+    record, nothing outside a part written."""
+    gb, ub, db = part_bytes
+    strides = dst_strides if dst_strides is not None else part_bytes
+    for i in range(count):
+        e = i if slots is None else int(slots[i])
+        if e < 0:
+            continue
+        base = i * src_stride
+        off = base
+        for dst, nbytes, st in ((gate, gb, strides[0]), (up, ub, strides[1]), (down, db, strides[2])):
+            dst[e * st:e * st + nbytes] = src[off:off + nbytes]
+            off += nbytes
+
+
+def moe_pack(gate: np.ndarray, up: np.ndarray, down: np.ndarray, experts, src_stride: int, part_bytes,
+             dst_strides=None, fill: int = 0) -> np.ndarray:
+    """The transfer records the unpack consumes, built the other way round
+    (expert rows concatenated, each record padded to src_stride with `fill`)
+    -- the inverse used to pin moe_unpack by round trip
+    (backends/ggml/ggml_moe_transfer_manager.cpp:700-712 copies one record of
+    weight_raw_expert_stride_ bytes per expert)."""
+    gb, ub, db = part_bytes
+    strides = dst_strides if dst_strides is not None else part_bytes
+    recs = []
+    for e in experts:
+        r = np.concatenate([gate[e * strides[0]:e * strides[0] + gb], up[e * strides[1]:e * strides[1] + ub],
+                            down[e * strides[2]:e * strides[2] + db]])
+        recs.append(np.concatenate([r, np.full(src_stride - r.size, fill, np.uint8)]))
+    return np.concatenate(recs) if recs else np.zeros(0, np.uint8)
+
+
 # ---------------------------------------------------------------- reference build (oracle/_ref)
 
 _ref = None

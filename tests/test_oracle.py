@@ -540,3 +540,37 @@ def test_glm_router_ties_and_nan():
     lg = np.array([[1, np.nan, 4, 3]], np.float32)
     _, ids, _ = O.glm5next_router_topk(lg, 3, gating=O.GATING_SIGMOID)
     assert list(ids[0]) == [2, 3, 0]  # a NaN elsewhere is never chosen
+
+
+# ------------------------------------------------------------------ expert records
+
+def test_moe_unpack_known_answer():
+    """Two 10-byte records [g g g | u u | d d d d d] + 2 bytes padding: the
+    hand-written destination bytes (kernels/math/ggml_moe_pack.cu:39-60)."""
+    src = np.arange(24, dtype=np.uint8)
+    g, u, d = (np.full(n, 255, np.uint8) for n in (8, 6, 12))
+    O.moe_unpack(src, g, u, d, 2, 12, (3, 2, 5), dst_strides=(4, 3, 6))
+    np.testing.assert_array_equal(g, [0, 1, 2, 255, 12, 13, 14, 255])
+    np.testing.assert_array_equal(u, [3, 4, 255, 15, 16, 255])
+    np.testing.assert_array_equal(d, [5, 6, 7, 8, 9, 255, 17, 18, 19, 20, 21, 255])
+
+
+def test_moe_unpack_inverts_pack_and_scatter_skips():
+    """pack (rows concatenated per expert) then scatter-unpack into fresh
+    tensors gives back exactly the packed experts' bytes; slot -1 records and
+    the bytes between experts stay untouched."""
+    rng = np.random.default_rng(3)
+    parts, strides, E = (1344, 1344, 1760), (1408, 1344, 1792), 6
+    planar = [rng.integers(0, 256, E * s, dtype=np.uint8) for s in strides]
+    experts = [4, 0, 5, 2]
+    rs = sum(parts) + 48
+    src = O.moe_pack(*planar, experts, rs, parts, strides, fill=0xAB)
+    slots = np.array([4, -1, 5, 2], np.int32)
+    out = [np.full(E * s, 7, np.uint8) for s in strides]
+    O.moe_unpack(src, *out, 4, rs, parts, strides, slots)
+    for p in range(3):
+        for e in range(E):
+            lo, hi = e * strides[p], e * strides[p] + parts[p]
+            want = planar[p][lo:hi] if e in (4, 5, 2) else np.full(parts[p], 7, np.uint8)
+            np.testing.assert_array_equal(out[p][lo:hi], want)
+            np.testing.assert_array_equal(out[p][hi:(e + 1) * strides[p]], 7)

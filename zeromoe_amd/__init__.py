@@ -18,15 +18,18 @@ libzeromoe_hip.so (include/zeromoe.h):
   (kernels/math/expert_activation.cu, expert_accum.cu,
   kernels/models/glm5next_router.cu) and :class:`ExpertExecutor`
   (core/gpu_expert_executor.hpp:42-58).
+* :func:`moe_unpack` -- expert-major [gate|up|down] transfer records to the
+  planar expert tensors (launch_ggml_moe_unpack[_scatter],
+  kernels/math/ggml_moe_pack.cu:127-179).
 
 Torch is used only for device memory and the current stream.
 """
 from __future__ import annotations
 
 from .ops import (GGML_TYPES, ExpertExecutor, MoELayer, block_dots, bucket, builtin_iq2xxs_grid, f32_matmul,
-                  glm5next_router_topk, init, mul_mat_id, mul_mat_id_f32, quantize_q8_K, router, row_size,
+                  glm5next_router_topk, init, moe_unpack, mul_mat_id, mul_mat_id_f32, quantize_q8_K, router, row_size,
                   scatter_accum, set_iq2xxs_grid, swiglu)
 
 __all__ = ["GGML_TYPES", "ExpertExecutor", "MoELayer", "block_dots", "bucket", "builtin_iq2xxs_grid", "f32_matmul",
-           "glm5next_router_topk", "init", "mul_mat_id", "mul_mat_id_f32", "quantize_q8_K", "router", "row_size",
+           "glm5next_router_topk", "init", "moe_unpack", "mul_mat_id", "mul_mat_id_f32", "quantize_q8_K", "router", "row_size",
            "scatter_accum", "set_iq2xxs_grid", "swiglu"]

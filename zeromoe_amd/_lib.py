@@ -68,6 +68,8 @@ SIGNATURES = {
     "launch_expert_swiglu": (None, [P, P, P, I, F, I, P, P]),
     "launch_expert_scatter_accum": (None, [P, P, P, P, I, I, I, P]),
     "launch_expert_scatter_add": (None, [P, P, P, I, I, I, P]),
+    "launch_ggml_moe_unpack": (I, [P, P, P, P, I] + [C.c_size_t] * 7 + [P]),
+    "launch_ggml_moe_unpack_scatter": (I, [P, P, P, P, P, I] + [C.c_size_t] * 7 + [P]),
     "launch_glm5next_router_topk": (None, [P, P, P, P, I, I, I, I, I, F, P]),
     "zm_expert_scratch_ensure": (I, [_XS, I, I, I, I]),
     "zm_expert_scratch_release": (None, [_XS]),

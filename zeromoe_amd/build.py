@@ -12,7 +12,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG_DIR)
 SRC = os.path.join(PKG_DIR, "csrc")
 OUT = os.path.join(PKG_DIR, "lib", "libzeromoe_hip.so")
-SOURCES = ("zm_api.hip", "zm_exec.hip")
+SOURCES = ("zm_api.hip", "zm_exec.hip", "zm_pack.hip")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # -ffp-contract=off: the quantizer, router and SwiGLU are bit-reproducible
@@ -23,14 +23,30 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-shared", "-std=c++17", "-ffp
 
 
 def build(verbose: bool = False) -> str:
+    """Compile each translation unit in parallel (hipcc -c), then link."""
     os.makedirs(os.path.dirname(OUT), exist_ok=True)
-    cmd = [HIPCC, *FLAGS, "-o", OUT, *[os.path.join(SRC, f) for f in SOURCES]]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    msgs = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in l)
+    obj_dir = os.path.join(PKG_DIR, "lib", "obj")
+    os.makedirs(obj_dir, exist_ok=True)
+    cflags = [f for f in FLAGS if f != "-shared"]
+    jobs = []
+    for f in SOURCES:
+        obj = os.path.join(obj_dir, f.replace(".hip", ".o"))
+        cmd = [HIPCC, *cflags, "-c", "-o", obj, os.path.join(SRC, f)]
+        jobs.append((cmd, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+    msgs, failed = [], None
+    for cmd, _, p in jobs:
+        out = p.communicate()[0]
+        msgs += [l for l in out.splitlines() if "packed-fp32-ops" not in l]
+        if p.returncode != 0 and failed is None:
+            failed = cmd
+    if failed is not None:
+        raise RuntimeError(f"hipcc failed:\n{' '.join(failed)}\n" + "\n".join(msgs))
+    link = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", OUT, *[o for _, o, _ in jobs]]
+    r = subprocess.run(link, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed:\n{' '.join(cmd)}\n{msgs}")
-    if verbose and msgs.strip():
-        print(msgs)
+        raise RuntimeError(f"link failed:\n{' '.join(link)}\n{r.stdout}{r.stderr}")
+    if verbose and any(m.strip() for m in msgs):
+        print("\n".join(msgs))
     return OUT
 
 

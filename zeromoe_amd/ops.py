@@ -347,3 +347,47 @@ class ExpertExecutor:
 
     def release(self):
         lib().zm_expert_scratch_release(C.byref(self.s))
+
+
+# ---------------------------------------------------------------- expert records
+
+
+def moe_unpack(src: torch.Tensor, gate: torch.Tensor, up: torch.Tensor, down: torch.Tensor, count: int,
+               src_stride: int, part_bytes, dst_strides=None, slots: Optional[torch.Tensor] = None,
+               stream=None) -> None:
+    """Unpack `count` expert-major [gate | up | down] records of `src` (uint8,
+    record i at byte i*src_stride) into the planar per-expert tensors `gate`,
+    `up`, `down` (uint8; expert e at byte e*dst_stride).  Record i lands at
+    expert i, or at slots[i] (int32 device tensor; negative = skip).
+    part_bytes = (gate_bytes, up_bytes, down_bytes); dst_strides defaults to
+    part_bytes.  With slots, every slot must be below the number of experts
+    the destinations hold (not checked: reading slots would synchronise).  launch_ggml_moe_unpack[_scatter]
+    (/root/reference/kernels/math/ggml_moe_pack.cu:127-179)."""
+    for t, n in ((src, "src"), (gate, "gate"), (up, "up"), (down, "down")):
+        _dev(t, n)
+    gb, ub, db = (int(b) for b in part_bytes)
+    gs, us, ds = (int(b) for b in (dst_strides if dst_strides is not None else part_bytes))
+    if count > 0:
+        if (count - 1) * src_stride + gb + ub + db > src.numel():
+            raise ValueError("src holds fewer than `count` records")
+        # expert slots every destination can hold; slot values are the caller's
+        # contract (checking them here would synchronise the stream)
+        cap = min(t.numel() // st if st else (1 << 62) for t, st, b in ((gate, gs, gb), (up, us, ub), (down, ds, db))
+                  if b > 0)
+        if any(b > st for b, st in ((gb, gs), (ub, us), (db, ds)) if b > 0):
+            raise ValueError("a destination stride is smaller than its part")
+        if slots is not None:
+            _dev(slots, "slots")
+            if slots.dtype != torch.int32 or slots.numel() < count:
+                raise ValueError("slots must be int32 with at least `count` entries")
+        elif count > cap:
+            raise ValueError("destination tensors too small for `count` experts")
+    if slots is None:
+        rc = lib().launch_ggml_moe_unpack(src.data_ptr(), gate.data_ptr(), up.data_ptr(), down.data_ptr(), count,
+                                          src_stride, gb, ub, db, gs, us, ds, _stream(stream))
+    else:
+        rc = lib().launch_ggml_moe_unpack_scatter(src.data_ptr(), gate.data_ptr(), up.data_ptr(), down.data_ptr(),
+                                                  slots.data_ptr(), count, src_stride, gb, ub, db, gs, us, ds,
+                                                  _stream(stream))
+    if rc != 0:
+        raise RuntimeError(f"launch_ggml_moe_unpack failed ({rc}): {lib().zm_last_error().decode()}")
