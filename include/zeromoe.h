@@ -17,6 +17,9 @@
 
 #include <stddef.h>
 #include <stdint.h>
+#ifndef __cplusplus
+#include <stdbool.h>
+#endif
 
 #ifdef __cplusplus
 extern "C" {
@@ -39,6 +42,8 @@ enum {
   ZM_TYPE_Q2_K = 10,
   ZM_TYPE_Q3_K = 11,
   ZM_TYPE_Q4_K = 12,
+  ZM_TYPE_Q5_K = 13,
+  ZM_TYPE_Q6_K = 14,
   ZM_TYPE_Q8_K = 15,
   ZM_TYPE_IQ2_XXS = 16,
   ZM_TYPE_I32 = 26,
@@ -71,7 +76,7 @@ int zm_mul_mat_id_negative_skip_batched(void);
 /* GGML_OP_MUL_MAT_ID hook: dst[:, id, t] = W[ids[id, t]] . src1[:, id % ne11, t]
  * with src1 quantized to Q8_K (ggml CPU semantics), id < 0 -> zero row,
  * id >= n_experts -> NaN row.
- *   src0: Q2_K / Q3_K / Q4_K / IQ2_XXS [I, O, E] (row-contiguous)
+ *   src0: Q2_K / Q3_K / Q4_K / Q5_K / Q6_K / IQ2_XXS [I, O, E] (row-contiguous)
  *   src1: F32 [I, ne11, S], ne11 == 1 or n_ids;  ids: I32 [n_ids, S]
  *   dst : F32 [O, n_ids, S]
  * execute = 0 is a pure capability query; execute = 1 launches on `stream`.
@@ -120,7 +125,8 @@ int zm_bucket(const int32_t *ids, int S, int K, int E, int32_t *counts, int32_t 
  * against f32 activations quantized to Q8_K: isum[b], imin[b] as defined in
  * oracle/zm_oracle.h (zmo_block_dots).  Both device dot paths (the bucketed
  * GEMV's and the fused decode kernel's) compute every block; where they
- * disagree isum[b] is INT32_MIN.  Not on the hot path. */
+ * disagree isum[b] is INT32_MIN (Q5_K / Q6_K have only the GEMV's path).
+ * Not on the hot path. */
 int zm_block_dots(int type, const void *w_row, const float *x, int n, int32_t *isum, int32_t *imin, void *stream);
 
 /* ---------------------------------------------------------------- routed layer */
@@ -163,7 +169,7 @@ int zm_moe_forward(const zm_moe_layer *layer, const float *x, const float *logit
  *
  * Quantized weights times f32 activations, no Q8_K step: the reference's CUDA
  * executor semantics, not ggml's CPU ones.  Weight rows are I/256 super-blocks
- * (Q2_K / Q3_K / Q4_K / IQ2_XXS); x must be 16-byte aligned.  Accumulation is
+ * (Q2_K / Q3_K / Q4_K / Q5_K / Q6_K / IQ2_XXS); x must be 16-byte aligned.  Accumulation is
  * fp32 in a fixed order (deterministic; not the reference's order).  The void
  * launchers keep the reference's signatures; a rejected call launches nothing
  * and leaves the reason in zm_last_error(). */
@@ -179,9 +185,23 @@ void launch_q3_K_matmul_stream(float *y, const float *x, const void *w, int S, i
 void launch_q4_K_matmul(float *y, const float *x, const void *w, int S, int I, int O);
 void launch_q4_K_matmul_stream(float *y, const float *x, const void *w, int S, int I, int O, void *stream);
 void launch_iq2_xxs_matmul(float *y, const float *x, const void *w, int S, int I, int O);
+/* Q5_K / Q6_K: replace launch_q5_K_matmul / launch_q6_K_matmul
+ * (kernels/quant/kquant_matmul.cu:615-629, declared at
+ * backends/cuda/cuda_kernel_dispatcher.cpp:23-26); the _stream variants have
+ * no reference counterpart and exist for symmetry with the other types. */
+void launch_q5_K_matmul(float *y, const float *x, const void *w, int S, int I, int O);
+void launch_q5_K_matmul_stream(float *y, const float *x, const void *w, int S, int I, int O, void *stream);
+void launch_q6_K_matmul(float *y, const float *x, const void *w, int S, int I, int O);
+void launch_q6_K_matmul_stream(float *y, const float *x, const void *w, int S, int I, int O, void *stream);
+/* y[g][O] = x[g][I] . dequant(W_g)^T for g < groups, W_g at byte
+ * g * group_stride_bytes (a multiple of 176), legacy default stream; returns
+ * false (launching nothing) on a rejected shape.  Replaces
+ * launch_q5_K_matmul_grouped (kernels/quant/kquant_matmul.cu:607-614). */
+bool launch_q5_K_matmul_grouped(float *y, const float *x, const void *w, int groups, size_t group_stride_bytes,
+                                 int I, int O);
 void launch_iq2_xxs_matmul_stream(float *y, const float *x, const void *w, int S, int I, int O, void *stream);
 /* The same by type id, returning 0 / -1.  Replaces CudaKernelDispatcher::matmul
- * (backends/cuda/cuda_kernel_dispatcher.cpp:109-189) for these four types. */
+ * (backends/cuda/cuda_kernel_dispatcher.cpp:109-189) for these six types. */
 int zm_f32_matmul(int type, float *y, const float *x, const void *w, int S, int I, int O, void *stream);
 
 /* FP32 quant-matmul hook with the acceptance rules of native_f32_quant_hook

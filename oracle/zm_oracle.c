@@ -9,6 +9,9 @@
  *   - Q4_K x Q8_K dot: bit-exact against the reference's 512-bit kernel
  *     (bench/q3k_q4k_dot_bench.cpp:73-125, itself checked bit-exact against
  *     ggml's stock at :187-200), built into oracle/_ref.
+ *   - Q5_K and Q6_K dots: per-block integer sums pinned against a brute force
+ *     over the dequantized weights as below; float order "parity unpinned"
+ *     beyond 1e-6 rel (no stock copy of either kernel in the reference tree).
  *   - Q3_K and IQ2_XXS dots: per-block integer sums pinned against a brute
  *     force over the dequantized weights (dequant(w) . dequant(q8) is an
  *     exact integer multiple); float accumulation order follows the AVX2
@@ -100,6 +103,8 @@ size_t zmo_row_size(int type, int64_t n) {
   case ZMO_TYPE_Q2_K: return (size_t)nb * sizeof(zmo_block_q2_K);
   case ZMO_TYPE_Q3_K: return (size_t)nb * sizeof(zmo_block_q3_K);
   case ZMO_TYPE_Q4_K: return (size_t)nb * sizeof(zmo_block_q4_K);
+  case ZMO_TYPE_Q5_K: return (size_t)nb * sizeof(zmo_block_q5_K);
+  case ZMO_TYPE_Q6_K: return (size_t)nb * sizeof(zmo_block_q6_K);
   case ZMO_TYPE_IQ2_XXS: return (size_t)nb * sizeof(zmo_block_iq2_xxs);
   case ZMO_TYPE_Q8_K: return (size_t)nb * sizeof(zmo_block_q8_K);
   case ZMO_TYPE_F32: return (size_t)n * 4;
@@ -538,6 +543,114 @@ void zmo_quantize_row_q4_K(const float *x, zmo_block_q4_K *y, int64_t k) {
   }
 }
 
+/* Q5_K: as Q4_K with 5-bit values (0..31): the low nibbles packed as Q4_K's
+ * qs, bit 4 of weight 64c + 32g + l in bit 2c + g of qh[l]
+ * (dequant at kquant_matmul.cu:94-117). */
+void zmo_quantize_row_q5_K(const float *x, zmo_block_q5_K *y, int64_t k) {
+  const int64_t nb = k / ZMO_QK_K;
+  uint8_t L[256];
+  float w[32], mins[8], scales[8];
+  for (int64_t i = 0; i < nb; ++i, x += ZMO_QK_K) {
+    float max_scale = 0, max_min = 0;
+    for (int j = 0; j < 8; ++j) {
+      float s2 = 0;
+      for (int l = 0; l < 32; ++l) s2 += x[32 * j + l] * x[32 * j + l];
+      const float av = sqrtf(s2 / 32);
+      for (int l = 0; l < 32; ++l) w[l] = av + fabsf(x[32 * j + l]);
+      scales[j] = fit_scale_min(32, 31, x + 32 * j, w, L + 32 * j, &mins[j], -0.5f, 0.1f, 15, 0);
+      if (scales[j] > max_scale) max_scale = scales[j];
+      if (mins[j] > max_min) max_min = mins[j];
+    }
+    const float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
+    const float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
+    memset(y[i].scales, 0, 12);
+    for (int j = 0; j < 8; ++j) {
+      int ls = zmo_nearest_int(inv_scale * scales[j]);
+      int lm = zmo_nearest_int(inv_min * mins[j]);
+      ls = ls > 63 ? 63 : ls;
+      lm = lm > 63 ? 63 : lm;
+      if (j < 4) {
+        y[i].scales[j] = (uint8_t)ls;
+        y[i].scales[j + 4] = (uint8_t)lm;
+      } else {
+        y[i].scales[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
+        y[i].scales[j - 4] |= (uint8_t)((ls >> 4) << 6);
+        y[i].scales[j - 0] |= (uint8_t)((lm >> 4) << 6);
+      }
+    }
+    y[i].d = zmo_fp32_to_fp16(max_scale / 63.f);
+    y[i].dmin = zmo_fp32_to_fp16(max_min / 63.f);
+    for (int j = 0; j < 8; ++j) {
+      uint8_t sc, m;
+      scale_min_k4(j, y[i].scales, &sc, &m);
+      const float d = zmo_fp16_to_fp32(y[i].d) * sc;
+      if (d == 0.0f) continue;
+      const float dm = zmo_fp16_to_fp32(y[i].dmin) * m;
+      for (int ii = 0; ii < 32; ++ii) {
+        int l = zmo_nearest_int((x[32 * j + ii] + dm) / d);
+        L[32 * j + ii] = (uint8_t)(l < 0 ? 0 : (l > 31 ? 31 : l));
+      }
+    }
+    memset(y[i].qh, 0, 32);
+    for (int c = 0; c < 4; ++c)
+      for (int l = 0; l < 32; ++l) {
+        const int lo = L[64 * c + l], hi = L[64 * c + 32 + l];
+        y[i].qs[32 * c + l] = (uint8_t)((lo & 15) | ((hi & 15) << 4));
+        y[i].qh[l] |= (uint8_t)(((lo >> 4) << (2 * c)) | ((hi >> 4) << (2 * c + 1)));
+      }
+  }
+}
+
+/* Q6_K: 16 sub-blocks of 16 with a signed 8-bit scale each, values q - 32 for
+ * 6-bit q; weight 128h + 32g + l (l < 32) keeps its low nibble in
+ * ql[64h + 32(g&1) + l] (high nibble when g >= 2) and its top two bits at
+ * bit 2g of qh[32h + l] (dequant at kquant_matmul.cu:119-140). */
+void zmo_quantize_row_q6_K(const float *x, zmo_block_q6_K *y, int64_t k) {
+  const int64_t nb = k / ZMO_QK_K;
+  int8_t L[256];
+  float scales[16];
+  for (int64_t i = 0; i < nb; ++i, x += ZMO_QK_K) {
+    float max_scale = 0, amax = 0;
+    for (int j = 0; j < 16; ++j) {
+      scales[j] = fit_symmetric(16, 32, x + 16 * j, L + 16 * j);
+      const float a = fabsf(scales[j]);
+      if (a > amax) {
+        amax = a;
+        max_scale = scales[j];
+      }
+    }
+    if (max_scale == 0.0f) {
+      memset(&y[i], 0, sizeof(y[i]));
+      continue;
+    }
+    const float iscale = -128.f / max_scale;
+    y[i].d = zmo_fp32_to_fp16(1 / iscale);
+    for (int j = 0; j < 16; ++j) {
+      const int l = zmo_nearest_int(iscale * scales[j]);
+      y[i].scales[j] = (int8_t)(l > 127 ? 127 : (l < -128 ? -128 : l));
+    }
+    for (int j = 0; j < 16; ++j) {
+      const float d = zmo_fp16_to_fp32(y[i].d) * y[i].scales[j];
+      if (d == 0.0f) {
+        for (int ii = 0; ii < 16; ++ii) L[16 * j + ii] = 32;
+        continue;
+      }
+      for (int ii = 0; ii < 16; ++ii) {
+        int l = zmo_nearest_int(x[16 * j + ii] / d);
+        l = l < -32 ? -32 : (l > 31 ? 31 : l);
+        L[16 * j + ii] = (int8_t)(l + 32);
+      }
+    }
+    for (int h = 0; h < 2; ++h)
+      for (int l = 0; l < 32; ++l) {
+        const int q0 = L[128 * h + l], q1 = L[128 * h + 32 + l], q2 = L[128 * h + 64 + l], q3 = L[128 * h + 96 + l];
+        y[i].ql[64 * h + l] = (uint8_t)((q0 & 15) | ((q2 & 15) << 4));
+        y[i].ql[64 * h + 32 + l] = (uint8_t)((q1 & 15) | ((q3 & 15) << 4));
+        y[i].qh[32 * h + l] = (uint8_t)((q0 >> 4) | ((q1 >> 4) << 2) | ((q2 >> 4) << 4) | ((q3 >> 4) << 6));
+      }
+  }
+}
+
 /* IQ2_XXS: per 8-weight group the sign pattern (even count of negatives; on
  * an odd count the smallest-magnitude weight keeps a positive sign) and the
  * nearest grid vector to |x|/scale; per 32-weight sub-block a 4-bit scale
@@ -645,6 +758,8 @@ void zmo_quantize_rows(int type, const float *x, void *dst, int64_t rows, int64_
     case ZMO_TYPE_Q2_K: zmo_quantize_row_q2_K(xr, (zmo_block_q2_K *)out, n); break;
     case ZMO_TYPE_Q3_K: zmo_quantize_row_q3_K(xr, (zmo_block_q3_K *)out, n); break;
     case ZMO_TYPE_Q4_K: zmo_quantize_row_q4_K(xr, (zmo_block_q4_K *)out, n); break;
+    case ZMO_TYPE_Q5_K: zmo_quantize_row_q5_K(xr, (zmo_block_q5_K *)out, n); break;
+    case ZMO_TYPE_Q6_K: zmo_quantize_row_q6_K(xr, (zmo_block_q6_K *)out, n); break;
     case ZMO_TYPE_IQ2_XXS: zmo_quantize_row_iq2_xxs(xr, (zmo_block_iq2_xxs *)out, n); break;
     case ZMO_TYPE_Q8_K: zmo_quantize_row_q8_K(xr, (zmo_block_q8_K *)out, n); break;
     default: break;
@@ -735,6 +850,39 @@ static void dequant_q4_K(const zmo_block_q4_K *x, float *y, int64_t k) {
   }
 }
 
+/* dequantize_row_q5_K (kquant_matmul.cu:94-117). */
+static void dequant_q5_K(const zmo_block_q5_K *x, float *y, int64_t k) {
+  for (int64_t i = 0; i < k / ZMO_QK_K; ++i) {
+    const float d = zmo_fp16_to_fp32(x[i].d), mn = zmo_fp16_to_fp32(x[i].dmin);
+    for (int c = 0; c < 4; ++c) {
+      uint8_t sc, m;
+      scale_min_k4(2 * c, x[i].scales, &sc, &m);
+      const float d1 = d * sc, m1 = mn * m;
+      scale_min_k4(2 * c + 1, x[i].scales, &sc, &m);
+      const float d2 = d * sc, m2 = mn * m;
+      const uint8_t *q = x[i].qs + 32 * c;
+      for (int l = 0; l < 32; ++l) *y++ = d1 * ((q[l] & 0xF) + ((x[i].qh[l] >> (2 * c)) & 1 ? 16 : 0)) - m1;
+      for (int l = 0; l < 32; ++l) *y++ = d2 * ((q[l] >> 4) + ((x[i].qh[l] >> (2 * c + 1)) & 1 ? 16 : 0)) - m2;
+    }
+  }
+}
+
+/* Q6_K value of weight t of a block, q6 - 32 in [-32, 31]. */
+static inline int q6_value(const zmo_block_q6_K *x, int t) {
+  const int h = t / 128, g = (t % 128) / 32, l = t % 32;
+  const uint8_t b = x->ql[64 * h + 32 * (g & 1) + l];
+  const int lo = g < 2 ? (b & 0xF) : (b >> 4);
+  return (lo | (((x->qh[32 * h + l] >> (2 * g)) & 3) << 4)) - 32;
+}
+
+/* dequantize_row_q6_K (kquant_matmul.cu:119-140): sub-block t/16. */
+static void dequant_q6_K(const zmo_block_q6_K *x, float *y, int64_t k) {
+  for (int64_t i = 0; i < k / ZMO_QK_K; ++i) {
+    const float d = zmo_fp16_to_fp32(x[i].d);
+    for (int t = 0; t < ZMO_QK_K; ++t) *y++ = d * x[i].scales[t / 16] * q6_value(&x[i], t);
+  }
+}
+
 /* dequantize_row_iq2_xxs (iq2_matmul.cu:73-91). */
 static void dequant_iq2_xxs(const zmo_block_iq2_xxs *x, float *y, int64_t k) {
   const uint64_t *grid = zmo_iq2xxs_grid();
@@ -759,6 +907,8 @@ void zmo_dequantize_row(int type, const void *src, float *y, int64_t n) {
   case ZMO_TYPE_Q2_K: dequant_q2_K((const zmo_block_q2_K *)src, y, n); break;
   case ZMO_TYPE_Q3_K: dequant_q3_K((const zmo_block_q3_K *)src, y, n); break;
   case ZMO_TYPE_Q4_K: dequant_q4_K((const zmo_block_q4_K *)src, y, n); break;
+  case ZMO_TYPE_Q5_K: dequant_q5_K((const zmo_block_q5_K *)src, y, n); break;
+  case ZMO_TYPE_Q6_K: dequant_q6_K((const zmo_block_q6_K *)src, y, n); break;
   case ZMO_TYPE_IQ2_XXS: dequant_iq2_xxs((const zmo_block_iq2_xxs *)src, y, n); break;
   case ZMO_TYPE_Q8_K: {
     const zmo_block_q8_K *b = (const zmo_block_q8_K *)src;
@@ -858,6 +1008,47 @@ static float dot_q4_K(int n, const zmo_block_q4_K *x, const zmo_block_q8_K *y) {
   return hsum8(acc) + (m01 + m23);
 }
 
+/* Q5_K: the Q4_K structure with 5-bit values -- 8-lane acc of d*sumi (lane l
+ * = bytes [4l,4l+4) of each 32-weight sub-block) and the mins term
+ * dmin * sum m_j*s32_j summed in integers per block and accumulated as one
+ * scalar.  Float order: parity unpinned (ggml's stock Q5_K dot is not in the
+ * reference tree). */
+static float dot_q5_K(int n, const zmo_block_q5_K *x, const zmo_block_q8_K *y) {
+  float acc[8] = {0}, summs = 0;
+  for (int i = 0; i < n / ZMO_QK_K; ++i) {
+    const float d = y[i].d * zmo_fp16_to_fp32(x[i].d);
+    const float dmin = -y[i].d * zmo_fp16_to_fp32(x[i].dmin);
+    uint8_t sc[8], m[8];
+    for (int j = 0; j < 8; ++j) scale_min_k4(j, x[i].scales, &sc[j], &m[j]);
+    int32_t prod = 0;
+    for (int j = 0; j < 8; ++j) prod += m[j] * (y[i].bsums[2 * j] + y[i].bsums[2 * j + 1]);
+    summs = fmaf(dmin, (float)prod, summs);
+    int32_t sumi[8] = {0};
+    for (int j = 0; j < 8; ++j)
+      for (int t = 0; t < 32; ++t) {
+        const uint8_t b = x[i].qs[32 * (j / 2) + t];
+        const int q = ((j & 1) ? (b >> 4) : (b & 0xF)) | (((x[i].qh[t] >> j) & 1) << 4);
+        sumi[t >> 2] += sc[j] * q * y[i].qs[32 * j + t];
+      }
+    for (int l = 0; l < 8; ++l) acc[l] = fmaf(d, (float)sumi[l], acc[l]);
+  }
+  return hsum8(acc) + summs;
+}
+
+/* Q6_K: per-lane integer sums of sc * (q6 - 32) * q8 (lane l = bytes
+ * [4l,4l+4) of each 32-weight chunk), one fma per lane per block.  Float
+ * order: parity unpinned, as for Q5_K. */
+static float dot_q6_K(int n, const zmo_block_q6_K *x, const zmo_block_q8_K *y) {
+  float acc[8] = {0};
+  for (int i = 0; i < n / ZMO_QK_K; ++i) {
+    const float d = y[i].d * zmo_fp16_to_fp32(x[i].d);
+    int32_t sumi[8] = {0};
+    for (int t = 0; t < ZMO_QK_K; ++t) sumi[(t & 31) >> 2] += x[i].scales[t / 16] * q6_value(&x[i], t) * y[i].qs[t];
+    for (int l = 0; l < 8; ++l) acc[l] = fmaf(d, (float)sumi[l], acc[l]);
+  }
+  return hsum8(acc);
+}
+
 /* ggml_vec_dot_iq2_xxs_q8_K, AVX2 / AVX-512BW order (patches/ggml/0009...:34-95,
  * bench/kernels/iq2xxs_dot_bench.cpp:26-50): lane l sums (2ls+1)*grid*sign*q8
  * over bytes [4l,4l+4) of each 32-weight sub-block; one fma per block with
@@ -890,6 +1081,8 @@ float zmo_vec_dot_q8_K(int type, int n, const void *x, const zmo_block_q8_K *y) 
   case ZMO_TYPE_Q2_K: return dot_q2_K(n, (const zmo_block_q2_K *)x, y);
   case ZMO_TYPE_Q3_K: return dot_q3_K(n, (const zmo_block_q3_K *)x, y);
   case ZMO_TYPE_Q4_K: return dot_q4_K(n, (const zmo_block_q4_K *)x, y);
+  case ZMO_TYPE_Q5_K: return dot_q5_K(n, (const zmo_block_q5_K *)x, y);
+  case ZMO_TYPE_Q6_K: return dot_q6_K(n, (const zmo_block_q6_K *)x, y);
   case ZMO_TYPE_IQ2_XXS: return dot_iq2_xxs(n, (const zmo_block_iq2_xxs *)x, y);
   default: return NAN;
   }
@@ -927,6 +1120,21 @@ void zmo_block_dots(int type, int n, const void *vx, const zmo_block_q8_K *y, in
           s += sc * ((j & 1) ? (b >> 4) : (b & 0xF)) * y[i].qs[t];
         }
       }
+    } else if (type == ZMO_TYPE_Q5_K) {
+      /* from the dequant with d = 1, dmin = 0: exact integers sc * q */
+      zmo_block_q5_K one = ((const zmo_block_q5_K *)vx)[i];
+      one.d = 0x3c00;
+      one.dmin = 0;
+      dequant_q5_K(&one, w, 256);
+      uint8_t sc, m;
+      for (int j = 0; j < 8; ++j) {
+        scale_min_k4(j, one.scales, &sc, &m);
+        mm += m * (y[i].bsums[2 * j] + y[i].bsums[2 * j + 1]);
+      }
+      for (int t = 0; t < 256; ++t) s += (int32_t)lrintf(w[t]) * y[i].qs[t];
+    } else if (type == ZMO_TYPE_Q6_K) {
+      const zmo_block_q6_K *x = (const zmo_block_q6_K *)vx + i;
+      for (int t = 0; t < 256; ++t) s += x->scales[t / 16] * q6_value(x, t) * y[i].qs[t];
     } else if (type == ZMO_TYPE_IQ2_XXS) {
       /* (2ls+1)*grid*sign = 8 * dequant / d: reuse the dequant as integers */
       zmo_block_iq2_xxs one = ((const zmo_block_iq2_xxs *)vx)[i];
@@ -942,7 +1150,8 @@ void zmo_block_dots(int type, int n, const void *vx, const zmo_block_q8_K *y, in
 /* ----------------------------------------------------------------- the op */
 
 static int type_ok(int t) {
-  return t == ZMO_TYPE_Q2_K || t == ZMO_TYPE_Q3_K || t == ZMO_TYPE_Q4_K || t == ZMO_TYPE_IQ2_XXS;
+  return t == ZMO_TYPE_Q2_K || t == ZMO_TYPE_Q3_K || t == ZMO_TYPE_Q4_K || t == ZMO_TYPE_Q5_K || t == ZMO_TYPE_Q6_K ||
+         t == ZMO_TYPE_IQ2_XXS;
 }
 
 int zmo_mul_mat_id(const zmo_tensor *src0, const zmo_tensor *src1, const zmo_tensor *ids, zmo_tensor *dst,

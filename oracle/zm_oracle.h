@@ -29,16 +29,21 @@ enum {
   ZMO_TYPE_Q2_K = 10,
   ZMO_TYPE_Q3_K = 11,
   ZMO_TYPE_Q4_K = 12,
+  ZMO_TYPE_Q5_K = 13,
+  ZMO_TYPE_Q6_K = 14,
   ZMO_TYPE_Q8_K = 15,
   ZMO_TYPE_IQ2_XXS = 16,
   ZMO_TYPE_I32 = 26,
 };
 
-/* Block layouts: /root/reference/kernels/quant/kquant_matmul.cu:35-39,
+/* Block layouts: /root/reference/kernels/quant/kquant_matmul.cu:35-39 (Q5_K
+ * and Q6_K at :37-38, sizes at backends/cpu/kquant_dequant.hpp:491-492),
  * kernels/quant/iq2_matmul.cu:27, backends/cpu/kernels_cpu.cpp:22-32. */
 typedef struct { uint8_t scales[16]; uint8_t qs[64]; uint16_t d, dmin; } zmo_block_q2_K;      /* 84 B  */
 typedef struct { uint8_t hmask[32]; uint8_t qs[64]; uint8_t scales[12]; uint16_t d; } zmo_block_q3_K; /* 110 B */
 typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; } zmo_block_q4_K;     /* 144 B */
+typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qh[32]; uint8_t qs[128]; } zmo_block_q5_K; /* 176 B */
+typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } zmo_block_q6_K;   /* 210 B */
 typedef struct { uint16_t d; uint16_t qs[32]; } zmo_block_iq2_xxs;                            /* 66 B  */
 typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } zmo_block_q8_K;                /* 292 B */
 
@@ -63,6 +68,8 @@ void zmo_quantize_row_q8_K(const float *x, zmo_block_q8_K *y, int64_t k);
 void zmo_quantize_row_q2_K(const float *x, zmo_block_q2_K *y, int64_t k);
 void zmo_quantize_row_q3_K(const float *x, zmo_block_q3_K *y, int64_t k);
 void zmo_quantize_row_q4_K(const float *x, zmo_block_q4_K *y, int64_t k);
+void zmo_quantize_row_q5_K(const float *x, zmo_block_q5_K *y, int64_t k);
+void zmo_quantize_row_q6_K(const float *x, zmo_block_q6_K *y, int64_t k);
 void zmo_quantize_row_iq2_xxs(const float *x, zmo_block_iq2_xxs *y, int64_t k);
 /* quantize `rows` rows of n floats of `type` into dst (rows * row_size bytes) */
 void zmo_quantize_rows(int type, const float *x, void *dst, int64_t rows, int64_t n);
@@ -73,7 +80,8 @@ void zmo_dequantize_row(int type, const void *src, float *y, int64_t n);
 /* ---- dots (ggml x86 float order where pinned) ---- */
 float zmo_vec_dot_q8_K(int type, int n, const void *x, const zmo_block_q8_K *y);
 /* Per-super-block integer parts: for K-quants isum = sum_j sc_j * dot_j and
- * imin = sum_j m_j * bsum_j (Q2_K/Q4_K; 0 for Q3_K); IQ2_XXS isum = sum_sub
+ * imin = sum_j m_j * bsum_j (Q2_K/Q4_K/Q5_K; 0 for Q3_K and Q6_K, whose
+ * values are signed: q - 4 for a clear Q3_K high bit, q6 - 32); IQ2_XXS isum = sum_sub
  * (2ls+1) * dot.  Written into isum[nb], imin[nb]. */
 void zmo_block_dots(int type, int n, const void *x, const zmo_block_q8_K *y, int32_t *isum, int32_t *imin);
 

@@ -12,12 +12,12 @@ import pytest
 import torch
 
 import zm_oracle as O
-from moe_cases import IQ2, Q2, Q3, Q4
+from moe_cases import IQ2, Q2, Q3, Q4, Q5, Q6
 
 pytestmark = pytest.mark.gpu
 
-TYPES = [Q2, Q3, Q4, IQ2]
-NAMES = {Q2: "q2_K", Q3: "q3_K", Q4: "q4_K", IQ2: "iq2_xxs"}
+TYPES = [Q2, Q3, Q4, Q5, Q6, IQ2]
+NAMES = {Q2: "q2_K", Q3: "q3_K", Q4: "q4_K", Q5: "q5_K", Q6: "q6_K", IQ2: "iq2_xxs"}
 MM_TOL = 2e-5
 
 
@@ -83,6 +83,28 @@ def test_launcher_rejects_bad_I():
     assert b"multiple of 256" in lib().zm_last_error()
     torch.cuda.synchronize()
     assert torch.all(y == 7.0)
+
+
+def test_q5_K_matmul_grouped():
+    """launch_q5_K_matmul_grouped: y[g] = x[g] . W_g^T with W_g at a padded
+    group stride; a stride that is not a whole number of blocks is rejected."""
+    from zeromoe_amd._lib import lib
+
+    G, I, Orows = 3, 1024, 40
+    row = (I // 256) * 176
+    stride = Orows * row + 2 * 176
+    W = O.random_blocks(Q5, G * (stride // row + 1), I, seed=9).reshape(-1)[:G * stride]
+    x = np.random.default_rng(3).standard_normal((G, I)).astype(np.float32)
+    y = torch.full((G, Orows), np.nan, device="cuda")
+    dW, dx = torch.from_numpy(np.ascontiguousarray(W)).cuda(), torch.from_numpy(x).cuda()
+    torch.cuda.synchronize()
+    assert lib().launch_q5_K_matmul_grouped(y.data_ptr(), dx.data_ptr(), dW.data_ptr(), G, stride, I, Orows)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    for g in range(G):
+        Wg = W[g * stride:g * stride + Orows * row].reshape(Orows, row)
+        _check_mm(got[g:g + 1], Wg, Q5, x[g:g + 1])
+    assert not lib().launch_q5_K_matmul_grouped(y.data_ptr(), dx.data_ptr(), dW.data_ptr(), G, stride + 1, I, Orows)
 
 
 # ------------------------------------------------------------------ FP32 MUL_MAT_ID hook
@@ -241,7 +263,7 @@ def test_glm5next_router_topk_ties_and_nan():
 
 # ------------------------------------------------------------------ per-expert executor
 
-@pytest.mark.parametrize("types", [(Q2, Q2, Q3), (Q4, Q4, Q4), (IQ2, IQ2, IQ2)])
+@pytest.mark.parametrize("types", [(Q2, Q2, Q3), (Q4, Q4, Q4), (IQ2, IQ2, IQ2), (Q4, Q4, Q6), (Q5, Q5, Q6)])
 @pytest.mark.parametrize("S", [1, 5])
 def test_expert_executor(types, S):
     import zeromoe_amd as Z

@@ -8,11 +8,11 @@ import pytest
 import torch
 
 import zm_oracle as O
-from moe_cases import CONFIGS, IQ2, Q2, Q3, Q4, Built, assert_close_layer, dev_random_blocks, reduced
+from moe_cases import CONFIGS, IQ2, Q2, Q3, Q4, Q5, Q6, Built, assert_close_layer, dev_random_blocks, reduced
 
 pytestmark = pytest.mark.gpu
 
-TYPES = [Q2, Q3, Q4, IQ2]
+TYPES = [Q2, Q3, Q4, Q5, Q6, IQ2]
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -207,6 +207,13 @@ LAYER_CASES = {
     "c5_S64_full": (CONFIGS["c5"], dict(S=64)),
     # prefill buckets on the MFMA path: 128 pairs per expert on average (two passes of 64)
     "c3_mmq": (CONFIGS["c3"], dict(S=256, H=1024, F=512, E=16)),
+    # mixed per-layer types of real checkpoints: Q4_K gate/up with a Q6_K down
+    # projection (decode and a small prefill), Q5_K gate/up with Q6_K down
+    "q4k_q6k_S1": (CONFIGS["c2"], dict(tg=Q4, td=Q6)),
+    "q4k_q6k_S16": (CONFIGS["c2"], dict(tg=Q4, td=Q6, S=16, H=2048, F=768)),
+    "q5k_q6k_S1": (CONFIGS["c2"], dict(tg=Q5, td=Q6)),
+    "q5k_q5k_S64": (CONFIGS["c3"], dict(tg=Q5, td=Q5, S=64, H=1024, F=512)),
+    "q4k_q5k_shared_q6k": (CONFIGS["c5"], dict(tg=Q4, td=Q5, t_shared=Q6, H=2048, F=512, F_shared=1024)),
 }
 
 

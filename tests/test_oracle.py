@@ -135,6 +135,56 @@ def test_q4_K_known_answer():
         assert y[i] == np.float32(0.5 * sc[j]) * q - np.float32(0.125 * mn[j]), i
 
 
+def test_q5_K_known_answer():
+    """Q4_K nibbles and scales plus a fifth bit: bit 2c (low nibble) / 2c+1
+    (high nibble) of qh[l] adds 16 to weight 64c+l / 64c+32+l
+    (kquant_matmul.cu:94-117)."""
+    b = _blank(O.TYPE_Q5_K)
+    _put_half(b, 0, 0.5)
+    _put_half(b, 2, 0.125)
+    sc = [1, 2, 3, 4, 5, 6, 7, 8]
+    mn = [9, 10, 11, 12, 13, 14, 15, 3]
+    raw = np.zeros(12, np.uint8)
+    for j in range(4):
+        raw[j] = sc[j]
+        raw[j + 4] = mn[j]
+    for j in range(4, 8):
+        raw[j + 4] = sc[j] | (mn[j] << 4)
+    b[4:16] = raw
+    qh, qs = 16, 48
+    b[qs + 32 * 1 + 9] = 7 | (3 << 4)   # c=1, l=9: w[73] low 7, w[105] high 3
+    b[qh + 9] = 1 << 2                   # bit 2c: +16 on w[73] only
+    b[qh + 31] = 1 << 7                  # c=3 high half, l=31: w[255] = 16 with a zero nibble
+    q = np.zeros(256)
+    q[73], q[105], q[255] = 7 + 16, 3, 16
+    y = O.dequantize(O.TYPE_Q5_K, b, 256)[0]
+    for i in range(256):
+        j = i // 32
+        assert y[i] == np.float32(0.5 * sc[j]) * q[i] - np.float32(0.125 * mn[j]), i
+
+
+def test_q6_K_known_answer():
+    """Weight 128h+32g+l: low nibble of ql[64h+l] (g=0) / ql[64h+32+l] (g=1),
+    high nibbles of the same bytes for g=2,3; two top bits at bit 2g of
+    qh[32h+l]; value d*scales[t/16]*(q-32) with signed 8-bit scales
+    (kquant_matmul.cu:119-140)."""
+    b = _blank(O.TYPE_Q6_K)
+    _put_half(b, 208, 0.25)
+    scales = np.array([3, -5, 7, -9, 11, -13, 15, -17, 19, -21, 23, -25, 27, -29, 31, -128], np.int8)
+    b[192:208] = scales.view(np.uint8)
+    b[64 + 32 + 5] = 0xA << 4          # h=1, g=3, l=5 -> t=229: nibble 10
+    b[128 + 32 + 5] = 2 << 6           # top bits 2 -> q=42
+    b[17] = 3                           # h=0, g=0, l=17 -> t=17: nibble 3
+    b[128 + 17] = 1                     # top bits 1 -> q=19
+    b[0] = 0xF << 4                     # h=0, g=2, l=0 -> t=64: nibble 15
+    b[128 + 0] = 3 << 4                 # top bits 3 -> q=63
+    q = np.zeros(256)
+    q[229], q[17], q[64] = 42, 19, 63
+    y = O.dequantize(O.TYPE_Q6_K, b, 256)[0]
+    for t in range(256):
+        assert y[t] == np.float32(np.float32(0.25 * scales[t // 16]) * (q[t] - 32)), t
+
+
 def test_iq2_xxs_known_answer():
     """value = d*(0.5+ls)*0.25*grid[idx][j]*sign, signs = ksigns[7-bit index]
     with the 8th sign = parity (iq2_matmul.cu:73-91, patches/ggml/0009...:69-75)."""
@@ -182,7 +232,7 @@ def test_iq2_grid_stand_in_properties():
 
 # ------------------------------------------------------------------ integer block dots == brute force over dequant
 
-@pytest.mark.parametrize("t", [O.TYPE_Q2_K, O.TYPE_Q3_K, O.TYPE_Q4_K, O.TYPE_IQ2_XXS])
+@pytest.mark.parametrize("t", [O.TYPE_Q2_K, O.TYPE_Q3_K, O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_IQ2_XXS])
 def test_block_dots_equal_dequant_brute_force(t):
     """sum_j sc*dot - dmin*sum m*bsum per block equals dequant(w).dequant(q8)
     scaled by the block scales, exactly in float64 (integers < 2^53)."""
@@ -203,17 +253,20 @@ def test_block_dots_equal_dequant_brute_force(t):
             exp = d * isum[b] - dm * imin[b]
         elif t == O.TYPE_Q3_K:
             exp = float(np.frombuffer(bb[108:110].tobytes(), np.float16)[0]) * isum[b]
-        elif t == O.TYPE_Q4_K:
+        elif t in (O.TYPE_Q4_K, O.TYPE_Q5_K):
             d = float(np.frombuffer(bb[0:2].tobytes(), np.float16)[0])
             dm = float(np.frombuffer(bb[2:4].tobytes(), np.float16)[0])
             exp = d * isum[b] - dm * imin[b]
+        elif t == O.TYPE_Q6_K:
+            assert imin[b] == 0
+            exp = float(np.frombuffer(bb[208:210].tobytes(), np.float16)[0]) * isum[b]
         else:
             exp = float(np.frombuffer(bb[0:2].tobytes(), np.float16)[0]) * isum[b] / 8.0
         got = float(np.dot(wd[256 * b:256 * b + 256], qv[256 * b:256 * b + 256]))
         assert abs(got - exp) <= 1e-9 * max(1.0, abs(exp)), (b, got, exp)
 
 
-@pytest.mark.parametrize("t", [O.TYPE_Q2_K, O.TYPE_Q3_K, O.TYPE_Q4_K, O.TYPE_IQ2_XXS])
+@pytest.mark.parametrize("t", [O.TYPE_Q2_K, O.TYPE_Q3_K, O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_IQ2_XXS])
 def test_vec_dot_matches_dequant_dot(t):
     rng = np.random.default_rng(5)
     n = 2048
@@ -419,7 +472,7 @@ def test_moe_forward_composition():
 
 
 @pytest.mark.parametrize("t,tol", [(O.TYPE_Q2_K, 0.40), (O.TYPE_Q3_K, 0.20), (O.TYPE_Q4_K, 0.09),
-                                   (O.TYPE_IQ2_XXS, 0.40)])
+                                   (O.TYPE_Q5_K, 0.045), (O.TYPE_Q6_K, 0.025), (O.TYPE_IQ2_XXS, 0.40)])
 def test_quantizer_round_trip(t, tol):
     x = O.fill_normal(42, 8 * 1024, 0.0, 0.02).reshape(8, 1024)
     y = O.dequantize(t, O.quantize(t, x), 1024)

@@ -68,6 +68,11 @@ SIGNATURES = {
     "launch_expert_swiglu": (None, [P, P, P, I, F, I, P, P]),
     "launch_expert_scatter_accum": (None, [P, P, P, P, I, I, I, P]),
     "launch_expert_scatter_add": (None, [P, P, P, I, I, I, P]),
+    "launch_q5_K_matmul": (None, [P, P, P, I, I, I]),
+    "launch_q5_K_matmul_stream": (None, [P, P, P, I, I, I, P]),
+    "launch_q6_K_matmul": (None, [P, P, P, I, I, I]),
+    "launch_q6_K_matmul_stream": (None, [P, P, P, I, I, I, P]),
+    "launch_q5_K_matmul_grouped": (C.c_bool, [P, P, P, I, C.c_size_t, I, I]),
     "launch_ggml_moe_unpack": (I, [P, P, P, P, I] + [C.c_size_t] * 7 + [P]),
     "launch_ggml_moe_unpack_scatter": (I, [P, P, P, P, P, I] + [C.c_size_t] * 7 + [P]),
     "launch_glm5next_router_topk": (None, [P, P, P, P, I, I, I, I, I, F, P]),

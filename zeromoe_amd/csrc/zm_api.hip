@@ -143,7 +143,9 @@ bool getenv_flag_off(const char *name) {
   return e && e[0] == '0';
 }
 
-bool type_supported(int t) { return t == T_Q2_K || t == T_Q3_K || t == T_Q4_K || t == T_IQ2_XXS; }
+bool type_supported(int t) {
+  return t == T_Q2_K || t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_IQ2_XXS;
+}
 
 size_t row_bytes(int t, int64_t n) { return (size_t)(n / QK) * block_bytes(t); }
 
@@ -175,6 +177,8 @@ int launch_gemv(int type, bool gateup, int np, const GemvArgs &a0, int n_groups,
   case T_Q2_K: rc = gateup ? launch_gemv_type<T_Q2_K, true>(np, U, grid, a, st) : launch_gemv_type<T_Q2_K, false>(np, U, grid, a, st); break;
   case T_Q3_K: rc = gateup ? launch_gemv_type<T_Q3_K, true>(np, U, grid, a, st) : launch_gemv_type<T_Q3_K, false>(np, U, grid, a, st); break;
   case T_Q4_K: rc = gateup ? launch_gemv_type<T_Q4_K, true>(np, U, grid, a, st) : launch_gemv_type<T_Q4_K, false>(np, U, grid, a, st); break;
+  case T_Q5_K: rc = gateup ? launch_gemv_type<T_Q5_K, true>(np, U, grid, a, st) : launch_gemv_type<T_Q5_K, false>(np, U, grid, a, st); break;
+  case T_Q6_K: rc = gateup ? launch_gemv_type<T_Q6_K, true>(np, U, grid, a, st) : launch_gemv_type<T_Q6_K, false>(np, U, grid, a, st); break;
   case T_IQ2_XXS: rc = gateup ? launch_gemv_type<T_IQ2_XXS, true>(np, U, grid, a, st) : launch_gemv_type<T_IQ2_XXS, false>(np, U, grid, a, st); break;
   default: return fail("unsupported weight type %d", type);
   }
@@ -449,20 +453,27 @@ __global__ void k_block_dots(const uint8_t *w, const uint8_t *xq, int nb, int32_
     load_q8_slice<T>(xq, nb, b, q, s);
     load_w_slice<T>(w + (size_t)b * block_bytes(T), q, ws);
     r = quarter_int<T>(ws, q, s, grid, signs);
-    if (q < unit_per_block<T>()) {
-      const rsrc_t rw = make_rsrc(w, (uint32_t)(nb * block_bytes(T)));
-      Unit<T> u[1];
-      load_unit<T>(rw, b * block_bytes(T), q, u[0]);
-      int ri[1], rm[1];
-      unit_ints<T, 1>(u, q, xblk_planar(xq, nb, b), grid, signs, ri, rm);
-      ui = ri[0];
-      um = rm[0];
+    if constexpr (has_unit<T>()) {
+      if (q < unit_per_block<T>()) {
+        const rsrc_t rw = make_rsrc(w, (uint32_t)(nb * block_bytes(T)));
+        Unit<T> u[1];
+        load_unit<T>(rw, b * block_bytes(T), q, u[0]);
+        int ri[1], rm[1];
+        unit_ints<T, 1>(u, q, xblk_planar(xq, nb, b), grid, signs, ri, rm);
+        ui = ri[0];
+        um = rm[0];
+      }
     }
   }
   r.isum = group_sum_i<4>(r.isum);
   r.imin = group_sum_i<4>(r.imin);
-  ui = group_sum_i<4>(ui);
-  um = group_sum_i<4>(um);
+  if constexpr (has_unit<T>()) {
+    ui = group_sum_i<4>(ui);
+    um = group_sum_i<4>(um);
+  } else {
+    ui = r.isum;  // no whole-block path for this type: the quarter sums are reported
+    um = r.imin;
+  }
   if (b < nb && q == 0) {
     const bool agree = ui == r.isum && um == r.imin;
     isum[b] = agree ? ui : INT32_MIN;
@@ -489,6 +500,8 @@ int zm_block_dots(int type, const void *w_row, const float *x, int n, int32_t *i
   case T_Q2_K: hipLaunchKernelGGL(k_block_dots<T_Q2_K>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->grid, d->signs); break;
   case T_Q3_K: hipLaunchKernelGGL(k_block_dots<T_Q3_K>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->grid, d->signs); break;
   case T_Q4_K: hipLaunchKernelGGL(k_block_dots<T_Q4_K>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->grid, d->signs); break;
+  case T_Q5_K: hipLaunchKernelGGL(k_block_dots<T_Q5_K>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->grid, d->signs); break;
+  case T_Q6_K: hipLaunchKernelGGL(k_block_dots<T_Q6_K>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->grid, d->signs); break;
   default: hipLaunchKernelGGL(k_block_dots<T_IQ2_XXS>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->grid, d->signs); break;
   }
   HIP_OK(hipGetLastError());

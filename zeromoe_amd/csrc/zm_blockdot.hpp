@@ -26,6 +26,12 @@ __host__ __device__ constexpr int unit_per_block() {
   return T == T_Q4_K ? 2 : 1;
 }
 
+// types with a whole-block unit (the fused decode kernel's dot)
+template <int T>
+__host__ __device__ constexpr bool has_unit() {
+  return T == T_Q2_K || T == T_Q3_K || T == T_Q4_K || T == T_IQ2_XXS;
+}
+
 template <int T>
 struct Unit;
 template <>

@@ -11,6 +11,12 @@
 //       16-weight sub-blocks 8h + 2j + qq.
 //   Q4_K quarter q: qs bytes [32q, +32) hold weights 64q + i (low nibble)
 //       and 64q + 32 + i (high nibble): sub-blocks 2q and 2q+1.
+//   Q5_K quarter q: as Q4_K, plus qh bytes [0, 32) whose bits 2q / 2q+1 are
+//       bit 4 of the low / high nibble values.
+//   Q6_K quarter q = (h, qq): weights 128h + 32g + 16qq + i (g = 0..3, i < 16):
+//       low nibbles in ql bytes [64h+16qq, +16) (g = 0, 2: low / high nibble)
+//       and [64h+32+16qq, +16) (g = 1, 3), top two bits at bit 2g of qh bytes
+//       [32h+16qq, +16); 16-weight sub-blocks 8h + 2g + qq.
 //   IQ2_XXS quarter q: 32-weight sub-blocks 2q and 2q+1 (16 bytes of qs).
 // Block layouts: /root/reference/kernels/quant/kquant_matmul.cu:35-39,
 // kernels/quant/iq2_matmul.cu:27.
@@ -32,13 +38,16 @@ enum : int {
   T_Q2_K = 10,
   T_Q3_K = 11,
   T_Q4_K = 12,
+  T_Q5_K = 13,
+  T_Q6_K = 14,
   T_Q8_K = 15,
   T_IQ2_XXS = 16,
   T_I32 = 26,
 };
 
 __host__ __device__ constexpr int block_bytes(int t) {
-  return t == T_Q2_K ? 84 : t == T_Q3_K ? 110 : t == T_Q4_K ? 144 : t == T_IQ2_XXS ? 66 : t == T_Q8_K ? 292 : 0;
+  return t == T_Q2_K ? 84 : t == T_Q3_K ? 110 : t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210
+       : t == T_IQ2_XXS ? 66 : t == T_Q8_K ? 292 : 0;
 }
 
 // ---------------------------------------------------------------- loads
@@ -282,7 +291,7 @@ __device__ __forceinline__ void load_q8_slice(const uint8_t *row, int nb, int b,
   const uint8_t *qs = row + (size_t)b * 256;
   const int16_t *bs = reinterpret_cast<const int16_t *>(row + q8_bs_off(nb)) + b * 16;
   s.d = reinterpret_cast<const float *>(row + q8_d_off(nb))[b];
-  if constexpr (T == T_Q2_K || T == T_Q3_K) {
+  if constexpr (T == T_Q2_K || T == T_Q3_K || T == T_Q6_K) {
     const int h = q >> 1, qq = q & 1;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -292,7 +301,7 @@ __device__ __forceinline__ void load_q8_slice(const uint8_t *row, int nb, int b,
   } else {
 #pragma unroll
     for (int j = 0; j < 4; ++j) s.q[j] = *reinterpret_cast<const uint4 *>(qs + 64 * q + 16 * j);
-    if constexpr (T == T_Q4_K) {
+    if constexpr (T == T_Q4_K || T == T_Q5_K) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) s.bs[j] = bs[4 * q + j];
     } else {
@@ -305,11 +314,13 @@ __device__ __forceinline__ void load_q8_slice(const uint8_t *row, int nb, int b,
 // ---------------------------------------------------------------- weight quarters
 
 struct WSlice {
-  uint4 a;     // Q2/Q3: qs16 ; Q4: qs[0..16) ; IQ2: qs 16 B
-  uint4 b;     // Q3: hmask16 ; Q4: qs[16..32)
-  uint4 c;     // Q4: header (d, dmin, scales) ; Q3: scales(12) + d in .w low half
-  uint2 e;     // Q2: scales[8h .. 8h+8)
-  uint32_t f;  // Q2: d|dmin ; IQ2: d
+  uint4 a;     // Q2/Q3: qs16 ; Q4/Q5: qs[0..16) ; Q6: ql[64h+16qq, +16) ; IQ2: qs 16 B
+  uint4 b;     // Q3: hmask16 ; Q4/Q5: qs[16..32) ; Q6: ql[64h+32+16qq, +16)
+  uint4 c;     // Q4/Q5: header (d, dmin, scales) ; Q3: scales(12) + d in .w low half
+  uint4 g;     // Q5: qh[0..16) ; Q6: qh[32h+16qq, +16)
+  uint4 hh;    // Q5: qh[16..32)
+  uint2 e;     // Q2: scales[8h .. 8h+8) ; Q6: scales[8h .. 8h+8)
+  uint32_t f;  // Q2: d|dmin ; Q6, IQ2: d
 };
 
 template <int T>
@@ -329,6 +340,19 @@ __device__ __forceinline__ void load_w_slice(const uint8_t *blk, int q, WSlice &
     w.c = ld16(blk);
     w.a = ld16(blk + 16 + 32 * q);
     w.b = ld16(blk + 32 + 32 * q);
+  } else if constexpr (T == T_Q5_K) {
+    w.c = ld16(blk);
+    w.g = ld16(blk + 16);
+    w.hh = ld16(blk + 32);
+    w.a = ld16(blk + 48 + 32 * q);
+    w.b = ld16(blk + 64 + 32 * q);
+  } else if constexpr (T == T_Q6_K) {
+    const int h = q >> 1, qq = q & 1;
+    w.a = ld16(blk + 64 * h + 16 * qq);
+    w.b = ld16(blk + 64 * h + 32 + 16 * qq);
+    w.g = ld16(blk + 128 + 32 * h + 16 * qq);
+    w.e = ld8(blk + 192 + 8 * h);
+    w.f = ld2(blk + 208);
   } else {  // IQ2_XXS
     w.f = ld2(blk);
     w.a = ld16(blk + 2 + 16 * q);
@@ -374,6 +398,19 @@ __device__ __forceinline__ void load_w_slice_b(rsrc_t r, int vo, int so, int q, 
     w.c = bld16(r, vo, so);
     w.a = bld16(r, vo + 16 + 32 * q, so);
     w.b = bld16(r, vo + 32 + 32 * q, so);
+  } else if constexpr (T == T_Q5_K) {
+    w.c = bld16(r, vo, so);
+    w.g = bld16(r, vo + 16, so);
+    w.hh = bld16(r, vo + 32, so);
+    w.a = bld16(r, vo + 48 + 32 * q, so);
+    w.b = bld16(r, vo + 64 + 32 * q, so);
+  } else if constexpr (T == T_Q6_K) {
+    const int h = q >> 1, qq = q & 1;
+    w.a = bld16(r, vo + 64 * h + 16 * qq, so);
+    w.b = bld16(r, vo + 64 * h + 32 + 16 * qq, so);
+    w.g = bld16(r, vo + 128 + 32 * h + 16 * qq, so);
+    w.e = bld8(r, vo + 192 + 8 * h, so);
+    w.f = bld2(r, vo + 208, so);
   } else {  // IQ2_XXS
     w.f = bld2(r, vo, so);
     w.a = bld16(r, vo + 2 + 16 * q, so);
@@ -440,7 +477,7 @@ __device__ __forceinline__ QInt quarter_int(const WSlice &w, int q, const Q8Slic
       s16 += sc * ((dj << (j == 0 ? 4 : (j == 1 ? 2 : 0))) - 64 * a.bs[j]);
     }
     r.isum = s16 >> 4;
-  } else if constexpr (T == T_Q4_K) {
+  } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
     // 6-bit (scale, min) of sub-blocks 2q and 2q+1 without a branch: scales bytes
     // 0..11 are header dwords y (A), z (B), w (C); sub-block j < 4 keeps them in
     // A[j] / B[j], j >= 4 splits them over C[j-4] (low bits) and the top bits of
@@ -458,18 +495,44 @@ __device__ __forceinline__ QInt quarter_int(const WSlice &w, int q, const Q8Slic
       m1 = lo_half ? (b1 & 63u) : ((c1 >> 4) | ((b1 >> 6) << 4));
     }
     // qs bytes [0,16) low nibbles pair with activations [0,16), bytes [16,32) with
-    // [16,32); the high nibbles with [32,48) and [48,64).
+    // [16,32); the high nibbles with [32,48) and [48,64).  Q5_K: bit 2q (low
+    // nibbles) / 2q+1 (high) of qh byte l is bit 4 of the value of weight l.
+    auto h5 = [&](const uint4 &hv, int i, int bit) -> uint32_t {
+      if constexpr (T == T_Q5_K) return ((u4_get(hv, i) >> bit) & 0x01010101u) << 4;
+      else return 0u;
+    };
+    const int bl = 2 * q, bh = 2 * q + 1;
     int dl = 0, dh = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dl = dot4(u4_get(w.a, i) & 0x0f0f0f0fu, u4_get(a.q[0], i), dl);
+    for (int i = 0; i < 4; ++i) dl = dot4((u4_get(w.a, i) & 0x0f0f0f0fu) | h5(w.g, i, bl), u4_get(a.q[0], i), dl);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dl = dot4(u4_get(w.b, i) & 0x0f0f0f0fu, u4_get(a.q[1], i), dl);
+    for (int i = 0; i < 4; ++i) dl = dot4((u4_get(w.b, i) & 0x0f0f0f0fu) | h5(w.hh, i, bl), u4_get(a.q[1], i), dl);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dh = dot4((u4_get(w.a, i) >> 4) & 0x0f0f0f0fu, u4_get(a.q[2], i), dh);
+    for (int i = 0; i < 4; ++i)
+      dh = dot4(((u4_get(w.a, i) >> 4) & 0x0f0f0f0fu) | h5(w.g, i, bh), u4_get(a.q[2], i), dh);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dh = dot4((u4_get(w.b, i) >> 4) & 0x0f0f0f0fu, u4_get(a.q[3], i), dh);
+    for (int i = 0; i < 4; ++i)
+      dh = dot4(((u4_get(w.b, i) >> 4) & 0x0f0f0f0fu) | h5(w.hh, i, bh), u4_get(a.q[3], i), dh);
     r.isum = (int)sc0 * dl + (int)sc1 * dh;
     r.imin = (int)m0 * (a.bs[0] + a.bs[1]) + (int)m1 * (a.bs[2] + a.bs[3]);
+  } else if constexpr (T == T_Q6_K) {
+    // group g: low nibbles of a (g = 0) / b (g = 1), high nibbles for g = 2, 3;
+    // top bits at bit 2g of the qh bytes; value q - 32 folded in as -32 * bsum;
+    // signed 8-bit scale of sub-block 8h + 2g + qq = byte qq + 2g of e
+    const int qq = q & 1;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint4 &src = (g & 1) ? w.b : w.a;
+      int dg = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = g < 2 ? (u4_get(src, i) & 0x0f0f0f0fu) : ((u4_get(src, i) >> 4) & 0x0f0f0f0fu);
+        const uint32_t hi = ((u4_get(w.g, i) >> (2 * g)) & 0x03030303u) << 4;
+        dg = dot4(lo | hi, u4_get(a.q[g], i), dg);
+      }
+      const int sc = __builtin_amdgcn_sbfe((int)(g < 2 ? w.e.x : w.e.y), 8 * (qq + 2 * (g & 1)), 8);
+      r.isum += sc * (dg - 32 * a.bs[g]);
+    }
   } else {  // IQ2_XXS: sub-blocks 2q, 2q+1; words (aux0, aux1) each
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
@@ -506,9 +569,11 @@ __device__ __forceinline__ float quarter_dot(const WSlice &w, int q, const Q8Sli
   } else if constexpr (T == T_Q3_K) {
     const float d = h2f((uint16_t)(w.c.w & 0xffffu));
     return (a.d * d) * (float)r.isum;
-  } else if constexpr (T == T_Q4_K) {
+  } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
     const float d = h2f((uint16_t)(w.c.x & 0xffffu)), dmin = h2f((uint16_t)(w.c.x >> 16));
     return (a.d * d) * (float)r.isum - (a.d * dmin) * (float)r.imin;
+  } else if constexpr (T == T_Q6_K) {
+    return (a.d * h2f((uint16_t)(w.f & 0xffffu))) * (float)r.isum;
   } else {
     const float d = h2f((uint16_t)(w.f & 0xffffu));
     return 0.125f * ((a.d * d) * (float)r.isum);

@@ -16,7 +16,9 @@ using namespace zm;
 
 namespace {
 
-bool f32_type(int t) { return t == T_Q2_K || t == T_Q3_K || t == T_Q4_K || t == T_IQ2_XXS; }
+bool f32_type(int t) {
+  return t == T_Q2_K || t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_IQ2_XXS;
+}
 
 template <int T>
 void launch_mm_t(const F32MMArgs &a, int n_route, hipStream_t st) {
@@ -36,6 +38,8 @@ int launch_mm(int type, F32MMArgs a, int n_route, hipStream_t st) {
   case T_Q2_K: launch_mm_t<T_Q2_K>(a, n_route, st); break;
   case T_Q3_K: launch_mm_t<T_Q3_K>(a, n_route, st); break;
   case T_Q4_K: launch_mm_t<T_Q4_K>(a, n_route, st); break;
+  case T_Q5_K: launch_mm_t<T_Q5_K>(a, n_route, st); break;
+  case T_Q6_K: launch_mm_t<T_Q6_K>(a, n_route, st); break;
   case T_IQ2_XXS: launch_mm_t<T_IQ2_XXS>(a, n_route, st); break;
   default: return fail("unsupported weight type %d", type);
   }
@@ -87,6 +91,45 @@ void launch_q4_K_matmul_stream(float *y, const float *x, const void *w, int S, i
 }
 void launch_q4_K_matmul(float *y, const float *x, const void *w, int S, int I, int O) {
   plain_matmul(T_Q4_K, y, x, w, S, I, O, nullptr);
+}
+void launch_q5_K_matmul_stream(float *y, const float *x, const void *w, int S, int I, int O, void *stream) {
+  plain_matmul(T_Q5_K, y, x, w, S, I, O, (hipStream_t)stream);
+}
+void launch_q5_K_matmul(float *y, const float *x, const void *w, int S, int I, int O) {
+  plain_matmul(T_Q5_K, y, x, w, S, I, O, nullptr);
+}
+void launch_q6_K_matmul_stream(float *y, const float *x, const void *w, int S, int I, int O, void *stream) {
+  plain_matmul(T_Q6_K, y, x, w, S, I, O, (hipStream_t)stream);
+}
+void launch_q6_K_matmul(float *y, const float *x, const void *w, int S, int I, int O) {
+  plain_matmul(T_Q6_K, y, x, w, S, I, O, nullptr);
+}
+// y[g][O] = x[g][I] . dequant(W_g)^T, W_g at g * group_stride_bytes; false when
+// the shape is rejected (the caller then loops over the groups itself)
+bool launch_q5_K_matmul_grouped(float *y, const float *x, const void *w, int groups, size_t group_stride_bytes, int I,
+                                int O) {
+  if (!y || !x || !w || groups <= 0 || groups > 65535 || O <= 0 || I <= 0 || I % QK || ((uintptr_t)x & 15) ||
+      group_stride_bytes % block_bytes(T_Q5_K) || group_stride_bytes < (size_t)O * (I / QK) * block_bytes(T_Q5_K)) {
+    fail("launch_q5_K_matmul_grouped: rejected shape (groups %d, I %d, O %d, stride %zu)", groups, I, O,
+         group_stride_bytes);
+    return false;
+  }
+  F32MMArgs a{};
+  a.w = (const uint8_t *)w;
+  a.w_row = (size_t)(I / QK) * block_bytes(T_Q5_K);
+  a.w_mat = group_stride_bytes;
+  a.x = x;
+  a.x_tok = (size_t)groups * I;
+  a.x_route = (size_t)I;
+  a.x_routes = groups;
+  a.y = y;
+  a.y_tok = (size_t)groups * O;
+  a.y_route = (size_t)O;
+  a.I = I;
+  a.O = O;
+  a.n_tok = 1;
+  a.mat_by_route = 1;
+  return launch_mm(T_Q5_K, a, groups, nullptr) == 0;
 }
 void launch_iq2_xxs_matmul_stream(float *y, const float *x, const void *w, int S, int I, int O, void *stream) {
   plain_matmul(T_IQ2_XXS, y, x, w, S, I, O, (hipStream_t)stream);

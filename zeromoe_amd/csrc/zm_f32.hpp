@@ -21,7 +21,9 @@ namespace zm {
 // Formulas: ggml's dequantize_row_* (restated from
 // /root/reference/kernels/quant/kquant_matmul.cu:55-92,161-200 and
 // kernels/quant/iq2_matmul.cu:73-91): w = d*sc*q - dmin*m for Q2_K/Q4_K,
-// d*(sc-32)*(q - 4*!h) for Q3_K, d*(0.5+s)*0.25*grid*sign for IQ2_XXS.
+// d*(sc-32)*(q - 4*!h) for Q3_K, d*sc*(q | h<<4) - dmin*m for Q5_K,
+// (d*sc)*(q6 - 32) for Q6_K (kquant_matmul.cu:94-147), d*(0.5+s)*0.25*grid*sign
+// for IQ2_XXS.
 __device__ __forceinline__ uint32_t byte_at(const uint8_t *p) { return *p; }
 
 template <int T>
@@ -50,10 +52,12 @@ __device__ __forceinline__ float4 deq4(const uint8_t *blk, int lane, const uint6
       const int qv = (int)((q >> (8 * i + 2 * j)) & 3) - (((hm >> (8 * i + bit)) & 1) ? 0 : 4);
       w[i] = dl * (float)qv;
     }
-  } else if constexpr (T == T_Q4_K) {
+  } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
     const int j = lane >> 4, l = (4 * lane) & 63, hi = l >> 5;
-    const uint32_t q = ld4(blk + 16 + 32 * j + (l & 31));
-    const uint32_t nib = hi ? ((q >> 4) & 0x0f0f0f0fu) : (q & 0x0f0f0f0fu);
+    constexpr int QS = T == T_Q5_K ? 48 : 16;
+    const uint32_t q = ld4(blk + QS + 32 * j + (l & 31));
+    uint32_t nib = hi ? ((q >> 4) & 0x0f0f0f0fu) : (q & 0x0f0f0f0fu);
+    if constexpr (T == T_Q5_K) nib |= ((ld4(blk + 16 + (l & 31)) >> (2 * j + hi)) & 0x01010101u) << 4;
     const int sub = 2 * j + hi;
     const uint8_t *s = blk + 4;
     uint32_t sc, m;
@@ -68,7 +72,17 @@ __device__ __forceinline__ float4 deq4(const uint8_t *blk, int lane, const uint6
     const float d1 = h2f((uint16_t)dd) * (float)sc;
     const float m1 = h2f((uint16_t)(dd >> 16)) * (float)m;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) w[i] = d1 * (float)((nib >> (8 * i)) & 15) - m1;
+    for (int i = 0; i < 4; ++i) w[i] = d1 * (float)((nib >> (8 * i)) & 31) - m1;
+  } else if constexpr (T == T_Q6_K) {
+    // weights 4*lane.. = 128h + 32g + l..l+3
+    const int h = lane >> 5, g = (lane >> 3) & 3, l = (4 * lane) & 31;
+    const uint32_t q = ld4(blk + 64 * h + 32 * (g & 1) + l);
+    const uint32_t lo = g < 2 ? (q & 0x0f0f0f0fu) : ((q >> 4) & 0x0f0f0f0fu);
+    const uint32_t v = lo | (((ld4(blk + 128 + 32 * h + l) >> (2 * g)) & 0x03030303u) << 4);
+    const int sc = (int)(int8_t)byte_at(blk + 192 + 8 * h + 2 * g + (l >> 4));
+    const float dl = h2f(ld2(blk + 208)) * (float)sc;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = dl * (float)((int)((v >> (8 * i)) & 63) - 32);
   } else {  // IQ2_XXS
     const int ib = lane >> 3, l = (lane >> 1) & 3, hb = lane & 1;
     const uint32_t a0 = ld4(blk + 2 + 8 * ib), a1 = ld4(blk + 6 + 8 * ib);

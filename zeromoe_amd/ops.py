@@ -9,8 +9,8 @@ import torch
 
 from ._lib import ZmExpertScratch, ZmMoeLayer, ZmRouterSpec, ZmTensor, check, lib
 
-GGML_TYPES = {"f32": 0, "q2_K": 10, "q3_K": 11, "q4_K": 12, "q8_K": 15, "iq2_xxs": 16, "i32": 26}
-BLOCK_BYTES = {10: 84, 11: 110, 12: 144, 15: 292, 16: 66}
+GGML_TYPES = {"f32": 0, "q2_K": 10, "q3_K": 11, "q4_K": 12, "q5_K": 13, "q6_K": 14, "q8_K": 15, "iq2_xxs": 16, "i32": 26}
+BLOCK_BYTES = {10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 15: 292, 16: 66}
 QK_K = 256
 GATING = {"softmax": 0, "sigmoid": 1, "sqrt_softplus": 2}
 
