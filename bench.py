@@ -28,8 +28,8 @@ sys.path.insert(0, ROOT)
 
 METRIC = "routed-expert layer µs + HBM GB/s (% of peak) at batch 1; prefill tok/s"
 HBM_PEAK_GBS = 8000.0
-Q2, Q3, Q4, IQ2 = 10, 11, 12, 16
-BB = {Q2: 84, Q3: 110, Q4: 144, IQ2: 66}
+Q2, Q3, Q4, Q5, Q6, IQ2 = 10, 11, 12, 13, 14, 16
+BB = {Q2: 84, Q3: 110, Q4: 144, Q5: 176, Q6: 210, IQ2: 66}
 
 CONFIGS = {
     # name: H, F, E, K, S, type gate/up, type down, extra
@@ -41,12 +41,14 @@ CONFIGS = {
                groups_used=4, norm=True, scale=2.5, F_shared=2048, t_shared=Q4, router_gemv=True),
 }
 CONFIGS["c5_s64"] = dict(CONFIGS["c5"], S=64)
+CONFIGS["q4k_q6k"] = dict(CONFIGS["c2"], tg=Q4, td=Q6)
 WORKLOAD = {
     "c1": "decode S=1, H=2048 F=768 E=128 top-8 softmax, Q4_K",
     "c2": "decode S=1, H=4096 F=1536 E=128 top-8 softmax, gate/up Q2_K, down Q3_K",
     "c3": "prefill S=512, H=4096 F=1536 E=128 top-8 softmax + per-expert logit bias N(0,1.5), Q4_K",
     "c4": "small batch S=4, H=5120 F=1536 E=160 top-8 softmax, IQ2_XXS",
     "c5": "full block S=1, H=7168 F=2048, 256 routed Q2_K (96 resident slots) + shared Q4_K, sigmoid 8 groups/top-4",
+    "q4k_q6k": "decode S=1 at c2's shape with Q4_K gate/up and a Q6_K down projection (mixed-type layer)",
     "c5_s64": "full block S=64, H=7168 F=2048, 256 routed Q2_K (96 resident slots) + shared Q4_K, sigmoid 8 groups/top-4",
 }
 
@@ -73,6 +75,11 @@ def dev_random_blocks(torch, t, rows, n, gen, scale=0.02):
     elif t == Q4:
         put(0, 0.5 * scale / 200, 1.5 * scale / 200)
         put(2, 0.5 * scale / 60, 1.5 * scale / 60)
+    elif t == Q5:
+        put(0, 0.5 * scale / 400, 1.5 * scale / 400)
+        put(2, 0.5 * scale / 60, 1.5 * scale / 60)
+    elif t == Q6:
+        put(208, 0.5 * scale / 2000, 1.5 * scale / 2000)
     else:
         put(0, 0.5 * scale / 40, 1.5 * scale / 40)
     return raw.view(rows, nb * BB[t])
@@ -363,7 +370,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--replicas", type=int, default=0, help="layer replicas (0 = enough to exceed the MALL)")
-    ap.add_argument("--extras", default="c1,c3,c4,c5,c5_s64", help="extra configs to report ('' for none)")
+    ap.add_argument("--extras", default="c1,c3,c4,c5,c5_s64,q4k_q6k", help="extra configs to report ('' for none)")
     ap.add_argument("--no-unpack", dest="unpack", action="store_false",
                     help="skip the expert-record unpack extra")
     ap.add_argument("--no-cpu", action="store_true")

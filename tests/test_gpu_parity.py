@@ -260,6 +260,9 @@ FUSED_CASES = {
     "c4": (CONFIGS["c4"], {}),
     "c5": (CONFIGS["c5"], {}),
     "c5_S2": (CONFIGS["c5"], dict(S=2)),
+    "q4k_q6k": (CONFIGS["c2"], dict(tg=Q4, td=Q6)),
+    "q4k_q6k_S4": (CONFIGS["c2"], dict(tg=Q4, td=Q6, S=4)),
+    "q5k_q6k": (CONFIGS["c2"], dict(tg=Q5, td=Q6)),
 }
 
 

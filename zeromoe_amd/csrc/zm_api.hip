@@ -584,7 +584,7 @@ int check_layer(const zm_moe_layer *L) {
   return 0;
 }
 using DecFn = void (*)(DecodeArgs);
-int units_per_block(int t) { return t == T_Q4_K ? 2 : 1; }
+int units_per_block(int t) { return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K ? 2 : 1; }
 
 template <int TG, int TD, int TS, int L1>
 DecFn dec_pick2(int ir, int is) {
@@ -610,6 +610,9 @@ DecFn find_decode(int tg, int td, int ts, int l1, int ir, int is) {
   if (tg == T_IQ2_XXS && td == T_IQ2_XXS && ts == 0) return dec_pick<T_IQ2_XXS, T_IQ2_XXS, 0>(l1, ir, is);
   if (tg == T_Q2_K && td == T_Q2_K && ts == T_Q4_K) return dec_pick<T_Q2_K, T_Q2_K, T_Q4_K>(l1, ir, is);
   if (tg == T_Q2_K && td == T_Q2_K && ts == 0) return dec_pick<T_Q2_K, T_Q2_K, 0>(l1, ir, is);
+  // mixed K-quant layers of real checkpoints: Q4_K / Q5_K gate and up with a Q6_K down projection
+  if (tg == T_Q4_K && td == T_Q6_K && ts == 0) return dec_pick<T_Q4_K, T_Q6_K, 0>(l1, ir, is);
+  if (tg == T_Q5_K && td == T_Q6_K && ts == 0) return dec_pick<T_Q5_K, T_Q6_K, 0>(l1, ir, is);
   return nullptr;
 }
 

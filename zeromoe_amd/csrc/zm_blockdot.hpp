@@ -1,7 +1,7 @@
 // zm_blockdot.hpp -- whole-super-block int8 dots for the fused decode kernel.
 //
 // One lane holds one "unit" of a weight row in registers: a whole super-block
-// (Q2_K, Q3_K, IQ2_XXS) or half of one (Q4_K), and reads the matching Q8_K
+// (Q2_K, Q3_K, IQ2_XXS) or half of one (Q4_K, Q5_K, Q6_K), and reads the matching Q8_K
 // block of the activation row from LDS (planar layout: qs | bsums | d).  A
 // unit's integer dot is the ggml per-block integer sum (kquant layouts of
 // /root/reference/kernels/quant/kquant_matmul.cu:35-200, iq2_matmul.cu:27-91);
@@ -23,13 +23,13 @@ namespace zm {
 
 template <int T>
 __host__ __device__ constexpr int unit_per_block() {
-  return T == T_Q4_K ? 2 : 1;
+  return T == T_Q4_K || T == T_Q5_K || T == T_Q6_K ? 2 : 1;
 }
 
 // types with a whole-block unit (the fused decode kernel's dot)
 template <int T>
 __host__ __device__ constexpr bool has_unit() {
-  return T == T_Q2_K || T == T_Q3_K || T == T_Q4_K || T == T_IQ2_XXS;
+  return T == T_Q2_K || T == T_Q3_K || T == T_Q4_K || T == T_Q5_K || T == T_Q6_K || T == T_IQ2_XXS;
 }
 
 template <int T>
@@ -53,13 +53,50 @@ struct Unit<T_Q4_K> {  // d, dmin, scales[12] | half of qs[128]
   uint4 q[4];
 };
 template <>
+struct Unit<T_Q5_K> {  // d, dmin, scales[12] | all of qh[32] | half of qs[128]
+  uint4 hdr;
+  uint4 qh[2];
+  uint4 q[4];
+};
+template <>
+struct Unit<T_Q6_K> {  // half h: ql[64h, +64) | qh[32h, +32) | scales[8h, +8) | d
+  uint32_t ql[16];
+  uint32_t qh[8];
+  uint32_t sc[2];
+  uint32_t d;
+};
+template <>
 struct Unit<T_IQ2_XXS> {  // d | qs u16[32]
   uint32_t d;
   uint4 q[4];
 };
 
+// N dwords from byte offset vo (vo even): dword-aligned loads shifted into
+// place, since 16-byte loads that are not dword aligned stream ~35% slower.
+// The extra dword read past the N (only when vo is not dword aligned) must lie
+// inside the resource: callers keep at least 2 more bytes of the block after
+// the region.
+template <int N>
+__device__ __forceinline__ void load_dwords_shifted(rsrc_t r, int vo, uint32_t (&o)[N]) {
+  const int sh = vo & 3, base = vo - sh;
+  uint32_t w[N + 1];
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i) {
+    const uint4 v = bld16(r, base + 16 * i, 0);
+    w[4 * i] = v.x;
+    w[4 * i + 1] = v.y;
+    w[4 * i + 2] = v.z;
+    w[4 * i + 3] = v.w;
+  }
+#pragma unroll
+  for (int i = 4 * (N / 4); i < N; ++i) w[i] = bld4(r, base + 4 * i, 0);
+  w[N] = bld4(r, sh ? base + 4 * N : OOR, 0);
+#pragma unroll
+  for (int k = 0; k < N; ++k) o[k] = __builtin_amdgcn_alignbyte(w[k + 1], w[k], (uint32_t)sh);
+}
+
 // vo: byte offset of the super-block in the resource (an out-of-range offset
-// loads zeros); part: which half for Q4_K
+// loads zeros); part: which half for Q4_K, Q5_K and Q6_K
 template <int T>
 __device__ __forceinline__ void load_unit(rsrc_t r, int vo, int part, Unit<T> &u) {
   if constexpr (T == T_Q2_K) {
@@ -101,6 +138,17 @@ __device__ __forceinline__ void load_unit(rsrc_t r, int vo, int part, Unit<T> &u
     u.hdr = bld16(r, vo, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) u.q[i] = bld16(r, vo + 16 + 64 * part + 16 * i, 0);
+  } else if constexpr (T == T_Q5_K) {  // 176-byte blocks stay 16-byte aligned
+    u.hdr = bld16(r, vo, 0);
+    u.qh[0] = bld16(r, vo + 16, 0);
+    u.qh[1] = bld16(r, vo + 32, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u.q[i] = bld16(r, vo + 48 + 64 * part + 16 * i, 0);
+  } else if constexpr (T == T_Q6_K) {  // 210-byte blocks: every other one starts 2 bytes off a dword
+    load_dwords_shifted<16>(r, vo + 64 * part, u.ql);
+    load_dwords_shifted<8>(r, vo + 128 + 32 * part, u.qh);
+    load_dwords_shifted<2>(r, vo + 192 + 8 * part, u.sc);
+    u.d = bld2(r, vo + 208, 0);
   } else {
     u.d = bld2(r, vo, 0);
 #pragma unroll
@@ -298,6 +346,81 @@ __device__ __forceinline__ void unit_ints(const Unit<T> (&w)[NW], int part, cons
       ri[n] = isum;
       rm[n] = imin;
     }
+  } else if constexpr (T == T_Q5_K) {
+    // Q4_K's structure; bit 2i / 2i+1 of qh byte l is bit 4 of the low / high
+    // nibble value of qs byte 32i + l
+    const uint4 b = x.bs[part];
+#pragma unroll
+    for (int n = 0; n < NW; ++n) {
+      const uint32_t u0 = w[n].hdr.y, u1 = w[n].hdr.z, u2 = w[n].hdr.w;
+      const uint32_t scv = part == 0 ? (u0 & 0x3f3f3f3fu) : ((u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4));
+      const uint32_t mv =
+          part == 0 ? (u1 & 0x3f3f3f3fu) : (((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4));
+      int isum = 0, imin = 0;
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const int i = 2 * part + g;
+        int slo = 0, shi = 0;
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm) {
+          const uint4 qv = w[n].q[2 * g + mm];
+          const uint4 hv = w[n].qh[mm];
+          const uint4 xl = x.q[4 * i + mm], xh = x.q[4 * i + 2 + mm];
+          auto lo = [&](uint32_t q, uint32_t h) { return (q & 0x0f0f0f0fu) | (((h >> (2 * i)) & 0x01010101u) << 4); };
+          auto hi = [&](uint32_t q, uint32_t h) {
+            return ((q >> 4) & 0x0f0f0f0fu) | (((h >> (2 * i + 1)) & 0x01010101u) << 4);
+          };
+          slo = dot4(lo(qv.x, hv.x), xl.x, slo);
+          slo = dot4(lo(qv.y, hv.y), xl.y, slo);
+          slo = dot4(lo(qv.z, hv.z), xl.z, slo);
+          slo = dot4(lo(qv.w, hv.w), xl.w, slo);
+          shi = dot4(hi(qv.x, hv.x), xh.x, shi);
+          shi = dot4(hi(qv.y, hv.y), xh.y, shi);
+          shi = dot4(hi(qv.z, hv.z), xh.z, shi);
+          shi = dot4(hi(qv.w, hv.w), xh.w, shi);
+        }
+        isum = mad24((int)((scv >> (16 * g)) & 0xffu), slo, isum);
+        isum = mad24((int)((scv >> (16 * g + 8)) & 0xffu), shi, isum);
+      }
+      imin = sdot2(__builtin_amdgcn_perm(0u, mv, 0x0c000c00u), b.x, imin);
+      imin = sdot2(__builtin_amdgcn_perm(0u, mv, 0x0c010c01u), b.y, imin);
+      imin = sdot2(__builtin_amdgcn_perm(0u, mv, 0x0c020c02u), b.z, imin);
+      imin = sdot2(__builtin_amdgcn_perm(0u, mv, 0x0c030c03u), b.w, imin);
+      ri[n] = isum;
+      rm[n] = imin;
+    }
+  } else if constexpr (T == T_Q6_K) {
+    // half h = part: weight 128h + 32g + l sits in activation chunk 8h + 2g + (l >> 4),
+    // which is also its 16-weight sub-block; value (nibble | 2 bits << 4) - 32,
+    // the -32 folded in as -32 * sum sc * bsum
+    const uint4 b0 = x.bs[0], b1 = x.bs[1];
+    const uint32_t bs[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int n = 0; n < NW; ++n) {
+      int isum = 0, soff = 0;
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const int c = 8 * part + 2 * g + kk;  // chunk = sub-block
+          const uint4 xv = x.q[c];
+          const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
+          int s = 0;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            const uint32_t q = w[n].ql[8 * (g & 1) + 4 * kk + d];
+            const uint32_t lo = g < 2 ? (q & 0x0f0f0f0fu) : ((q >> 4) & 0x0f0f0f0fu);
+            const uint32_t hb = ((w[n].qh[4 * kk + d] >> (2 * g)) & 0x03030303u) << 4;
+            s = dot4(lo | hb, xs[d], s);
+          }
+          const int sl = 2 * g + kk;  // scale byte within the half
+          const int sc = __builtin_amdgcn_sbfe((int)w[n].sc[sl >> 2], 8 * (sl & 3), 8);
+          isum = mad24(sc, s, isum);
+          soff = mad24(sc, __builtin_amdgcn_sbfe((int)bs[c >> 1], 16 * (c & 1), 16), soff);
+        }
+      ri[n] = isum - 32 * soff;
+      rm[n] = 0;
+    }
   } else {  // IQ2_XXS: sub-block ib uses qs dwords 2ib (4 grid indices), 2ib+1 (4 x 7-bit signs, 4-bit scale)
     int isum[NW];
 #pragma unroll
@@ -339,9 +462,11 @@ __device__ __forceinline__ float unit_float(const Unit<T> &w, float xd, int isum
     return (xd * d) * (float)isum - (xd * dmin) * (float)imin;
   } else if constexpr (T == T_Q3_K) {
     return (xd * h2f((uint16_t)(w.d & 0xffffu))) * (float)isum;
-  } else if constexpr (T == T_Q4_K) {
+  } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
     const float d = h2f((uint16_t)(w.hdr.x & 0xffffu)), dmin = h2f((uint16_t)(w.hdr.x >> 16));
     return (xd * d) * (float)isum - (xd * dmin) * (float)imin;
+  } else if constexpr (T == T_Q6_K) {
+    return (xd * h2f((uint16_t)(w.d & 0xffffu))) * (float)isum;
   } else {
     return 0.125f * ((xd * h2f((uint16_t)(w.d & 0xffffu))) * (float)isum);
   }
