@@ -583,37 +583,11 @@ int check_layer(const zm_moe_layer *L) {
   if (L->router_w && L->H % 4) return fail("router GEMV needs H %% 4 == 0");
   return 0;
 }
-using DecFn = void (*)(DecodeArgs);
 int units_per_block(int t) { return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K ? 2 : 1; }
 
-template <int TG, int TD, int TS, int L1>
-DecFn dec_pick2(int ir, int is) {
-  if (is != (TS ? 1 : 0)) return nullptr;
-  constexpr int IS = TS ? 1 : 0;
-  if (ir <= 2) return k_moe_decode<TG, TD, TS, L1, 2, IS>;
-  if (ir <= 3) return k_moe_decode<TG, TD, TS, L1, 3, IS>;
-  return nullptr;
-}
-
-// L1: lanes per routed gate/up row (16 or 32, one unit each; shared rows use
-// 64); IR / IS: 32-lane iterations over the routed / shared units of a down row
-template <int TG, int TD, int TS>
-DecFn dec_pick(int l1, int ir, int is) {
-  if (l1 == 16) return dec_pick2<TG, TD, TS, 16>(ir, is);
-  if (l1 == 32) return dec_pick2<TG, TD, TS, 32>(ir, is);
-  return nullptr;
-}
-
 DecFn find_decode(int tg, int td, int ts, int l1, int ir, int is) {
-  if (tg == T_Q4_K && td == T_Q4_K && ts == 0) return dec_pick<T_Q4_K, T_Q4_K, 0>(l1, ir, is);
-  if (tg == T_Q2_K && td == T_Q3_K && ts == 0) return dec_pick<T_Q2_K, T_Q3_K, 0>(l1, ir, is);
-  if (tg == T_IQ2_XXS && td == T_IQ2_XXS && ts == 0) return dec_pick<T_IQ2_XXS, T_IQ2_XXS, 0>(l1, ir, is);
-  if (tg == T_Q2_K && td == T_Q2_K && ts == T_Q4_K) return dec_pick<T_Q2_K, T_Q2_K, T_Q4_K>(l1, ir, is);
-  if (tg == T_Q2_K && td == T_Q2_K && ts == 0) return dec_pick<T_Q2_K, T_Q2_K, 0>(l1, ir, is);
-  // mixed K-quant layers of real checkpoints: Q4_K / Q5_K gate and up with a Q6_K down projection
-  if (tg == T_Q4_K && td == T_Q6_K && ts == 0) return dec_pick<T_Q4_K, T_Q6_K, 0>(l1, ir, is);
-  if (tg == T_Q5_K && td == T_Q6_K && ts == 0) return dec_pick<T_Q5_K, T_Q6_K, 0>(l1, ir, is);
-  return nullptr;
+  if (DecFn f = find_decode_a(tg, td, ts, l1, ir, is)) return f;
+  return find_decode_b(tg, td, ts, l1, ir, is);
 }
 
 bool fused_enabled() {

@@ -546,4 +546,30 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
 
 #undef ZM_TRACE
 
+using DecFn = void (*)(DecodeArgs);
+
+template <int TG, int TD, int TS, int L1>
+DecFn dec_pick2(int ir, int is) {
+  if (is != (TS ? 1 : 0)) return nullptr;
+  constexpr int IS = TS ? 1 : 0;
+  if (ir <= 2) return k_moe_decode<TG, TD, TS, L1, 2, IS>;
+  if (ir <= 3) return k_moe_decode<TG, TD, TS, L1, 3, IS>;
+  return nullptr;
+}
+
+// L1: lanes per routed gate/up row (16 or 32, one unit each; shared rows use
+// 64); IR / IS: 32-lane iterations over the routed / shared units of a down row
+template <int TG, int TD, int TS>
+DecFn dec_pick(int l1, int ir, int is) {
+  if (l1 == 16) return dec_pick2<TG, TD, TS, 16>(ir, is);
+  if (l1 == 32) return dec_pick2<TG, TD, TS, 32>(ir, is);
+  return nullptr;
+}
+
+// The instantiated decode kernels, split over two translation units so they
+// compile in parallel (zm_dec_a.hip, zm_dec_b.hip); nullptr when the layer's
+// (gate, down, shared) types or unit counts have no instantiation.
+DecFn find_decode_a(int tg, int td, int ts, int l1, int ir, int is);
+DecFn find_decode_b(int tg, int td, int ts, int l1, int ir, int is);
+
 }  // namespace zm

@@ -10,6 +10,10 @@
 
 #include "zm_device.hpp"
 
+// The non-template kernels below have internal linkage: this header is
+// included by more than one translation unit (the decode-kernel instantiation
+// units take its device functions only).
+
 namespace zm {
 
 // ============================================================ Q8_K quantization
@@ -87,7 +91,7 @@ __device__ __forceinline__ Q8Out quant_block_wave(float4 v, int lane) {
 }
 
 // rows x nb blocks; planar != 0 writes the internal planar layout, else ggml block_q8_K
-__global__ __launch_bounds__(256) void k_quant_q8K(const float *__restrict__ x, size_t x_rstride, int nb, int rows,
+static __global__ __launch_bounds__(256) void k_quant_q8K(const float *__restrict__ x, size_t x_rstride, int nb, int rows,
                                                    uint8_t *__restrict__ y, size_t y_rstride, int planar) {
   const int lane = threadIdx.x & 63;
   const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -338,7 +342,7 @@ __device__ __forceinline__ WaveRoute route_token(const RouterArgs &a, int s, flo
 }
 
 // one wave per token, 4 tokens per workgroup
-__global__ __launch_bounds__(256) void k_router(RouterArgs a, int S) {
+static __global__ __launch_bounds__(256) void k_router(RouterArgs a, int S) {
   __shared__ float scr[4][ROUTER_MAX_E];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int s = blockIdx.x * 4 + wave;
@@ -424,7 +428,7 @@ __device__ __forceinline__ void store_q8_16(uint8_t *row, int nb, int blk, const
 // per-wave counts, so the order is exactly the sequential one.
 constexpr int BUCKET_MAX_E = 512;
 
-__global__ __launch_bounds__(1024) void k_bucket(const int32_t *__restrict__ ids, int n_pairs, int E,
+static __global__ __launch_bounds__(1024) void k_bucket(const int32_t *__restrict__ ids, int n_pairs, int E,
                                                  int32_t *__restrict__ counts, int32_t *__restrict__ offs,
                                                  int32_t *__restrict__ pairs, int32_t *__restrict__ active,
                                                  int32_t *__restrict__ n_active) {
@@ -540,7 +544,7 @@ struct GemvArgs {
 };
 
 template <int T, int LPR, int ITER, int NP, bool GATEUP>
-__global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
+static __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   __shared__ uint64_t s_grid[T == T_IQ2_XXS ? 256 : 1];
   __shared__ uint64_t s_signs[T == T_IQ2_XXS ? 128 : 1];
   if constexpr (T == T_IQ2_XXS) {
@@ -630,7 +634,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
 // ============================================================ combine
 // ggml_mul(down, weights) then sum_topk (moe_routed_ggml.hpp:198-214):
 // out = ((w0*y0 + w1*y1) + w2*y2) + ...   (+ shared, moe_block.hpp:201-202)
-__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, const float *__restrict__ w,
+static __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, const float *__restrict__ w,
                                                  const float *__restrict__ shared, int H, int K,
                                                  float *__restrict__ out) {
   const int s = blockIdx.y;
@@ -645,7 +649,7 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, co
 
 // zero (negative id) or NaN (id >= n_experts) rows of routes the GEMV skips
 // (patches/ggml/0002...:50-54; kernels/quant/kquant_matmul.cu:660-663)
-__global__ void k_fill_skipped(const int32_t *__restrict__ ids, size_t id_s, size_t id_k, int n_ids, int S,
+static __global__ void k_fill_skipped(const int32_t *__restrict__ ids, size_t id_s, size_t id_k, int n_ids, int S,
                                int n_experts, int O, float *out, size_t out_s, size_t out_k) {
   const int pair = blockIdx.y;
   const int s = pair / n_ids, k = pair % n_ids;
@@ -657,7 +661,7 @@ __global__ void k_fill_skipped(const int32_t *__restrict__ ids, size_t id_s, siz
 
 // ============================================================ fp32 router GEMV
 // logits[s][e] = sum_i W[e][i] * x[s][i] (ggml_mul_mat(router, cur), moe_routed_ggml.hpp:55)
-__global__ __launch_bounds__(256) void k_router_gemv(const float *__restrict__ W, const float *__restrict__ x,
+static __global__ __launch_bounds__(256) void k_router_gemv(const float *__restrict__ W, const float *__restrict__ x,
                                                      int H, int E, int S, float *__restrict__ logits) {
   __shared__ float part[4][64];
   const int e = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -695,7 +699,7 @@ __global__ __launch_bounds__(256) void k_router_gemv(const float *__restrict__ W
 // feeds token / expert n with the 4 consecutive values k0 + 4g .. 4g+3 of each
 // 16-wide K chunk, one per MFMA.  H % (64 * KS) == 0.
 typedef float v4f_rt __attribute__((ext_vector_type(4)));
-__global__ __launch_bounds__(256) void k_router_gemm(const float *__restrict__ W, const float *__restrict__ x, int H,
+static __global__ __launch_bounds__(256) void k_router_gemm(const float *__restrict__ W, const float *__restrict__ x, int H,
                                                      int E, int S, float *__restrict__ part) {
   __shared__ float red[4][64][4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -740,7 +744,7 @@ __global__ __launch_bounds__(256) void k_router_gemm(const float *__restrict__ W
     }
   }
 }
-__global__ __launch_bounds__(256) void k_router_sum(const float *__restrict__ part, int n, int KS,
+static __global__ __launch_bounds__(256) void k_router_sum(const float *__restrict__ part, int n, int KS,
                                                     float *__restrict__ logits) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
