@@ -118,10 +118,10 @@ def test_mul_mat_id_skewed_prefill_buckets():
     np.testing.assert_allclose(got, ref, rtol=1e-3, atol=1e-3 * np.abs(ref).max())
 
 
-@pytest.mark.parametrize("t", [Q4, Q2])
+@pytest.mark.parametrize("t", [Q4, Q2, Q6])
 @pytest.mark.parametrize("ne11", [1, 8])
 def test_mul_mat_id_mfma_buckets_per_element(ne11, t):
-    """Buckets of 64-80 pairs take the int8-MFMA path for Q4_K and Q2_K: every
+    """Buckets of 64-80 pairs take the int8-MFMA path for Q4_K, Q2_K and Q6_K: every
     output element within 1e-3 relative of the oracle (the op alone, no
     re-quantization)."""
     rng = np.random.default_rng(11 + ne11)
@@ -326,6 +326,9 @@ PREFILL_CASES = {
     "c3_skewed": (CONFIGS["c3"], dict(S=192, H=2048, F=768, E=64)),
     # Q2_K routed experts (few pairs each) + Q4_K shared expert, slot table
     "c5_S64": (CONFIGS["c5"], dict(S=64, H=2048, F=1024, F_shared=1024)),
+    # mixed-type layers: Q4_K gate/up with a Q6_K down projection; all Q6_K
+    "q4k_q6k_mmq": (CONFIGS["c3"], dict(td=Q6, S=256, H=1024, F=512, E=16)),
+    "q6k_q6k_mmq": (CONFIGS["c3"], dict(tg=Q6, td=Q6, S=128, H=1024, F=768, E=16)),
 }
 
 

@@ -414,9 +414,9 @@ __device__ __forceinline__ void unit_ints(const Unit<T> (&w)[NW], int part, cons
             s = dot4(lo | hb, xs[d], s);
           }
           const int sl = 2 * g + kk;  // scale byte within the half
-          const int sc = __builtin_amdgcn_sbfe((int)w[n].sc[sl >> 2], 8 * (sl & 3), 8);
+          const int sc = (int)(int8_t)(w[n].sc[sl >> 2] >> (8 * (sl & 3)));
           isum = mad24(sc, s, isum);
-          soff = mad24(sc, __builtin_amdgcn_sbfe((int)bs[c >> 1], 16 * (c & 1), 16), soff);
+          soff = mad24(sc, (int)(int16_t)(bs[c >> 1] >> (16 * (c & 1))), soff);
         }
       ri[n] = isum - 32 * soff;
       rm[n] = 0;

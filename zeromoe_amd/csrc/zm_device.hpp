@@ -530,7 +530,7 @@ __device__ __forceinline__ QInt quarter_int(const WSlice &w, int q, const Q8Slic
         const uint32_t hi = ((u4_get(w.g, i) >> (2 * g)) & 0x03030303u) << 4;
         dg = dot4(lo | hi, u4_get(a.q[g], i), dg);
       }
-      const int sc = __builtin_amdgcn_sbfe((int)(g < 2 ? w.e.x : w.e.y), 8 * (qq + 2 * (g & 1)), 8);
+      const int sc = (int)(int8_t)((g < 2 ? w.e.x : w.e.y) >> (8 * (qq + 2 * (g & 1))));
       r.isum += sc * (dg - 32 * a.bs[g]);
     }
   } else {  // IQ2_XXS: sub-blocks 2q, 2q+1; words (aux0, aux1) each

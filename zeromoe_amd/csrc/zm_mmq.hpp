@@ -31,6 +31,19 @@
 // mins term sum_sb m * bsum16 goes through four v_mfma_f32_16x16x4f32 (K = 16
 // sub-blocks), and f += d_x * (d * isum - dmin * imin) (ggml's vec_dot_q2_K_q8_K).  Activations are the planar Q8_K rows of the decode
 // path (qs | bsums | d).
+//
+// Q6_K (a 6-bit value and a signed 8-bit scale per 16-weight sub-block: the
+// product does not fit int8) keeps the scales out of the weights and uses
+// v_mfma_i32_16x16x32_i8, whose K = 32 spans two sub-blocks (lane groups 0-1
+// and 2-3): each pair of sub-blocks is issued twice with the other half of
+// the B operand zeroed, giving one exact 16x16 integer dot per sub-block,
+// scaled per lane (a lane's outputs share one weight row) and summed:
+//   isum[t][r] = sum_sb sc[r][sb] * (q[r] . x[t])_sb            (q = 0..63)
+//   off[t][r]  = sum_sb sc[r][sb] * bsum16[t][sb]               (v_mfma_f32_16x16x4f32, exact)
+//   f[t][r]   += d_x[t] * d[r] * (isum - 32 * off)   (the value is q - 32; ggml's vec_dot_q6_K_q8_K)
+// Lane (row n, group g) of sub-block pair p holds weights 32p + 8g .. +7:
+// low (p & 3 < 2) or high nibbles of ql bytes 64(p >> 2) + 32(p & 1) + 8g .. +7,
+// top bits 2(p & 3) of qh bytes 32(p >> 2) + 8g .. +7.
 #pragma once
 
 #include "zm_kernels.hpp"
@@ -100,12 +113,19 @@ struct MmqW<T_Q2_K> {  // scales | this lane's 2 x 16 bytes of qs | d, dmin
   uint4 qs[2];
   uint32_t dd;
 };
+template <>
+struct MmqW<T_Q6_K> {  // this lane's 4 x 8 bytes of ql, 2 x 8 bytes of qh | scales | d
+  uint2 ql[4];
+  uint2 qh[2];
+  uint4 sc;
+  uint32_t d;
+};
 
 template <int T, bool GATEUP, int TT>
 __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
   constexpr int TOK = 16 * TT;  // pairs per work item
-  static_assert(T == T_Q4_K || T == T_Q2_K, "MFMA prefill types");
-  constexpr int NBS = T == T_Q4_K ? 8 : 16;  // bsums per block used: 32-sums (Q4_K) or 16-sums (Q2_K)
+  static_assert(T == T_Q4_K || T == T_Q2_K || T == T_Q6_K, "MFMA prefill types");
+  constexpr int NBS = T == T_Q4_K ? 8 : 16;  // bsums per block used: 32-sums (Q4_K) or 16-sums (Q2_K, Q6_K)
   __shared__ __attribute__((aligned(16))) uint8_t s_xq[2][TOK][MMQ_XS];
   __shared__ int s_bs[2][TOK][NBS];
   __shared__ float s_xd[2][TOK];
@@ -158,6 +178,13 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
         w[m].hdr = bld16(rw[m], vo, 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) w[m].qs[i] = bld16(rw[m], vo + 16 + 32 * i + 16 * (g & 1), 0);
+      } else if constexpr (T == T_Q6_K) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[m].ql[i] = bld8(rw[m], vo + 64 * (i >> 1) + 32 * (i & 1) + 8 * g, 0);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) w[m].qh[h] = bld8(rw[m], vo + 128 + 32 * h + 8 * g, 0);
+        w[m].sc = bld16(rw[m], vo + 192, 0);
+        w[m].d = bld2(rw[m], vo + 208, 0);
       } else {
         w[m].sc = bld16(rw[m], vo, 0);
 #pragma unroll
@@ -281,6 +308,57 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           f[m][t][j] += s_xd[buf][16 * t + 4 * g + j] * (d * (float)(dlo[j] + 8 * dhi[j]) - dmin * mn[j]);
+      }
+    }
+    } else if constexpr (T == T_Q6_K) {
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      const float d = h2f((uint16_t)(wcur[m].d & 0xffffu));
+      const uint32_t scb[4] = {wcur[m].sc.x, wcur[m].sc.y, wcur[m].sc.z, wcur[m].sc.w};
+      // B operand of the offset product: sc[row][sb] for sb = 4i + g
+      float mb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mb[i] = (float)(int)(int8_t)(scb[i] >> (8 * g));
+      // 6-bit values of the 8 sub-block pairs, each issued with the lane's half
+      // (groups 0-1: sub-block 2p, groups 2-3: 2p + 1) and zeros in the other
+      const uint32_t keep0 = g < 2 ? 0xffffffffu : 0u;
+      long b0[8], b1[8];
+      int s0[8], s1[8];
+#pragma unroll
+      for (int p = 0; p < 8; ++p) {
+        const int h = p >> 2, G = p & 3;
+        const uint2 q = wcur[m].ql[2 * h + (p & 1)];
+        const uint2 hb = wcur[m].qh[h];
+        const uint32_t lx = G < 2 ? (q.x & 0x0f0f0f0fu) : ((q.x >> 4) & 0x0f0f0f0fu);
+        const uint32_t ly = G < 2 ? (q.y & 0x0f0f0f0fu) : ((q.y >> 4) & 0x0f0f0f0fu);
+        const uint32_t vx = lx | (((hb.x >> (2 * G)) & 0x03030303u) << 4);
+        const uint32_t vy = ly | (((hb.y >> (2 * G)) & 0x03030303u) << 4);
+        b0[p] = (long)(((uint64_t)(vy & keep0) << 32) | (vx & keep0));
+        b1[p] = (long)(((uint64_t)(vy & ~keep0) << 32) | (vx & ~keep0));
+        s0[p] = (int)(int8_t)(scb[p >> 1] >> (16 * (p & 1)));
+        s1[p] = (int)(int8_t)(scb[p >> 1] >> (16 * (p & 1) + 8));
+      }
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        if (t >= nt) continue;
+        const uint8_t *xr = &s_xq[buf][16 * t + n][0];
+        int isum[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+          const long xa = *reinterpret_cast<const long *>(xr + 32 * p + 8 * g);
+          const v4i_t z = {0, 0, 0, 0};
+          const v4i_t d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa, b0[p], z, 0, 0, 0);
+          const v4i_t d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa, b1[p], z, 0, 0, 0);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) isum[j] = __mul24(s0[p], d0[j]) + __mul24(s1[p], d1[j]) + isum[j];
+        }
+        v4f_t off = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          off = __builtin_amdgcn_mfma_f32_16x16x4f32((float)s_bs[buf][16 * t + n][4 * i + g], mb[i], off, 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          f[m][t][j] += s_xd[buf][16 * t + 4 * g + j] * (d * (float)(isum[j] - 32 * (int)off[j]));
       }
     }
     } else {
