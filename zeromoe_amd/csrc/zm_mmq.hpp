@@ -22,6 +22,9 @@
 // block for all MMQ_TT token tiles of the work item.
 // No dequantized weight copy is materialized.
 //
+// Q5_K adds the fifth bit of each value as a third chain: the bit (0/1) times
+// the whole 6-bit scale (<= 63) is int8 too, and isum = D_lo + 8 D_hi + 16 D_5.
+//
 // Q2_K uses v_mfma_i32_16x16x64_i8 with the 4-bit sub-block scale folded into
 // the weights (q * sc <= 45 fits int8): lane (row n, k-group g) of 64-weight
 // chunk c = 2h + jp holds bit-plane j = 2jp + (g >> 1) of qs bytes
@@ -108,6 +111,12 @@ struct MmqW<T_Q4_K> {  // d, dmin, scales | this lane's 4 x 16 bytes of qs
   uint4 qs[4];
 };
 template <>
+struct MmqW<T_Q5_K> {  // d, dmin, scales | this lane's 16 bytes of qh | 4 x 16 bytes of qs
+  uint4 hdr;
+  uint4 qh;
+  uint4 qs[4];
+};
+template <>
 struct MmqW<T_Q2_K> {  // scales | this lane's 2 x 16 bytes of qs | d, dmin
   uint4 sc;
   uint4 qs[2];
@@ -124,8 +133,9 @@ struct MmqW<T_Q6_K> {  // this lane's 4 x 8 bytes of ql, 2 x 8 bytes of qh | sca
 template <int T, bool GATEUP, int TT>
 __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
   constexpr int TOK = 16 * TT;  // pairs per work item
-  static_assert(T == T_Q4_K || T == T_Q2_K || T == T_Q6_K, "MFMA prefill types");
-  constexpr int NBS = T == T_Q4_K ? 8 : 16;  // bsums per block used: 32-sums (Q4_K) or 16-sums (Q2_K, Q6_K)
+  static_assert(T == T_Q4_K || T == T_Q5_K || T == T_Q2_K || T == T_Q6_K, "MFMA prefill types");
+  constexpr bool K45 = T == T_Q4_K || T == T_Q5_K;
+  constexpr int NBS = K45 ? 8 : 16;  // bsums per block used: 32-sums (Q4_K, Q5_K) or 16-sums (Q2_K, Q6_K)
   __shared__ __attribute__((aligned(16))) uint8_t s_xq[2][TOK][MMQ_XS];
   __shared__ int s_bs[2][TOK][NBS];
   __shared__ float s_xd[2][TOK];
@@ -178,6 +188,11 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
         w[m].hdr = bld16(rw[m], vo, 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) w[m].qs[i] = bld16(rw[m], vo + 16 + 32 * i + 16 * (g & 1), 0);
+      } else if constexpr (T == T_Q5_K) {
+        w[m].hdr = bld16(rw[m], vo, 0);
+        w[m].qh = bld16(rw[m], vo + 16 + 16 * (g & 1), 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[m].qs[i] = bld16(rw[m], vo + 48 + 32 * i + 16 * (g & 1), 0);
       } else if constexpr (T == T_Q6_K) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) w[m].ql[i] = bld8(rw[m], vo + 64 * (i >> 1) + 32 * (i & 1) + 8 * g, 0);
@@ -234,7 +249,7 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
       const int c = tid + 256 * r;
       if (c < TOK * 8) {
         const int lo = (int)(int16_t)(x.bs[r] & 0xffffu), hi = (int)(int16_t)(x.bs[r] >> 16);
-        if constexpr (T == T_Q4_K) {
+        if constexpr (K45) {
           s_bs[buf][c >> 3][c & 7] = lo + hi;
         } else {
           s_bs[buf][c >> 3][2 * (c & 7)] = lo;
@@ -263,7 +278,7 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
   for (int b = 0; b < nb; ++b) {
     const int buf = b & 1;
     load_w(b + 1, wnxt);
-    if constexpr (T == T_Q4_K) {
+    if constexpr (K45) {
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
       const uint32_t u0 = wcur[m].hdr.y, u1 = wcur[m].hdr.z, u2 = wcur[m].hdr.w;
@@ -275,7 +290,9 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
       const float mb0 = (float)((mn_lo >> (8 * g)) & 0xffu), mb1 = (float)((mn_hi >> (8 * g)) & 0xffu);
       // scale-folded weights of the 4 chunks: lane's sub-block 2i + (g >> 1),
       // sc = 8 * hi + lo
-      v4i_t bl[4], bh[4];
+      // Q5_K: the fifth bit (bit 2i + (g >> 1) of the lane's qh bytes) is a third
+      // chain with the whole scale, isum = D_lo + 8 * D_hi + 16 * D_5
+      v4i_t bl[4], bh[4], b5[K45 && T == T_Q5_K ? 4 : 1];
       const int hs = 8 * (g >> 1), ns = 4 * (g >> 1);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -289,25 +306,30 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
           const uint32_t nib = (qw[c] >> ns) & 0x0f0f0f0fu;
           bl[i][c] = (int)mul_bytes(nib, lo);
           bh[i][c] = (int)mul_bytes(nib, hi);
+          if constexpr (T == T_Q5_K) {
+            const uint32_t hq[4] = {wcur[m].qh.x, wcur[m].qh.y, wcur[m].qh.z, wcur[m].qh.w};
+            b5[i][c] = (int)mul_bytes((hq[c] >> (2 * i + (g >> 1))) & 0x01010101u, sc);
+          }
         }
       }
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
         if (t >= nt) continue;
         const uint8_t *xr = &s_xq[buf][16 * t + n][0];
-        v4i_t dlo = {0, 0, 0, 0}, dhi = {0, 0, 0, 0};
+        v4i_t dlo = {0, 0, 0, 0}, dhi = {0, 0, 0, 0}, d5 = {0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const v4i_t xa = *reinterpret_cast<const v4i_t *>(xr + 64 * i + 16 * g);
           dlo = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, bl[i], dlo, 0, 0, 0);
           dhi = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, bh[i], dhi, 0, 0, 0);
+          if constexpr (T == T_Q5_K) d5 = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, b5[i], d5, 0, 0, 0);
         }
         v4f_t mn = {0.f, 0.f, 0.f, 0.f};
         mn = __builtin_amdgcn_mfma_f32_16x16x4f32((float)s_bs[buf][16 * t + n][g], mb0, mn, 0, 0, 0);
         mn = __builtin_amdgcn_mfma_f32_16x16x4f32((float)s_bs[buf][16 * t + n][g + 4], mb1, mn, 0, 0, 0);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          f[m][t][j] += s_xd[buf][16 * t + 4 * g + j] * (d * (float)(dlo[j] + 8 * dhi[j]) - dmin * mn[j]);
+          f[m][t][j] += s_xd[buf][16 * t + 4 * g + j] * (d * (float)(dlo[j] + 8 * dhi[j] + 16 * d5[j]) - dmin * mn[j]);
       }
     }
     } else if constexpr (T == T_Q6_K) {
