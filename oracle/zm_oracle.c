@@ -24,6 +24,9 @@
  *     hand-picked rows); bit identity with ggml's own build "parity unpinned".
  *   - K-quant / IQ2_XXS weight quantizers: produce valid blocks; ggml's byte
  *     choices are "parity unpinned" (the op is checked on identical bytes).
+ *   - IQ4_XS: per-block integer sums pinned by brute force over the dequant
+ *     (exact); table values ggml's published kvalues_iq4nl, "parity unpinned"
+ *     (not in the reference tree); float order unpinned.
  *   - IQ2_XXS grid: a stand-in table (ggml's 256 x u64 values are not in the
  *     reference tree); the sign table is closed form (0009...:69-75).
  *   - Router, bucketing, SwiGLU, combine: closed forms, brute-force checked.
@@ -106,6 +109,7 @@ size_t zmo_row_size(int type, int64_t n) {
   case ZMO_TYPE_Q5_K: return (size_t)nb * sizeof(zmo_block_q5_K);
   case ZMO_TYPE_Q6_K: return (size_t)nb * sizeof(zmo_block_q6_K);
   case ZMO_TYPE_IQ2_XXS: return (size_t)nb * sizeof(zmo_block_iq2_xxs);
+  case ZMO_TYPE_IQ4_XS: return (size_t)nb * sizeof(zmo_block_iq4_xs);
   case ZMO_TYPE_Q8_K: return (size_t)nb * sizeof(zmo_block_q8_K);
   case ZMO_TYPE_F32: return (size_t)n * 4;
   default: return 0;
@@ -217,6 +221,13 @@ void zmo_set_iq2xxs_grid(const uint64_t grid[256]) {
   memcpy(g_iq2xxs_grid, grid, sizeof(g_iq2xxs_grid));
   g_iq2xxs_ready = 1;
 }
+
+/* ------------------------------------------------------------ IQ4_XS table */
+
+static int8_t g_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+const int8_t *zmo_iq4nl_table(void) { return g_iq4nl; }
+void zmo_set_iq4nl_table(const int8_t table[16]) { memcpy(g_iq4nl, table, 16); }
 
 /* ---------------------------------------------------------------- Q8_K quant */
 
@@ -748,6 +759,70 @@ void zmo_quantize_row_iq2_xxs(const float *x, zmo_block_iq2_xxs *y, int64_t k) {
   }
 }
 
+/* IQ4_XS: per 32-weight sub-block a 6-bit scale ls (value ls - 32) and 4-bit
+ * indices into the 16-entry table; weight = d * (ls - 32) * table[idx]
+ * (dequant at kernels/quant/iq4xs_matmul.cu:80-99).  The scale of a
+ * sub-block maps its largest |x| to the table's largest |value|; the block d
+ * fits the largest sub-block scale into ls - 32 in [-32, 31]; indices are
+ * the nearest table values under the stored scale. */
+static int nearest_iq4(const int8_t *t, float v) {
+  int best = 0;
+  float be = fabsf(v - t[0]);
+  for (int i = 1; i < 16; ++i) {
+    const float e = fabsf(v - t[i]);
+    if (e < be) {
+      be = e;
+      best = i;
+    }
+  }
+  return best;
+}
+
+void zmo_quantize_row_iq4_xs(const float *x, zmo_block_iq4_xs *y, int64_t k) {
+  const int8_t *t = zmo_iq4nl_table();
+  int tmax = 0;
+  for (int i = 0; i < 16; ++i) tmax = abs(t[i]) > tmax ? abs(t[i]) : tmax;
+  for (int64_t i = 0; i < k / ZMO_QK_K; ++i, x += ZMO_QK_K) {
+    float sc[8], amax_sc = 0.f;
+    for (int ib = 0; ib < 8; ++ib) {
+      float amax = 0.f, mx = 0.f;
+      for (int j = 0; j < 32; ++j) {
+        const float a = fabsf(x[32 * ib + j]);
+        if (a > amax) {
+          amax = a;
+          mx = x[32 * ib + j];
+        }
+      }
+      /* the extreme maps to -tmax (the table's most negative value) */
+      sc[ib] = amax > 0.f ? -mx / (float)tmax : 0.f;
+      if (fabsf(sc[ib]) > amax_sc) amax_sc = fabsf(sc[ib]);
+    }
+    memset(&y[i], 0, sizeof(y[i]));
+    if (amax_sc == 0.f) {
+      for (int ib = 0; ib < 8; ++ib) { /* ls = 32: value 0 */
+        y[i].scales_l[ib / 2] |= (uint8_t)(0 << (4 * (ib & 1)));
+        y[i].scales_h |= (uint16_t)(2 << (2 * ib));
+      }
+      continue;
+    }
+    const float d = amax_sc / 32.f;
+    y[i].d = zmo_fp32_to_fp16(d);
+    const float dd = zmo_fp16_to_fp32(y[i].d);
+    for (int ib = 0; ib < 8; ++ib) {
+      int ls = dd > 0.f ? zmo_nearest_int(sc[ib] / dd) : 0;
+      ls = (ls < -32 ? -32 : (ls > 31 ? 31 : ls)) + 32;
+      y[i].scales_l[ib / 2] |= (uint8_t)((ls & 15) << (4 * (ib & 1)));
+      y[i].scales_h |= (uint16_t)((ls >> 4) << (2 * ib));
+      const float s = dd * (float)(ls - 32);
+      for (int j = 0; j < 16; ++j) {
+        const int lo = s != 0.f ? nearest_iq4(t, x[32 * ib + j] / s) : 8;
+        const int hi = s != 0.f ? nearest_iq4(t, x[32 * ib + 16 + j] / s) : 8;
+        y[i].qs[16 * ib + j] = (uint8_t)(lo | (hi << 4));
+      }
+    }
+  }
+}
+
 void zmo_quantize_rows(int type, const float *x, void *dst, int64_t rows, int64_t n) {
   const size_t rs = zmo_row_size(type, n);
 #pragma omp parallel for schedule(dynamic, 4)
@@ -761,6 +836,7 @@ void zmo_quantize_rows(int type, const float *x, void *dst, int64_t rows, int64_
     case ZMO_TYPE_Q5_K: zmo_quantize_row_q5_K(xr, (zmo_block_q5_K *)out, n); break;
     case ZMO_TYPE_Q6_K: zmo_quantize_row_q6_K(xr, (zmo_block_q6_K *)out, n); break;
     case ZMO_TYPE_IQ2_XXS: zmo_quantize_row_iq2_xxs(xr, (zmo_block_iq2_xxs *)out, n); break;
+    case ZMO_TYPE_IQ4_XS: zmo_quantize_row_iq4_xs(xr, (zmo_block_iq4_xs *)out, n); break;
     case ZMO_TYPE_Q8_K: zmo_quantize_row_q8_K(xr, (zmo_block_q8_K *)out, n); break;
     default: break;
     }
@@ -883,6 +959,26 @@ static void dequant_q6_K(const zmo_block_q6_K *x, float *y, int64_t k) {
   }
 }
 
+/* IQ4_XS 6-bit sub-block scale (value ls - 32). */
+static inline int iq4_ls(const zmo_block_iq4_xs *x, int ib) {
+  return (((x->scales_l[ib / 2] >> (4 * (ib & 1))) & 0xF) | (((x->scales_h >> (2 * ib)) & 3) << 4)) - 32;
+}
+
+/* dequantize_row_iq4_xs (kernels/quant/iq4xs_matmul.cu:80-99): sub-block ib,
+ * byte j of its 16 qs bytes: low nibble -> weight 32ib + j, high -> 32ib + 16 + j. */
+static void dequant_iq4_xs(const zmo_block_iq4_xs *x, float *y, int64_t k) {
+  const int8_t *t = zmo_iq4nl_table();
+  for (int64_t i = 0; i < k / ZMO_QK_K; ++i) {
+    const float d = zmo_fp16_to_fp32(x[i].d);
+    for (int ib = 0; ib < 8; ++ib) {
+      const float dl = d * (float)iq4_ls(&x[i], ib);
+      for (int j = 0; j < 16; ++j) y[32 * ib + j] = dl * (float)t[x[i].qs[16 * ib + j] & 0xF];
+      for (int j = 0; j < 16; ++j) y[32 * ib + 16 + j] = dl * (float)t[x[i].qs[16 * ib + j] >> 4];
+    }
+    y += ZMO_QK_K;
+  }
+}
+
 /* dequantize_row_iq2_xxs (iq2_matmul.cu:73-91). */
 static void dequant_iq2_xxs(const zmo_block_iq2_xxs *x, float *y, int64_t k) {
   const uint64_t *grid = zmo_iq2xxs_grid();
@@ -910,6 +1006,7 @@ void zmo_dequantize_row(int type, const void *src, float *y, int64_t n) {
   case ZMO_TYPE_Q5_K: dequant_q5_K((const zmo_block_q5_K *)src, y, n); break;
   case ZMO_TYPE_Q6_K: dequant_q6_K((const zmo_block_q6_K *)src, y, n); break;
   case ZMO_TYPE_IQ2_XXS: dequant_iq2_xxs((const zmo_block_iq2_xxs *)src, y, n); break;
+  case ZMO_TYPE_IQ4_XS: dequant_iq4_xs((const zmo_block_iq4_xs *)src, y, n); break;
   case ZMO_TYPE_Q8_K: {
     const zmo_block_q8_K *b = (const zmo_block_q8_K *)src;
     for (int64_t i = 0; i < n / ZMO_QK_K; ++i)
@@ -1049,6 +1146,27 @@ static float dot_q6_K(int n, const zmo_block_q6_K *x, const zmo_block_q8_K *y) {
   return hsum8(acc);
 }
 
+/* IQ4_XS: isum = sum_ib (ls - 32) * sum table[q] * q8 per block, one fma
+ * with d * d_y per block.  Float order: parity unpinned (ggml's stock
+ * IQ4_XS dot is not in the reference tree). */
+static float dot_iq4_xs(int n, const zmo_block_iq4_xs *x, const zmo_block_q8_K *y) {
+  const int8_t *t = zmo_iq4nl_table();
+  float acc = 0.f;
+  for (int i = 0; i < n / ZMO_QK_K; ++i) {
+    int32_t isum = 0;
+    for (int ib = 0; ib < 8; ++ib) {
+      int32_t s = 0;
+      for (int j = 0; j < 16; ++j) {
+        s += t[x[i].qs[16 * ib + j] & 0xF] * y[i].qs[32 * ib + j];
+        s += t[x[i].qs[16 * ib + j] >> 4] * y[i].qs[32 * ib + 16 + j];
+      }
+      isum += iq4_ls(&x[i], ib) * s;
+    }
+    acc = fmaf(zmo_fp16_to_fp32(x[i].d) * y[i].d, (float)isum, acc);
+  }
+  return acc;
+}
+
 /* ggml_vec_dot_iq2_xxs_q8_K, AVX2 / AVX-512BW order (patches/ggml/0009...:34-95,
  * bench/kernels/iq2xxs_dot_bench.cpp:26-50): lane l sums (2ls+1)*grid*sign*q8
  * over bytes [4l,4l+4) of each 32-weight sub-block; one fma per block with
@@ -1084,6 +1202,7 @@ float zmo_vec_dot_q8_K(int type, int n, const void *x, const zmo_block_q8_K *y) 
   case ZMO_TYPE_Q5_K: return dot_q5_K(n, (const zmo_block_q5_K *)x, y);
   case ZMO_TYPE_Q6_K: return dot_q6_K(n, (const zmo_block_q6_K *)x, y);
   case ZMO_TYPE_IQ2_XXS: return dot_iq2_xxs(n, (const zmo_block_iq2_xxs *)x, y);
+  case ZMO_TYPE_IQ4_XS: return dot_iq4_xs(n, (const zmo_block_iq4_xs *)x, y);
   default: return NAN;
   }
 }
@@ -1135,6 +1254,12 @@ void zmo_block_dots(int type, int n, const void *vx, const zmo_block_q8_K *y, in
     } else if (type == ZMO_TYPE_Q6_K) {
       const zmo_block_q6_K *x = (const zmo_block_q6_K *)vx + i;
       for (int t = 0; t < 256; ++t) s += x->scales[t / 16] * q6_value(x, t) * y[i].qs[t];
+    } else if (type == ZMO_TYPE_IQ4_XS) {
+      /* (ls - 32) * table value = dequant / d: reuse the dequant as integers */
+      zmo_block_iq4_xs one = ((const zmo_block_iq4_xs *)vx)[i];
+      one.d = 0x3c00;
+      dequant_iq4_xs(&one, w, 256);
+      for (int t = 0; t < 256; ++t) s += (int32_t)lrintf(w[t]) * y[i].qs[t];
     } else if (type == ZMO_TYPE_IQ2_XXS) {
       /* (2ls+1)*grid*sign = 8 * dequant / d: reuse the dequant as integers */
       zmo_block_iq2_xxs one = ((const zmo_block_iq2_xxs *)vx)[i];
@@ -1151,7 +1276,7 @@ void zmo_block_dots(int type, int n, const void *vx, const zmo_block_q8_K *y, in
 
 static int type_ok(int t) {
   return t == ZMO_TYPE_Q2_K || t == ZMO_TYPE_Q3_K || t == ZMO_TYPE_Q4_K || t == ZMO_TYPE_Q5_K || t == ZMO_TYPE_Q6_K ||
-         t == ZMO_TYPE_IQ2_XXS;
+         t == ZMO_TYPE_IQ2_XXS || t == ZMO_TYPE_IQ4_XS;
 }
 
 int zmo_mul_mat_id(const zmo_tensor *src0, const zmo_tensor *src1, const zmo_tensor *ids, zmo_tensor *dst,

@@ -12,7 +12,7 @@ import torch
 import zm_oracle as O
 
 Q2, Q3, Q4, IQ2 = O.TYPE_Q2_K, O.TYPE_Q3_K, O.TYPE_Q4_K, O.TYPE_IQ2_XXS
-Q5, Q6 = O.TYPE_Q5_K, O.TYPE_Q6_K
+Q5, Q6, IQ4 = O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_IQ4_XS
 
 
 def dev_random_blocks(t: int, rows: int, n: int, seed: int, device="cuda", scale=0.02) -> torch.Tensor:
@@ -41,6 +41,8 @@ def dev_random_blocks(t: int, rows: int, n: int, seed: int, device="cuda", scale
         put(2, 0.5 * scale / 60, 1.5 * scale / 60)
     elif t == Q6:
         put(208, 0.5 * scale / 2000, 1.5 * scale / 2000)
+    elif t == IQ4:
+        put(0, 0.5 * scale / 2000, 1.5 * scale / 2000)
     else:
         put(0, 0.5 * scale / 40, 1.5 * scale / 40)
     return raw.view(rows, nb * bb)

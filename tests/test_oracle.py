@@ -185,6 +185,30 @@ def test_q6_K_known_answer():
         assert y[t] == np.float32(np.float32(0.25 * scales[t // 16]) * (q[t] - 32)), t
 
 
+def test_iq4_xs_known_answer():
+    """Sub-block ib: 6-bit scale = nibble (ib & 1) of scales_l[ib // 2] plus
+    bits 2ib..2ib+1 of scales_h as bits 4-5, value ls - 32; qs byte 16ib + j:
+    low nibble -> weight 32ib + j, high -> 32ib + 16 + j, through the table
+    (kernels/quant/iq4xs_matmul.cu:80-99)."""
+    t = O.iq4nl_table().astype(np.int64)
+    b = _blank(O.TYPE_IQ4_XS)
+    _put_half(b, 0, 0.5)
+    ls = [32, 33, 31, 0, 63, 40, 20, 45]     # values 0, 1, -1, -32, 31, 8, -12, 13
+    sh = 0
+    for ib, v in enumerate(ls):
+        b[4 + ib // 2] |= (v & 15) << (4 * (ib & 1))
+        sh |= (v >> 4) << (2 * ib)
+    b[2], b[3] = sh & 0xFF, sh >> 8
+    b[8 + 16 * 3 + 5] = 0x9 | (0xE << 4)      # ib 3, j 5: w[101] = t[9], w[117] = t[14]
+    b[8 + 16 * 6 + 0] = 0xF                   # ib 6, j 0: w[192] = t[15], w[208] = t[0]
+    y = O.dequantize(O.TYPE_IQ4_XS, b, 256)[0]
+    idx = np.zeros(256, np.int64)
+    idx[101], idx[117], idx[192] = 9, 14, 15
+    for i in range(256):
+        assert y[i] == np.float32(np.float32(0.5 * (ls[i // 32] - 32)) * t[idx[i]]), i
+    assert list(t[[0, 8, 15]]) == [-127, 1, 113] and np.all(np.diff(t) > 0)
+
+
 def test_iq2_xxs_known_answer():
     """value = d*(0.5+ls)*0.25*grid[idx][j]*sign, signs = ksigns[7-bit index]
     with the 8th sign = parity (iq2_matmul.cu:73-91, patches/ggml/0009...:69-75)."""
@@ -232,7 +256,8 @@ def test_iq2_grid_stand_in_properties():
 
 # ------------------------------------------------------------------ integer block dots == brute force over dequant
 
-@pytest.mark.parametrize("t", [O.TYPE_Q2_K, O.TYPE_Q3_K, O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_IQ2_XXS])
+@pytest.mark.parametrize("t", [O.TYPE_Q2_K, O.TYPE_Q3_K, O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_IQ2_XXS,
+                               O.TYPE_IQ4_XS])
 def test_block_dots_equal_dequant_brute_force(t):
     """sum_j sc*dot - dmin*sum m*bsum per block equals dequant(w).dequant(q8)
     scaled by the block scales, exactly in float64 (integers < 2^53)."""
@@ -260,13 +285,16 @@ def test_block_dots_equal_dequant_brute_force(t):
         elif t == O.TYPE_Q6_K:
             assert imin[b] == 0
             exp = float(np.frombuffer(bb[208:210].tobytes(), np.float16)[0]) * isum[b]
+        elif t == O.TYPE_IQ4_XS:
+            exp = float(np.frombuffer(bb[0:2].tobytes(), np.float16)[0]) * isum[b]
         else:
             exp = float(np.frombuffer(bb[0:2].tobytes(), np.float16)[0]) * isum[b] / 8.0
         got = float(np.dot(wd[256 * b:256 * b + 256], qv[256 * b:256 * b + 256]))
         assert abs(got - exp) <= 1e-9 * max(1.0, abs(exp)), (b, got, exp)
 
 
-@pytest.mark.parametrize("t", [O.TYPE_Q2_K, O.TYPE_Q3_K, O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_IQ2_XXS])
+@pytest.mark.parametrize("t", [O.TYPE_Q2_K, O.TYPE_Q3_K, O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_IQ2_XXS,
+                               O.TYPE_IQ4_XS])
 def test_vec_dot_matches_dequant_dot(t):
     rng = np.random.default_rng(5)
     n = 2048
@@ -472,7 +500,8 @@ def test_moe_forward_composition():
 
 
 @pytest.mark.parametrize("t,tol", [(O.TYPE_Q2_K, 0.40), (O.TYPE_Q3_K, 0.20), (O.TYPE_Q4_K, 0.09),
-                                   (O.TYPE_Q5_K, 0.045), (O.TYPE_Q6_K, 0.025), (O.TYPE_IQ2_XXS, 0.40)])
+                                   (O.TYPE_Q5_K, 0.045), (O.TYPE_Q6_K, 0.025), (O.TYPE_IQ2_XXS, 0.40),
+                                   (O.TYPE_IQ4_XS, 0.12)])
 def test_quantizer_round_trip(t, tol):
     x = O.fill_normal(42, 8 * 1024, 0.0, 0.02).reshape(8, 1024)
     y = O.dequantize(t, O.quantize(t, x), 1024)

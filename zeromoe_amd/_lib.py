@@ -48,6 +48,8 @@ SIGNATURES = {
     "zm_version": (C.c_char_p, []),
     "zm_set_iq2xxs_grid": (I, [P]),
     "zm_iq2xxs_builtin_grid": (None, [P]),
+    "zm_set_iq4nl_table": (I, [P]),
+    "zm_iq4nl_builtin_table": (None, [P]),
     "zm_mul_mat_id_negative_skip": (I, []),
     "zm_mul_mat_id_negative_skip_batched": (I, []),
     "zm_mul_mat_id": (I, [C.POINTER(ZmTensor)] * 3 + [C.POINTER(ZmTensor), P, I]),
@@ -72,6 +74,8 @@ SIGNATURES = {
     "launch_q5_K_matmul_stream": (None, [P, P, P, I, I, I, P]),
     "launch_q6_K_matmul": (None, [P, P, P, I, I, I]),
     "launch_q6_K_matmul_stream": (None, [P, P, P, I, I, I, P]),
+    "launch_iq4_xs_matmul": (None, [P, P, P, I, I, I]),
+    "launch_iq4_xs_matmul_stream": (None, [P, P, P, I, I, I, P]),
     "launch_q5_K_matmul_grouped": (C.c_bool, [P, P, P, I, C.c_size_t, I, I]),
     "launch_ggml_moe_unpack": (I, [P, P, P, P, I] + [C.c_size_t] * 7 + [P]),
     "launch_ggml_moe_unpack_scatter": (I, [P, P, P, P, P, I] + [C.c_size_t] * 7 + [P]),

@@ -42,6 +42,7 @@ struct DeviceState {
   bool ready = false;
   uint64_t *grid = nullptr;   // IQ2_XXS grid, 256 x u64
   uint64_t *signs = nullptr;  // 128 x u64 byte masks of ksigns_iq2xs
+  uint64_t *iq4 = nullptr;    // IQ4_XS value table, 16 x i8
   void *ws = nullptr;         // zm_mul_mat_id workspace
   size_t ws_size = 0;
   uint64_t *trace = nullptr;  // decode-kernel phase timestamps (ZEROMOE_TRACE=1)
@@ -74,6 +75,13 @@ void builtin_grid(uint64_t grid[256]) {
     }
 }
 
+// ggml's kvalues_iq4nl (the table IQ4_NL / IQ4_XS index); replaceable with
+// zm_set_iq4nl_table
+void builtin_iq4nl(int8_t t[16]) {
+  static const int8_t v[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+  for (int i = 0; i < 16; ++i) t[i] = v[i];
+}
+
 int device_state(DeviceState **out) {
   int dev = 0;
   HIP_OK(hipGetDevice(&dev));
@@ -94,6 +102,10 @@ int device_state(DeviceState **out) {
     HIP_OK(hipMalloc(&d.signs, sizeof(signs)));
     HIP_OK(hipMemcpy(d.grid, grid, sizeof(grid), hipMemcpyHostToDevice));
     HIP_OK(hipMemcpy(d.signs, signs, sizeof(signs), hipMemcpyHostToDevice));
+    int8_t tab[16];
+    builtin_iq4nl(tab);
+    HIP_OK(hipMalloc(&d.iq4, 16));
+    HIP_OK(hipMemcpy(d.iq4, tab, 16, hipMemcpyHostToDevice));
     d.ready = true;
   }
   *out = &d;
@@ -106,6 +118,13 @@ int zm::device_grid(const uint64_t **grid) {
   DeviceState *d;
   if (device_state(&d)) return -1;
   *grid = d->grid;
+  return 0;
+}
+
+int zm::device_table(int type, const uint64_t **table) {
+  DeviceState *d;
+  if (device_state(&d)) return -1;
+  *table = type == T_IQ4_XS ? d->iq4 : d->grid;
   return 0;
 }
 
@@ -144,7 +163,7 @@ bool getenv_flag_off(const char *name) {
 }
 
 bool type_supported(int t) {
-  return t == T_Q2_K || t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_IQ2_XXS;
+  return t == T_Q2_K || t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_IQ2_XXS || t == T_IQ4_XS;
 }
 
 size_t row_bytes(int t, int64_t n) { return (size_t)(n / QK) * block_bytes(t); }
@@ -169,6 +188,7 @@ int pick_tile(int nrows, int U, int n_groups) {
 
 int launch_gemv(int type, bool gateup, int np, const GemvArgs &a0, int n_groups, hipStream_t st) {
   GemvArgs a = a0;
+  if (type == T_IQ4_XS && device_table(T_IQ4_XS, &a.grid)) return -1;
   const int U = a.nb * 4;
   a.tile_rows = pick_tile(a.nrows, U, n_groups);
   dim3 grid((a.nrows + a.tile_rows - 1) / a.tile_rows, n_groups);
@@ -179,6 +199,7 @@ int launch_gemv(int type, bool gateup, int np, const GemvArgs &a0, int n_groups,
   case T_Q4_K: rc = gateup ? launch_gemv_type<T_Q4_K, true>(np, U, grid, a, st) : launch_gemv_type<T_Q4_K, false>(np, U, grid, a, st); break;
   case T_Q5_K: rc = gateup ? launch_gemv_type<T_Q5_K, true>(np, U, grid, a, st) : launch_gemv_type<T_Q5_K, false>(np, U, grid, a, st); break;
   case T_Q6_K: rc = gateup ? launch_gemv_type<T_Q6_K, true>(np, U, grid, a, st) : launch_gemv_type<T_Q6_K, false>(np, U, grid, a, st); break;
+  case T_IQ4_XS: rc = gateup ? launch_gemv_type<T_IQ4_XS, true>(np, U, grid, a, st) : launch_gemv_type<T_IQ4_XS, false>(np, U, grid, a, st); break;
   case T_IQ2_XXS: rc = gateup ? launch_gemv_type<T_IQ2_XXS, true>(np, U, grid, a, st) : launch_gemv_type<T_IQ2_XXS, false>(np, U, grid, a, st); break;
   default: return fail("unsupported weight type %d", type);
   }
@@ -275,6 +296,15 @@ int zm_set_iq2xxs_grid(const uint64_t grid[256]) {
   DeviceState *d;
   if (device_state(&d)) return -1;
   HIP_OK(hipMemcpy(d->grid, grid, 256 * sizeof(uint64_t), hipMemcpyHostToDevice));
+  return 0;
+}
+
+void zm_iq4nl_builtin_table(int8_t table[16]) { builtin_iq4nl(table); }
+
+int zm_set_iq4nl_table(const int8_t table[16]) {
+  DeviceState *d;
+  if (device_state(&d)) return -1;
+  HIP_OK(hipMemcpy(d->iq4, table, 16, hipMemcpyHostToDevice));
   return 0;
 }
 
@@ -509,6 +539,7 @@ int zm_block_dots(int type, const void *w_row, const float *x, int n, int32_t *i
   case T_Q4_K: hipLaunchKernelGGL(k_block_dots<T_Q4_K>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->grid, d->signs); break;
   case T_Q5_K: hipLaunchKernelGGL(k_block_dots<T_Q5_K>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->grid, d->signs); break;
   case T_Q6_K: hipLaunchKernelGGL(k_block_dots<T_Q6_K>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->grid, d->signs); break;
+  case T_IQ4_XS: hipLaunchKernelGGL(k_block_dots<T_IQ4_XS>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->iq4, d->signs); break;
   default: hipLaunchKernelGGL(k_block_dots<T_IQ2_XXS>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->grid, d->signs); break;
   }
   HIP_OK(hipGetLastError());

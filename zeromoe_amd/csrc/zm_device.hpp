@@ -18,6 +18,8 @@
 //       and [64h+32+16qq, +16) (g = 1, 3), top two bits at bit 2g of qh bytes
 //       [32h+16qq, +16); 16-weight sub-blocks 8h + 2g + qq.
 //   IQ2_XXS quarter q: 32-weight sub-blocks 2q and 2q+1 (16 bytes of qs).
+//   IQ4_XS quarter q: 32-weight sub-blocks 2q and 2q+1 = qs bytes [32q, +32)
+//       (byte j of a sub-block: low nibble weight j, high nibble weight 16 + j).
 // Block layouts: /root/reference/kernels/quant/kquant_matmul.cu:35-39,
 // kernels/quant/iq2_matmul.cu:27.
 #pragma once
@@ -42,12 +44,13 @@ enum : int {
   T_Q6_K = 14,
   T_Q8_K = 15,
   T_IQ2_XXS = 16,
+  T_IQ4_XS = 23,
   T_I32 = 26,
 };
 
 __host__ __device__ constexpr int block_bytes(int t) {
   return t == T_Q2_K ? 84 : t == T_Q3_K ? 110 : t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210
-       : t == T_IQ2_XXS ? 66 : t == T_Q8_K ? 292 : 0;
+       : t == T_IQ2_XXS ? 66 : t == T_IQ4_XS ? 136 : t == T_Q8_K ? 292 : 0;
 }
 
 // ---------------------------------------------------------------- loads
@@ -346,6 +349,10 @@ __device__ __forceinline__ void load_w_slice(const uint8_t *blk, int q, WSlice &
     w.hh = ld16(blk + 32);
     w.a = ld16(blk + 48 + 32 * q);
     w.b = ld16(blk + 64 + 32 * q);
+  } else if constexpr (T == T_IQ4_XS) {
+    w.e = ld8(blk);  // d | scales_h, scales_l
+    w.a = ld16(blk + 8 + 32 * q);
+    w.b = ld16(blk + 24 + 32 * q);
   } else if constexpr (T == T_Q6_K) {
     const int h = q >> 1, qq = q & 1;
     w.a = ld16(blk + 64 * h + 16 * qq);
@@ -404,6 +411,10 @@ __device__ __forceinline__ void load_w_slice_b(rsrc_t r, int vo, int so, int q, 
     w.hh = bld16(r, vo + 32, so);
     w.a = bld16(r, vo + 48 + 32 * q, so);
     w.b = bld16(r, vo + 64 + 32 * q, so);
+  } else if constexpr (T == T_IQ4_XS) {
+    w.e = bld8(r, vo, so);
+    w.a = bld16(r, vo + 8 + 32 * q, so);
+    w.b = bld16(r, vo + 24 + 32 * q, so);
   } else if constexpr (T == T_Q6_K) {
     const int h = q >> 1, qq = q & 1;
     w.a = bld16(r, vo + 64 * h + 16 * qq, so);
@@ -421,6 +432,21 @@ __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirs
 
 __device__ __forceinline__ uint32_t u4_get(const uint4 &v, int i) {
   return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+
+// four 4-bit indices (one per byte) -> the four signed table bytes of a
+// 16-entry table held as four dwords (two byte permutes and a select on bit 3)
+__device__ __forceinline__ uint32_t lut16(uint32_t idx, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+  const uint32_t sel = idx & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel), hi = __builtin_amdgcn_perm(t3, t2, sel);
+  const uint32_t m = ((idx >> 3) & 0x01010101u) * 0xffu;
+  return (hi & m) | (lo & ~m);
+}
+
+// 6-bit IQ4_XS scale of sub-block ib (value ls - 32) from the header dwords
+// x = d | scales_h << 16, y = scales_l
+__device__ __forceinline__ int iq4_scale(uint32_t x, uint32_t y, int ib) {
+  return (int)(((y >> (4 * ib)) & 15u) | (((x >> (16 + 2 * ib)) & 3u) << 4)) - 32;
 }
 
 // Integer parts of one quarter: isum = sum_sub sc*dot (Q3_K: includes the
@@ -515,6 +541,20 @@ __device__ __forceinline__ QInt quarter_int(const WSlice &w, int q, const Q8Slic
       dh = dot4(((u4_get(w.b, i) >> 4) & 0x0f0f0f0fu) | h5(w.hh, i, bh), u4_get(a.q[3], i), dh);
     r.isum = (int)sc0 * dl + (int)sc1 * dh;
     r.imin = (int)m0 * (a.bs[0] + a.bs[1]) + (int)m1 * (a.bs[2] + a.bs[3]);
+  } else if constexpr (T == T_IQ4_XS) {
+    // lds_grid holds the 16-byte value table; sub-block 2q: bytes of a (low
+    // nibbles -> activations [0,16), high -> [16,32)), 2q + 1: bytes of b
+    const uint32_t t0 = (uint32_t)lds_grid[0], t1 = (uint32_t)(lds_grid[0] >> 32);
+    const uint32_t t2 = (uint32_t)lds_grid[1], t3 = (uint32_t)(lds_grid[1] >> 32);
+    int d0 = 0, d1 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      d0 = dot4(lut16(u4_get(w.a, i) & 0x0f0f0f0fu, t0, t1, t2, t3), u4_get(a.q[0], i), d0);
+      d0 = dot4(lut16((u4_get(w.a, i) >> 4) & 0x0f0f0f0fu, t0, t1, t2, t3), u4_get(a.q[1], i), d0);
+      d1 = dot4(lut16(u4_get(w.b, i) & 0x0f0f0f0fu, t0, t1, t2, t3), u4_get(a.q[2], i), d1);
+      d1 = dot4(lut16((u4_get(w.b, i) >> 4) & 0x0f0f0f0fu, t0, t1, t2, t3), u4_get(a.q[3], i), d1);
+    }
+    r.isum = iq4_scale(w.e.x, w.e.y, 2 * q) * d0 + iq4_scale(w.e.x, w.e.y, 2 * q + 1) * d1;
   } else if constexpr (T == T_Q6_K) {
     // group g: low nibbles of a (g = 0) / b (g = 1), high nibbles for g = 2, 3;
     // top bits at bit 2g of the qh bytes; value q - 32 folded in as -32 * bsum;
@@ -574,6 +614,8 @@ __device__ __forceinline__ float quarter_dot(const WSlice &w, int q, const Q8Sli
     return (a.d * d) * (float)r.isum - (a.d * dmin) * (float)r.imin;
   } else if constexpr (T == T_Q6_K) {
     return (a.d * h2f((uint16_t)(w.f & 0xffffu))) * (float)r.isum;
+  } else if constexpr (T == T_IQ4_XS) {
+    return (a.d * h2f((uint16_t)(w.e.x & 0xffffu))) * (float)r.isum;
   } else {
     const float d = h2f((uint16_t)(w.f & 0xffffu));
     return 0.125f * ((a.d * d) * (float)r.isum);

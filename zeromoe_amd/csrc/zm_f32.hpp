@@ -22,6 +22,7 @@ namespace zm {
 // /root/reference/kernels/quant/kquant_matmul.cu:55-92,161-200 and
 // kernels/quant/iq2_matmul.cu:73-91): w = d*sc*q - dmin*m for Q2_K/Q4_K,
 // d*(sc-32)*(q - 4*!h) for Q3_K, d*sc*(q | h<<4) - dmin*m for Q5_K,
+// (d*(ls-32))*table[q] for IQ4_XS (kernels/quant/iq4xs_matmul.cu:80-99),
 // (d*sc)*(q6 - 32) for Q6_K (kquant_matmul.cu:94-147), d*(0.5+s)*0.25*grid*sign
 // for IQ2_XXS.
 __device__ __forceinline__ uint32_t byte_at(const uint8_t *p) { return *p; }
@@ -83,6 +84,18 @@ __device__ __forceinline__ float4 deq4(const uint8_t *blk, int lane, const uint6
     const float dl = h2f(ld2(blk + 208)) * (float)sc;
 #pragma unroll
     for (int i = 0; i < 4; ++i) w[i] = dl * (float)((int)((v >> (8 * i)) & 63) - 32);
+  } else if constexpr (T == T_IQ4_XS) {
+    // weights 4*lane.. = sub-block ib, positions j0..j0+3: low nibbles of qs
+    // bytes 16ib + j0.. for j0 < 16, high nibbles of 16ib + j0 - 16.. otherwise
+    const int ib = lane >> 3, j0 = (4 * lane) & 31;
+    const uint32_t q = ld4(blk + 8 + 16 * ib + (j0 & 15));
+    const uint32_t idx = j0 < 16 ? (q & 0x0f0f0f0fu) : ((q >> 4) & 0x0f0f0f0fu);
+    const uint32_t hdr = ld4(blk), sl = ld4(blk + 4);
+    const float dl = h2f((uint16_t)(hdr & 0xffffu)) * (float)iq4_scale(hdr, sl, ib);
+    const uint32_t v = lut16(idx, (uint32_t)s_grid[0], (uint32_t)(s_grid[0] >> 32), (uint32_t)s_grid[1],
+                             (uint32_t)(s_grid[1] >> 32));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = dl * (float)(int)(int8_t)(v >> (8 * i));
   } else {  // IQ2_XXS
     const int ib = lane >> 3, l = (lane >> 1) & 3, hb = lane & 1;
     const uint32_t a0 = ld4(blk + 2 + 8 * ib), a1 = ld4(blk + 6 + 8 * ib);
@@ -132,7 +145,7 @@ constexpr int F32_RPW = 4;
 template <int T, int NT>
 __global__ __launch_bounds__(256) void k_f32_mm(F32MMArgs a) {
   __shared__ float4 s_x[NT][F32_CH * 64];
-  __shared__ uint64_t s_grid[T == T_IQ2_XXS ? 256 : 1];
+  __shared__ uint64_t s_grid[T == T_IQ2_XXS ? 256 : (T == T_IQ4_XS ? 2 : 1)];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int route = blockIdx.z, t0 = blockIdx.y * NT;
   const int row0 = (blockIdx.x * 4 + wave) * F32_RPW;
@@ -149,6 +162,8 @@ __global__ __launch_bounds__(256) void k_f32_mm(F32MMArgs a) {
   }
   if constexpr (T == T_IQ2_XXS) {
     s_grid[threadIdx.x] = a.grid[threadIdx.x];
+  } else if constexpr (T == T_IQ4_XS) {
+    if (threadIdx.x < 2) s_grid[threadIdx.x] = a.grid[threadIdx.x];
   }
   constexpr int BB = block_bytes(T);
   const int nb = a.I / QK;

@@ -12,6 +12,9 @@ namespace zm {
 int fail(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
 // the current device's IQ2_XXS grid (256 x u64, device memory), set up on first use
 int device_grid(const uint64_t **grid);
+// the current device's lookup table of a weight type: the IQ4_XS value table
+// (16 x i8) for T_IQ4_XS, the IQ2_XXS grid otherwise
+int device_table(int type, const uint64_t **table);
 // one more executed MUL_MAT_ID hook launch (zm_mul_mat_id_launches)
 void count_mmid_launch();
 

@@ -9,8 +9,8 @@ import torch
 
 from ._lib import ZmExpertScratch, ZmMoeLayer, ZmRouterSpec, ZmTensor, check, lib
 
-GGML_TYPES = {"f32": 0, "q2_K": 10, "q3_K": 11, "q4_K": 12, "q5_K": 13, "q6_K": 14, "q8_K": 15, "iq2_xxs": 16, "i32": 26}
-BLOCK_BYTES = {10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 15: 292, 16: 66}
+GGML_TYPES = {"f32": 0, "q2_K": 10, "q3_K": 11, "q4_K": 12, "q5_K": 13, "q6_K": 14, "q8_K": 15, "iq2_xxs": 16, "iq4_xs": 23, "i32": 26}
+BLOCK_BYTES = {10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 15: 292, 16: 66, 23: 136}
 QK_K = 256
 GATING = {"softmax": 0, "sigmoid": 1, "sqrt_softplus": 2}
 
@@ -43,6 +43,24 @@ def set_iq2xxs_grid(grid) -> None:
     g = np.ascontiguousarray(grid, dtype=np.uint64)
     assert g.shape == (256,)
     check(lib().zm_set_iq2xxs_grid(g.ctypes.data), "zm_set_iq2xxs_grid")
+
+
+def set_iq4nl_table(table) -> None:
+    """Load the IQ4_XS value table (16 int8) for the current device."""
+    import numpy as np
+
+    t = np.ascontiguousarray(np.asarray(table, np.int8))
+    if t.shape != (16,):
+        raise ValueError("the IQ4_XS table has 16 entries")
+    check(lib().zm_set_iq4nl_table(t.ctypes.data), "zm_set_iq4nl_table")
+
+
+def builtin_iq4nl_table():
+    import numpy as np
+
+    t = np.zeros(16, np.int8)
+    lib().zm_iq4nl_builtin_table(t.ctypes.data)
+    return t
 
 
 def builtin_iq2xxs_grid():
