@@ -132,8 +132,7 @@ int zm_bucket(const int32_t *ids, int S, int K, int E, int32_t *counts, int32_t 
  * against f32 activations quantized to Q8_K: isum[b], imin[b] as defined in
  * oracle/zm_oracle.h (zmo_block_dots).  Both device dot paths (the bucketed
  * GEMV's and the fused decode kernel's) compute every block; where they
- * disagree isum[b] is INT32_MIN (IQ4_XS has only the GEMV's path).
- * Not on the hot path. */
+ * disagree isum[b] is INT32_MIN.  Not on the hot path. */
 int zm_block_dots(int type, const void *w_row, const float *x, int n, int32_t *isum, int32_t *imin, void *stream);
 
 /* ---------------------------------------------------------------- routed layer */

@@ -286,6 +286,8 @@ FUSED_CASES = {
     "q4k_q6k": (CONFIGS["c2"], dict(tg=Q4, td=Q6)),
     "q4k_q6k_S4": (CONFIGS["c2"], dict(tg=Q4, td=Q6, S=4)),
     "q5k_q6k": (CONFIGS["c2"], dict(tg=Q5, td=Q6)),
+    "iq4xs": (CONFIGS["c2"], dict(tg=IQ4, td=IQ4)),
+    "iq4xs_S3": (CONFIGS["c2"], dict(tg=IQ4, td=IQ4, S=3)),
 }
 
 

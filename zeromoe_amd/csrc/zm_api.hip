@@ -621,7 +621,7 @@ int check_layer(const zm_moe_layer *L) {
   if (L->router_w && L->H % 4) return fail("router GEMV needs H %% 4 == 0");
   return 0;
 }
-int units_per_block(int t) { return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K ? 2 : 1; }
+int units_per_block(int t) { return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_IQ4_XS ? 2 : 1; }
 
 DecFn find_decode(int tg, int td, int ts, int l1, int ir, int is) {
   if (DecFn f = find_decode_a(tg, td, ts, l1, ir, is)) return f;
@@ -724,7 +724,8 @@ int launch_fused(const zm_moe_layer *L, const float *x, const float *logits, int
   }
   a.act = w.f_act;
   a.sync = w.f_sync;
-  a.grid = d->grid;
+  const bool iq4 = L->type_gate == T_IQ4_XS || L->type_down == T_IQ4_XS || (Fs && L->type_shared == T_IQ4_XS);
+  a.grid = iq4 ? d->iq4 : d->grid;
   a.signs = d->signs;
   a.spin_limit = 1 << 23;
   if (const char *tr = getenv("ZEROMOE_TRACE"); tr && tr[0] == '1') {

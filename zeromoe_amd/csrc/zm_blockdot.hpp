@@ -23,13 +23,14 @@ namespace zm {
 
 template <int T>
 __host__ __device__ constexpr int unit_per_block() {
-  return T == T_Q4_K || T == T_Q5_K || T == T_Q6_K ? 2 : 1;
+  return T == T_Q4_K || T == T_Q5_K || T == T_Q6_K || T == T_IQ4_XS ? 2 : 1;
 }
 
 // types with a whole-block unit (the fused decode kernel's dot)
 template <int T>
 __host__ __device__ constexpr bool has_unit() {
-  return T == T_Q2_K || T == T_Q3_K || T == T_Q4_K || T == T_Q5_K || T == T_Q6_K || T == T_IQ2_XXS;
+  return T == T_Q2_K || T == T_Q3_K || T == T_Q4_K || T == T_Q5_K || T == T_Q6_K || T == T_IQ2_XXS ||
+         T == T_IQ4_XS;
 }
 
 template <int T>
@@ -64,6 +65,11 @@ struct Unit<T_Q6_K> {  // half h: ql[64h, +64) | qh[32h, +32) | scales[8h, +8) |
   uint32_t qh[8];
   uint32_t sc[2];
   uint32_t d;
+};
+template <>
+struct Unit<T_IQ4_XS> {  // d, scales_h, scales_l | half of qs[128] (4 sub-blocks)
+  uint2 hdr;
+  uint4 q[4];
 };
 template <>
 struct Unit<T_IQ2_XXS> {  // d | qs u16[32]
@@ -144,6 +150,10 @@ __device__ __forceinline__ void load_unit(rsrc_t r, int vo, int part, Unit<T> &u
     u.qh[1] = bld16(r, vo + 32, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) u.q[i] = bld16(r, vo + 48 + 64 * part + 16 * i, 0);
+  } else if constexpr (T == T_IQ4_XS) {  // 136-byte blocks stay 8-byte aligned
+    u.hdr = bld8(r, vo, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u.q[i] = bld16(r, vo + 8 + 64 * part + 16 * i, 0);
   } else if constexpr (T == T_Q6_K) {  // 210-byte blocks: every other one starts 2 bytes off a dword
     load_dwords_shifted<16>(r, vo + 64 * part, u.ql);
     load_dwords_shifted<8>(r, vo + 128 + 32 * part, u.qh);
@@ -389,6 +399,34 @@ __device__ __forceinline__ void unit_ints(const Unit<T> (&w)[NW], int part, cons
       ri[n] = isum;
       rm[n] = imin;
     }
+  } else if constexpr (T == T_IQ4_XS) {
+    // part p: sub-blocks 4p..4p+3, sub-block ib's 16 qs bytes in q[ib - 4p]: low
+    // nibbles pair with activation chunk 2ib, high nibbles with 2ib + 1; the
+    // 16-byte value table is in lds_grid
+    const uint32_t t0 = (uint32_t)lds_grid[0], t1 = (uint32_t)(lds_grid[0] >> 32);
+    const uint32_t t2 = (uint32_t)lds_grid[1], t3 = (uint32_t)(lds_grid[1] >> 32);
+#pragma unroll
+    for (int n = 0; n < NW; ++n) {
+      int isum = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ib = 4 * part + i;
+        const uint4 qv = w[n].q[i];
+        const uint4 xl = x.q[2 * ib], xh = x.q[2 * ib + 1];
+        int s = 0;
+        s = dot4(lut16(qv.x & 0x0f0f0f0fu, t0, t1, t2, t3), xl.x, s);
+        s = dot4(lut16(qv.y & 0x0f0f0f0fu, t0, t1, t2, t3), xl.y, s);
+        s = dot4(lut16(qv.z & 0x0f0f0f0fu, t0, t1, t2, t3), xl.z, s);
+        s = dot4(lut16(qv.w & 0x0f0f0f0fu, t0, t1, t2, t3), xl.w, s);
+        s = dot4(lut16((qv.x >> 4) & 0x0f0f0f0fu, t0, t1, t2, t3), xh.x, s);
+        s = dot4(lut16((qv.y >> 4) & 0x0f0f0f0fu, t0, t1, t2, t3), xh.y, s);
+        s = dot4(lut16((qv.z >> 4) & 0x0f0f0f0fu, t0, t1, t2, t3), xh.z, s);
+        s = dot4(lut16((qv.w >> 4) & 0x0f0f0f0fu, t0, t1, t2, t3), xh.w, s);
+        isum = mad24(iq4_scale(w[n].hdr.x, w[n].hdr.y, ib), s, isum);
+      }
+      ri[n] = isum;
+      rm[n] = 0;
+    }
   } else if constexpr (T == T_Q6_K) {
     // half h = part: weight 128h + 32g + l sits in activation chunk 8h + 2g + (l >> 4),
     // which is also its 16-weight sub-block; value (nibble | 2 bits << 4) - 32,
@@ -467,6 +505,8 @@ __device__ __forceinline__ float unit_float(const Unit<T> &w, float xd, int isum
     return (xd * d) * (float)isum - (xd * dmin) * (float)imin;
   } else if constexpr (T == T_Q6_K) {
     return (xd * h2f((uint16_t)(w.d & 0xffffu))) * (float)isum;
+  } else if constexpr (T == T_IQ4_XS) {
+    return (xd * h2f((uint16_t)(w.hdr.x & 0xffffu))) * (float)isum;
   } else {
     return 0.125f * ((xd * h2f((uint16_t)(w.d & 0xffffu))) * (float)isum);
   }

@@ -136,7 +136,9 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t s_q8[DEC_LDS_Q8];
   __shared__ float4 s_stage[DEC_WAVES][256];  // per wave: router scratch, then the act transpose
   constexpr bool kIQ2 = TG == T_IQ2_XXS || TD == T_IQ2_XXS || TS == T_IQ2_XXS;
-  __shared__ uint64_t s_grid[kIQ2 ? 256 : 1];
+  constexpr bool kIQ4 = TG == T_IQ4_XS || TD == T_IQ4_XS || TS == T_IQ4_XS;
+  static_assert(!(kIQ2 && kIQ4), "one lookup table per layer");
+  __shared__ uint64_t s_grid[kIQ2 ? 256 : (kIQ4 ? 2 : 1)];
   __shared__ uint64_t s_signs[kIQ2 ? 128 : 1];
   static_assert(IS == 0 || TS != 0, "shared iterations need a shared type");
   static_assert(L1 == 16 || L1 == 32, "lanes per routed gate/up row");
@@ -182,6 +184,8 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   if constexpr (kIQ2) {
     for (int i = tid; i < 256; i += DEC_THREADS) s_grid[i] = a.grid[i];
     for (int i = tid; i < 128; i += DEC_THREADS) s_signs[i] = a.signs[i];
+  } else if constexpr (kIQ4) {  // a.grid: the IQ4_XS value table
+    if (tid < 2) s_grid[tid] = a.grid[tid];
   }
   ZM_TRACE(6);
   for (int grp = wi; grp * 4 < nxb; grp += DEC_WAVES) {
