@@ -44,6 +44,7 @@ CONFIGS["c5_s64"] = dict(CONFIGS["c5"], S=64)
 CONFIGS["q4k_q6k"] = dict(CONFIGS["c2"], tg=Q4, td=Q6)
 CONFIGS["c3_q6k"] = dict(CONFIGS["c3"], td=Q6)
 CONFIGS["iq4xs"] = dict(CONFIGS["c2"], tg=IQ4X, td=IQ4X)
+CONFIGS["c3_iq4xs"] = dict(CONFIGS["c3"], tg=IQ4X, td=IQ4X)
 WORKLOAD = {
     "c1": "decode S=1, H=2048 F=768 E=128 top-8 softmax, Q4_K",
     "c2": "decode S=1, H=4096 F=1536 E=128 top-8 softmax, gate/up Q2_K, down Q3_K",
@@ -51,6 +52,7 @@ WORKLOAD = {
     "c4": "small batch S=4, H=5120 F=1536 E=160 top-8 softmax, IQ2_XXS",
     "c5": "full block S=1, H=7168 F=2048, 256 routed Q2_K (96 resident slots) + shared Q4_K, sigmoid 8 groups/top-4",
     "iq4xs": "decode S=1 at c2's shape with IQ4_XS gate/up/down",
+    "c3_iq4xs": "prefill S=512 at c3's shape and routing with IQ4_XS gate/up/down",
     "c3_q6k": "prefill S=512 at c3's shape and routing with a Q6_K down projection (mixed-type layer)",
     "q4k_q6k": "decode S=1 at c2's shape with Q4_K gate/up and a Q6_K down projection (mixed-type layer)",
     "c5_s64": "full block S=64, H=7168 F=2048, 256 routed Q2_K (96 resident slots) + shared Q4_K, sigmoid 8 groups/top-4",
@@ -376,7 +378,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--replicas", type=int, default=0, help="layer replicas (0 = enough to exceed the MALL)")
-    ap.add_argument("--extras", default="c1,c3,c4,c5,c5_s64,q4k_q6k,c3_q6k,iq4xs", help="extra configs to report ('' for none)")
+    ap.add_argument("--extras", default="c1,c3,c4,c5,c5_s64,q4k_q6k,c3_q6k,iq4xs,c3_iq4xs", help="extra configs to report ('' for none)")
     ap.add_argument("--no-unpack", dest="unpack", action="store_false",
                     help="skip the expert-record unpack extra")
     ap.add_argument("--no-cpu", action="store_true")
@@ -431,7 +433,7 @@ def main():
     traffic = committed_traffic()
     extras = {}
     for name in [n for n in args.extras.split(",") if n]:
-        st = max(10, args.steps // 4) if name in ("c3", "c5_s64", "c3_q6k") else args.steps
+        st = max(10, args.steps // 4) if name in ("c3", "c5_s64", "c3_q6k", "c3_iq4xs") else args.steps
         r = run_config(torch, Z, name, st, max(3, args.warmup // 2), reps(name), use_graph=not args.eager)
         extras[name] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}
         extras[name]["workload"] = WORKLOAD[name]

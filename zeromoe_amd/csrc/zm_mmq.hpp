@@ -22,6 +22,11 @@
 // block for all MMQ_TT token tiles of the work item.
 // No dequantized weight copy is materialized.
 //
+// IQ4_XS (a 16-entry value table, up to |127|, and a 6-bit signed scale per
+// 32-weight sub-block) dots each 64-weight chunk as its two sub-blocks on
+// v_mfma_i32_16x16x64_i8 with half of B zeroed, values looked up from the
+// table in registers; the scales apply per lane as for Q6_K, no min term.
+//
 // Q5_K adds the fifth bit of each value as a third chain: the bit (0/1) times
 // the whole 6-bit scale (<= 63) is int8 too, and isum = D_lo + 8 D_hi + 16 D_5.
 //
@@ -123,6 +128,11 @@ struct MmqW<T_Q2_K> {  // scales | this lane's 2 x 16 bytes of qs | d, dmin
   uint32_t dd;
 };
 template <>
+struct MmqW<T_IQ4_XS> {  // d, scales_h, scales_l | this lane's 16 qs bytes of each chunk
+  uint2 hdr;
+  uint4 qs[4];
+};
+template <>
 struct MmqW<T_Q6_K> {  // this lane's 4 x 8 bytes of ql, 2 x 8 bytes of qh | scales | d
   uint2 ql[4];
   uint2 qh[2];
@@ -133,7 +143,7 @@ struct MmqW<T_Q6_K> {  // this lane's 4 x 8 bytes of ql, 2 x 8 bytes of qh | sca
 template <int T, bool GATEUP, int TT>
 __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
   constexpr int TOK = 16 * TT;  // pairs per work item
-  static_assert(T == T_Q4_K || T == T_Q5_K || T == T_Q2_K || T == T_Q6_K, "MFMA prefill types");
+  static_assert(T == T_Q4_K || T == T_Q5_K || T == T_Q2_K || T == T_Q6_K || T == T_IQ4_XS, "MFMA prefill types");
   constexpr bool K45 = T == T_Q4_K || T == T_Q5_K;
   constexpr int NBS = K45 ? 8 : 16;  // bsums per block used: 32-sums (Q4_K, Q5_K) or 16-sums (Q2_K, Q6_K)
   __shared__ __attribute__((aligned(16))) uint8_t s_xq[2][TOK][MMQ_XS];
@@ -169,6 +179,14 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
   const int Kp = a.dense_S > 0 ? 1 : a.K;
   const int nb = a.nb;
   const int nt = min(TT, (p1 - pc + 15) / 16);
+  uint32_t tab[4] = {0, 0, 0, 0};  // IQ4_XS value table (a.grid), wave-uniform
+  if constexpr (T == T_IQ4_XS) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      tab[2 * i] = (uint32_t)a.grid[i];
+      tab[2 * i + 1] = (uint32_t)(a.grid[i] >> 32);
+    }
+  }
 
   if (tid < TOK) {
     const int p = pc + tid;
@@ -193,6 +211,10 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
         w[m].qh = bld16(rw[m], vo + 16 + 16 * (g & 1), 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) w[m].qs[i] = bld16(rw[m], vo + 48 + 32 * i + 16 * (g & 1), 0);
+      } else if constexpr (T == T_IQ4_XS) {
+        w[m].hdr = bld8(rw[m], vo, 0);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) w[m].qs[c] = bld16(rw[m], vo + 8 + 32 * c + 16 * (g >> 1), 0);
       } else if constexpr (T == T_Q6_K) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) w[m].ql[i] = bld8(rw[m], vo + 64 * (i >> 1) + 32 * (i & 1) + 8 * g, 0);
@@ -330,6 +352,49 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           f[m][t][j] += s_xd[buf][16 * t + 4 * g + j] * (d * (float)(dlo[j] + 8 * dhi[j] + 16 * d5[j]) - dmin * mn[j]);
+      }
+    }
+    } else if constexpr (T == T_IQ4_XS) {
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      const float d = h2f((uint16_t)(wcur[m].hdr.x & 0xffffu));
+      // chunk c = sub-blocks 2c (lane groups 0-1) and 2c + 1 (groups 2-3); group
+      // g takes the low (g even) or high nibbles of its sub-block's 16 qs bytes,
+      // through the value table; each chunk is issued twice, the other
+      // sub-block's half of B zeroed
+      const uint32_t keep0 = g < 2 ? 0xffffffffu : 0u;
+      const int ns = 4 * (g & 1);
+      v4i_t b0[4], b1[4];
+      int s0[4], s1[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint4 q = wcur[m].qs[c];
+        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t v = lut16((qw[k] >> ns) & 0x0f0f0f0fu, tab[0], tab[1], tab[2], tab[3]);
+          b0[c][k] = (int)(v & keep0);
+          b1[c][k] = (int)(v & ~keep0);
+        }
+        s0[c] = iq4_scale(wcur[m].hdr.x, wcur[m].hdr.y, 2 * c);
+        s1[c] = iq4_scale(wcur[m].hdr.x, wcur[m].hdr.y, 2 * c + 1);
+      }
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        if (t >= nt) continue;
+        const uint8_t *xr = &s_xq[buf][16 * t + n][0];
+        int isum[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const v4i_t xa = *reinterpret_cast<const v4i_t *>(xr + 64 * c + 16 * g);
+          const v4i_t z = {0, 0, 0, 0};
+          const v4i_t d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, b0[c], z, 0, 0, 0);
+          const v4i_t d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, b1[c], z, 0, 0, 0);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) isum[j] = __mul24(s0[c], d0[j]) + __mul24(s1[c], d1[j]) + isum[j];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) f[m][t][j] += s_xd[buf][16 * t + 4 * g + j] * (d * (float)isum[j]);
       }
     }
     } else if constexpr (T == T_Q6_K) {
