@@ -28,8 +28,8 @@ sys.path.insert(0, ROOT)
 
 METRIC = "routed-expert layer µs + HBM GB/s (% of peak) at batch 1; prefill tok/s"
 HBM_PEAK_GBS = 8000.0
-Q2, Q3, Q4, Q5, Q6, IQ2, IQ4X = 10, 11, 12, 13, 14, 16, 23
-BB = {Q2: 84, Q3: 110, Q4: 144, Q5: 176, Q6: 210, IQ2: 66, IQ4X: 136}
+Q2, Q3, Q4, Q5, Q6, IQ2, IQ3X, IQ4X = 10, 11, 12, 13, 14, 16, 18, 23
+BB = {Q2: 84, Q3: 110, Q4: 144, Q5: 176, Q6: 210, IQ2: 66, IQ3X: 98, IQ4X: 136}
 
 CONFIGS = {
     # name: H, F, E, K, S, type gate/up, type down, extra
@@ -45,6 +45,7 @@ CONFIGS["q4k_q6k"] = dict(CONFIGS["c2"], tg=Q4, td=Q6)
 CONFIGS["c3_q6k"] = dict(CONFIGS["c3"], td=Q6)
 CONFIGS["iq4xs"] = dict(CONFIGS["c2"], tg=IQ4X, td=IQ4X)
 CONFIGS["c3_iq4xs"] = dict(CONFIGS["c3"], tg=IQ4X, td=IQ4X)
+CONFIGS["iq3xxs"] = dict(CONFIGS["c2"], tg=IQ3X, td=IQ3X)
 WORKLOAD = {
     "c1": "decode S=1, H=2048 F=768 E=128 top-8 softmax, Q4_K",
     "c2": "decode S=1, H=4096 F=1536 E=128 top-8 softmax, gate/up Q2_K, down Q3_K",
@@ -52,6 +53,7 @@ WORKLOAD = {
     "c4": "small batch S=4, H=5120 F=1536 E=160 top-8 softmax, IQ2_XXS",
     "c5": "full block S=1, H=7168 F=2048, 256 routed Q2_K (96 resident slots) + shared Q4_K, sigmoid 8 groups/top-4",
     "iq4xs": "decode S=1 at c2's shape with IQ4_XS gate/up/down",
+    "iq3xxs": "decode S=1 at c2's shape with IQ3_XXS gate/up/down (stand-in grid)",
     "c3_iq4xs": "prefill S=512 at c3's shape and routing with IQ4_XS gate/up/down",
     "c3_q6k": "prefill S=512 at c3's shape and routing with a Q6_K down projection (mixed-type layer)",
     "q4k_q6k": "decode S=1 at c2's shape with Q4_K gate/up and a Q6_K down projection (mixed-type layer)",
@@ -88,6 +90,8 @@ def dev_random_blocks(torch, t, rows, n, gen, scale=0.02):
         put(208, 0.5 * scale / 2000, 1.5 * scale / 2000)
     elif t == IQ4X:
         put(0, 0.5 * scale / 2000, 1.5 * scale / 2000)
+    elif t == IQ3X:
+        put(0, 0.5 * scale / 150, 1.5 * scale / 150)
     else:
         put(0, 0.5 * scale / 40, 1.5 * scale / 40)
     return raw.view(rows, nb * BB[t])
@@ -378,7 +382,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--replicas", type=int, default=0, help="layer replicas (0 = enough to exceed the MALL)")
-    ap.add_argument("--extras", default="c1,c3,c4,c5,c5_s64,q4k_q6k,c3_q6k,iq4xs,c3_iq4xs", help="extra configs to report ('' for none)")
+    ap.add_argument("--extras", default="c1,c3,c4,c5,c5_s64,q4k_q6k,c3_q6k,iq4xs,c3_iq4xs,iq3xxs", help="extra configs to report ('' for none)")
     ap.add_argument("--no-unpack", dest="unpack", action="store_false",
                     help="skip the expert-record unpack extra")
     ap.add_argument("--no-cpu", action="store_true")

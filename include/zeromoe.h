@@ -46,6 +46,7 @@ enum {
   ZM_TYPE_Q6_K = 14,
   ZM_TYPE_Q8_K = 15,
   ZM_TYPE_IQ2_XXS = 16,
+  ZM_TYPE_IQ3_XXS = 18,
   ZM_TYPE_IQ4_XS = 23,
   ZM_TYPE_I32 = 26,
 };
@@ -69,6 +70,11 @@ void zm_iq2xxs_builtin_grid(uint64_t grid[256]);
  * (kernels/quant/iq4xs_matmul.cu:41-49). */
 int zm_set_iq4nl_table(const int8_t table[16]);
 void zm_iq4nl_builtin_table(int8_t table[16]);
+/* Load the IQ3_XXS grid (256 x u32, ggml's iq3xxs_grid) for the current
+ * device.  Without a call a stand-in grid is used.  Replaces the grid copy
+ * of init_iq3_grids (kernels/quant/iq3_matmul.cu:66-78). */
+int zm_set_iq3xxs_grid(const uint32_t grid[256]);
+void zm_iq3xxs_builtin_grid(uint32_t grid[256]);
 
 /* Capability flags the graph builders probe before emitting negative
  * (inactive) expert ids: both are 1, the HIP path skips id < 0 in decode and
@@ -83,7 +89,7 @@ int zm_mul_mat_id_negative_skip_batched(void);
 /* GGML_OP_MUL_MAT_ID hook: dst[:, id, t] = W[ids[id, t]] . src1[:, id % ne11, t]
  * with src1 quantized to Q8_K (ggml CPU semantics), id < 0 -> zero row,
  * id >= n_experts -> NaN row.
- *   src0: Q2_K / Q3_K / Q4_K / Q5_K / Q6_K / IQ2_XXS / IQ4_XS [I, O, E] (row-contiguous)
+ *   src0: Q2_K / Q3_K / Q4_K / Q5_K / Q6_K / IQ2_XXS / IQ3_XXS / IQ4_XS [I, O, E] (row-contiguous)
  *   src1: F32 [I, ne11, S], ne11 == 1 or n_ids;  ids: I32 [n_ids, S]
  *   dst : F32 [O, n_ids, S]
  * execute = 0 is a pure capability query; execute = 1 launches on `stream`.
@@ -175,7 +181,7 @@ int zm_moe_forward(const zm_moe_layer *layer, const float *x, const float *logit
  *
  * Quantized weights times f32 activations, no Q8_K step: the reference's CUDA
  * executor semantics, not ggml's CPU ones.  Weight rows are I/256 super-blocks
- * (Q2_K / Q3_K / Q4_K / Q5_K / Q6_K / IQ2_XXS / IQ4_XS); x must be 16-byte aligned.  Accumulation is
+ * (Q2_K / Q3_K / Q4_K / Q5_K / Q6_K / IQ2_XXS / IQ3_XXS / IQ4_XS); x must be 16-byte aligned.  Accumulation is
  * fp32 in a fixed order (deterministic; not the reference's order).  The void
  * launchers keep the reference's signatures; a rejected call launches nothing
  * and leaves the reason in zm_last_error(). */
@@ -202,6 +208,9 @@ void launch_q6_K_matmul_stream(float *y, const float *x, const void *w, int S, i
 /* IQ4_XS: replaces launch_iq4_xs_matmul (kernels/quant/iq4xs_matmul.cu:137-140,
  * declared at backends/cuda/cuda_kernel_dispatcher.cpp:37). */
 void launch_iq4_xs_matmul(float *y, const float *x, const void *w, int S, int I, int O);
+/* IQ3_XXS: replaces launch_iq3_xxs_matmul (kernels/quant/iq3_matmul.cu:159-162). */
+void launch_iq3_xxs_matmul(float *y, const float *x, const void *w, int S, int I, int O);
+void launch_iq3_xxs_matmul_stream(float *y, const float *x, const void *w, int S, int I, int O, void *stream);
 void launch_iq4_xs_matmul_stream(float *y, const float *x, const void *w, int S, int I, int O, void *stream);
 /* y[g][O] = x[g][I] . dequant(W_g)^T for g < groups, W_g at byte
  * g * group_stride_bytes (a multiple of 176), legacy default stream; returns
@@ -211,7 +220,7 @@ bool launch_q5_K_matmul_grouped(float *y, const float *x, const void *w, int gro
                                  int I, int O);
 void launch_iq2_xxs_matmul_stream(float *y, const float *x, const void *w, int S, int I, int O, void *stream);
 /* The same by type id, returning 0 / -1.  Replaces CudaKernelDispatcher::matmul
- * (backends/cuda/cuda_kernel_dispatcher.cpp:109-189) for these seven types. */
+ * (backends/cuda/cuda_kernel_dispatcher.cpp:109-189) for these eight types. */
 int zm_f32_matmul(int type, float *y, const float *x, const void *w, int S, int I, int O, void *stream);
 
 /* FP32 quant-matmul hook with the acceptance rules of native_f32_quant_hook

@@ -27,6 +27,9 @@
  *   - IQ4_XS: per-block integer sums pinned by brute force over the dequant
  *     (exact); table values ggml's published kvalues_iq4nl, "parity unpinned"
  *     (not in the reference tree); float order unpinned.
+ *   - IQ3_XXS: per-block integer sums pinned by brute force over the dequant;
+ *     the grid is a stand-in (ggml's iq3xxs_grid is not in the reference
+ *     tree): "parity unpinned" for its values; float order unpinned.
  *   - IQ2_XXS grid: a stand-in table (ggml's 256 x u64 values are not in the
  *     reference tree); the sign table is closed form (0009...:69-75).
  *   - Router, bucketing, SwiGLU, combine: closed forms, brute-force checked.
@@ -110,6 +113,7 @@ size_t zmo_row_size(int type, int64_t n) {
   case ZMO_TYPE_Q6_K: return (size_t)nb * sizeof(zmo_block_q6_K);
   case ZMO_TYPE_IQ2_XXS: return (size_t)nb * sizeof(zmo_block_iq2_xxs);
   case ZMO_TYPE_IQ4_XS: return (size_t)nb * sizeof(zmo_block_iq4_xs);
+  case ZMO_TYPE_IQ3_XXS: return (size_t)nb * sizeof(zmo_block_iq3_xxs);
   case ZMO_TYPE_Q8_K: return (size_t)nb * sizeof(zmo_block_q8_K);
   case ZMO_TYPE_F32: return (size_t)n * 4;
   default: return 0;
@@ -228,6 +232,40 @@ static int8_t g_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25
 
 const int8_t *zmo_iq4nl_table(void) { return g_iq4nl; }
 void zmo_set_iq4nl_table(const int8_t table[16]) { memcpy(g_iq4nl, table, 16); }
+
+/* ----------------------------------------------------------- IQ3_XXS grid */
+
+/* Stand-in grid: the 256 vectors of four 3-bit digits d with
+ * d0 + 2 d1 + 4 d2 + 8 d3 = 0 mod 16 (one in 16 of the 4096 digit vectors,
+ * spread evenly), in increasing order of d0 + 8 d1 + 64 d2 + 512 d3, each digit stored
+ * as one byte 4 + 8 d (62 for d = 7): the byte levels ggml's grid uses.
+ * ggml's own table is a different selection and is loaded at run time by
+ * callers that have it. */
+void zmo_iq3xxs_standin_grid(uint32_t grid[256]) {
+  static const uint8_t lev[8] = {4, 12, 20, 28, 36, 44, 52, 62};
+  int n = 0;
+  for (int v = 0; v < 4096 && n < 256; ++v) {
+    const int d0 = v & 7, d1 = (v >> 3) & 7, d2 = (v >> 6) & 7, d3 = (v >> 9) & 7;
+    if ((d0 + 2 * d1 + 4 * d2 + 8 * d3) % 16) continue;
+    grid[n++] = (uint32_t)lev[d0] | ((uint32_t)lev[d1] << 8) | ((uint32_t)lev[d2] << 16) | ((uint32_t)lev[d3] << 24);
+  }
+}
+
+static uint32_t g_iq3xxs_grid[256];
+static int g_iq3xxs_ready = 0;
+
+const uint32_t *zmo_iq3xxs_grid(void) {
+  if (!g_iq3xxs_ready) {
+    zmo_iq3xxs_standin_grid(g_iq3xxs_grid);
+    g_iq3xxs_ready = 1;
+  }
+  return g_iq3xxs_grid;
+}
+
+void zmo_set_iq3xxs_grid(const uint32_t grid[256]) {
+  memcpy(g_iq3xxs_grid, grid, sizeof(g_iq3xxs_grid));
+  g_iq3xxs_ready = 1;
+}
 
 /* ---------------------------------------------------------------- Q8_K quant */
 
@@ -823,6 +861,75 @@ void zmo_quantize_row_iq4_xs(const float *x, zmo_block_iq4_xs *y, int64_t k) {
   }
 }
 
+/* IQ3_XXS: per 8-weight group an 8-bit sign pattern of even parity (7 bits
+ * stored, as IQ2_XXS) and two grid indices (four |values| each); per
+ * 32-weight sub-block a 4-bit scale ls with value d * (0.5 + ls) * 0.5
+ * (dequant at kernels/quant/iq3_matmul.cu:104-122). */
+static int nearest_grid4(const float *a, float inv, const uint32_t *grid) {
+  int best = 0;
+  float be = 3.4e38f;
+  for (int g = 0; g < 256; ++g) {
+    float e = 0;
+    for (int j = 0; j < 4; ++j) {
+      const float dd = a[j] * inv - (float)((grid[g] >> (8 * j)) & 0xff);
+      e += dd * dd;
+    }
+    if (e < be) {
+      be = e;
+      best = g;
+    }
+  }
+  return best;
+}
+
+void zmo_quantize_row_iq3_xxs(const float *x, zmo_block_iq3_xxs *y, int64_t k) {
+  const uint32_t *grid = zmo_iq3xxs_grid();
+  for (int64_t i = 0; i < k / ZMO_QK_K; ++i, x += ZMO_QK_K) {
+    float a[256], sub[8], max_sub = 0.f;
+    uint8_t sign[32];
+    for (int g = 0; g < 32; ++g) {
+      int neg = 0, minj = 0;
+      float mina = 3.4e38f;
+      uint8_t sg = 0;
+      for (int j = 0; j < 8; ++j) {
+        a[8 * g + j] = fabsf(x[8 * g + j]);
+        if (x[8 * g + j] < 0) {
+          ++neg;
+          sg |= (uint8_t)(1u << j);
+        }
+        if (a[8 * g + j] < mina) {
+          mina = a[8 * g + j];
+          minj = j;
+        }
+      }
+      if (neg & 1) sg ^= (uint8_t)(1u << minj);
+      sign[g] = sg;
+    }
+    for (int ib = 0; ib < 8; ++ib) {
+      float amax = 0.f;
+      for (int j = 0; j < 32; ++j) amax = a[32 * ib + j] > amax ? a[32 * ib + j] : amax;
+      sub[ib] = amax / 62.f;
+      max_sub = sub[ib] > max_sub ? sub[ib] : max_sub;
+    }
+    memset(&y[i], 0, sizeof(y[i]));
+    if (max_sub == 0.f) continue;
+    y[i].d = zmo_fp32_to_fp16(max_sub / (0.5f * 15.5f));
+    const float dq = zmo_fp16_to_fp32(y[i].d);
+    for (int ib = 0; ib < 8; ++ib) {
+      int ls = dq > 0.f ? zmo_nearest_int(sub[ib] / (0.5f * dq) - 0.5f) : 0;
+      ls = ls < 0 ? 0 : (ls > 15 ? 15 : ls);
+      const float s = dq * (0.5f + ls) * 0.5f;
+      uint32_t aux = (uint32_t)ls << 28;
+      for (int l = 0; l < 4; ++l) {
+        for (int h = 0; h < 2; ++h)
+          y[i].qs[8 * ib + 2 * l + h] = (uint8_t)(s > 0.f ? nearest_grid4(a + 32 * ib + 8 * l + 4 * h, 1.f / s, grid) : 0);
+        aux |= (uint32_t)(sign[4 * ib + l] & 127u) << (7 * l);
+      }
+      memcpy(y[i].qs + 64 + 4 * ib, &aux, 4);
+    }
+  }
+}
+
 void zmo_quantize_rows(int type, const float *x, void *dst, int64_t rows, int64_t n) {
   const size_t rs = zmo_row_size(type, n);
 #pragma omp parallel for schedule(dynamic, 4)
@@ -837,6 +944,7 @@ void zmo_quantize_rows(int type, const float *x, void *dst, int64_t rows, int64_
     case ZMO_TYPE_Q6_K: zmo_quantize_row_q6_K(xr, (zmo_block_q6_K *)out, n); break;
     case ZMO_TYPE_IQ2_XXS: zmo_quantize_row_iq2_xxs(xr, (zmo_block_iq2_xxs *)out, n); break;
     case ZMO_TYPE_IQ4_XS: zmo_quantize_row_iq4_xs(xr, (zmo_block_iq4_xs *)out, n); break;
+    case ZMO_TYPE_IQ3_XXS: zmo_quantize_row_iq3_xxs(xr, (zmo_block_iq3_xxs *)out, n); break;
     case ZMO_TYPE_Q8_K: zmo_quantize_row_q8_K(xr, (zmo_block_q8_K *)out, n); break;
     default: break;
     }
@@ -979,6 +1087,30 @@ static void dequant_iq4_xs(const zmo_block_iq4_xs *x, float *y, int64_t k) {
   }
 }
 
+/* dequantize_row_iq3_xxs (kernels/quant/iq3_matmul.cu:104-122): sub-block
+ * ib: scales+signs word u = qs[64 + 4ib ..]; group l of 8 weights: grid
+ * entries qs[8ib + 2l] (weights 0..3) and qs[8ib + 2l + 1] (4..7), signs
+ * ksigns_iq2xs[(u >> 7l) & 127], value d * (0.5 + (u >> 28)) * 0.5 * grid. */
+static void dequant_iq3_xxs(const zmo_block_iq3_xxs *x, float *y, int64_t k) {
+  const uint32_t *grid = zmo_iq3xxs_grid();
+  for (int64_t i = 0; i < k / ZMO_QK_K; ++i) {
+    const float d = zmo_fp16_to_fp32(x[i].d);
+    for (int ib = 0; ib < 8; ++ib) {
+      uint32_t u;
+      memcpy(&u, x[i].qs + 64 + 4 * ib, 4);
+      const float db = d * (0.5f + (float)(u >> 28)) * 0.5f;
+      for (int l = 0; l < 4; ++l) {
+        const uint8_t signs = zmo_ksigns_iq2xs((int)((u >> (7 * l)) & 127));
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t g = grid[x[i].qs[8 * ib + 2 * l + (j >> 2)]];
+          const float v = db * (float)((g >> (8 * (j & 3))) & 0xff);
+          *y++ = ((signs >> j) & 1) ? -v : v;
+        }
+      }
+    }
+  }
+}
+
 /* dequantize_row_iq2_xxs (iq2_matmul.cu:73-91). */
 static void dequant_iq2_xxs(const zmo_block_iq2_xxs *x, float *y, int64_t k) {
   const uint64_t *grid = zmo_iq2xxs_grid();
@@ -1007,6 +1139,7 @@ void zmo_dequantize_row(int type, const void *src, float *y, int64_t n) {
   case ZMO_TYPE_Q6_K: dequant_q6_K((const zmo_block_q6_K *)src, y, n); break;
   case ZMO_TYPE_IQ2_XXS: dequant_iq2_xxs((const zmo_block_iq2_xxs *)src, y, n); break;
   case ZMO_TYPE_IQ4_XS: dequant_iq4_xs((const zmo_block_iq4_xs *)src, y, n); break;
+  case ZMO_TYPE_IQ3_XXS: dequant_iq3_xxs((const zmo_block_iq3_xxs *)src, y, n); break;
   case ZMO_TYPE_Q8_K: {
     const zmo_block_q8_K *b = (const zmo_block_q8_K *)src;
     for (int64_t i = 0; i < n / ZMO_QK_K; ++i)
@@ -1167,6 +1300,35 @@ static float dot_iq4_xs(int n, const zmo_block_iq4_xs *x, const zmo_block_q8_K *
   return acc;
 }
 
+/* ggml_vec_dot_iq3_xxs_q8_K, scalar order: per block d = fp16(d) * d_y,
+ * bsum = sum_ib (2 ls + 1) * sum grid * sign * q8, sumf += d * bsum; result
+ * 0.25 * sumf.  Float order: parity unpinned (no stock copy in the reference
+ * tree). */
+static float dot_iq3_xxs(int n, const zmo_block_iq3_xxs *x, const zmo_block_q8_K *y) {
+  const uint32_t *grid = zmo_iq3xxs_grid();
+  float sumf = 0.f;
+  for (int i = 0; i < n / ZMO_QK_K; ++i) {
+    const float d = zmo_fp16_to_fp32(x[i].d) * y[i].d;
+    int32_t bsum = 0;
+    for (int ib = 0; ib < 8; ++ib) {
+      uint32_t u;
+      memcpy(&u, x[i].qs + 64 + 4 * ib, 4);
+      int32_t sumi = 0;
+      for (int l = 0; l < 4; ++l) {
+        const uint8_t signs = zmo_ksigns_iq2xs((int)((u >> (7 * l)) & 127));
+        for (int j = 0; j < 8; ++j) {
+          const int g = (int)((grid[x[i].qs[8 * ib + 2 * l + (j >> 2)]] >> (8 * (j & 3))) & 0xff);
+          const int q8 = y[i].qs[32 * ib + 8 * l + j];
+          sumi += ((signs >> j) & 1) ? -g * q8 : g * q8;
+        }
+      }
+      bsum += (2 * (int32_t)(u >> 28) + 1) * sumi;
+    }
+    sumf += d * (float)bsum;
+  }
+  return 0.25f * sumf;
+}
+
 /* ggml_vec_dot_iq2_xxs_q8_K, AVX2 / AVX-512BW order (patches/ggml/0009...:34-95,
  * bench/kernels/iq2xxs_dot_bench.cpp:26-50): lane l sums (2ls+1)*grid*sign*q8
  * over bytes [4l,4l+4) of each 32-weight sub-block; one fma per block with
@@ -1203,6 +1365,7 @@ float zmo_vec_dot_q8_K(int type, int n, const void *x, const zmo_block_q8_K *y) 
   case ZMO_TYPE_Q6_K: return dot_q6_K(n, (const zmo_block_q6_K *)x, y);
   case ZMO_TYPE_IQ2_XXS: return dot_iq2_xxs(n, (const zmo_block_iq2_xxs *)x, y);
   case ZMO_TYPE_IQ4_XS: return dot_iq4_xs(n, (const zmo_block_iq4_xs *)x, y);
+  case ZMO_TYPE_IQ3_XXS: return dot_iq3_xxs(n, (const zmo_block_iq3_xxs *)x, y);
   default: return NAN;
   }
 }
@@ -1254,6 +1417,12 @@ void zmo_block_dots(int type, int n, const void *vx, const zmo_block_q8_K *y, in
     } else if (type == ZMO_TYPE_Q6_K) {
       const zmo_block_q6_K *x = (const zmo_block_q6_K *)vx + i;
       for (int t = 0; t < 256; ++t) s += x->scales[t / 16] * q6_value(x, t) * y[i].qs[t];
+    } else if (type == ZMO_TYPE_IQ3_XXS) {
+      /* (2ls+1)*grid*sign = 4 * dequant / d: reuse the dequant as integers */
+      zmo_block_iq3_xxs one = ((const zmo_block_iq3_xxs *)vx)[i];
+      one.d = 0x3c00;
+      dequant_iq3_xxs(&one, w, 256);
+      for (int t = 0; t < 256; ++t) s += (int32_t)lrintf(w[t] * 4.0f) * y[i].qs[t];
     } else if (type == ZMO_TYPE_IQ4_XS) {
       /* (ls - 32) * table value = dequant / d: reuse the dequant as integers */
       zmo_block_iq4_xs one = ((const zmo_block_iq4_xs *)vx)[i];
@@ -1276,7 +1445,7 @@ void zmo_block_dots(int type, int n, const void *vx, const zmo_block_q8_K *y, in
 
 static int type_ok(int t) {
   return t == ZMO_TYPE_Q2_K || t == ZMO_TYPE_Q3_K || t == ZMO_TYPE_Q4_K || t == ZMO_TYPE_Q5_K || t == ZMO_TYPE_Q6_K ||
-         t == ZMO_TYPE_IQ2_XXS || t == ZMO_TYPE_IQ4_XS;
+         t == ZMO_TYPE_IQ2_XXS || t == ZMO_TYPE_IQ3_XXS || t == ZMO_TYPE_IQ4_XS;
 }
 
 int zmo_mul_mat_id(const zmo_tensor *src0, const zmo_tensor *src1, const zmo_tensor *ids, zmo_tensor *dst,

@@ -33,6 +33,7 @@ enum {
   ZMO_TYPE_Q6_K = 14,
   ZMO_TYPE_Q8_K = 15,
   ZMO_TYPE_IQ2_XXS = 16,
+  ZMO_TYPE_IQ3_XXS = 18,
   ZMO_TYPE_IQ4_XS = 23,
   ZMO_TYPE_I32 = 26,
 };
@@ -46,7 +47,8 @@ typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; } zmo_bl
 typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qh[32]; uint8_t qs[128]; } zmo_block_q5_K; /* 176 B */
 typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } zmo_block_q6_K;   /* 210 B */
 typedef struct { uint16_t d; uint16_t qs[32]; } zmo_block_iq2_xxs;
-typedef struct { uint16_t d; uint16_t scales_h; uint8_t scales_l[4]; uint8_t qs[128]; } zmo_block_iq4_xs; /* 136 B */                            /* 66 B  */
+typedef struct { uint16_t d; uint16_t scales_h; uint8_t scales_l[4]; uint8_t qs[128]; } zmo_block_iq4_xs; /* 136 B */
+typedef struct { uint16_t d; uint8_t qs[96]; } zmo_block_iq3_xxs; /* 98 B: grid indices[64] | scales+signs u32[8] */                            /* 66 B  */
 typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } zmo_block_q8_K;                /* 292 B */
 
 /* ---- helpers ---- */
@@ -69,6 +71,12 @@ uint8_t zmo_ksigns_iq2xs(int i);
  * are not in the reference tree; the default is ggml's published table and
  * zmo_set_iq4nl_table() replaces it. */
 const int8_t *zmo_iq4nl_table(void);
+
+/* IQ3_XXS grid (256 x u32, four byte values each; ggml's iq3xxs_grid, not in
+ * the reference tree): a stand-in by default, replaced by zmo_set_iq3xxs_grid. */
+const uint32_t *zmo_iq3xxs_grid(void);
+void zmo_set_iq3xxs_grid(const uint32_t grid[256]);
+void zmo_iq3xxs_standin_grid(uint32_t grid[256]);
 void zmo_set_iq4nl_table(const int8_t table[16]);
 
 /* ---- quantizers (valid blocks; bit identity with ggml's quantizer bytes is unpinned) ---- */
@@ -80,6 +88,7 @@ void zmo_quantize_row_q5_K(const float *x, zmo_block_q5_K *y, int64_t k);
 void zmo_quantize_row_q6_K(const float *x, zmo_block_q6_K *y, int64_t k);
 void zmo_quantize_row_iq2_xxs(const float *x, zmo_block_iq2_xxs *y, int64_t k);
 void zmo_quantize_row_iq4_xs(const float *x, zmo_block_iq4_xs *y, int64_t k);
+void zmo_quantize_row_iq3_xxs(const float *x, zmo_block_iq3_xxs *y, int64_t k);
 /* quantize `rows` rows of n floats of `type` into dst (rows * row_size bytes) */
 void zmo_quantize_rows(int type, const float *x, void *dst, int64_t rows, int64_t n);
 

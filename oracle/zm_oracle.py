@@ -18,9 +18,9 @@ REF_PATH = os.path.join(HERE, "_ref", "libzmref.so")
 
 QK_K = 256
 TYPE_F32, TYPE_Q2_K, TYPE_Q3_K, TYPE_Q4_K, TYPE_Q8_K, TYPE_IQ2_XXS, TYPE_I32 = 0, 10, 11, 12, 15, 16, 26
-TYPE_Q5_K, TYPE_Q6_K, TYPE_IQ4_XS = 13, 14, 23
-BLOCK_BYTES = {TYPE_Q2_K: 84, TYPE_Q3_K: 110, TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210, TYPE_IQ4_XS: 136, TYPE_IQ2_XXS: 66, TYPE_Q8_K: 292}
-TYPE_NAMES = {TYPE_Q2_K: "q2_K", TYPE_Q3_K: "q3_K", TYPE_Q4_K: "q4_K", TYPE_Q5_K: "q5_K", TYPE_Q6_K: "q6_K", TYPE_IQ4_XS: "iq4_xs", TYPE_IQ2_XXS: "iq2_xxs", TYPE_Q8_K: "q8_K"}
+TYPE_Q5_K, TYPE_Q6_K, TYPE_IQ4_XS, TYPE_IQ3_XXS = 13, 14, 23, 18
+BLOCK_BYTES = {TYPE_Q2_K: 84, TYPE_Q3_K: 110, TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210, TYPE_IQ4_XS: 136, TYPE_IQ3_XXS: 98, TYPE_IQ2_XXS: 66, TYPE_Q8_K: 292}
+TYPE_NAMES = {TYPE_Q2_K: "q2_K", TYPE_Q3_K: "q3_K", TYPE_Q4_K: "q4_K", TYPE_Q5_K: "q5_K", TYPE_Q6_K: "q6_K", TYPE_IQ4_XS: "iq4_xs", TYPE_IQ3_XXS: "iq3_xxs", TYPE_IQ2_XXS: "iq2_xxs", TYPE_Q8_K: "q8_K"}
 GATING_SOFTMAX, GATING_SIGMOID, GATING_SQRT_SOFTPLUS = 0, 1, 2
 
 Q8K_DTYPE = np.dtype([("d", "<f4"), ("qs", "i1", (256,)), ("bsums", "<i2", (16,))])
@@ -55,6 +55,8 @@ def lib():
         L.zmo_iq2xxs_grid.restype = P
         L.zmo_set_iq2xxs_grid.argtypes = [P]
         L.zmo_iq2xxs_standin_grid.argtypes = [P]
+        L.zmo_iq3xxs_grid.restype = P
+        L.zmo_set_iq3xxs_grid.argtypes = [P]
         L.zmo_iq4nl_table.restype = P
         L.zmo_set_iq4nl_table.argtypes = [P]
         L.zmo_ksigns_iq2xs.restype = C.c_uint8
@@ -110,6 +112,11 @@ def fp32_to_fp16(f: float) -> int:
 def iq2xxs_grid() -> np.ndarray:
     ptr = lib().zmo_iq2xxs_grid()
     return np.ctypeslib.as_array(C.cast(ptr, C.POINTER(C.c_uint64)), (256,)).copy()
+
+
+def iq3xxs_grid() -> np.ndarray:
+    ptr = lib().zmo_iq3xxs_grid()
+    return np.ctypeslib.as_array(C.cast(ptr, C.POINTER(C.c_uint32)), (256,)).copy()
 
 
 def iq4nl_table() -> np.ndarray:
@@ -195,6 +202,8 @@ def random_blocks(t: int, n_rows: int, n: int, seed: int, scale: float = 0.02) -
         put16(2, rng.uniform(0.5, 1.5, shp) * scale / 60)
     elif t == TYPE_Q6_K:  # q-32 in -32..31, sc in -128..127
         put16(208, rng.uniform(0.5, 1.5, shp) * scale / 2000)
+    elif t == TYPE_IQ3_XXS:  # grid 4..62, (0.5+ls)*0.5 up to ~8
+        put16(0, rng.uniform(0.5, 1.5, shp) * scale / 150)
     elif t == TYPE_IQ4_XS:  # table up to 127, ls-32 in -32..31
         put16(0, rng.uniform(0.5, 1.5, shp) * scale / 2000)
     elif t == TYPE_IQ2_XXS:  # grid 8..43, (0.5+ls)*0.25 up to ~4

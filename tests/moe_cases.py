@@ -12,7 +12,7 @@ import torch
 import zm_oracle as O
 
 Q2, Q3, Q4, IQ2 = O.TYPE_Q2_K, O.TYPE_Q3_K, O.TYPE_Q4_K, O.TYPE_IQ2_XXS
-Q5, Q6, IQ4 = O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_IQ4_XS
+Q5, Q6, IQ4, IQ3 = O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_IQ4_XS, O.TYPE_IQ3_XXS
 
 
 def dev_random_blocks(t: int, rows: int, n: int, seed: int, device="cuda", scale=0.02) -> torch.Tensor:
@@ -43,6 +43,8 @@ def dev_random_blocks(t: int, rows: int, n: int, seed: int, device="cuda", scale
         put(208, 0.5 * scale / 2000, 1.5 * scale / 2000)
     elif t == IQ4:
         put(0, 0.5 * scale / 2000, 1.5 * scale / 2000)
+    elif t == IQ3:
+        put(0, 0.5 * scale / 150, 1.5 * scale / 150)
     else:
         put(0, 0.5 * scale / 40, 1.5 * scale / 40)
     return raw.view(rows, nb * bb)

@@ -12,12 +12,12 @@ import pytest
 import torch
 
 import zm_oracle as O
-from moe_cases import IQ2, IQ4, Q2, Q3, Q4, Q5, Q6
+from moe_cases import IQ2, IQ3, IQ4, Q2, Q3, Q4, Q5, Q6
 
 pytestmark = pytest.mark.gpu
 
-TYPES = [Q2, Q3, Q4, Q5, Q6, IQ2, IQ4]
-NAMES = {Q2: "q2_K", Q3: "q3_K", Q4: "q4_K", Q5: "q5_K", Q6: "q6_K", IQ2: "iq2_xxs", IQ4: "iq4_xs"}
+TYPES = [Q2, Q3, Q4, Q5, Q6, IQ2, IQ3, IQ4]
+NAMES = {Q2: "q2_K", Q3: "q3_K", Q4: "q4_K", Q5: "q5_K", Q6: "q6_K", IQ2: "iq2_xxs", IQ3: "iq3_xxs", IQ4: "iq4_xs"}
 MM_TOL = 2e-5
 
 

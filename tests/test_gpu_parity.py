@@ -8,11 +8,11 @@ import pytest
 import torch
 
 import zm_oracle as O
-from moe_cases import CONFIGS, IQ2, IQ4, Q2, Q3, Q4, Q5, Q6, Built, assert_close_layer, dev_random_blocks, reduced
+from moe_cases import CONFIGS, IQ2, IQ3, IQ4, Q2, Q3, Q4, Q5, Q6, Built, assert_close_layer, dev_random_blocks, reduced
 
 pytestmark = pytest.mark.gpu
 
-TYPES = [Q2, Q3, Q4, Q5, Q6, IQ2, IQ4]
+TYPES = [Q2, Q3, Q4, Q5, Q6, IQ2, IQ3, IQ4]
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -153,6 +153,27 @@ def test_iq4_xs_custom_table():
         lib_o.zmo_set_iq4nl_table(default.ctypes.data)
 
 
+def test_iq3_xxs_custom_grid():
+    """zm_set_iq3xxs_grid replaces the device grid: the op then matches the
+    oracle run with the same grid (the stand-in in reverse order here)."""
+    import zeromoe_amd as Z
+
+    default = Z.builtin_iq3xxs_grid()
+    np.testing.assert_array_equal(default, O.iq3xxs_grid())
+    custom = np.ascontiguousarray(default[::-1])
+    lib_o = O.lib()
+    try:
+        Z.set_iq3xxs_grid(custom)
+        lib_o.zmo_set_iq3xxs_grid(custom.ctypes.data)
+        rng = np.random.default_rng(3)
+        ids = np.stack([rng.permutation(6)[:4] for _ in range(3)]).astype(np.int32)
+        got, ref = _mmid_case(IQ3, 1024, 40, 6, ids, 1, seed=5)
+        np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-5 * np.abs(ref).max())
+    finally:
+        Z.set_iq3xxs_grid(default)
+        lib_o.zmo_set_iq3xxs_grid(default.ctypes.data)
+
+
 def test_mul_mat_id_out_of_range_is_nan():
     ids = np.array([[2, 99]], np.int32)
     got, _ = _mmid_case(Q2, 512, 8, 4, np.array([[2, 1]], np.int32), 1, seed=1)
@@ -236,6 +257,8 @@ LAYER_CASES = {
     "q5k_q5k_S64": (CONFIGS["c3"], dict(tg=Q5, td=Q5, S=64, H=1024, F=512)),
     "q4k_iq4xs_S1": (CONFIGS["c2"], dict(tg=Q4, td=IQ4)),
     "iq4xs_S16": (CONFIGS["c2"], dict(tg=IQ4, td=IQ4, S=16, H=2048, F=768)),
+    "iq3xxs_S1": (CONFIGS["c2"], dict(tg=IQ3, td=IQ3)),
+    "iq3xxs_S16": (CONFIGS["c2"], dict(tg=IQ3, td=IQ3, S=16, H=2048, F=768)),
     "q4k_q5k_shared_q6k": (CONFIGS["c5"], dict(tg=Q4, td=Q5, t_shared=Q6, H=2048, F=512, F_shared=1024)),
 }
 
@@ -288,6 +311,7 @@ FUSED_CASES = {
     "q5k_q6k": (CONFIGS["c2"], dict(tg=Q5, td=Q6)),
     "iq4xs": (CONFIGS["c2"], dict(tg=IQ4, td=IQ4)),
     "iq4xs_S3": (CONFIGS["c2"], dict(tg=IQ4, td=IQ4, S=3)),
+    "iq3xxs": (CONFIGS["c2"], dict(tg=IQ3, td=IQ3)),
 }
 
 

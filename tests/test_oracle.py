@@ -209,6 +209,43 @@ def test_iq4_xs_known_answer():
     assert list(t[[0, 8, 15]]) == [-127, 1, 113] and np.all(np.diff(t) > 0)
 
 
+def test_iq3_xxs_known_answer():
+    """Sub-block ib, group l of 8 weights: grid entries qs[8ib + 2l] (weights
+    0..3) and qs[8ib + 2l + 1] (4..7), byte j of an entry = weight j; the
+    scales+signs word at 64 + 4ib: sign index (u >> 7l) & 127 through
+    ksigns, scale d * (0.5 + (u >> 28)) * 0.5 (kernels/quant/iq3_matmul.cu:104-122)."""
+    grid = O.iq3xxs_grid()
+    b = _blank(O.TYPE_IQ3_XXS)
+    _put_half(b, 0, 1.0)
+    ib, l = 5, 2
+    b[2 + 8 * ib + 2 * l] = 37
+    b[2 + 8 * ib + 2 * l + 1] = 200
+    sidx = 0b0000011                    # weights 0 and 1 negative (parity even)
+    u = (sidx << (7 * l)) | (9 << 28)
+    b[2 + 64 + 4 * ib:2 + 64 + 4 * ib + 4] = np.frombuffer(np.uint32(u).tobytes(), np.uint8)
+    y = O.dequantize(O.TYPE_IQ3_XXS, b, 256)[0]
+    g0 = [(int(grid[0]) >> (8 * j)) & 0xFF for j in range(4)]
+    for s in range(8):
+        scale = (0.5 + (9 if s == ib else 0)) * 0.5
+        for ll in range(4):
+            for j in range(8):
+                i = 32 * s + 8 * ll + j
+                if s == ib and ll == l:
+                    e = int(grid[37 if j < 4 else 200]) >> (8 * (j & 3)) & 0xFF
+                    exp = scale * e * (-1 if j in (0, 1) else 1)
+                else:
+                    exp = scale * g0[j & 3]
+                assert y[i] == np.float32(exp), (s, ll, j)
+
+
+def test_iq3_grid_stand_in_properties():
+    g = O.iq3xxs_grid()
+    assert len(set(g.tolist())) == 256
+    levels = {4, 12, 20, 28, 36, 44, 52, 62}
+    for v in g.tolist():
+        assert {(v >> (8 * j)) & 0xFF for j in range(4)} <= levels
+
+
 def test_iq2_xxs_known_answer():
     """value = d*(0.5+ls)*0.25*grid[idx][j]*sign, signs = ksigns[7-bit index]
     with the 8th sign = parity (iq2_matmul.cu:73-91, patches/ggml/0009...:69-75)."""
@@ -257,7 +294,7 @@ def test_iq2_grid_stand_in_properties():
 # ------------------------------------------------------------------ integer block dots == brute force over dequant
 
 @pytest.mark.parametrize("t", [O.TYPE_Q2_K, O.TYPE_Q3_K, O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_IQ2_XXS,
-                               O.TYPE_IQ4_XS])
+                               O.TYPE_IQ3_XXS, O.TYPE_IQ4_XS])
 def test_block_dots_equal_dequant_brute_force(t):
     """sum_j sc*dot - dmin*sum m*bsum per block equals dequant(w).dequant(q8)
     scaled by the block scales, exactly in float64 (integers < 2^53)."""
@@ -287,6 +324,8 @@ def test_block_dots_equal_dequant_brute_force(t):
             exp = float(np.frombuffer(bb[208:210].tobytes(), np.float16)[0]) * isum[b]
         elif t == O.TYPE_IQ4_XS:
             exp = float(np.frombuffer(bb[0:2].tobytes(), np.float16)[0]) * isum[b]
+        elif t == O.TYPE_IQ3_XXS:
+            exp = float(np.frombuffer(bb[0:2].tobytes(), np.float16)[0]) * isum[b] / 4.0
         else:
             exp = float(np.frombuffer(bb[0:2].tobytes(), np.float16)[0]) * isum[b] / 8.0
         got = float(np.dot(wd[256 * b:256 * b + 256], qv[256 * b:256 * b + 256]))
@@ -294,7 +333,7 @@ def test_block_dots_equal_dequant_brute_force(t):
 
 
 @pytest.mark.parametrize("t", [O.TYPE_Q2_K, O.TYPE_Q3_K, O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_IQ2_XXS,
-                               O.TYPE_IQ4_XS])
+                               O.TYPE_IQ3_XXS, O.TYPE_IQ4_XS])
 def test_vec_dot_matches_dequant_dot(t):
     rng = np.random.default_rng(5)
     n = 2048
@@ -501,7 +540,7 @@ def test_moe_forward_composition():
 
 @pytest.mark.parametrize("t,tol", [(O.TYPE_Q2_K, 0.40), (O.TYPE_Q3_K, 0.20), (O.TYPE_Q4_K, 0.09),
                                    (O.TYPE_Q5_K, 0.045), (O.TYPE_Q6_K, 0.025), (O.TYPE_IQ2_XXS, 0.40),
-                                   (O.TYPE_IQ4_XS, 0.12)])
+                                   (O.TYPE_IQ4_XS, 0.12), (O.TYPE_IQ3_XXS, 0.3)])
 def test_quantizer_round_trip(t, tol):
     x = O.fill_normal(42, 8 * 1024, 0.0, 0.02).reshape(8, 1024)
     y = O.dequantize(t, O.quantize(t, x), 1024)

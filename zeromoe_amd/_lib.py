@@ -49,6 +49,8 @@ SIGNATURES = {
     "zm_set_iq2xxs_grid": (I, [P]),
     "zm_iq2xxs_builtin_grid": (None, [P]),
     "zm_set_iq4nl_table": (I, [P]),
+    "zm_set_iq3xxs_grid": (I, [P]),
+    "zm_iq3xxs_builtin_grid": (None, [P]),
     "zm_iq4nl_builtin_table": (None, [P]),
     "zm_mul_mat_id_negative_skip": (I, []),
     "zm_mul_mat_id_negative_skip_batched": (I, []),
@@ -75,6 +77,8 @@ SIGNATURES = {
     "launch_q6_K_matmul": (None, [P, P, P, I, I, I]),
     "launch_q6_K_matmul_stream": (None, [P, P, P, I, I, I, P]),
     "launch_iq4_xs_matmul": (None, [P, P, P, I, I, I]),
+    "launch_iq3_xxs_matmul": (None, [P, P, P, I, I, I]),
+    "launch_iq3_xxs_matmul_stream": (None, [P, P, P, I, I, I, P]),
     "launch_iq4_xs_matmul_stream": (None, [P, P, P, I, I, I, P]),
     "launch_q5_K_matmul_grouped": (C.c_bool, [P, P, P, I, C.c_size_t, I, I]),
     "launch_ggml_moe_unpack": (I, [P, P, P, P, I] + [C.c_size_t] * 7 + [P]),

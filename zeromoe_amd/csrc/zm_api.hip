@@ -43,6 +43,7 @@ struct DeviceState {
   uint64_t *grid = nullptr;   // IQ2_XXS grid, 256 x u64
   uint64_t *signs = nullptr;  // 128 x u64 byte masks of ksigns_iq2xs
   uint64_t *iq4 = nullptr;    // IQ4_XS value table, 16 x i8
+  uint64_t *iq3 = nullptr;    // IQ3_XXS grid, 256 x u32
   void *ws = nullptr;         // zm_mul_mat_id workspace
   size_t ws_size = 0;
   uint64_t *trace = nullptr;  // decode-kernel phase timestamps (ZEROMOE_TRACE=1)
@@ -82,6 +83,20 @@ void builtin_iq4nl(int8_t t[16]) {
   for (int i = 0; i < 16; ++i) t[i] = v[i];
 }
 
+// stand-in IQ3_XXS grid: the 256 vectors of four 3-bit digits d with
+// d0 + 2 d1 + 4 d2 + 8 d3 = 0 mod 16, in increasing order of the digit
+// vector read as a base-8 number, digit d stored as the byte 4 + 8 d (62 for
+// 7); ggml's own table is loaded with zm_set_iq3xxs_grid
+void builtin_iq3_grid(uint32_t g[256]) {
+  static const uint8_t lev[8] = {4, 12, 20, 28, 36, 44, 52, 62};
+  int n = 0;
+  for (int v = 0; v < 4096 && n < 256; ++v) {
+    const int d0 = v & 7, d1 = (v >> 3) & 7, d2 = (v >> 6) & 7, d3 = (v >> 9) & 7;
+    if ((d0 + 2 * d1 + 4 * d2 + 8 * d3) % 16) continue;
+    g[n++] = (uint32_t)lev[d0] | ((uint32_t)lev[d1] << 8) | ((uint32_t)lev[d2] << 16) | ((uint32_t)lev[d3] << 24);
+  }
+}
+
 int device_state(DeviceState **out) {
   int dev = 0;
   HIP_OK(hipGetDevice(&dev));
@@ -106,6 +121,10 @@ int device_state(DeviceState **out) {
     builtin_iq4nl(tab);
     HIP_OK(hipMalloc(&d.iq4, 16));
     HIP_OK(hipMemcpy(d.iq4, tab, 16, hipMemcpyHostToDevice));
+    uint32_t g3[256];
+    builtin_iq3_grid(g3);
+    HIP_OK(hipMalloc(&d.iq3, sizeof(g3)));
+    HIP_OK(hipMemcpy(d.iq3, g3, sizeof(g3), hipMemcpyHostToDevice));
     d.ready = true;
   }
   *out = &d;
@@ -124,7 +143,7 @@ int zm::device_grid(const uint64_t **grid) {
 int zm::device_table(int type, const uint64_t **table) {
   DeviceState *d;
   if (device_state(&d)) return -1;
-  *table = type == T_IQ4_XS ? d->iq4 : d->grid;
+  *table = type == T_IQ4_XS ? d->iq4 : (type == T_IQ3_XXS ? d->iq3 : d->grid);
   return 0;
 }
 
@@ -163,7 +182,8 @@ bool getenv_flag_off(const char *name) {
 }
 
 bool type_supported(int t) {
-  return t == T_Q2_K || t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_IQ2_XXS || t == T_IQ4_XS;
+  return t == T_Q2_K || t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_IQ2_XXS || t == T_IQ3_XXS ||
+         t == T_IQ4_XS;
 }
 
 size_t row_bytes(int t, int64_t n) { return (size_t)(n / QK) * block_bytes(t); }
@@ -188,7 +208,7 @@ int pick_tile(int nrows, int U, int n_groups) {
 
 int launch_gemv(int type, bool gateup, int np, const GemvArgs &a0, int n_groups, hipStream_t st) {
   GemvArgs a = a0;
-  if (type == T_IQ4_XS && device_table(T_IQ4_XS, &a.grid)) return -1;
+  if ((type == T_IQ4_XS || type == T_IQ3_XXS) && device_table(type, &a.grid)) return -1;
   const int U = a.nb * 4;
   a.tile_rows = pick_tile(a.nrows, U, n_groups);
   dim3 grid((a.nrows + a.tile_rows - 1) / a.tile_rows, n_groups);
@@ -199,6 +219,7 @@ int launch_gemv(int type, bool gateup, int np, const GemvArgs &a0, int n_groups,
   case T_Q4_K: rc = gateup ? launch_gemv_type<T_Q4_K, true>(np, U, grid, a, st) : launch_gemv_type<T_Q4_K, false>(np, U, grid, a, st); break;
   case T_Q5_K: rc = gateup ? launch_gemv_type<T_Q5_K, true>(np, U, grid, a, st) : launch_gemv_type<T_Q5_K, false>(np, U, grid, a, st); break;
   case T_Q6_K: rc = gateup ? launch_gemv_type<T_Q6_K, true>(np, U, grid, a, st) : launch_gemv_type<T_Q6_K, false>(np, U, grid, a, st); break;
+  case T_IQ3_XXS: rc = gateup ? launch_gemv_type<T_IQ3_XXS, true>(np, U, grid, a, st) : launch_gemv_type<T_IQ3_XXS, false>(np, U, grid, a, st); break;
   case T_IQ4_XS: rc = gateup ? launch_gemv_type<T_IQ4_XS, true>(np, U, grid, a, st) : launch_gemv_type<T_IQ4_XS, false>(np, U, grid, a, st); break;
   case T_IQ2_XXS: rc = gateup ? launch_gemv_type<T_IQ2_XXS, true>(np, U, grid, a, st) : launch_gemv_type<T_IQ2_XXS, false>(np, U, grid, a, st); break;
   default: return fail("unsupported weight type %d", type);
@@ -305,6 +326,15 @@ int zm_set_iq2xxs_grid(const uint64_t grid[256]) {
 }
 
 void zm_iq4nl_builtin_table(int8_t table[16]) { builtin_iq4nl(table); }
+
+void zm_iq3xxs_builtin_grid(uint32_t grid[256]) { builtin_iq3_grid(grid); }
+
+int zm_set_iq3xxs_grid(const uint32_t grid[256]) {
+  DeviceState *d;
+  if (device_state(&d)) return -1;
+  HIP_OK(hipMemcpy(d->iq3, grid, 256 * sizeof(uint32_t), hipMemcpyHostToDevice));
+  return 0;
+}
 
 int zm_set_iq4nl_table(const int8_t table[16]) {
   DeviceState *d;
@@ -545,6 +575,7 @@ int zm_block_dots(int type, const void *w_row, const float *x, int n, int32_t *i
   case T_Q5_K: hipLaunchKernelGGL(k_block_dots<T_Q5_K>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->grid, d->signs); break;
   case T_Q6_K: hipLaunchKernelGGL(k_block_dots<T_Q6_K>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->grid, d->signs); break;
   case T_IQ4_XS: hipLaunchKernelGGL(k_block_dots<T_IQ4_XS>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->iq4, d->signs); break;
+  case T_IQ3_XXS: hipLaunchKernelGGL(k_block_dots<T_IQ3_XXS>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->iq3, d->signs); break;
   default: hipLaunchKernelGGL(k_block_dots<T_IQ2_XXS>, g, dim3(64), 0, st, w, xq, nb, isum, imin, d->grid, d->signs); break;
   }
   HIP_OK(hipGetLastError());
@@ -626,7 +657,9 @@ int check_layer(const zm_moe_layer *L) {
   if (L->router_w && L->H % 4) return fail("router GEMV needs H %% 4 == 0");
   return 0;
 }
-int units_per_block(int t) { return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_IQ4_XS ? 2 : 1; }
+int units_per_block(int t) {
+  return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_IQ4_XS || t == T_IQ3_XXS ? 2 : 1;
+}
 
 DecFn find_decode(int tg, int td, int ts, int l1, int ir, int is) {
   if (DecFn f = find_decode_a(tg, td, ts, l1, ir, is)) return f;
@@ -729,8 +762,8 @@ int launch_fused(const zm_moe_layer *L, const float *x, const float *logits, int
   }
   a.act = w.f_act;
   a.sync = w.f_sync;
-  const bool iq4 = L->type_gate == T_IQ4_XS || L->type_down == T_IQ4_XS || (Fs && L->type_shared == T_IQ4_XS);
-  a.grid = iq4 ? d->iq4 : d->grid;
+  auto uses = [&](int t) { return L->type_gate == t || L->type_down == t || (Fs && L->type_shared == t); };
+  a.grid = uses(T_IQ4_XS) ? d->iq4 : (uses(T_IQ3_XXS) ? d->iq3 : d->grid);
   a.signs = d->signs;
   a.spin_limit = 1 << 23;
   if (const char *tr = getenv("ZEROMOE_TRACE"); tr && tr[0] == '1') {

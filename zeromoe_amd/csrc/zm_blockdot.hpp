@@ -23,14 +23,14 @@ namespace zm {
 
 template <int T>
 __host__ __device__ constexpr int unit_per_block() {
-  return T == T_Q4_K || T == T_Q5_K || T == T_Q6_K || T == T_IQ4_XS ? 2 : 1;
+  return T == T_Q4_K || T == T_Q5_K || T == T_Q6_K || T == T_IQ4_XS || T == T_IQ3_XXS ? 2 : 1;
 }
 
 // types with a whole-block unit (the fused decode kernel's dot)
 template <int T>
 __host__ __device__ constexpr bool has_unit() {
   return T == T_Q2_K || T == T_Q3_K || T == T_Q4_K || T == T_Q5_K || T == T_Q6_K || T == T_IQ2_XXS ||
-         T == T_IQ4_XS;
+         T == T_IQ3_XXS || T == T_IQ4_XS;
 }
 
 template <int T>
@@ -65,6 +65,12 @@ struct Unit<T_Q6_K> {  // half h: ql[64h, +64) | qh[32h, +32) | scales[8h, +8) |
   uint32_t qh[8];
   uint32_t sc[2];
   uint32_t d;
+};
+template <>
+struct Unit<T_IQ3_XXS> {  // d | half of the grid indices (4 sub-blocks) | their scale+sign words
+  uint32_t d;
+  uint32_t gi[8];
+  uint4 sas;
 };
 template <>
 struct Unit<T_IQ4_XS> {  // d, scales_h, scales_l | half of qs[128] (4 sub-blocks)
@@ -150,6 +156,10 @@ __device__ __forceinline__ void load_unit(rsrc_t r, int vo, int part, Unit<T> &u
     u.qh[1] = bld16(r, vo + 32, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) u.q[i] = bld16(r, vo + 48 + 64 * part + 16 * i, 0);
+  } else if constexpr (T == T_IQ3_XXS) {  // 98-byte blocks: the index region is loaded dword-aligned
+    u.d = bld2(r, vo, 0);
+    load_dwords_shifted<8>(r, vo + 2 + 32 * part, u.gi);
+    u.sas = bld16(r, vo + 66 + 16 * part, 0);  // ends the block: no shifted over-read past it
   } else if constexpr (T == T_IQ4_XS) {  // 136-byte blocks stay 8-byte aligned
     u.hdr = bld8(r, vo, 0);
 #pragma unroll
@@ -399,6 +409,34 @@ __device__ __forceinline__ void unit_ints(const Unit<T> (&w)[NW], int part, cons
       ri[n] = isum;
       rm[n] = imin;
     }
+  } else if constexpr (T == T_IQ3_XXS) {
+    // part p: sub-blocks 4p + i; group l of 8 weights takes grid entries from
+    // index bytes 2l, 2l + 1 of the sub-block and its 7-bit sign pattern
+    const uint32_t *g3 = reinterpret_cast<const uint32_t *>(lds_grid);
+#pragma unroll
+    for (int n = 0; n < NW; ++n) {
+      int isum = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ib = 4 * part + i;
+        const uint32_t aux = u4c(w[n].sas, i);
+        const uint4 xa = x.q[2 * ib], xb = x.q[2 * ib + 1];
+        const uint32_t xs[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+        int s = 0;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+          const uint32_t iw = w[n].gi[2 * i + (l >> 1)];
+          const uint32_t g1 = g3[(iw >> (16 * (l & 1))) & 0xffu], g2 = g3[(iw >> (16 * (l & 1) + 8)) & 0xffu];
+          const uint64_t m = lds_signs[(aux >> (7 * l)) & 127u];
+          const uint32_t mlo = (uint32_t)m, mhi = (uint32_t)(m >> 32);
+          s = dot4((g1 ^ mlo) + (mlo & 0x01010101u), xs[2 * l], s);
+          s = dot4((g2 ^ mhi) + (mhi & 0x01010101u), xs[2 * l + 1], s);
+        }
+        isum = mad24(2 * (int)(aux >> 28) + 1, s, isum);
+      }
+      ri[n] = isum;
+      rm[n] = 0;
+    }
   } else if constexpr (T == T_IQ4_XS) {
     // part p: sub-blocks 4p..4p+3, sub-block ib's 16 qs bytes in q[ib - 4p]: low
     // nibbles pair with activation chunk 2ib, high nibbles with 2ib + 1; the
@@ -507,6 +545,8 @@ __device__ __forceinline__ float unit_float(const Unit<T> &w, float xd, int isum
     return (xd * h2f((uint16_t)(w.d & 0xffffu))) * (float)isum;
   } else if constexpr (T == T_IQ4_XS) {
     return (xd * h2f((uint16_t)(w.hdr.x & 0xffffu))) * (float)isum;
+  } else if constexpr (T == T_IQ3_XXS) {
+    return 0.25f * ((xd * h2f((uint16_t)(w.d & 0xffffu))) * (float)isum);
   } else {
     return 0.125f * ((xd * h2f((uint16_t)(w.d & 0xffffu))) * (float)isum);
   }

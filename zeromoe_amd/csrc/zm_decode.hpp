@@ -137,9 +137,10 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   __shared__ float4 s_stage[DEC_WAVES][256];  // per wave: router scratch, then the act transpose
   constexpr bool kIQ2 = TG == T_IQ2_XXS || TD == T_IQ2_XXS || TS == T_IQ2_XXS;
   constexpr bool kIQ4 = TG == T_IQ4_XS || TD == T_IQ4_XS || TS == T_IQ4_XS;
-  static_assert(!(kIQ2 && kIQ4), "one lookup table per layer");
-  __shared__ uint64_t s_grid[kIQ2 ? 256 : (kIQ4 ? 2 : 1)];
-  __shared__ uint64_t s_signs[kIQ2 ? 128 : 1];
+  constexpr bool kIQ3 = TG == T_IQ3_XXS || TD == T_IQ3_XXS || TS == T_IQ3_XXS;
+  static_assert((int)kIQ2 + (int)kIQ3 + (int)kIQ4 <= 1, "one lookup table per layer");
+  __shared__ uint64_t s_grid[kIQ2 ? 256 : (kIQ3 ? 128 : (kIQ4 ? 2 : 1))];
+  __shared__ uint64_t s_signs[kIQ2 || kIQ3 ? 128 : 1];
   static_assert(IS == 0 || TS != 0, "shared iterations need a shared type");
   static_assert(L1 == 16 || L1 == 32, "lanes per routed gate/up row");
   constexpr int L2 = 32;  // lanes per down row (2 rows per wave step)
@@ -183,6 +184,9 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   }
   if constexpr (kIQ2) {
     for (int i = tid; i < 256; i += DEC_THREADS) s_grid[i] = a.grid[i];
+    for (int i = tid; i < 128; i += DEC_THREADS) s_signs[i] = a.signs[i];
+  } else if constexpr (kIQ3) {  // a.grid: the IQ3_XXS grid (256 x u32)
+    for (int i = tid; i < 128; i += DEC_THREADS) s_grid[i] = a.grid[i];
     for (int i = tid; i < 128; i += DEC_THREADS) s_signs[i] = a.signs[i];
   } else if constexpr (kIQ4) {  // a.grid: the IQ4_XS value table
     if (tid < 2) s_grid[tid] = a.grid[tid];

@@ -18,6 +18,8 @@
 //       and [64h+32+16qq, +16) (g = 1, 3), top two bits at bit 2g of qh bytes
 //       [32h+16qq, +16); 16-weight sub-blocks 8h + 2g + qq.
 //   IQ2_XXS quarter q: 32-weight sub-blocks 2q and 2q+1 (16 bytes of qs).
+//   IQ3_XXS quarter q: 32-weight sub-blocks 2q and 2q+1: grid indices at
+//       bytes [2 + 16q, +16), scale+sign words at [66 + 8q, +8).
 //   IQ4_XS quarter q: 32-weight sub-blocks 2q and 2q+1 = qs bytes [32q, +32)
 //       (byte j of a sub-block: low nibble weight j, high nibble weight 16 + j).
 // Block layouts: /root/reference/kernels/quant/kquant_matmul.cu:35-39,
@@ -44,13 +46,14 @@ enum : int {
   T_Q6_K = 14,
   T_Q8_K = 15,
   T_IQ2_XXS = 16,
+  T_IQ3_XXS = 18,
   T_IQ4_XS = 23,
   T_I32 = 26,
 };
 
 __host__ __device__ constexpr int block_bytes(int t) {
   return t == T_Q2_K ? 84 : t == T_Q3_K ? 110 : t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210
-       : t == T_IQ2_XXS ? 66 : t == T_IQ4_XS ? 136 : t == T_Q8_K ? 292 : 0;
+       : t == T_IQ2_XXS ? 66 : t == T_IQ3_XXS ? 98 : t == T_IQ4_XS ? 136 : t == T_Q8_K ? 292 : 0;
 }
 
 // ---------------------------------------------------------------- loads
@@ -349,6 +352,10 @@ __device__ __forceinline__ void load_w_slice(const uint8_t *blk, int q, WSlice &
     w.hh = ld16(blk + 32);
     w.a = ld16(blk + 48 + 32 * q);
     w.b = ld16(blk + 64 + 32 * q);
+  } else if constexpr (T == T_IQ3_XXS) {
+    w.f = ld2(blk);
+    w.a = ld16(blk + 2 + 16 * q);
+    w.e = ld8(blk + 66 + 8 * q);
   } else if constexpr (T == T_IQ4_XS) {
     w.e = ld8(blk);  // d | scales_h, scales_l
     w.a = ld16(blk + 8 + 32 * q);
@@ -411,6 +418,10 @@ __device__ __forceinline__ void load_w_slice_b(rsrc_t r, int vo, int so, int q, 
     w.hh = bld16(r, vo + 32, so);
     w.a = bld16(r, vo + 48 + 32 * q, so);
     w.b = bld16(r, vo + 64 + 32 * q, so);
+  } else if constexpr (T == T_IQ3_XXS) {
+    w.f = bld2(r, vo, so);
+    w.a = bld16(r, vo + 2 + 16 * q, so);
+    w.e = bld8(r, vo + 66 + 8 * q, so);
   } else if constexpr (T == T_IQ4_XS) {
     w.e = bld8(r, vo, so);
     w.a = bld16(r, vo + 8 + 32 * q, so);
@@ -541,6 +552,27 @@ __device__ __forceinline__ QInt quarter_int(const WSlice &w, int q, const Q8Slic
       dh = dot4(((u4_get(w.b, i) >> 4) & 0x0f0f0f0fu) | h5(w.hh, i, bh), u4_get(a.q[3], i), dh);
     r.isum = (int)sc0 * dl + (int)sc1 * dh;
     r.imin = (int)m0 * (a.bs[0] + a.bs[1]) + (int)m1 * (a.bs[2] + a.bs[3]);
+  } else if constexpr (T == T_IQ3_XXS) {
+    // lds_grid holds the 256 x u32 grid; sub-block 2q + sb: grid-index dwords
+    // 2sb, 2sb + 1 of a (two entries = 8 weights per group l), word e.x / e.y
+    const uint32_t *g3 = reinterpret_cast<const uint32_t *>(lds_grid);
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      const uint32_t aux = sb == 0 ? w.e.x : w.e.y;
+      const uint32_t i0 = u4_get(w.a, 2 * sb), i1 = u4_get(w.a, 2 * sb + 1);
+      int dsum = 0;
+#pragma unroll
+      for (int l = 0; l < 4; ++l) {
+        const uint32_t iw = l < 2 ? i0 : i1;
+        const uint32_t g1 = g3[(iw >> (16 * (l & 1))) & 0xffu], g2 = g3[(iw >> (16 * (l & 1) + 8)) & 0xffu];
+        const uint64_t m = lds_signs[(aux >> (7 * l)) & 127u];
+        const uint32_t mlo = (uint32_t)m, mhi = (uint32_t)(m >> 32);
+        const int qi = 2 * (4 * sb + l);  // dword index inside the 64 activations
+        dsum = dot4((g1 ^ mlo) + (mlo & 0x01010101u), u4_get(a.q[qi >> 2], qi & 3), dsum);
+        dsum = dot4((g2 ^ mhi) + (mhi & 0x01010101u), u4_get(a.q[(qi + 1) >> 2], (qi + 1) & 3), dsum);
+      }
+      r.isum += (2 * (int)(aux >> 28) + 1) * dsum;
+    }
   } else if constexpr (T == T_IQ4_XS) {
     // lds_grid holds the 16-byte value table; sub-block 2q: bytes of a (low
     // nibbles -> activations [0,16), high -> [16,32)), 2q + 1: bytes of b
@@ -616,6 +648,8 @@ __device__ __forceinline__ float quarter_dot(const WSlice &w, int q, const Q8Sli
     return (a.d * h2f((uint16_t)(w.f & 0xffffu))) * (float)r.isum;
   } else if constexpr (T == T_IQ4_XS) {
     return (a.d * h2f((uint16_t)(w.e.x & 0xffffu))) * (float)r.isum;
+  } else if constexpr (T == T_IQ3_XXS) {
+    return 0.25f * ((a.d * h2f((uint16_t)(w.f & 0xffffu))) * (float)r.isum);
   } else {
     const float d = h2f((uint16_t)(w.f & 0xffffu));
     return 0.125f * ((a.d * d) * (float)r.isum);

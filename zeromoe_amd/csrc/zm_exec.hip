@@ -17,7 +17,8 @@ using namespace zm;
 namespace {
 
 bool f32_type(int t) {
-  return t == T_Q2_K || t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_IQ2_XXS || t == T_IQ4_XS;
+  return t == T_Q2_K || t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_IQ2_XXS || t == T_IQ3_XXS ||
+         t == T_IQ4_XS;
 }
 
 template <int T>
@@ -33,7 +34,7 @@ void launch_mm_t(const F32MMArgs &a, int n_route, hipStream_t st) {
 
 // a validated F32MMArgs; n_route <= 65535, n_tok <= 65535 (* 4 without ids)
 int launch_mm(int type, F32MMArgs a, int n_route, hipStream_t st) {
-  if ((type == T_IQ2_XXS || type == T_IQ4_XS) && device_table(type, &a.grid)) return -1;
+  if ((type == T_IQ2_XXS || type == T_IQ3_XXS || type == T_IQ4_XS) && device_table(type, &a.grid)) return -1;
   switch (type) {
   case T_Q2_K: launch_mm_t<T_Q2_K>(a, n_route, st); break;
   case T_Q3_K: launch_mm_t<T_Q3_K>(a, n_route, st); break;
@@ -41,6 +42,7 @@ int launch_mm(int type, F32MMArgs a, int n_route, hipStream_t st) {
   case T_Q5_K: launch_mm_t<T_Q5_K>(a, n_route, st); break;
   case T_Q6_K: launch_mm_t<T_Q6_K>(a, n_route, st); break;
   case T_IQ4_XS: launch_mm_t<T_IQ4_XS>(a, n_route, st); break;
+  case T_IQ3_XXS: launch_mm_t<T_IQ3_XXS>(a, n_route, st); break;
   case T_IQ2_XXS: launch_mm_t<T_IQ2_XXS>(a, n_route, st); break;
   default: return fail("unsupported weight type %d", type);
   }
@@ -131,6 +133,12 @@ bool launch_q5_K_matmul_grouped(float *y, const float *x, const void *w, int gro
   a.n_tok = 1;
   a.mat_by_route = 1;
   return launch_mm(T_Q5_K, a, groups, nullptr) == 0;
+}
+void launch_iq3_xxs_matmul(float *y, const float *x, const void *w, int S, int I, int O) {
+  plain_matmul(T_IQ3_XXS, y, x, w, S, I, O, nullptr);
+}
+void launch_iq3_xxs_matmul_stream(float *y, const float *x, const void *w, int S, int I, int O, void *stream) {
+  plain_matmul(T_IQ3_XXS, y, x, w, S, I, O, (hipStream_t)stream);
 }
 void launch_iq4_xs_matmul(float *y, const float *x, const void *w, int S, int I, int O) {
   plain_matmul(T_IQ4_XS, y, x, w, S, I, O, nullptr);

@@ -23,6 +23,7 @@ namespace zm {
 // kernels/quant/iq2_matmul.cu:73-91): w = d*sc*q - dmin*m for Q2_K/Q4_K,
 // d*(sc-32)*(q - 4*!h) for Q3_K, d*sc*(q | h<<4) - dmin*m for Q5_K,
 // (d*(ls-32))*table[q] for IQ4_XS (kernels/quant/iq4xs_matmul.cu:80-99),
+// d*(0.5+s)*0.5*grid*sign for IQ3_XXS (kernels/quant/iq3_matmul.cu:104-122),
 // (d*sc)*(q6 - 32) for Q6_K (kquant_matmul.cu:94-147), d*(0.5+s)*0.25*grid*sign
 // for IQ2_XXS.
 __device__ __forceinline__ uint32_t byte_at(const uint8_t *p) { return *p; }
@@ -84,6 +85,21 @@ __device__ __forceinline__ float4 deq4(const uint8_t *blk, int lane, const uint6
     const float dl = h2f(ld2(blk + 208)) * (float)sc;
 #pragma unroll
     for (int i = 0; i < 4; ++i) w[i] = dl * (float)((int)((v >> (8 * i)) & 63) - 32);
+  } else if constexpr (T == T_IQ3_XXS) {
+    // weights 4*lane.. = sub-block ib, group l, half h: grid entry
+    // qs[8ib + 2l + h], signs ksigns[(u >> 7l) & 127] bits 4h..4h+3
+    const int ib = lane >> 3, l = (lane >> 1) & 3, h = lane & 1;
+    const uint32_t idx = byte_at(blk + 2 + 8 * ib + 2 * l + h);
+    const uint32_t u = ld4(blk + 66 + 4 * ib);
+    const float db = h2f(ld2(blk)) * (0.5f + (float)(u >> 28)) * 0.5f;
+    const uint32_t gv = reinterpret_cast<const uint32_t *>(s_grid)[idx];
+    const uint32_t si = (u >> (7 * l)) & 127;
+    const uint32_t signs = si | ((__builtin_popcount(si) & 1) << 7);  // ksigns_iq2xs
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v = db * (float)((gv >> (8 * i)) & 255);
+      w[i] = ((signs >> (4 * h + i)) & 1) ? -v : v;
+    }
   } else if constexpr (T == T_IQ4_XS) {
     // weights 4*lane.. = sub-block ib, positions j0..j0+3: low nibbles of qs
     // bytes 16ib + j0.. for j0 < 16, high nibbles of 16ib + j0 - 16.. otherwise
@@ -145,7 +161,7 @@ constexpr int F32_RPW = 4;
 template <int T, int NT>
 __global__ __launch_bounds__(256) void k_f32_mm(F32MMArgs a) {
   __shared__ float4 s_x[NT][F32_CH * 64];
-  __shared__ uint64_t s_grid[T == T_IQ2_XXS ? 256 : (T == T_IQ4_XS ? 2 : 1)];
+  __shared__ uint64_t s_grid[T == T_IQ2_XXS ? 256 : (T == T_IQ3_XXS ? 128 : (T == T_IQ4_XS ? 2 : 1))];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int route = blockIdx.z, t0 = blockIdx.y * NT;
   const int row0 = (blockIdx.x * 4 + wave) * F32_RPW;
@@ -162,6 +178,8 @@ __global__ __launch_bounds__(256) void k_f32_mm(F32MMArgs a) {
   }
   if constexpr (T == T_IQ2_XXS) {
     s_grid[threadIdx.x] = a.grid[threadIdx.x];
+  } else if constexpr (T == T_IQ3_XXS) {
+    if (threadIdx.x < 128) s_grid[threadIdx.x] = a.grid[threadIdx.x];
   } else if constexpr (T == T_IQ4_XS) {
     if (threadIdx.x < 2) s_grid[threadIdx.x] = a.grid[threadIdx.x];
   }

@@ -536,7 +536,7 @@ struct GemvArgs {
   float *out;
   size_t out_s, out_k;  // in floats
   int tile_rows;
-  const uint64_t *grid;   // IQ2_XXS grid / IQ4_XS value table (global), staged into LDS
+  const uint64_t *grid;   // IQ2_XXS / IQ3_XXS grid or IQ4_XS value table (global), staged into LDS
   const uint64_t *signs;
   // int8-MFMA path: (expert, first pair) work items of up to 32 pairs each
   const int32_t *items, *n_items;
@@ -545,10 +545,10 @@ struct GemvArgs {
 
 template <int T, int LPR, int ITER, int NP, bool GATEUP>
 static __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
-  __shared__ uint64_t s_grid[T == T_IQ2_XXS ? 256 : (T == T_IQ4_XS ? 2 : 1)];
-  __shared__ uint64_t s_signs[T == T_IQ2_XXS ? 128 : 1];
-  if constexpr (T == T_IQ2_XXS) {
-    for (int i = threadIdx.x; i < 256; i += 256) s_grid[i] = a.grid[i];
+  __shared__ uint64_t s_grid[T == T_IQ2_XXS ? 256 : (T == T_IQ3_XXS ? 128 : (T == T_IQ4_XS ? 2 : 1))];
+  __shared__ uint64_t s_signs[T == T_IQ2_XXS || T == T_IQ3_XXS ? 128 : 1];
+  if constexpr (T == T_IQ2_XXS || T == T_IQ3_XXS) {  // IQ3_XXS: 256 x u32 grid
+    for (int i = threadIdx.x; i < (T == T_IQ2_XXS ? 256 : 128); i += 256) s_grid[i] = a.grid[i];
     if (threadIdx.x < 128) s_signs[threadIdx.x] = a.signs[threadIdx.x];
     __syncthreads();
   } else if constexpr (T == T_IQ4_XS) {  // a.grid: the 16-byte value table

@@ -9,8 +9,8 @@ import torch
 
 from ._lib import ZmExpertScratch, ZmMoeLayer, ZmRouterSpec, ZmTensor, check, lib
 
-GGML_TYPES = {"f32": 0, "q2_K": 10, "q3_K": 11, "q4_K": 12, "q5_K": 13, "q6_K": 14, "q8_K": 15, "iq2_xxs": 16, "iq4_xs": 23, "i32": 26}
-BLOCK_BYTES = {10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 15: 292, 16: 66, 23: 136}
+GGML_TYPES = {"f32": 0, "q2_K": 10, "q3_K": 11, "q4_K": 12, "q5_K": 13, "q6_K": 14, "q8_K": 15, "iq2_xxs": 16, "iq3_xxs": 18, "iq4_xs": 23, "i32": 26}
+BLOCK_BYTES = {10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 15: 292, 16: 66, 18: 98, 23: 136}
 QK_K = 256
 GATING = {"softmax": 0, "sigmoid": 1, "sqrt_softplus": 2}
 
@@ -53,6 +53,24 @@ def set_iq4nl_table(table) -> None:
     if t.shape != (16,):
         raise ValueError("the IQ4_XS table has 16 entries")
     check(lib().zm_set_iq4nl_table(t.ctypes.data), "zm_set_iq4nl_table")
+
+
+def set_iq3xxs_grid(grid) -> None:
+    """Load the IQ3_XXS grid (256 uint32) for the current device."""
+    import numpy as np
+
+    g = np.ascontiguousarray(np.asarray(grid, np.uint32))
+    if g.shape != (256,):
+        raise ValueError("the IQ3_XXS grid has 256 entries")
+    check(lib().zm_set_iq3xxs_grid(g.ctypes.data), "zm_set_iq3xxs_grid")
+
+
+def builtin_iq3xxs_grid():
+    import numpy as np
+
+    g = np.zeros(256, np.uint32)
+    lib().zm_iq3xxs_builtin_grid(g.ctypes.data)
+    return g
 
 
 def builtin_iq4nl_table():
