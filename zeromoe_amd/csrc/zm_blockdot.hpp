@@ -13,8 +13,8 @@
 // Bit-plane trick (Q2_K, Q3_K): the 2-bit value of plane j is masked in place
 // (x & (3 << 2j) per byte), so v_dot4 yields 4^j times the plane's dot; the
 // sums are kept per plane and shifted back exactly at the end.  v_dot4 reads
-// signed bytes, so a field in bit 7 is first moved down one or two bits (plane
-// 3 is used as (x >> 2) & 0x30, scale 16; the Q3_K high bit 7 as bit 6).
+// signed bytes, so a field in bit 7 is first moved down (plane 3 is used as
+// (x >> 2) & 0x30, scale 16); Q3_K's high bit joins its plane as the bit above.
 #pragma once
 
 #include "zm_device.hpp"
@@ -267,17 +267,18 @@ __device__ __forceinline__ void unit_ints(const Unit<T> (&w)[NW], int part, cons
       rm[n] = imin;
     }
   } else if constexpr (T == T_Q3_K) {
-    // q3 = q2 - 4 * (hmask bit clear); hmask byte l (l = 4k + i) holds bit 4h + j of
-    // weight 128h + 32j + l.  Plane dots (scale 4^j) and cleared-bit dots (scale
-    // 2^(4h+j)) are kept apart and shifted back at the end.
-    int accq[NW][4], acch[NW][8];
+    // q3 = q2 + 4 * hbit - 4; hmask byte l (l = 4k + i) holds bit 4h + j of
+    // weight 128h + 32j + l.  Plane j is kept in place (bits 2j..2j+1, scale
+    // 4^j; plane 3 moved to bits 4-5, scale 16) with its high bit moved next to
+    // it (bit 2j + 2, or 6 for plane 3), so one v_dot4 per 4 weights gives
+    // 4^j * (q2 + 4 * hbit) . x; the -4 goes through the 16-weight bsums.
+    int accq[NW][4], soff[NW];
     uint32_t s4[NW][4];
 #pragma unroll
     for (int n = 0; n < NW; ++n) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) accq[n][j] = 0;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acch[n][j] = 0;
+      soff[n] = 0;
       // 6-bit scales as bytes (ggml's aux[] unpacking), xor 32: a 6-bit signed field is sc - 32
       const uint32_t a0 = w[n].sc[0], a1 = w[n].sc[1], a2 = w[n].sc[2];
       s4[n][0] = ((a0 & 0x0f0f0f0fu) | ((a2 & 0x03030303u) << 4)) ^ 0x20202020u;
@@ -285,46 +286,40 @@ __device__ __forceinline__ void unit_ints(const Unit<T> (&w)[NW], int part, cons
       s4[n][2] = (((a0 >> 4) & 0x0f0f0f0fu) | (((a2 >> 4) & 0x03030303u) << 4)) ^ 0x20202020u;
       s4[n][3] = (((a1 >> 4) & 0x0f0f0f0fu) | (((a2 >> 6) & 0x03030303u) << 4)) ^ 0x20202020u;
     }
+    const uint4 b0 = x.bs[0], b1 = x.bs[1];
+    const uint32_t bsw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        // plane j in place (scale 4^j; plane 3 at bits 4-5, scale 16); cleared high
-        // bit 4h+j in place (bit 7 moved to bit 6)
-        auto pl = [&](uint32_t b) { return j < 3 ? (b & (0x03030303u << (2 * j))) : ((b >> 2) & 0x30303030u); };
-        auto hb = [&](uint32_t b) {
-          return 4 * h + j < 7 ? (~b & (0x01010101u << (4 * h + j))) : ((~b >> 1) & 0x40404040u);
+        const int t = j < 3 ? 2 * j + 2 : 6, sft = t - (4 * h + j);
+        auto val = [&](uint32_t b, uint32_t m) {
+          const uint32_t pl = j < 3 ? (b & (0x03030303u << (2 * j))) : ((b >> 2) & 0x30303030u);
+          const uint32_t hs = sft >= 0 ? (m << sft) : (m >> -sft);
+          return pl | (hs & (0x01010101u << t));
         };
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           const uint4 xv = x.q[8 * h + 2 * j + kk];
           const int sb = 8 * h + 2 * j + kk;
+          const int bs = (int)(int16_t)(bsw[sb >> 1] >> (16 * (sb & 1)));
 #pragma unroll
           for (int n = 0; n < NW; ++n) {
             const uint4 q = w[n].q[2 * h + kk];
             const uint4 hm = w[n].hm[kk];
-            int sq = dot4(pl(q.x), xv.x, 0);
-            sq = dot4(pl(q.y), xv.y, sq);
-            sq = dot4(pl(q.z), xv.z, sq);
-            sq = dot4(pl(q.w), xv.w, sq);
-            int sh = dot4(hb(hm.x), xv.x, 0);
-            sh = dot4(hb(hm.y), xv.y, sh);
-            sh = dot4(hb(hm.z), xv.z, sh);
-            sh = dot4(hb(hm.w), xv.w, sh);
+            int sq = dot4(val(q.x, hm.x), xv.x, 0);
+            sq = dot4(val(q.y, hm.y), xv.y, sq);
+            sq = dot4(val(q.z, hm.z), xv.z, sq);
+            sq = dot4(val(q.w, hm.w), xv.w, sq);
             const int sc = __builtin_amdgcn_sbfe((int)s4[n][sb >> 2], 8 * (sb & 3), 6);
             accq[n][j] = mad24(sc, sq, accq[n][j]);
-            acch[n][4 * h + j] = mad24(sc, sh, acch[n][4 * h + j]);
+            soff[n] = mad24(sc, bs, soff[n]);
           }
         }
       }
 #pragma unroll
     for (int n = 0; n < NW; ++n) {
-      const int q = accq[n][0] + (accq[n][1] >> 2) + ((accq[n][2] + accq[n][3]) >> 4);
-      int hsum = 0;
-#pragma unroll
-      for (int i = 0; i < 7; ++i) hsum += acch[n][i] >> i;
-      hsum += acch[n][7] >> 6;
-      ri[n] = q - 4 * hsum;
+      ri[n] = accq[n][0] + (accq[n][1] >> 2) + ((accq[n][2] + accq[n][3]) >> 4) - 4 * soff[n];
       rm[n] = 0;
     }
   } else if constexpr (T == T_Q4_K) {
