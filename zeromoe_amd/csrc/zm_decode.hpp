@@ -21,9 +21,10 @@
 //       No grid-wide barrier: blocks finished early are quantized while the
 //       last gate/up rows are still being computed elsewhere.
 // Counters come in two sets used by alternate calls: an epoch word selects the
-// set; workgroup 0 zeroes the other set when it starts and, at its end, bumps
-// the epoch once every workgroup has arrived (all of them have read it by
-// then), so no workgroup waits on an atomic's return value.
+// set; the other set is zeroed at the end of the call (by the first and last
+// workgroups, off the critical path), and workgroup 0 bumps the epoch once
+// every workgroup has arrived (all of them have read it by then), so no
+// workgroup waits on an atomic's return value.
 // The hot loops are straight-line code: a lane or row without work loads and
 // stores through an out-of-range buffer offset (loads return zeros, stores are
 // dropped), so every load of a batch is issued unconditionally and the
@@ -153,15 +154,10 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   const size_t q8F = q8l_row_bytes(a.nbF);
   const size_t q8Fs = a.Fs > 0 ? q8l_row_bytes(a.nbFs) : 0;
   ZM_TRACE(0);
-  // arrival-counter set of this call; workgroup 0 clears the other set
+  // counter set of this call (the other set is cleared at the end, for the next call)
   const uint32_t epoch = __builtin_amdgcn_readfirstlane(ld_co(&a.sync[0]));
   uint32_t *const cnt = a.sync + DEC_CNT_STRIDE * (1 + DEC_NCNT * (int)(epoch & 1u));
   uint32_t *const bcnt = a.sync + DEC_BLK_BASE + DEC_BCNT_STRIDE * DEC_MAX_ABLK * (int)(epoch & 1u);
-  if (g == 0) {
-    if (tid < DEC_NCNT) st_co(a.sync + DEC_CNT_STRIDE * (1 + DEC_NCNT * (int)((epoch + 1u) & 1u) + tid), 0u);
-    uint32_t *const other = a.sync + DEC_BLK_BASE + DEC_BCNT_STRIDE * DEC_MAX_ABLK * (int)((epoch + 1u) & 1u);
-    for (int i = tid; i < DEC_MAX_ABLK; i += DEC_THREADS) st_co(other + DEC_BCNT_STRIDE * i, 0u);
-  }
 
   // ---------------------------------------------------------------- P0: route, quantize x
   // Wave w < S routes token w (its loads go out first); the other waves
@@ -531,6 +527,16 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     }
   }
   ZM_TRACE(5);
+  // clear the other counter set for the next call: its last users were the
+  // previous call's workgroups, all finished.  Done here, off the critical
+  // path: at the start these stores sat in the memory counter ahead of the
+  // router's loads and delayed workgroup 0 by ~2 us.
+  {
+    uint32_t *const other = a.sync + DEC_BLK_BASE + DEC_BCNT_STRIDE * DEC_MAX_ABLK * (int)((epoch + 1u) & 1u);
+    for (int i = g * DEC_THREADS + tid; i < DEC_MAX_ABLK; i += G * DEC_THREADS) st_co(other + DEC_BCNT_STRIDE * i, 0u);
+    if (g == G - 1 && tid < DEC_NCNT)
+      st_co(a.sync + DEC_CNT_STRIDE * (1 + DEC_NCNT * (int)((epoch + 1u) & 1u) + tid), 0u);
+  }
   // workgroup 0 retires the epoch once every workgroup has arrived (each read
   // the epoch before arriving); after an expired wait the epoch stays (the host
   // resets the sync words)
