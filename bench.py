@@ -46,6 +46,7 @@ CONFIGS["c3_q6k"] = dict(CONFIGS["c3"], td=Q6)
 CONFIGS["iq4xs"] = dict(CONFIGS["c2"], tg=IQ4X, td=IQ4X)
 CONFIGS["c3_iq4xs"] = dict(CONFIGS["c3"], tg=IQ4X, td=IQ4X)
 CONFIGS["iq3xxs"] = dict(CONFIGS["c2"], tg=IQ3X, td=IQ3X)
+CONFIGS["c3_iq2xxs"] = dict(CONFIGS["c3"], tg=IQ2, td=IQ2)
 WORKLOAD = {
     "c1": "decode S=1, H=2048 F=768 E=128 top-8 softmax, Q4_K",
     "c2": "decode S=1, H=4096 F=1536 E=128 top-8 softmax, gate/up Q2_K, down Q3_K",
@@ -53,6 +54,7 @@ WORKLOAD = {
     "c4": "small batch S=4, H=5120 F=1536 E=160 top-8 softmax, IQ2_XXS",
     "c5": "full block S=1, H=7168 F=2048, 256 routed Q2_K (96 resident slots) + shared Q4_K, sigmoid 8 groups/top-4",
     "iq4xs": "decode S=1 at c2's shape with IQ4_XS gate/up/down",
+    "c3_iq2xxs": "prefill S=512 at c3's shape and routing with IQ2_XXS gate/up/down (stand-in grid)",
     "iq3xxs": "decode S=1 at c2's shape with IQ3_XXS gate/up/down (stand-in grid)",
     "c3_iq4xs": "prefill S=512 at c3's shape and routing with IQ4_XS gate/up/down",
     "c3_q6k": "prefill S=512 at c3's shape and routing with a Q6_K down projection (mixed-type layer)",
@@ -382,7 +384,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--replicas", type=int, default=0, help="layer replicas (0 = enough to exceed the MALL)")
-    ap.add_argument("--extras", default="c1,c3,c4,c5,c5_s64,q4k_q6k,c3_q6k,iq4xs,c3_iq4xs,iq3xxs", help="extra configs to report ('' for none)")
+    ap.add_argument("--extras", default="c1,c3,c4,c5,c5_s64,q4k_q6k,c3_q6k,iq4xs,c3_iq4xs,iq3xxs,c3_iq2xxs", help="extra configs to report ('' for none)")
     ap.add_argument("--no-unpack", dest="unpack", action="store_false",
                     help="skip the expert-record unpack extra")
     ap.add_argument("--no-cpu", action="store_true")
@@ -437,7 +439,7 @@ def main():
     traffic = committed_traffic()
     extras = {}
     for name in [n for n in args.extras.split(",") if n]:
-        st = max(10, args.steps // 4) if name in ("c3", "c5_s64", "c3_q6k", "c3_iq4xs") else args.steps
+        st = max(10, args.steps // 4) if name in ("c3", "c5_s64", "c3_q6k", "c3_iq4xs", "c3_iq2xxs") else args.steps
         r = run_config(torch, Z, name, st, max(3, args.warmup // 2), reps(name), use_graph=not args.eager)
         extras[name] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}
         extras[name]["workload"] = WORKLOAD[name]

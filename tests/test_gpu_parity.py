@@ -118,7 +118,7 @@ def test_mul_mat_id_skewed_prefill_buckets():
     np.testing.assert_allclose(got, ref, rtol=1e-3, atol=1e-3 * np.abs(ref).max())
 
 
-@pytest.mark.parametrize("t", [Q4, Q2, Q5, Q6, IQ4])
+@pytest.mark.parametrize("t", [Q4, Q2, Q5, Q6, IQ4, IQ2, IQ3])
 @pytest.mark.parametrize("ne11", [1, 8])
 def test_mul_mat_id_mfma_buckets_per_element(ne11, t):
     """Buckets of 64-80 pairs take the int8-MFMA path for Q4_K, Q2_K, Q5_K and Q6_K: every
@@ -380,6 +380,8 @@ PREFILL_CASES = {
     "q6k_q6k_mmq": (CONFIGS["c3"], dict(tg=Q6, td=Q6, S=128, H=1024, F=768, E=16)),
     "q5k_q6k_mmq": (CONFIGS["c3"], dict(tg=Q5, td=Q6, S=256, H=1024, F=512, E=16)),
     "iq4xs_mmq": (CONFIGS["c3"], dict(tg=IQ4, td=IQ4, S=256, H=1024, F=512, E=16)),
+    "iq2xxs_mmq": (CONFIGS["c3"], dict(tg=IQ2, td=IQ2, S=256, H=1024, F=512, E=16)),
+    "iq3xxs_mmq": (CONFIGS["c3"], dict(tg=IQ3, td=IQ3, S=256, H=1024, F=512, E=16)),
 }
 
 

@@ -229,12 +229,14 @@ int launch_gemv(int type, bool gateup, int np, const GemvArgs &a0, int n_groups,
   return 0;
 }
 
-// MFMA path for prefill-sized buckets: Q4_K, Q5_K, Q6_K and IQ4_XS weights with at least 8
+// MFMA path for prefill-sized buckets: Q4_K, Q5_K, Q6_K, IQ2_XXS, IQ3_XXS and IQ4_XS weights with at least 8
 // pairs per active expert on average, Q2_K weights with at least 2.  a.items / a.n_items (or a.dense_S) must be set;
 // max_items bounds *a.n_items.  Returns 1 when the path does not apply (the
 // caller takes the GEMV path).
 bool mmq_applies(int type, double avg_pairs) {
-  return (((type == T_Q4_K || type == T_Q5_K || type == T_Q6_K || type == T_IQ4_XS) && avg_pairs >= 8.0) ||
+  return (((type == T_Q4_K || type == T_Q5_K || type == T_Q6_K || type == T_IQ4_XS || type == T_IQ2_XXS ||
+            type == T_IQ3_XXS) &&
+           avg_pairs >= 8.0) ||
           (type == T_Q2_K && avg_pairs >= 2.0)) &&
          !getenv_flag_off("ZEROMOE_MMQ");
 }
@@ -260,11 +262,19 @@ int launch_mmq(int type, bool gateup, const GemvArgs &a, int max_items, double a
   } else if (type == T_Q5_K) {
     if (tt == 4) launch_mmq_t<T_Q5_K, 4>(gateup, grid, a, st);
     else launch_mmq_t<T_Q5_K, 2>(gateup, grid, a, st);
-  } else if (type == T_IQ4_XS) {
+  } else if (type == T_IQ4_XS || type == T_IQ3_XXS || type == T_IQ2_XXS) {
     GemvArgs b = a;
-    if (device_table(T_IQ4_XS, &b.grid)) return -1;
-    if (tt == 4) launch_mmq_t<T_IQ4_XS, 4>(gateup, grid, b, st);
-    else launch_mmq_t<T_IQ4_XS, 2>(gateup, grid, b, st);
+    if (device_table(type, &b.grid)) return -1;
+    if (type == T_IQ4_XS) {
+      if (tt == 4) launch_mmq_t<T_IQ4_XS, 4>(gateup, grid, b, st);
+      else launch_mmq_t<T_IQ4_XS, 2>(gateup, grid, b, st);
+    } else if (type == T_IQ3_XXS) {
+      if (tt == 4) launch_mmq_t<T_IQ3_XXS, 4>(gateup, grid, b, st);
+      else launch_mmq_t<T_IQ3_XXS, 2>(gateup, grid, b, st);
+    } else {
+      if (tt == 4) launch_mmq_t<T_IQ2_XXS, 4>(gateup, grid, b, st);
+      else launch_mmq_t<T_IQ2_XXS, 2>(gateup, grid, b, st);
+    }
   } else if (type == T_Q6_K) {
     if (tt == 4) launch_mmq_t<T_Q6_K, 4>(gateup, grid, a, st);
     else launch_mmq_t<T_Q6_K, 2>(gateup, grid, a, st);

@@ -22,6 +22,11 @@
 // block for all MMQ_TT token tiles of the work item.
 // No dequantized weight copy is materialized.
 //
+// IQ2_XXS / IQ3_XXS (grid values up to 43 / 62 with per-8-weight signs, and a
+// (2 ls + 1) <= 31 scale per 32-weight sub-block) take the same per-sub-block
+// route as IQ4_XS: signed grid bytes from the LDS-staged grid and sign masks,
+// two half-masked MFMAs per chunk, scales per lane.
+//
 // IQ4_XS (a 16-entry value table, up to |127|, and a 6-bit signed scale per
 // 32-weight sub-block) dots each 64-weight chunk as its two sub-blocks on
 // v_mfma_i32_16x16x64_i8 with half of B zeroed, values looked up from the
@@ -128,6 +133,17 @@ struct MmqW<T_Q2_K> {  // scales | this lane's 2 x 16 bytes of qs | d, dmin
   uint32_t dd;
 };
 template <>
+struct MmqW<T_IQ2_XXS> {  // d | all 64 bytes of qs (grid-index and sign+scale words per sub-block)
+  uint32_t d;
+  uint4 q[4];
+};
+template <>
+struct MmqW<T_IQ3_XXS> {  // d | 64 grid-index bytes | 8 scale+sign words
+  uint32_t d;
+  uint4 gi[4];
+  uint4 sas[2];
+};
+template <>
 struct MmqW<T_IQ4_XS> {  // d, scales_h, scales_l | this lane's 16 qs bytes of each chunk
   uint2 hdr;
   uint4 qs[4];
@@ -143,7 +159,12 @@ struct MmqW<T_Q6_K> {  // this lane's 4 x 8 bytes of ql, 2 x 8 bytes of qh | sca
 template <int T, bool GATEUP, int TT>
 __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
   constexpr int TOK = 16 * TT;  // pairs per work item
-  static_assert(T == T_Q4_K || T == T_Q5_K || T == T_Q2_K || T == T_Q6_K || T == T_IQ4_XS, "MFMA prefill types");
+  static_assert(T == T_Q4_K || T == T_Q5_K || T == T_Q2_K || T == T_Q6_K || T == T_IQ4_XS || T == T_IQ2_XXS ||
+                    T == T_IQ3_XXS,
+                "MFMA prefill types");
+  constexpr bool kGrid = T == T_IQ2_XXS || T == T_IQ3_XXS;
+  __shared__ uint64_t s_grid[kGrid ? (T == T_IQ2_XXS ? 256 : 128) : 1];  // IQ3_XXS: 256 x u32
+  __shared__ uint64_t s_signs[kGrid ? 128 : 1];
   constexpr bool K45 = T == T_Q4_K || T == T_Q5_K;
   constexpr int NBS = K45 ? 8 : 16;  // bsums per block used: 32-sums (Q4_K, Q5_K) or 16-sums (Q2_K, Q6_K)
   __shared__ __attribute__((aligned(16))) uint8_t s_xq[2][TOK][MMQ_XS];
@@ -188,6 +209,10 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
     }
   }
 
+  if constexpr (kGrid) {
+    for (int i = tid; i < (T == T_IQ2_XXS ? 256 : 128); i += 256) s_grid[i] = a.grid[i];
+    if (tid < 128) s_signs[tid] = a.signs[tid];
+  }
   if (tid < TOK) {
     const int p = pc + tid;
     const bool ok = p < p1;
@@ -211,6 +236,16 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
         w[m].qh = bld16(rw[m], vo + 16 + 16 * (g & 1), 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) w[m].qs[i] = bld16(rw[m], vo + 48 + 32 * i + 16 * (g & 1), 0);
+      } else if constexpr (T == T_IQ2_XXS) {
+        w[m].d = bld2(rw[m], vo, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[m].q[i] = bld16(rw[m], vo + 2 + 16 * i, 0);
+      } else if constexpr (T == T_IQ3_XXS) {
+        w[m].d = bld2(rw[m], vo, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[m].gi[i] = bld16(rw[m], vo + 2 + 16 * i, 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) w[m].sas[i] = bld16(rw[m], vo + 66 + 16 * i, 0);
       } else if constexpr (T == T_IQ4_XS) {
         w[m].hdr = bld8(rw[m], vo, 0);
 #pragma unroll
@@ -352,6 +387,81 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           f[m][t][j] += s_xd[buf][16 * t + 4 * g + j] * (d * (float)(dlo[j] + 8 * dhi[j] + 16 * d5[j]) - dmin * mn[j]);
+      }
+    }
+    } else if constexpr (kGrid) {
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      // chunk c = sub-blocks 2c (lane groups 0-1) and 2c + 1 (groups 2-3); group
+      // g holds weights 16(g & 1) .. +15 of its sub-block = the two 8-weight
+      // groups l = 2(g & 1), 2(g & 1) + 1: grid values with their signs applied
+      // (conditional byte negate), the other sub-block's half of B zeroed;
+      // scales (2 ls + 1) per lane afterwards, the 1/8 (IQ2_XXS) or 1/4
+      // (IQ3_XXS) folded into d
+      constexpr float kf = T == T_IQ2_XXS ? 0.125f : 0.25f;
+      const float d = kf * h2f((uint16_t)(wcur[m].d & 0xffffu));
+      const uint32_t keep0 = g < 2 ? 0xffffffffu : 0u;
+      const int hl = g & 1;
+      v4i_t b0[4], b1[4];
+      int s0[4], s1[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int ib = 2 * c + (g >> 1);
+        uint32_t v[4];
+        if constexpr (T == T_IQ2_XXS) {
+          // sub-block ib: words 2ib (grid indices), 2ib + 1 (signs, scale)
+          const uint32_t aux0 = u4_get(wcur[m].q[ib >> 1], 2 * (ib & 1)), aux1 = u4_get(wcur[m].q[ib >> 1], 2 * (ib & 1) + 1);
+#pragma unroll
+          for (int li = 0; li < 2; ++li) {
+            const int l = 2 * hl + li;
+            const uint64_t gg = s_grid[(aux0 >> (8 * l)) & 0xffu];
+            const uint64_t mm = s_signs[(aux1 >> (7 * l)) & 127u];
+            const uint32_t glo = (uint32_t)gg, ghi = (uint32_t)(gg >> 32), mlo = (uint32_t)mm, mhi = (uint32_t)(mm >> 32);
+            v[2 * li] = (glo ^ mlo) + (mlo & 0x01010101u);
+            v[2 * li + 1] = (ghi ^ mhi) + (mhi & 0x01010101u);
+          }
+          const uint32_t a0 = u4_get(wcur[m].q[c], 1), a1 = u4_get(wcur[m].q[c], 3);  // sub-blocks 2c, 2c + 1
+          s0[c] = 2 * (int)(a0 >> 28) + 1;
+          s1[c] = 2 * (int)(a1 >> 28) + 1;
+        } else {
+          // sub-block ib: grid-index bytes 8ib .. +7 (two per 8-weight group), word ib
+          const uint32_t iw = u4_get(wcur[m].gi[ib >> 1], 2 * (ib & 1) + hl);
+          const uint32_t aux = u4_get(wcur[m].sas[ib >> 2], ib & 3);
+          const uint32_t *g3 = reinterpret_cast<const uint32_t *>(s_grid);
+#pragma unroll
+          for (int li = 0; li < 2; ++li) {
+            const int l = 2 * hl + li;
+            const uint32_t g1 = g3[(iw >> (16 * li)) & 0xffu], g2 = g3[(iw >> (16 * li + 8)) & 0xffu];
+            const uint64_t mm = s_signs[(aux >> (7 * l)) & 127u];
+            const uint32_t mlo = (uint32_t)mm, mhi = (uint32_t)(mm >> 32);
+            v[2 * li] = (g1 ^ mlo) + (mlo & 0x01010101u);
+            v[2 * li + 1] = (g2 ^ mhi) + (mhi & 0x01010101u);
+          }
+          s0[c] = 2 * (int)(u4_get(wcur[m].sas[c >> 1], 2 * (c & 1)) >> 28) + 1;
+          s1[c] = 2 * (int)(u4_get(wcur[m].sas[c >> 1], 2 * (c & 1) + 1) >> 28) + 1;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          b0[c][k] = (int)(v[k] & keep0);
+          b1[c][k] = (int)(v[k] & ~keep0);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        if (t >= nt) continue;
+        const uint8_t *xr = &s_xq[buf][16 * t + n][0];
+        int isum[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const v4i_t xa = *reinterpret_cast<const v4i_t *>(xr + 64 * c + 16 * g);
+          const v4i_t z = {0, 0, 0, 0};
+          const v4i_t d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, b0[c], z, 0, 0, 0);
+          const v4i_t d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, b1[c], z, 0, 0, 0);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) isum[j] = __mul24(s0[c], d0[j]) + __mul24(s1[c], d1[j]) + isum[j];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) f[m][t][j] += s_xd[buf][16 * t + 4 * g + j] * (d * (float)isum[j]);
       }
     }
     } else if constexpr (T == T_IQ4_XS) {
