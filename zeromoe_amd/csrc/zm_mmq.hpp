@@ -336,36 +336,43 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
     const int buf = b & 1;
     load_w(b + 1, wnxt);
     if constexpr (K45) {
-#pragma unroll
-    for (int m = 0; m < NM; ++m) {
-      const uint32_t u0 = wcur[m].hdr.y, u1 = wcur[m].hdr.z, u2 = wcur[m].hdr.w;
-      const uint32_t sc_lo = u0 & 0x3f3f3f3fu, mn_lo = u1 & 0x3f3f3f3fu;
-      const uint32_t sc_hi = (u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4);
-      const uint32_t mn_hi = ((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4);
-      const float d = h2f((uint16_t)(wcur[m].hdr.x & 0xffffu)), dmin = h2f((uint16_t)(wcur[m].hdr.x >> 16));
-      // B operand of the min product: m[row][sb] for sb = g and g + 4
-      const float mb0 = (float)((mn_lo >> (8 * g)) & 0xffu), mb1 = (float)((mn_hi >> (8 * g)) & 0xffu);
-      // scale-folded weights of the 4 chunks: lane's sub-block 2i + (g >> 1),
-      // sc = 8 * hi + lo
-      // Q5_K: the fifth bit (bit 2i + (g >> 1) of the lane's qh bytes) is a third
-      // chain with the whole scale, isum = D_lo + 8 * D_hi + 16 * D_5
-      v4i_t bl[4], bh[4], b5[K45 && T == T_Q5_K ? 4 : 1];
+      // both matrices' operands first, then one pass over the token tiles: the
+      // activation operand (and the bsums of the min product) is read from LDS
+      // once per tile for gate and up together
+      constexpr int N5 = T == T_Q5_K ? 4 : 1;
+      v4i_t bl[NM][4], bh[NM][4], b5[NM][N5];
+      float dd[NM], dm[NM], mb0[NM], mb1[NM];
       const int hs = 8 * (g >> 1), ns = 4 * (g >> 1);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t scw = i < 2 ? sc_lo : sc_hi;
-        const uint32_t sc = (scw >> (16 * (i & 1) + hs)) & 0xffu;
-        const uint32_t lo = sc & 7u, hi = sc >> 3;
-        const uint4 q = wcur[m].qs[i];
-        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+      for (int m = 0; m < NM; ++m) {
+        const uint32_t u0 = wcur[m].hdr.y, u1 = wcur[m].hdr.z, u2 = wcur[m].hdr.w;
+        const uint32_t sc_lo = u0 & 0x3f3f3f3fu, mn_lo = u1 & 0x3f3f3f3fu;
+        const uint32_t sc_hi = (u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4);
+        const uint32_t mn_hi = ((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4);
+        dd[m] = h2f((uint16_t)(wcur[m].hdr.x & 0xffffu));
+        dm[m] = h2f((uint16_t)(wcur[m].hdr.x >> 16));
+        // B operand of the min product: m[row][sb] for sb = g and g + 4
+        mb0[m] = (float)((mn_lo >> (8 * g)) & 0xffu);
+        mb1[m] = (float)((mn_hi >> (8 * g)) & 0xffu);
+        // scale-folded weights of the 4 chunks: lane's sub-block 2i + (g >> 1),
+        // sc = 8 * hi + lo; Q5_K: the fifth bit (bit 2i + (g >> 1) of the lane's
+        // qh bytes) is a third chain with the whole scale, isum = D_lo + 8 D_hi + 16 D_5
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const uint32_t nib = (qw[c] >> ns) & 0x0f0f0f0fu;
-          bl[i][c] = (int)mul_bytes(nib, lo);
-          bh[i][c] = (int)mul_bytes(nib, hi);
-          if constexpr (T == T_Q5_K) {
-            const uint32_t hq[4] = {wcur[m].qh.x, wcur[m].qh.y, wcur[m].qh.z, wcur[m].qh.w};
-            b5[i][c] = (int)mul_bytes((hq[c] >> (2 * i + (g >> 1))) & 0x01010101u, sc);
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t scw = i < 2 ? sc_lo : sc_hi;
+          const uint32_t sc = (scw >> (16 * (i & 1) + hs)) & 0xffu;
+          const uint32_t lo = sc & 7u, hi = sc >> 3;
+          const uint4 q = wcur[m].qs[i];
+          const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const uint32_t nib = (qw[c] >> ns) & 0x0f0f0f0fu;
+            bl[m][i][c] = (int)mul_bytes(nib, lo);
+            bh[m][i][c] = (int)mul_bytes(nib, hi);
+            if constexpr (T == T_Q5_K) {
+              const uint32_t hq[4] = {wcur[m].qh.x, wcur[m].qh.y, wcur[m].qh.z, wcur[m].qh.w};
+              b5[m][i][c] = (int)mul_bytes((hq[c] >> (2 * i + (g >> 1))) & 0x01010101u, sc);
+            }
           }
         }
       }
@@ -373,22 +380,30 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
       for (int t = 0; t < TT; ++t) {
         if (t >= nt) continue;
         const uint8_t *xr = &s_xq[buf][16 * t + n][0];
-        v4i_t dlo = {0, 0, 0, 0}, dhi = {0, 0, 0, 0}, d5 = {0, 0, 0, 0};
+        v4i_t xa[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const v4i_t xa = *reinterpret_cast<const v4i_t *>(xr + 64 * i + 16 * g);
-          dlo = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, bl[i], dlo, 0, 0, 0);
-          dhi = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, bh[i], dhi, 0, 0, 0);
-          if constexpr (T == T_Q5_K) d5 = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, b5[i], d5, 0, 0, 0);
+        for (int i = 0; i < 4; ++i) xa[i] = *reinterpret_cast<const v4i_t *>(xr + 64 * i + 16 * g);
+        const float bs0 = (float)s_bs[buf][16 * t + n][g], bs1 = (float)s_bs[buf][16 * t + n][g + 4];
+        float xdj[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xdj[j] = s_xd[buf][16 * t + 4 * g + j];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          v4i_t dlo = {0, 0, 0, 0}, dhi = {0, 0, 0, 0}, d5 = {0, 0, 0, 0};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            dlo = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[i], bl[m][i], dlo, 0, 0, 0);
+            dhi = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[i], bh[m][i], dhi, 0, 0, 0);
+            if constexpr (T == T_Q5_K) d5 = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[i], b5[m][i], d5, 0, 0, 0);
+          }
+          v4f_t mn = {0.f, 0.f, 0.f, 0.f};
+          mn = __builtin_amdgcn_mfma_f32_16x16x4f32(bs0, mb0[m], mn, 0, 0, 0);
+          mn = __builtin_amdgcn_mfma_f32_16x16x4f32(bs1, mb1[m], mn, 0, 0, 0);
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            f[m][t][j] += xdj[j] * (dd[m] * (float)(dlo[j] + 8 * dhi[j] + 16 * d5[j]) - dm[m] * mn[j]);
         }
-        v4f_t mn = {0.f, 0.f, 0.f, 0.f};
-        mn = __builtin_amdgcn_mfma_f32_16x16x4f32((float)s_bs[buf][16 * t + n][g], mb0, mn, 0, 0, 0);
-        mn = __builtin_amdgcn_mfma_f32_16x16x4f32((float)s_bs[buf][16 * t + n][g + 4], mb1, mn, 0, 0, 0);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          f[m][t][j] += s_xd[buf][16 * t + 4 * g + j] * (d * (float)(dlo[j] + 8 * dhi[j] + 16 * d5[j]) - dmin * mn[j]);
       }
-    }
     } else if constexpr (kGrid) {
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
