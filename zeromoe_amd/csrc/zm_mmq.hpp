@@ -574,47 +574,56 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
       }
     }
     } else {
+      // Q2_K: both matrices' operands first, then one pass over the token tiles
+      // (the activation tile and its bsums read once for gate and up)
+      v4i_t bq[NM][4];
+      float dd[NM], dm[NM], mb[NM][4];
 #pragma unroll
-    for (int m = 0; m < NM; ++m) {
-      const float d = h2f((uint16_t)(wcur[m].dd & 0xffffu)), dmin = h2f((uint16_t)(wcur[m].dd >> 16));
-      const uint32_t scb[4] = {wcur[m].sc.x, wcur[m].sc.y, wcur[m].sc.z, wcur[m].sc.w};
-      // B operand of the min product: m[row][sb] for sb = 4i + g
-      float mb[4];
+      for (int m = 0; m < NM; ++m) {
+        dd[m] = h2f((uint16_t)(wcur[m].dd & 0xffffu));
+        dm[m] = h2f((uint16_t)(wcur[m].dd >> 16));
+        const uint32_t scb[4] = {wcur[m].sc.x, wcur[m].sc.y, wcur[m].sc.z, wcur[m].sc.w};
+        // B operand of the min product: m[row][sb] for sb = 4i + g
 #pragma unroll
-      for (int i = 0; i < 4; ++i) mb[i] = (float)((scb[i] >> (8 * g + 4)) & 15u);
-      // scale-folded weights of the 4 chunks c = 2h + jp: plane j = 2jp + (g >> 1),
-      // sub-block 8h + 2j + (g & 1)
-      v4i_t bq[4];
+        for (int i = 0; i < 4; ++i) mb[m][i] = (float)((scb[i] >> (8 * g + 4)) & 15u);
+        // scale-folded weights of the 4 chunks c = 2h + jp: plane j = 2jp + (g >> 1),
+        // sub-block 8h + 2j + (g & 1)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int h = c >> 1, jp = c & 1;
-        const int j = 2 * jp + (g >> 1);
-        const int sb = 8 * h + 2 * j + (g & 1);
-        const uint32_t sc = (scb[sb >> 2] >> (8 * (sb & 3))) & 15u;
-        const uint4 q = wcur[m].qs[h];
-        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+        for (int c = 0; c < 4; ++c) {
+          const int h = c >> 1, jp = c & 1;
+          const int j = 2 * jp + (g >> 1);
+          const int sb = 8 * h + 2 * j + (g & 1);
+          const uint32_t sc = (scb[sb >> 2] >> (8 * (sb & 3))) & 15u;
+          const uint4 q = wcur[m].qs[h];
+          const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-        for (int k = 0; k < 4; ++k) bq[c][k] = (int)mul_bytes((qw[k] >> (2 * j)) & 0x03030303u, sc);
+          for (int k = 0; k < 4; ++k) bq[m][c][k] = (int)mul_bytes((qw[k] >> (2 * j)) & 0x03030303u, sc);
+        }
       }
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
         if (t >= nt) continue;
         const uint8_t *xr = &s_xq[buf][16 * t + n][0];
-        v4i_t isum = {0, 0, 0, 0};
+        v4i_t xa[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const v4i_t xa = *reinterpret_cast<const v4i_t *>(xr + 64 * c + 16 * g);
-          isum = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, bq[c], isum, 0, 0, 0);
+        for (int c = 0; c < 4; ++c) xa[c] = *reinterpret_cast<const v4i_t *>(xr + 64 * c + 16 * g);
+        float bs[4], xdj[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bs[i] = (float)s_bs[buf][16 * t + n][4 * i + g];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xdj[j] = s_xd[buf][16 * t + 4 * g + j];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          v4i_t isum = {0, 0, 0, 0};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) isum = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[c], bq[m][c], isum, 0, 0, 0);
+          v4f_t mn = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mn = __builtin_amdgcn_mfma_f32_16x16x4f32(bs[i], mb[m][i], mn, 0, 0, 0);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) f[m][t][j] += xdj[j] * (dd[m] * (float)isum[j] - dm[m] * mn[j]);
         }
-        v4f_t mn = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          mn = __builtin_amdgcn_mfma_f32_16x16x4f32((float)s_bs[buf][16 * t + n][4 * i + g], mb[i], mn, 0, 0, 0);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          f[m][t][j] += s_xd[buf][16 * t + 4 * g + j] * (d * (float)isum[j] - dmin * mn[j]);
       }
-    }
     }
     // block b+1 into the other buffer (its readers finished at the last barrier),
     // then request block b+2
