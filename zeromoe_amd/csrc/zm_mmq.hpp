@@ -405,6 +405,9 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
         }
       }
     } else if constexpr (kGrid) {
+      v4i_t B0[NM][4], B1[NM][4];
+      int S0[NM][4], S1[NM][4];
+      float DD[NM];
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
       // chunk c = sub-blocks 2c (lane groups 0-1) and 2c + 1 (groups 2-3); group
@@ -414,11 +417,9 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
       // scales (2 ls + 1) per lane afterwards, the 1/8 (IQ2_XXS) or 1/4
       // (IQ3_XXS) folded into d
       constexpr float kf = T == T_IQ2_XXS ? 0.125f : 0.25f;
-      const float d = kf * h2f((uint16_t)(wcur[m].d & 0xffffu));
+      DD[m] = kf * h2f((uint16_t)(wcur[m].d & 0xffffu));
       const uint32_t keep0 = g < 2 ? 0xffffffffu : 0u;
       const int hl = g & 1;
-      v4i_t b0[4], b1[4];
-      int s0[4], s1[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int ib = 2 * c + (g >> 1);
@@ -436,8 +437,8 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
             v[2 * li + 1] = (ghi ^ mhi) + (mhi & 0x01010101u);
           }
           const uint32_t a0 = u4_get(wcur[m].q[c], 1), a1 = u4_get(wcur[m].q[c], 3);  // sub-blocks 2c, 2c + 1
-          s0[c] = 2 * (int)(a0 >> 28) + 1;
-          s1[c] = 2 * (int)(a1 >> 28) + 1;
+          S0[m][c] = 2 * (int)(a0 >> 28) + 1;
+          S1[m][c] = 2 * (int)(a1 >> 28) + 1;
         } else {
           // sub-block ib: grid-index bytes 8ib .. +7 (two per 8-weight group), word ib
           const uint32_t iw = u4_get(wcur[m].gi[ib >> 1], 2 * (ib & 1) + hl);
@@ -452,33 +453,41 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
             v[2 * li] = (g1 ^ mlo) + (mlo & 0x01010101u);
             v[2 * li + 1] = (g2 ^ mhi) + (mhi & 0x01010101u);
           }
-          s0[c] = 2 * (int)(u4_get(wcur[m].sas[c >> 1], 2 * (c & 1)) >> 28) + 1;
-          s1[c] = 2 * (int)(u4_get(wcur[m].sas[c >> 1], 2 * (c & 1) + 1) >> 28) + 1;
+          S0[m][c] = 2 * (int)(u4_get(wcur[m].sas[c >> 1], 2 * (c & 1)) >> 28) + 1;
+          S1[m][c] = 2 * (int)(u4_get(wcur[m].sas[c >> 1], 2 * (c & 1) + 1) >> 28) + 1;
         }
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          b0[c][k] = (int)(v[k] & keep0);
-          b1[c][k] = (int)(v[k] & ~keep0);
+          B0[m][c][k] = (int)(v[k] & keep0);
+          B1[m][c][k] = (int)(v[k] & ~keep0);
         }
       }
+    }
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
         if (t >= nt) continue;
         const uint8_t *xr = &s_xq[buf][16 * t + n][0];
-        int isum[4] = {0, 0, 0, 0};
+        v4i_t xa[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const v4i_t xa = *reinterpret_cast<const v4i_t *>(xr + 64 * c + 16 * g);
-          const v4i_t z = {0, 0, 0, 0};
-          const v4i_t d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, b0[c], z, 0, 0, 0);
-          const v4i_t d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, b1[c], z, 0, 0, 0);
+        for (int c = 0; c < 4; ++c) xa[c] = *reinterpret_cast<const v4i_t *>(xr + 64 * c + 16 * g);
+        float xdj[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) isum[j] = __mul24(s0[c], d0[j]) + __mul24(s1[c], d1[j]) + isum[j];
+        for (int j = 0; j < 4; ++j) xdj[j] = s_xd[buf][16 * t + 4 * g + j];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          int isum[4] = {0, 0, 0, 0};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const v4i_t z = {0, 0, 0, 0};
+            const v4i_t d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[c], B0[m][c], z, 0, 0, 0);
+            const v4i_t d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[c], B1[m][c], z, 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) isum[j] = __mul24(S0[m][c], d0[j]) + __mul24(S1[m][c], d1[j]) + isum[j];
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) f[m][t][j] += xdj[j] * (DD[m] * (float)isum[j]);
         }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) f[m][t][j] += s_xd[buf][16 * t + 4 * g + j] * (d * (float)isum[j]);
       }
-    }
     } else if constexpr (T == T_IQ4_XS) {
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
