@@ -41,6 +41,16 @@ def test_quantize_q8_K_bit_exact():
     special[2048:2304] = 0.0                      # an all-zero block
     special[3072:3328] = np.linspace(-127, 127, 256)  # exact half-way roundings
     rows.append(special)
+    ties = np.zeros(4096)
+    ties[10] = np.inf                             # an infinite maximum: q = 0, d = -inf
+    ties[256 + 3], ties[256 + 200] = -np.inf, np.inf
+    ties[512 + 17], ties[512 + 40] = 5.0, -5.0    # +/- tie across lanes: the first (+5) wins
+    ties[768 + 33], ties[768 + 32] = 7.0, -7.0    # +/- tie inside one lane's 16: the first (-7) wins
+    ties[1024 + 255], ties[1024 + 240] = -1e-30, 1e-30
+    ties[1280:1536] = rng.standard_normal(256)
+    ties[1280 + 100] = -np.abs(ties[1280:1536]).max()  # negative maximum with its positive twin later
+    ties[1280 + 101] = -ties[1280 + 100]
+    rows.append(ties)
     x = np.stack(rows).astype(np.float32)
     got = Z.quantize_q8_K(torch.from_numpy(x).cuda()).cpu().numpy()
     ref = O.quantize_q8_K(x).view(np.uint8).reshape(got.shape)

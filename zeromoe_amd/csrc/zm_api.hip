@@ -292,8 +292,8 @@ int mmq_max_items(int n_pairs, int n_experts) {
 int launch_quant(const float *x, size_t x_rstride, int nb, int rows, uint8_t *y, size_t y_rstride, int planar,
                  hipStream_t st) {
   if (rows <= 0) return 0;
-  const long waves = (long)rows * nb;
-  hipLaunchKernelGGL(k_quant_q8K, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, x, x_rstride, nb, rows, y,
+  const long blocks = (long)rows * nb;  // 16 per workgroup
+  hipLaunchKernelGGL(k_quant_q8K, dim3((unsigned)((blocks + 15) / 16)), dim3(256), 0, st, x, x_rstride, nb, rows, y,
                      y_rstride, planar);
   HIP_OK(hipGetLastError());
   return 0;

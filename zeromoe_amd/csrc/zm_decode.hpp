@@ -106,9 +106,11 @@ __device__ __forceinline__ void bst_co(rsrc_t r, int vo, float v) {
 __device__ __forceinline__ void bst(rsrc_t r, int vo, float v) {
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, vo, 0, 0);
 }
-#define ZM_TRACE(slot)                                                         \
-  do {                                                                         \
-    if (a.trace && tid == 0) a.trace[(size_t)g * 8 + (slot)] = wall_clock64(); \
+// phase timestamps are kept in registers and written at the end of the kernel,
+// so that no trace store sits in the in-order memory counter of a later wait
+#define ZM_TRACE(slot)                           \
+  do {                                           \
+    if (a.trace) trace_t[(slot)] = wall_clock64(); \
   } while (0)
 
 // Q8_K block (16 lanes) into an LDS activation row (q8l layout)
@@ -153,6 +155,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   const size_t q8x = q8l_row_bytes(a.nbH);
   const size_t q8F = q8l_row_bytes(a.nbF);
   const size_t q8Fs = a.Fs > 0 ? q8l_row_bytes(a.nbFs) : 0;
+  uint64_t trace_t[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   ZM_TRACE(0);
   // counter set of this call (the other set is cleared at the end, for the next call)
   const uint32_t epoch = __builtin_amdgcn_readfirstlane(ld_co(&a.sync[0]));
@@ -416,6 +419,31 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     const int kq = lane >> 4;
     const int T1b = T1r >> 8;
     for (int base = wave * 4; base < nb_all; base += DEC_WAVES * 4 * QR) {
+      // act offsets of this round's blocks (wave-uniform), worked out before
+      // the wait: the divisions and slot-table reads are ~2 us of scalar code
+      int aoffs[QR][4];
+#pragma unroll
+      for (int r = 0; r < QR; ++r) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          int aoff, nb, blk;
+          uint8_t *row;
+          const int bi = base + r * DEC_WAVES * 4 + k;
+          info(min(bi, nb_all - 1), aoff, row, nb, blk);
+          aoffs[r][k] = bi >= nb_all ? OOR : aoff;
+        }
+      }
+      // and where this lane's block of each round goes in LDS: row offset
+      // (< 64 KiB) | block << 16 | blocks in the row << 24, or ~0u past the end
+      uint32_t sinfo[QR];
+#pragma unroll
+      for (int r = 0; r < QR; ++r) {
+        const int bi = base + r * DEC_WAVES * 4 + kq;
+        int aoff, nb, blk;
+        uint8_t *row;
+        info(min(bi, nb_all - 1), aoff, row, nb, blk);
+        sinfo[r] = bi < nb_all ? (uint32_t)(row - s_q8) | (uint32_t)blk << 16 | (uint32_t)nb << 24 : ~0u;
+      }
       {
         int bid = -1;
         const int bi = base + (lane >> 2) * DEC_WAVES * 4 + (lane & 3);
@@ -450,11 +478,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
       for (int r = 0; r < QR; ++r) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          int aoff, nb, blk;
-          uint8_t *row;
-          const int bi = base + r * DEC_WAVES * 4 + k;
-          info(min(bi, nb_all - 1), aoff, row, nb, blk);
-          const int vo = (bi >= nb_all || aoff == OOR) ? OOR : aoff + 16 * lane;
+          const int vo = aoffs[r][k] == OOR ? OOR : aoffs[r][k] + 16 * lane;
           const auto v4 = __builtin_amdgcn_raw_buffer_load_b128(ract, vo, 0, 16);
           ld[r][k] = make_float4(__uint_as_float(v4[0]), __uint_as_float(v4[1]), __uint_as_float(v4[2]),
                                  __uint_as_float(v4[3]));
@@ -477,13 +501,9 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
           xv16[4 * i + 3] = f.w;
         }
         stage_sync();
-        const int bi = base + r * DEC_WAVES * 4 + kq;
-        if (bi < nb_all) {
-          int aoff, nb, blk;
-          uint8_t *row;
-          info(bi, aoff, row, nb, blk);
-          store_q8_16l(row, nb, blk, quant_block16(xv16, l16), l16);  // a zero block for a skipped route
-        }
+        if (sinfo[r] != ~0u)  // a zero block for a skipped route
+          store_q8_16l(s_q8 + (sinfo[r] & 0xffffu), (int)(sinfo[r] >> 24), (int)((sinfo[r] >> 16) & 0xffu),
+                       quant_block16(xv16, l16), l16);
       }
     }
   }
@@ -555,6 +575,10 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
       }
     }
     if (ok && lane == 0 && !s_err) st_co(&a.sync[0], epoch + 1u);
+  }
+  if (a.trace && tid == 0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a.trace[(size_t)g * 8 + i] = trace_t[i];
   }
 }
 

@@ -1,6 +1,6 @@
 // zm_kernels.hpp -- the routed-expert kernels for gfx950 (wave64, CDNA4).
 //
-//   k_quant_q8K  : f32 rows -> Q8_K (one wave per 256-value block)
+//   k_quant_q8K  : f32 rows -> Q8_K (16 lanes per 256-value block)
 //   k_router     : gating + (grouped) top-k + weights + slot table, one wave per token
 //   k_bucket     : stable counting sort of (token, slot) pairs by expert
 //   k_gemv       : bucketed MUL_MAT_ID GEMV over Q8_K activations (decode path)
@@ -21,99 +21,113 @@ namespace zm {
 // ggml quantize_row_q8_K (restated in oracle/zm_oracle.c): the signed value of
 // largest magnitude (first on ties) gives iscale = -127/max; q = min(127,
 // round_half_even(iscale*x)); d = 1/iscale; bsums = sums of 16.
-// The 256 values of a block sit 4 per lane.
-struct Q8Out {
-  int8_t q[4];
+// Lane l of a 16-lane group holds values [16l, 16l+16) of the block, so the
+// block's maximum takes four in-row DPP steps and each lane's 16 values are
+// exactly one of the block's 16-sums.
+struct Q8Out16 {
+  uint4 q;     // 16 int8
   float d;
-  int bsum16;  // valid on lanes with (lane & 3) == 0: sum of values 16*(lane/4) .. +16
+  int bsum;
 };
 
-__device__ __forceinline__ Q8Out quant_block_wave(float4 v, int lane) {
-  float vals[4] = {v.x, v.y, v.z, v.w};
-  float amax = 0.f, mx = 0.f;
-  int idx = 0x7fffffff;
+__device__ __forceinline__ Q8Out16 quant_block16(const float (&x)[16], int l16) {
+  // largest and smallest value of the block; a NaN drops out of fmaxf/fminf
+  // exactly as it drops out of ggml's |x| > amax comparison
+  float hi = x[0], lo = x[0];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float ax = __builtin_fabsf(vals[j]);
-    if (ax > amax) {
-      amax = ax;
-      mx = vals[j];
-      idx = 4 * lane + j;
-    }
+  for (int j = 1; j < 16; ++j) {
+    hi = fmaxf(hi, x[j]);
+    lo = fminf(lo, x[j]);
   }
-  // (|x|, first index) maximum over the wave; the signed value rides along
-  auto take = [&](float oa, float om, int oi) {
-    if (oa > amax || (oa == amax && oi < idx)) {
-      amax = oa;
-      mx = om;
-      idx = oi;
-    }
-  };
-  take(dpp_f<DPP_XOR1>(amax), dpp_f<DPP_XOR1>(mx), dpp_i<DPP_XOR1>(idx));
-  take(dpp_f<DPP_XOR2>(amax), dpp_f<DPP_XOR2>(mx), dpp_i<DPP_XOR2>(idx));
-  take(dpp_f<DPP_HALF_MIRROR>(amax), dpp_f<DPP_HALF_MIRROR>(mx), dpp_i<DPP_HALF_MIRROR>(idx));
-  take(dpp_f<DPP_MIRROR>(amax), dpp_f<DPP_MIRROR>(mx), dpp_i<DPP_MIRROR>(idx));
-  {
-    float ra[4], rm[4];
-    int ri[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      ra[r] = readlane_f(amax, 16 * r);
-      rm[r] = readlane_f(mx, 16 * r);
-      ri[r] = __builtin_amdgcn_readlane(idx, 16 * r);
-    }
-    amax = ra[0];
-    mx = rm[0];
-    idx = ri[0];
-#pragma unroll
-    for (int r = 1; r < 4; ++r) take(ra[r], rm[r], ri[r]);
-  }
-  Q8Out o;
-  if (amax == 0.0f) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) o.q[j] = 0;
+  hi = fmaxf(hi, dpp_f<DPP_XOR1>(hi));
+  lo = fminf(lo, dpp_f<DPP_XOR1>(lo));
+  hi = fmaxf(hi, dpp_f<DPP_XOR2>(hi));
+  lo = fminf(lo, dpp_f<DPP_XOR2>(lo));
+  hi = fmaxf(hi, dpp_f<DPP_HALF_MIRROR>(hi));
+  lo = fminf(lo, dpp_f<DPP_HALF_MIRROR>(lo));
+  hi = fmaxf(hi, dpp_f<DPP_MIRROR>(hi));
+  lo = fminf(lo, dpp_f<DPP_MIRROR>(lo));
+  const float amax = fmaxf(hi, -lo);
+  Q8Out16 o;
+  if (!(amax > 0.0f)) {  // all zero (or no finite/infinite value at all)
+    o.q = make_uint4(0, 0, 0, 0);
     o.d = 0.0f;
-    o.bsum16 = 0;
+    o.bsum = 0;
     return o;
   }
-  const float iscale = -127.f / mx;
-  int s = 0;
+  // the signed value of largest magnitude; when +amax and -amax both occur,
+  // the first in block order wins: each lane finds its first, the lowest lane
+  // of the 16 with one decides
+  float mx = hi > -lo ? hi : lo;
+  if (hi == -lo) {
+    int key = 64;  // (lane << 1 | negative) of this lane's first hit
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    int q = nearest_int(iscale * vals[j]);
-    q = q < 127 ? q : 127;
-    o.q[j] = (int8_t)q;
-    s += q;
+    for (int j = 15; j >= 0; --j) key = __builtin_fabsf(x[j]) == amax ? (l16 << 1) | (x[j] < 0.f) : key;
+    key = min(key, dpp_i<DPP_XOR1>(key));
+    key = min(key, dpp_i<DPP_XOR2>(key));
+    key = min(key, dpp_i<DPP_HALF_MIRROR>(key));
+    key = min(key, dpp_i<DPP_MIRROR>(key));
+    mx = (key & 1) ? lo : hi;
   }
-  o.bsum16 = group_sum_i<4>(s);
+  const float iscale = -127.f / mx;
+  // ggml's q = min(127, nearest_int(v)) as a byte: nearest_int keeps the low
+  // 23 bits of v + 1.5*2^23 less 2^22, so clamping those bits at 2^22 + 127
+  // and keeping their low byte gives the same int8 for every input
+  uint32_t t[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float v = iscale * x[j] + 12582912.f;
+    t[j] = min(__float_as_uint(v) & 0x007fffffu, 0x0040007fu);
+  }
+  uint32_t w[4];
+  int bs = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    w[k] = __builtin_amdgcn_perm(t[4 * k + 1], t[4 * k], 0x0c0c0400u) |
+           __builtin_amdgcn_perm(t[4 * k + 3], t[4 * k + 2], 0x04000c0cu);
+    bs = __builtin_amdgcn_sdot4((int)w[k], 0x01010101, bs, false);
+  }
+  o.q = make_uint4(w[0], w[1], w[2], w[3]);
   o.d = 1.0f / iscale;
+  o.bsum = bs;
   return o;
 }
 
-// rows x nb blocks; planar != 0 writes the internal planar layout, else ggml block_q8_K
+// one Q8_K block (planar row layout) from the 16 values of this lane
+__device__ __forceinline__ void store_q8_16(uint8_t *row, int nb, int blk, const Q8Out16 &o, int l16) {
+  *reinterpret_cast<uint4 *>(row + (size_t)blk * QK + 16 * l16) = o.q;
+  if (l16 == 0) reinterpret_cast<float *>(row + q8_d_off(nb))[blk] = o.d;
+  reinterpret_cast<int16_t *>(row + q8_bs_off(nb))[blk * 16 + l16] = (int16_t)o.bsum;
+}
+
+// rows x nb blocks, 16 lanes per block (quant_block16); planar != 0 writes the
+// internal planar layout, else ggml block_q8_K
 static __global__ __launch_bounds__(256) void k_quant_q8K(const float *__restrict__ x, size_t x_rstride, int nb, int rows,
                                                    uint8_t *__restrict__ y, size_t y_rstride, int planar) {
-  const int lane = threadIdx.x & 63;
-  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int row = gw / nb, b = gw % nb;
+  const int l16 = threadIdx.x & 15;
+  const int gb = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int row = gb / nb, b = gb % nb;
   if (row >= rows) return;
-  const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)row * x_rstride + (size_t)b * QK + 4 * lane);
-  const Q8Out o = quant_block_wave(v, lane);
-  uint32_t packed = (uint32_t)(uint8_t)o.q[0] | ((uint32_t)(uint8_t)o.q[1] << 8) | ((uint32_t)(uint8_t)o.q[2] << 16) |
-                    ((uint32_t)(uint8_t)o.q[3] << 24);
+  const float4 *src = reinterpret_cast<const float4 *>(x + (size_t)row * x_rstride + (size_t)b * QK + 16 * l16);
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 f = src[i];
+    v[4 * i] = f.x;
+    v[4 * i + 1] = f.y;
+    v[4 * i + 2] = f.z;
+    v[4 * i + 3] = f.w;
+  }
+  const Q8Out16 o = quant_block16(v, l16);
   uint8_t *yr = y + (size_t)row * y_rstride;
   if (planar) {
-    *reinterpret_cast<uint32_t *>(yr + (size_t)b * QK + 4 * lane) = packed;
-    if (lane == 0) reinterpret_cast<float *>(yr + q8_d_off(nb))[b] = o.d;
-    if ((lane & 3) == 0) reinterpret_cast<int16_t *>(yr + q8_bs_off(nb))[b * 16 + (lane >> 2)] = (int16_t)o.bsum16;
+    store_q8_16(yr, nb, b, o, l16);
   } else {
     uint8_t *blk = yr + (size_t)b * 292;
-    __builtin_memcpy(blk + 4 + 4 * lane, &packed, 4);
-    if (lane == 0) __builtin_memcpy(blk, &o.d, 4);
-    if ((lane & 3) == 0) {
-      const int16_t bs = (int16_t)o.bsum16;
-      __builtin_memcpy(blk + 260 + 2 * (lane >> 2), &bs, 2);
-    }
+    __builtin_memcpy(blk + 4 + 16 * l16, &o.q, 16);
+    if (l16 == 0) __builtin_memcpy(blk, &o.d, 4);
+    const int16_t bs = (int16_t)o.bsum;
+    __builtin_memcpy(blk + 260 + 2 * l16, &bs, 2);
   }
 }
 
@@ -352,71 +366,6 @@ static __global__ __launch_bounds__(256) void k_router(RouterArgs a, int S) {
     a.ids[(size_t)s * a.K + lane] = r.id;
     a.weights[(size_t)s * a.K + lane] = r.w;
   }
-}
-
-// ============================================================ Q8_K with 16 lanes per block
-//
-// Lane l of a 16-lane group holds values [16l, 16l+16) of the block: the
-// (|x|, first index) maximum needs only the four in-row DPP steps, and each
-// lane's 16 values are exactly one of the block's 16-sums.  Same arithmetic as
-// quant_block_wave (bit-identical results).
-struct Q8Out16 {
-  uint4 q;     // 16 int8
-  float d;
-  int bsum;
-};
-
-__device__ __forceinline__ Q8Out16 quant_block16(const float (&x)[16], int l16) {
-  float amax = 0.f, mx = 0.f;
-  int idx = 0x7fffffff;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const float ax = __builtin_fabsf(x[j]);
-    if (ax > amax) {
-      amax = ax;
-      mx = x[j];
-      idx = 16 * l16 + j;
-    }
-  }
-  auto take = [&](float oa, float om, int oi) {
-    if (oa > amax || (oa == amax && oi < idx)) {
-      amax = oa;
-      mx = om;
-      idx = oi;
-    }
-  };
-  take(dpp_f<DPP_XOR1>(amax), dpp_f<DPP_XOR1>(mx), dpp_i<DPP_XOR1>(idx));
-  take(dpp_f<DPP_XOR2>(amax), dpp_f<DPP_XOR2>(mx), dpp_i<DPP_XOR2>(idx));
-  take(dpp_f<DPP_HALF_MIRROR>(amax), dpp_f<DPP_HALF_MIRROR>(mx), dpp_i<DPP_HALF_MIRROR>(idx));
-  take(dpp_f<DPP_MIRROR>(amax), dpp_f<DPP_MIRROR>(mx), dpp_i<DPP_MIRROR>(idx));
-  Q8Out16 o;
-  if (amax == 0.0f) {
-    o.q = make_uint4(0, 0, 0, 0);
-    o.d = 0.0f;
-    o.bsum = 0;
-    return o;
-  }
-  const float iscale = -127.f / mx;
-  uint32_t w[4] = {0, 0, 0, 0};
-  int s = 0;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    int q = nearest_int(iscale * x[j]);
-    q = q < 127 ? q : 127;
-    s += q;
-    w[j >> 2] |= (uint32_t)(uint8_t)q << (8 * (j & 3));
-  }
-  o.q = make_uint4(w[0], w[1], w[2], w[3]);
-  o.d = 1.0f / iscale;
-  o.bsum = s;
-  return o;
-}
-
-// one Q8_K block (planar row layout) from the 16 values of this lane
-__device__ __forceinline__ void store_q8_16(uint8_t *row, int nb, int blk, const Q8Out16 &o, int l16) {
-  *reinterpret_cast<uint4 *>(row + (size_t)blk * QK + 16 * l16) = o.q;
-  if (l16 == 0) reinterpret_cast<float *>(row + q8_d_off(nb))[blk] = o.d;
-  reinterpret_cast<int16_t *>(row + q8_bs_off(nb))[blk * 16 + l16] = (int16_t)o.bsum;
 }
 
 // ============================================================ bucketing
