@@ -228,6 +228,31 @@ def test_router_ties_lowest_index():
     np.testing.assert_array_equal(ids.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("E,K,gating,groups", [
+    (32, 4, 0, (0, 0)), (64, 8, 0, (0, 0)), (128, 1, 0, (0, 0)), (128, 8, 0, (0, 0)), (128, 12, 1, (0, 0)),
+    (160, 8, 0, (0, 0)), (256, 8, 1, (8, 4)), (256, 16, 0, (0, 0)), (256, 20, 0, (0, 0)), (512, 8, 1, (0, 0)),
+    (1000, 6, 0, (0, 0)),
+])
+@pytest.mark.parametrize("ties", [False, True])
+def test_router_selection_paths(E, K, gating, groups, ties):
+    """Top-k selection: the candidate-ranking path (K <= 16, at most 64
+    experts at or above the subset-maxima bound) and the K-round path it falls
+    back to (K > 16, heavy ties, E < 64 subsets) give the oracle's ids and
+    weights.  Rounded logits make exact score ties common."""
+    import zeromoe_amd as Z
+
+    rng = np.random.default_rng(E * 31 + K)
+    lg = rng.standard_normal((96, E)) * 2.0
+    if ties:
+        lg = np.round(lg)
+    lg = lg.astype(np.float32)
+    ids_r, w_r = O.router(lg, K, gating, None, None, groups[0], groups[1], True, 0.0)
+    ids, w = Z.router(torch.from_numpy(lg).cuda(), K, {0: "softmax", 1: "sigmoid"}[gating], n_groups=groups[0],
+                      n_groups_used=groups[1], weights_norm=True)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_r)
+    np.testing.assert_allclose(w.cpu().numpy(), w_r, rtol=1e-6, atol=0)
+
+
 @pytest.mark.parametrize("S,K,E", [(1, 8, 128), (512, 8, 128), (4, 8, 160), (64, 8, 96), (3000, 8, 256)])
 def test_bucket_bit_exact(S, K, E):
     import zeromoe_amd as Z

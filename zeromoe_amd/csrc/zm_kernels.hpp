@@ -283,9 +283,7 @@ __device__ __forceinline__ WaveRoute router_wave(const RouterArgs &a, int s, flo
       if (!((keep >> ((lane + 64 * i) / gs)) & 1ull)) sel[i] = NEG_INF;
     stage_sync();  // scr is reused by the caller
   }
-  // top-K: K rounds of a wave-wide 32-bit score-key maximum; the winner is the
-  // lowest expert index holding it (register i = 0 first, then the lowest lane
-  // in the ballot), so the order is "higher score, then lower index"
+  // top-K in the order "higher score, then lower expert index"
   uint32_t key[P];
 #pragma unroll
   for (int i = 0; i < P; ++i) key[i] = lane + 64 * i < E ? score_key(sel[i]) : 0u;
@@ -294,7 +292,104 @@ __device__ __forceinline__ WaveRoute router_wave(const RouterArgs &a, int s, flo
   for (int i = 0; i < P; ++i) valid |= (lane + 64 * i < E ? 1u : 0u) << i;
   int myid = 0;
   float myw = 0.f, mymask = 1.0f;
-  for (int k = 0; k < K; ++k) {
+  // Fast path (K <= 16): a lower bound L on the K-th largest key is the
+  // smallest of NS >= K subset maxima (NS distinct experts are >= it); only
+  // the experts with key >= L can be selected.  When at most 64 remain they
+  // are compacted in index order into LDS and each is ranked against all of
+  // them at once (independent compares instead of K dependent wave-wide
+  // rounds); the ranks < K are the routes, in order.
+  bool routed = false;
+  if (K <= 16) {
+    uint32_t lm = 0;
+#pragma unroll
+    for (int i = 0; i < P; ++i) lm = ((valid >> i) & 1u) && key[i] > lm ? key[i] : lm;
+    lm = max(lm, (uint32_t)dpp_i<DPP_XOR1>((int)lm));
+    lm = max(lm, (uint32_t)dpp_i<DPP_XOR2>((int)lm));  // maxima of 16 subsets of 4 lanes
+    if (K <= 8) {
+      lm = max(lm, (uint32_t)dpp_i<DPP_HALF_MIRROR>((int)lm));  // 8 subsets of 8 lanes
+    } else {
+      lm = min(lm, (uint32_t)dpp_i<DPP_HALF_MIRROR>((int)lm));
+    }
+    lm = min(lm, (uint32_t)dpp_i<DPP_MIRROR>((int)lm));
+    const uint32_t L = min(min((uint32_t)__builtin_amdgcn_readlane((int)lm, 0), (uint32_t)__builtin_amdgcn_readlane((int)lm, 16)),
+                           min((uint32_t)__builtin_amdgcn_readlane((int)lm, 32), (uint32_t)__builtin_amdgcn_readlane((int)lm, 48)));
+    unsigned long long bal[P];
+    int C = 0;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      bal[i] = __ballot(((valid >> i) & 1u) && key[i] >= L);
+      C += __popcll(bal[i]);
+    }
+    if (C >= K && C <= 64) {
+      uint32_t *ck = reinterpret_cast<uint32_t *>(scr);  // [0,64) keys, [64,128) ids, [128,192) p, [192,256) slot, [256,320) mask
+      uint32_t *co = ck + 320;                           // [320,384): routes (id, p, slot, mask) x 16
+      int base = 0;
+#pragma unroll
+      for (int i = 0; i < P; ++i) {
+        if ((bal[i] >> lane) & 1ull) {
+          const int pos = base + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal[i] >> 32),
+                                                            __builtin_amdgcn_mbcnt_lo((uint32_t)bal[i], 0));
+          ck[pos] = key[i];
+          ck[64 + pos] = (uint32_t)(lane + 64 * i);
+          ck[128 + pos] = __float_as_uint(v[i]);
+          ck[192 + pos] = (uint32_t)rm[i];
+          ck[256 + pos] = __float_as_uint(rk[i]);
+        }
+        base += __popcll(bal[i]);
+      }
+      if (lane >= C) ck[lane] = 0u;  // all 64 key slots defined; padding never outranks
+      stage_sync();
+      // rank = candidates before this one in (key descending, position
+      // ascending) order.  First the larger keys (one compare and one
+      // carry-add per candidate, 16 keys read per step); the counts are then
+      // 0..C-1 exactly when no key repeats, else the equal keys at earlier
+      // positions are added
+      int rank = 0;
+      uint32_t mk = 0;
+      if (lane < C) {
+        mk = ck[lane];
+        for (int t = 0; t < C; t += 16) {
+          uint4 kt[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) kt[q] = *reinterpret_cast<const uint4 *>(ck + t + 4 * q);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t kq[4] = {kt[q].x, kt[q].y, kt[q].z, kt[q].w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+              asm("v_cmp_gt_u32_e32 vcc, %1, %2\n\tv_addc_co_u32_e32 %0, vcc, 0, %0, vcc"
+                  : "+v"(rank)
+                  : "v"(kq[u]), "v"(mk)
+                  : "vcc");
+          }
+        }
+      }
+      if (group_sum_i<64>(rank) != C * (C - 1) / 2 && lane < C)
+        for (int t = 0; t < lane; ++t) rank += ck[t] == mk;
+      if (lane < C && rank < K) {
+        co[4 * rank] = ck[64 + lane];
+        co[4 * rank + 1] = ck[128 + lane];
+        co[4 * rank + 2] = ck[192 + lane];
+        co[4 * rank + 3] = ck[256 + lane];
+      }
+      stage_sync();
+      if (lane < K) {
+        const int e = (int)co[4 * lane];
+        myw = __uint_as_float(co[4 * lane + 1]);
+        myid = e;
+        if (a.route_map) {
+          myid = (int)co[4 * lane + 2];
+          mymask = a.route_mask ? __uint_as_float(co[4 * lane + 3]) : (myid >= 0 ? 1.0f : 0.0f);
+        }
+      }
+      stage_sync();  // scr is reused by the caller
+      routed = true;
+    }
+  }
+  // General path: K rounds of a wave-wide 32-bit score-key maximum; the winner
+  // is the lowest expert index holding it (register i = 0 first, then the
+  // lowest lane in the ballot)
+  for (int k = 0; !routed && k < K; ++k) {
     uint32_t m = 0;
 #pragma unroll
     for (int i = 0; i < P; ++i) m = ((valid >> i) & 1u) && key[i] >= m ? key[i] : m;
@@ -334,8 +429,11 @@ __device__ __forceinline__ WaveRoute router_wave(const RouterArgs &a, int s, flo
   // weights: norm in k order (double, as ggml's sum_rows), scale, slot mask
   float w = myw;
   if (a.weights_norm) {
+    // the lane values are read out first; only the additions are serial
+    const double dw = (double)myw;
     double sum = 0.0;
-    for (int k = 0; k < K; ++k) sum += (double)readlane_f(myw, k);
+    for (int k = 0; k < K; ++k) sum += __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(dw), k),
+                                                         __builtin_amdgcn_readlane(__double2loint(dw), k));
     float fs = (float)sum;
     fs = fs < 6.103515625e-5f ? 6.103515625e-5f : fs;
     w = w / fs;
