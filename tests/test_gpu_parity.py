@@ -378,6 +378,37 @@ def test_fused_decode_vs_multikernel_and_oracle(case, monkeypatch):
     assert_close_layer(out1.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("case", ["c5_S2", "c2_S8"])
+def test_fused_decode_varying_routes(case, monkeypatch):
+    """Consecutive fused launches whose routing differs (with c5's slot table a
+    different number of routes is resident each time, so the act rows stored
+    per call change): every launch matches the oracle.  The two act buffers
+    alternate between calls and each call clears the rows the other one holds,
+    so no row of an earlier call can be read as stored."""
+    c, kw = FUSED_CASES[case]
+    c = reduced(c, **kw)
+    b = Built(c, seed=23)
+    L = b.layer()
+    rng = np.random.default_rng(5)
+    monkeypatch.setenv("ZEROMOE_FUSED_DECODE", "1")
+    n_routes = set()
+    for i in range(10):
+        b.x = (rng.standard_normal(b.x.shape) * (0.5 + i % 3)).astype(np.float32)
+        x = torch.from_numpy(b.x).cuda()
+        lg_np = None if c.router_gemv else (rng.standard_normal(b.logits.shape) * (0.5 + i % 3)).astype(np.float32)
+        out, ids, w = L.forward(x, None if lg_np is None else torch.from_numpy(lg_np).cuda())
+        _sync()
+        ids_h, w_h = ids.cpu().numpy(), w.cpu().numpy()
+        ids_r, _ = b.oracle_route(lg_np)
+        np.testing.assert_array_equal(ids_h, ids_r)
+        n_routes.add(int((ids_h >= 0).sum()))
+        ref = b.oracle_forward(ids_h, w_h)
+        assert_close_layer(out.cpu().numpy(), ref, slack=lambda: b.requant_slack(ids_h, w_h))
+    assert L.status(c.S) == 0
+    if b.route_map is not None:
+        assert len(n_routes) > 1, n_routes
+
+
 @pytest.mark.parametrize("case", ["c2", "c3_small"])
 def test_hip_graph_replay_matches_eager(case):
     """The layer recorded into a HIP graph and replayed several times, with eager
