@@ -364,7 +364,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         issue(st + 2, A, ra);
         __builtin_amdgcn_sched_barrier(0);
-        compute(B, rb);
+        if (st + 1 < nst) compute(B, rb);  // an odd step count leaves B empty: no dots on zeros
         __builtin_amdgcn_sched_barrier(0);
       }
     };
@@ -542,7 +542,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
       acc = group_sum<L2>(acc);
       bst(rout, (li2 == 0 && valid) ? 4 * (s * H + h) : OOR, acc);
       __builtin_amdgcn_sched_barrier(0);
-      load_step2(st + 1, c2r, c2s);
+      if (st + 1 < nst2) load_step2(st + 1, c2r, c2s);  // (the unpacking of a unit costs VALU even when out of range)
       __builtin_amdgcn_sched_barrier(0);
     }
   }
