@@ -134,6 +134,9 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   __shared__ float s_w[DEC_MAX_PAIRS];
   __shared__ int s_cidx[DEC_MAX_PAIRS];  // pair -> compact routed index (or -1)
   __shared__ int s_vp[DEC_MAX_PAIRS];    // compact index -> pair
+  __shared__ int s_goff[DEC_MAX_PAIRS];  // compact index -> gate/up expert byte offset
+  __shared__ int s_gtok[DEC_MAX_PAIRS];  // compact index -> token
+  __shared__ int s_doff[DEC_MAX_PAIRS];  // pair -> down expert byte offset (or -1)
   __shared__ int s_nvp;
   __shared__ int s_err;
   __shared__ __attribute__((aligned(16))) uint8_t s_q8[DEC_LDS_Q8];
@@ -227,7 +230,17 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     stage_sync();
     for (int p0 = 0; p0 < S * K; p0 += 64) {
       const int p = p0 + lane;
-      if (p < S * K && s_cidx[p] >= 0) s_vp[s_cidx[p]] = p;
+      if (p < S * K) {
+        // per-pair offsets worked out once: the per-row address math then
+        // needs only 24-bit multiplies (row < 2^14, row stride < 2^24)
+        const int id = s_ids[p];
+        s_doff[p] = id >= 0 ? id * (int)a.d_estride : -1;
+        if (s_cidx[p] >= 0) {
+          s_vp[s_cidx[p]] = p;
+          s_goff[s_cidx[p]] = id * (int)a.g_estride;
+          s_gtok[s_cidx[p]] = p / K;
+        }
+      }
     }
     if (lane == 0) s_nvp = n;
   }
@@ -270,16 +283,17 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     for (int it = 0; it < IR; ++it) {
       const int u = li2 + L2 * it;
       const int k = u / URb, rem = u - k * URb;
-      const int e = s_ids[s * K + min(k, K - 1)];
-      const bool ok = valid && u < URd && e >= 0;
-      load_unit<TD>(rd, ok ? e * (int)a.d_estride + h * (int)a.d_rstride + (rem / UPD) * BD : OOR, rem % UPD, wr[it]);
+      const int eoff = s_doff[s * K + min(k, K - 1)];
+      const bool ok = valid && u < URd && eoff >= 0;
+      load_unit<TD>(rd, ok ? eoff + (int)__umul24((uint32_t)h, (uint32_t)a.d_rstride) + (rem / UPD) * BD : OOR,
+                    rem % UPD, wr[it]);
     }
     if constexpr (IS > 0) {
 #pragma unroll
       for (int it = 0; it < IS; ++it) {
         const int u = li2 + L2 * it;
         const bool ok = valid && u < USd;
-        load_unit<TS>(rsd, ok ? h * (int)a.sd_rstride + (u / UPS) * BSD : OOR, u % UPS, ws[it]);
+        load_unit<TS>(rsd, ok ? (int)__umul24((uint32_t)h, (uint32_t)a.sd_rstride) + (u / UPS) * BSD : OOR, u % UPS, ws[it]);
       }
     }
   };
@@ -323,12 +337,11 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
         if constexpr (SH) {
           divmod24(j - T1r, a.Fs, invFs, q, n);
           tok = q;
-          roff = n * (int)a.sg_rstride;
+          roff = (int)__umul24((uint32_t)n, (uint32_t)a.sg_rstride);
         } else {
           divmod24(j, F, invF, q, n);
-          const int p = s_vp[q];
-          tok = p / K;
-          roff = s_ids[p] * (int)a.g_estride + n * (int)a.g_rstride;
+          tok = s_gtok[q];
+          roff = s_goff[q] + (int)__umul24((uint32_t)n, (uint32_t)a.g_rstride);
         }
       };
       // a step's row (valid, j, token) is worked out once, when its loads are issued
