@@ -174,12 +174,23 @@ __device__ __forceinline__ void stage_sync() {
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
+// the value of lane ^ 16 / lane ^ 32, through the gfx950 row-swap permutes
+// (no trip through scalar registers); every lane of the wave must be active
+__device__ __forceinline__ int lane_xor16(int v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return (threadIdx.x & 16) ? (int)r[0] : (int)r[1];
+}
+__device__ __forceinline__ int lane_xor32(int v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (threadIdx.x & 32) ? (int)r[0] : (int)r[1];
+}
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_f<DPP_XOR1>(v));
   v = fmaxf(v, dpp_f<DPP_XOR2>(v));
   v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
   v = fmaxf(v, dpp_f<DPP_MIRROR>(v));
-  return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+  v = fmaxf(v, __int_as_float(lane_xor16(__float_as_int(v))));
+  return fmaxf(v, __int_as_float(lane_xor32(__float_as_int(v))));
 }
 __device__ __forceinline__ double wave_sum_f64(double v) {
   auto step = [](double x, auto ctrl_tag) -> double {
@@ -192,12 +203,19 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
   v = step(v, std::integral_constant<int, DPP_XOR2>{});
   v = step(v, std::integral_constant<int, DPP_HALF_MIRROR>{});
   v = step(v, std::integral_constant<int, DPP_MIRROR>{});
-  auto rl = [](double x, int l) {
+  // rows (0 + 1) + (2 + 3), the same sums in every lane (addition commutes)
+  auto x16 = [](double x) {
     const long long b = __double_as_longlong(x);
-    const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffffll), l), hi = __builtin_amdgcn_readlane((int)(b >> 32), l);
+    const int lo = lane_xor16((int)(b & 0xffffffffll)), hi = lane_xor16((int)(b >> 32));
     return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
   };
-  return (rl(v, 0) + rl(v, 16)) + (rl(v, 32) + rl(v, 48));
+  auto x32 = [](double x) {
+    const long long b = __double_as_longlong(x);
+    const int lo = lane_xor32((int)(b & 0xffffffffll)), hi = lane_xor32((int)(b >> 32));
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+  };
+  v = v + x16(v);
+  return v + x32(v);
 }
 
 // Strict order "higher score, then lower index" as one 64-bit key: the
@@ -224,10 +242,8 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t k) {
   step(std::integral_constant<int, DPP_XOR2>{});
   step(std::integral_constant<int, DPP_HALF_MIRROR>{});
   step(std::integral_constant<int, DPP_MIRROR>{});
-  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)k, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)k, 16);
-  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)k, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)k, 48);
-  const uint32_t ab = a > b ? a : b, cd = c > d ? c : d;
-  return ab > cd ? ab : cd;
+  k = max(k, (uint32_t)lane_xor16((int)k));
+  return max(k, (uint32_t)lane_xor32((int)k));
 }
 // inverse of score_key (-0 comes back as +0)
 __device__ __forceinline__ float score_from_key(uint32_t k) {
@@ -244,14 +260,8 @@ __device__ __forceinline__ uint32_t group_max_u32(uint32_t k, int W) {
   step(std::integral_constant<int, DPP_XOR2>{});
   step(std::integral_constant<int, DPP_HALF_MIRROR>{});
   step(std::integral_constant<int, DPP_MIRROR>{});
-  if (W >= 32) {
-    // the four 16-lane row maxima through scalar registers
-    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)k, 0), r1 = (uint32_t)__builtin_amdgcn_readlane((int)k, 16);
-    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)k, 32), r3 = (uint32_t)__builtin_amdgcn_readlane((int)k, 48);
-    const uint32_t lo = r0 > r1 ? r0 : r1, hi = r2 > r3 ? r2 : r3;
-    if (W >= 64) return lo > hi ? lo : hi;
-    k = (threadIdx.x & 32) ? hi : lo;
-  }
+  if (W >= 32) k = max(k, (uint32_t)lane_xor16((int)k));
+  if (W >= 64) k = max(k, (uint32_t)lane_xor32((int)k));
   return k;
 }
 __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k) {

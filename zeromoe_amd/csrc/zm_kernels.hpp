@@ -233,21 +233,34 @@ __device__ __forceinline__ WaveRoute router_wave(const RouterArgs &a, int s, flo
     if (gs == 16 || gs == 32 || gs == 64) {
       // a group is gs consecutive lanes of one register: two group-wide key
       // maxima, the first one's lowest lane taken out for the second; a score
-      // is recovered from its key (the map is a bijection up to -0 -> +0)
-      const unsigned long long lanes_all = ~0ull;
+      // is recovered from its key (the map is a bijection up to -0 -> +0).
+      // Each phase runs over all registers before the next, so the P
+      // independent DPP chains interleave.
+      auto groups = [&](auto gs_tag) {
+        constexpr int GS = decltype(gs_tag)::value;
+        const int base = lane & ~(GS - 1);
+        const unsigned long long gmask = (GS == 64 ? ~0ull : ((1ull << (GS & 63)) - 1ull)) << base;
+        uint32_t k0[P], k1[P];
 #pragma unroll
-      for (int i = 0; i < P; ++i) {
-        const bool ok = lane + 64 * i < E;
-        const uint32_t k0 = ok ? score_key(sel[i]) : 0u;
-        const int base = lane & ~(gs - 1);
-        const unsigned long long gmask = (gs == 64 ? lanes_all : ((1ull << gs) - 1ull)) << base;
-        const uint32_t k1 = group_max_u32(k0, gs);
-        const unsigned long long b1 = __ballot(ok && k0 == k1) & gmask;
-        const bool first = b1 != 0ull && lane == (int)__builtin_ctzll(b1);
-        const uint32_t k2 = group_max_u32(first ? 0u : k0, gs);
-        const float s1 = score_from_key(k1), s2 = score_from_key(k2);
-        if (ok && (lane & (gs - 1)) == 0) scr[(lane + 64 * i) / gs] = gs >= 2 ? s1 + s2 : s1;
-      }
+        for (int i = 0; i < P; ++i) k0[i] = lane + 64 * i < E ? score_key(sel[i]) : 0u;
+#pragma unroll
+        for (int i = 0; i < P; ++i) k1[i] = group_max_u32(k0[i], GS);
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+          const unsigned long long b1 = __ballot(lane + 64 * i < E && k0[i] == k1[i]) & gmask;
+          const bool first = b1 != 0ull && lane == (int)__builtin_ctzll(b1);
+          k0[i] = first ? 0u : k0[i];
+        }
+#pragma unroll
+        for (int i = 0; i < P; ++i) k0[i] = group_max_u32(k0[i], GS);
+#pragma unroll
+        for (int i = 0; i < P; ++i)
+          if (lane + 64 * i < E && (lane & (GS - 1)) == 0)
+            scr[(lane + 64 * i) / GS] = score_from_key(k1[i]) + score_from_key(k0[i]);
+      };
+      if (gs == 16) groups(std::integral_constant<int, 16>{});
+      else if (gs == 32) groups(std::integral_constant<int, 32>{});
+      else groups(std::integral_constant<int, 64>{});
       stage_sync();
       if (lane < G) gsc = scr[lane];
     } else {
