@@ -126,7 +126,8 @@ __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + exp_f32(
 // Cross-lane steps use DPP (a VALU operand modifier, no LDS round trip):
 // quad_perm(1,0,3,2) = xor 1, quad_perm(2,3,0,1) = xor 2, row_half_mirror and
 // row_mirror combine 4- and 8-lane halves once every lane of the half holds the
-// same partial; the four 16-lane rows are then combined through readlane.
+// same partial; the four 16-lane rows are then combined with the row-swap
+// permutes (lane_xor16 / lane_xor32).
 // Every lane ends with the same result, in a fixed order (deterministic).
 constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
 
@@ -142,38 +143,6 @@ __device__ __forceinline__ float readlane_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
-// sum over aligned groups of W lanes (W = 4, 8, 16, 32, 64); all lanes of a group get it
-template <int W>
-__device__ __forceinline__ float group_sum(float v) {
-  static_assert(W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "group width");
-  v += dpp_f<DPP_XOR1>(v);
-  v += dpp_f<DPP_XOR2>(v);
-  if constexpr (W >= 8) v += dpp_f<DPP_HALF_MIRROR>(v);
-  if constexpr (W >= 16) v += dpp_f<DPP_MIRROR>(v);
-  if constexpr (W == 32) v += __shfl_xor(v, 16, 64);
-  if constexpr (W == 64)
-    v = (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
-  return v;
-}
-template <int W>
-__device__ __forceinline__ int group_sum_i(int v) {
-  static_assert(W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "group width");
-  v += dpp_i<DPP_XOR1>(v);
-  v += dpp_i<DPP_XOR2>(v);
-  if constexpr (W >= 8) v += dpp_i<DPP_HALF_MIRROR>(v);
-  if constexpr (W >= 16) v += dpp_i<DPP_MIRROR>(v);
-  if constexpr (W == 32) v += __shfl_xor(v, 16, 64);
-  if constexpr (W == 64)
-    v = (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
-        (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
-  return v;
-}
-// LDS writes of this wave visible to its other lanes
-__device__ __forceinline__ void stage_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 // the value of lane ^ 16 / lane ^ 32, through the gfx950 row-swap permutes
 // (no trip through scalar registers); every lane of the wave must be active
 __device__ __forceinline__ int lane_xor16(int v) {
@@ -183,6 +152,36 @@ __device__ __forceinline__ int lane_xor16(int v) {
 __device__ __forceinline__ int lane_xor32(int v) {
   const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
   return (threadIdx.x & 32) ? (int)r[0] : (int)r[1];
+}
+// sum over aligned groups of W lanes (W = 4, 8, 16, 32, 64); all lanes of a group get it
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "group width");
+  v += dpp_f<DPP_XOR1>(v);
+  v += dpp_f<DPP_XOR2>(v);
+  if constexpr (W >= 8) v += dpp_f<DPP_HALF_MIRROR>(v);
+  if constexpr (W >= 16) v += dpp_f<DPP_MIRROR>(v);
+  // rows (0 + 1) + (2 + 3) in every lane (addition commutes)
+  if constexpr (W >= 32) v += __int_as_float(lane_xor16(__float_as_int(v)));
+  if constexpr (W == 64) v += __int_as_float(lane_xor32(__float_as_int(v)));
+  return v;
+}
+template <int W>
+__device__ __forceinline__ int group_sum_i(int v) {
+  static_assert(W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "group width");
+  v += dpp_i<DPP_XOR1>(v);
+  v += dpp_i<DPP_XOR2>(v);
+  if constexpr (W >= 8) v += dpp_i<DPP_HALF_MIRROR>(v);
+  if constexpr (W >= 16) v += dpp_i<DPP_MIRROR>(v);
+  if constexpr (W >= 32) v += lane_xor16(v);
+  if constexpr (W == 64) v += lane_xor32(v);
+  return v;
+}
+// LDS writes of this wave visible to its other lanes
+__device__ __forceinline__ void stage_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_f<DPP_XOR1>(v));
