@@ -183,6 +183,23 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
         a.r.weights[wave * K + lane] = r.w;
       }
     }
+    if (S == 1) {
+      // one token: its routing wave compacts the routed pairs itself (see
+      // below), which saves a workgroup barrier
+      const bool ok = lane < K && r.id >= 0;
+      const unsigned long long m = __ballot(ok);
+      const int c = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+      if (lane < K) {
+        s_cidx[lane] = ok ? c : -1;
+        s_doff[lane] = ok ? r.id * (int)a.d_estride : -1;
+      }
+      if (ok) {
+        s_vp[c] = lane;
+        s_goff[c] = r.id * (int)a.g_estride;
+        s_gtok[c] = 0;
+      }
+      if (lane == 0) s_nvp = __popcll(m);
+    }
   }
   if constexpr (kIQ2) {
     for (int i = tid; i < 256; i += DEC_THREADS) s_grid[i] = a.grid[i];
@@ -213,7 +230,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   }
   ZM_TRACE(7);
   __syncthreads();
-  if (wave == 0) {
+  if (S > 1 && wave == 0) {
     // compact the routed pairs (id >= 0) in pair order: ballot + prefix count
     int n = 0;
     for (int p0 = 0; p0 < S * K; p0 += 64) {
@@ -244,7 +261,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     }
     if (lane == 0) s_nvp = n;
   }
-  __syncthreads();
+  if (S > 1) __syncthreads();
   ZM_TRACE(1);
   const int nvp = s_nvp;
   const int T1r = nvp * F;
