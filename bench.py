@@ -28,6 +28,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "routed-expert layer µs + HBM GB/s (% of peak) at batch 1; prefill tok/s"
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_OPS = 5.0e15  # MI355X dense int8 MFMA, ops/s
 Q2, Q3, Q4, Q5, Q6, IQ2, IQ3X, IQ4X = 10, 11, 12, 13, 14, 16, 18, 23
 BB = {Q2: 84, Q3: 110, Q4: 144, Q5: 176, Q6: 210, IQ2: 66, IQ3X: 98, IQ4X: 136}
 
@@ -198,6 +199,13 @@ def run_config(torch, Z, name, steps, warmup, replicas, use_graph=True, kernel_l
     res = dict(us_per_layer=ms * 1e3, ms_per_step=ms, GBps=gbs, frac_hbm_peak=gbs / HBM_PEAK_GBS,
                bytes_per_layer=bytes_step, unique_experts=mean_uniq, tok_per_s=S / (ms * 1e-3),
                wall_s=wall, replicas=replicas)
+    if S >= 32:
+        # algorithmic int8 ops (2 per multiply-add; gate, up and down of every
+        # routed pair, plus the shared expert) against the dense int8 MFMA peak
+        pairs = float((ids[warmup:] >= 0).sum().item()) / steps
+        ops = 2 * 3 * H * c["F"] * pairs + (2 * 3 * H * c["F_shared"] * S if c.get("F_shared") else 0)
+        res.update(int8_ops_per_layer=ops, int8_TOPs=ops / (ms * 1e-3) / 1e12,
+                   mfma_frac=ops / (ms * 1e-3) / INT8_PEAK_OPS)
     if kernel_launches:
         res["kernel_us"] = time_launches(torch, step, warmup, min(steps, kernel_launches))
     return res
@@ -345,6 +353,43 @@ def pmc_summary(fetch_dir, write_dir, out_path, command):
     print("\n".join(lines))
 
 
+def mfma_summary(d, out_path, command, pattern="k_mmq", peak_ops=5.0e15):
+    """int8 MFMA utilisation of the prefill kernels from one rocprofv3 --pmc run:
+    per kernel, the mean per dispatch of each counter, the int8 MFMA ops
+    (SQ_INSTS_VALU_MFMA_MOPS_I8 counts units of 512 ops) and their rate over
+    the dispatch's duration against the dense int8 peak."""
+    import csv
+    import glob
+    import re
+
+    per = {}  # kernel -> {counter: [values]}, plus durations
+    for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                if pattern not in r["Kernel_Name"]:
+                    continue
+                name = re.sub(r"\(.*", "", r["Kernel_Name"].replace("void ", ""))[:60]
+                e = per.setdefault(name, {"_dur": {}})
+                e.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+                e["_dur"][r["Dispatch_Id"]] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9
+    if not per:
+        raise SystemExit(f"mfma_summary: no {pattern} dispatches under {d}")
+    lines = ["# int8 MFMA utilisation of the prefill kernels (c3, bench.py --profile c3)", f"# command: {command}"]
+    for name, e in sorted(per.items()):
+        durs = list(e.pop("_dur").values())
+        dur = sum(durs) / len(durs)
+        lines.append(f"{name}: dispatches {len(durs)}, mean duration under counters {dur * 1e6:.1f} us")
+        for c, vs in sorted(e.items()):
+            lines.append(f"  {c}: {sum(vs) / len(vs):.6g} per dispatch")
+        if "SQ_INSTS_VALU_MFMA_MOPS_I8" in e:
+            ops = sum(e["SQ_INSTS_VALU_MFMA_MOPS_I8"]) / len(e["SQ_INSTS_VALU_MFMA_MOPS_I8"]) * 512
+            lines.append(f"  int8 MFMA ops: {ops / 1e9:.2f} G per dispatch -> {ops / dur / 1e12:.1f} TOP/s = "
+                         f"{ops / dur / peak_ops:.4f} of {peak_ops / 1e15:.1f} POP/s")
+    with open(out_path, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def stats_summary(d, out_path, command, top=8):
     """Top kernels of a rocprofv3 --kernel-trace --stats run, as text."""
     import csv
@@ -395,6 +440,8 @@ def main():
     ap.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "OUT"),
                     help="summarize two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of --profile c2")
     ap.add_argument("--stats-summary", nargs=2, metavar=("DIR", "OUT"), help="summarize a rocprofv3 --stats run")
+    ap.add_argument("--mfma-summary", nargs=2, metavar=("DIR", "OUT"),
+                    help="int8 MFMA utilisation of the prefill kernels from a rocprofv3 --pmc run of --profile c3")
     ap.add_argument("--command", default="", help="command line recorded in a summary")
     args = ap.parse_args()
     if args.pmc_summary:
@@ -402,6 +449,9 @@ def main():
         return
     if args.stats_summary:
         stats_summary(*args.stats_summary, args.command)
+        return
+    if args.mfma_summary:
+        mfma_summary(*args.mfma_summary, args.command)
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the expert axis would "
