@@ -410,6 +410,16 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     const int b = (t0 >> 8) + tid - 1;
     atomicAdd(&bcnt[DEC_BCNT_STRIDE * b], (uint32_t)(min(t1, (b + 1) << 8) - max(t0, b << 8)));
   }
+  // Clear the other counter set for the next call: its last users were the
+  // previous call's workgroups, all finished.  Issued here by wave 0, behind
+  // its atomics (at the start these stores sat in the memory counter ahead of
+  // the router's loads; at the end their acknowledgements delayed the exit).
+  {
+    uint32_t *const other = a.sync + DEC_BLK_BASE + DEC_BCNT_STRIDE * DEC_MAX_ABLK * (int)((epoch + 1u) & 1u);
+    for (int i = g + G * tid; tid < 64 && i < DEC_MAX_ABLK; i += G * 64) st_co(other + DEC_BCNT_STRIDE * i, 0u);
+    if (g == G - 1 && tid < DEC_NCNT)
+      st_co(a.sync + DEC_CNT_STRIDE * (1 + DEC_NCNT * (int)((epoch + 1u) & 1u) + tid), 0u);
+  }
   ZM_TRACE(3);
 
   // act rows of this workgroup's tokens (at most two) -> Q8_K in LDS; the rows
@@ -539,6 +549,14 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   }
   __syncthreads();
   ZM_TRACE(4);
+  // workgroup 0 reads the arrival counters now, so that the read is back by
+  // the end of the down rows (all workgroups have arrived by then in practice:
+  // their arrivals precede the act blocks this workgroup has just waited for)
+  int arrived = 0;
+  if (g == 0 && wave == 0) {
+    const int c = lane < DEC_NCNT ? (int)ld_co(&cnt[DEC_CNT_STRIDE * lane]) : 0;
+    arrived = __builtin_amdgcn_readlane(group_sum_i<16>(c), 0);
+  }
 
   if (!s_err) {
     for (int st = 0; st < nst2; ++st) {
@@ -577,23 +595,13 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     }
   }
   ZM_TRACE(5);
-  // clear the other counter set for the next call: its last users were the
-  // previous call's workgroups, all finished.  Done here, off the critical
-  // path: at the start these stores sat in the memory counter ahead of the
-  // router's loads and delayed workgroup 0 by ~2 us.
-  {
-    uint32_t *const other = a.sync + DEC_BLK_BASE + DEC_BCNT_STRIDE * DEC_MAX_ABLK * (int)((epoch + 1u) & 1u);
-    for (int i = g * DEC_THREADS + tid; i < DEC_MAX_ABLK; i += G * DEC_THREADS) st_co(other + DEC_BCNT_STRIDE * i, 0u);
-    if (g == G - 1 && tid < DEC_NCNT)
-      st_co(a.sync + DEC_CNT_STRIDE * (1 + DEC_NCNT * (int)((epoch + 1u) & 1u) + tid), 0u);
-  }
   // workgroup 0 retires the epoch once every workgroup has arrived (each read
   // the epoch before arriving); after an expired wait the epoch stays (the host
   // resets the sync words)
   if (g == 0 && wave == 0) {
     int spins = 0;
     bool ok = true;
-    while (true) {
+    while (arrived < G) {
       const int c = lane < DEC_NCNT ? (int)ld_co(&cnt[DEC_CNT_STRIDE * lane]) : 0;
       const int total = __builtin_amdgcn_readlane(group_sum_i<16>(c), 0);
       if (total >= G) break;
