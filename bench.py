@@ -183,6 +183,7 @@ def run_config(torch, Z, name, steps, warmup, replicas, use_graph=True, kernel_l
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / steps
+    check_status(layers, S, name)
     # algorithmic bytes: each touched resident expert's gate+up+down once, plus
     # shared expert, fp32 router and f32 activations in/out
     ids_h = ids[warmup:].cpu().numpy().reshape(steps, -1)
@@ -208,7 +209,19 @@ def run_config(torch, Z, name, steps, warmup, replicas, use_graph=True, kernel_l
                    mfma_frac=ops / (ms * 1e-3) / INT8_PEAK_OPS)
     if kernel_launches:
         res["kernel_us"] = time_launches(torch, step, warmup, min(steps, kernel_launches))
+        check_status(layers, S, name)
     return res
+
+
+def check_status(layers, S, name):
+    """Every layer replica's error word after a timed region: a decode launch
+    whose bounded wait expired writes NaN rows instead of results, and a
+    number measured over such launches is not reported."""
+    bad = {i: st for i, L in enumerate(layers) if (st := L.status(S)) != 0}
+    if bad:
+        print(f"bench.py: {name}: decode wait expired on layer replicas {bad}; no result is reported",
+              file=sys.stderr)
+        sys.exit(3)
 
 
 def time_launches(torch, step, first, n):

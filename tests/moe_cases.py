@@ -70,6 +70,8 @@ class Cfg:
     F_shared: int = 0
     t_shared: int = Q4
     router_gemv: bool = False
+    sel_bias_sd: float = 0.0        # selection-only bias N(0, sd) (moe_routed_ggml.hpp:77-104)
+    route_mask: bool = False        # non-binary per-expert mask with the slot table (moe_partial_route_ggml.hpp:21-35)
 
 
 CONFIGS = {
@@ -109,6 +111,15 @@ class Built:
             rmap = np.full(c.E, -1, np.int32)
             rmap[perm[: c.n_slots]] = np.arange(c.n_slots, dtype=np.int32)
             self.route_map = rmap
+        self.sel_bias = (rng.standard_normal(c.E) * c.sel_bias_sd).astype(np.float32) if c.sel_bias_sd else None
+        self.route_mask = None
+        if c.route_mask:
+            # resident experts: weights in [0.25, 1.25) with every 7th one 0 (the
+            # route runs, its output is weighted out); others: arbitrary values
+            # that the slot table's -1 must override
+            m = rng.uniform(0.25, 1.25, c.E).astype(np.float32)
+            m[::7] = 0.0
+            self.route_mask = m
         self.router_w = None
         if c.router_gemv:
             self.router_w = (rng.standard_normal((c.E, c.H)) * 0.02).astype(np.float32)
@@ -128,7 +139,7 @@ class Built:
                           gating={0: "softmax", 1: "sigmoid", 2: "sqrt_softplus"}[c.gating],
                           n_groups=c.groups, n_groups_used=c.groups_used, weights_norm=c.norm,
                           weights_scale=c.scale, router_w=t(self.router_w), logit_bias=t(self.logit_bias),
-                          route_map=t(self.route_map),
+                          sel_bias=t(self.sel_bias), route_map=t(self.route_map), route_mask=t(self.route_mask),
                           F_shared=c.F_shared, type_shared=c.t_shared,
                           ws_gate=self.sg if c.F_shared else None, ws_up=self.su if c.F_shared else None,
                           ws_down=self.sd if c.F_shared else None)
@@ -141,9 +152,10 @@ class Built:
     def oracle_route(self, logits=None):
         c = self.c
         lg = self.oracle_logits() if logits is None else logits
-        ids, w = O.router(lg, c.K, c.gating, self.logit_bias, None, c.groups, c.groups_used, c.norm, c.scale)
+        ids, w = O.router(lg, c.K, c.gating, self.logit_bias, self.sel_bias, c.groups, c.groups_used, c.norm,
+                          c.scale)
         if self.route_map is not None:
-            ids, w = O.apply_slot_table(self.route_map, ids, w)
+            ids, w = O.apply_slot_table(self.route_map, ids, w, self.route_mask)
         return ids, w
 
     def oracle_forward(self, ids, w, nthreads=8):

@@ -219,6 +219,44 @@ def test_router_ids_bit_exact(name):
         np.testing.assert_allclose(w2.cpu().numpy(), w_r2, rtol=1e-6, atol=0)
 
 
+@pytest.mark.parametrize("gating", [0, 1])
+def test_router_sel_bias_and_route_mask(gating):
+    """Selection bias (added for selection only; the weights gather the
+    unbiased probabilities, moe_routed_ggml.hpp:77-141) and a non-binary
+    route_mask with the slot table (w' = w * mask[id], ids' = route_map[id],
+    moe_partial_route_ggml.hpp:21-35): ids bit-exact, weights to 1e-6."""
+    import zeromoe_amd as Z
+
+    rng = np.random.default_rng(17 + gating)
+    S, E, K = 96, 256, 8
+    lg = rng.standard_normal((S, E)).astype(np.float32)
+    sb = (rng.standard_normal(E) * (0.3 if gating else 0.05)).astype(np.float32)
+    lb = (rng.standard_normal(E) * 0.5).astype(np.float32)
+    groups = (8, 4) if gating else (0, 0)
+    ids_r, w_r = O.router(lg, K, gating, lb, sb, groups[0], groups[1], True, 2.5)
+    # biased selection must differ from the unbiased one somewhere, or the test pins nothing
+    ids_u, _ = O.router(lg, K, gating, lb, None, groups[0], groups[1], True, 2.5)
+    assert not np.array_equal(ids_u, ids_r)
+    perm = rng.permutation(E)
+    rmap = np.full(E, -1, np.int32)
+    rmap[perm[:96]] = np.arange(96, dtype=np.int32)
+    mask = rng.uniform(0.25, 1.25, E).astype(np.float32)
+    mask[::7] = 0.0
+    t = lambda a: torch.from_numpy(a).cuda()
+    g = {0: "softmax", 1: "sigmoid"}[gating]
+    ids, w = Z.router(t(lg), K, g, logit_bias=t(lb), sel_bias=t(sb), n_groups=groups[0], n_groups_used=groups[1],
+                      weights_norm=True, weights_scale=2.5)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_r)
+    np.testing.assert_allclose(w.cpu().numpy(), w_r, rtol=1e-6, atol=0)
+    ids2, w2 = Z.router(t(lg), K, g, logit_bias=t(lb), sel_bias=t(sb), n_groups=groups[0],
+                        n_groups_used=groups[1], weights_norm=True, weights_scale=2.5, route_map=t(rmap),
+                        route_mask=t(mask))
+    i_r2, w_r2 = O.apply_slot_table(rmap, ids_r, w_r, mask)
+    np.testing.assert_array_equal(ids2.cpu().numpy(), i_r2)
+    np.testing.assert_allclose(w2.cpu().numpy(), w_r2, rtol=1e-6, atol=0)
+    assert (i_r2 < 0).any() and ((w_r2 == 0) & (i_r2 >= 0)).any()
+
+
 def test_router_ties_lowest_index():
     import zeromoe_amd as Z
 
@@ -295,6 +333,12 @@ LAYER_CASES = {
     "iq3xxs_S1": (CONFIGS["c2"], dict(tg=IQ3, td=IQ3)),
     "iq3xxs_S16": (CONFIGS["c2"], dict(tg=IQ3, td=IQ3, S=16, H=2048, F=768)),
     "q4k_q5k_shared_q6k": (CONFIGS["c5"], dict(tg=Q4, td=Q5, t_shared=Q6, H=2048, F=512, F_shared=1024)),
+    # selection-only bias and a non-binary slot-table mask (fused decode at S=1,
+    # the multi-kernel path at S=64), and a selection bias on softmax gating
+    "c5_selbias_mask_S1": (CONFIGS["c5"], dict(sel_bias_sd=0.3, route_mask=True)),
+    "c5_selbias_mask_S64": (CONFIGS["c5"], dict(S=64, H=2048, F=1024, F_shared=1024, sel_bias_sd=0.3,
+                                                route_mask=True)),
+    "c2_selbias_S4": (CONFIGS["c2"], dict(S=4, sel_bias_sd=0.05)),
 }
 
 
@@ -347,6 +391,8 @@ FUSED_CASES = {
     "iq4xs": (CONFIGS["c2"], dict(tg=IQ4, td=IQ4)),
     "iq4xs_S3": (CONFIGS["c2"], dict(tg=IQ4, td=IQ4, S=3)),
     "iq3xxs": (CONFIGS["c2"], dict(tg=IQ3, td=IQ3)),
+    "c5_selbias_mask": (CONFIGS["c5"], dict(sel_bias_sd=0.3, route_mask=True)),
+    "c5_S3_selbias_mask": (CONFIGS["c5"], dict(S=3, sel_bias_sd=0.3, route_mask=True)),
 }
 
 
@@ -407,6 +453,41 @@ def test_fused_decode_varying_routes(case, monkeypatch):
     assert L.status(c.S) == 0
     if b.route_map is not None:
         assert len(n_routes) > 1, n_routes
+
+
+def test_fused_decode_expired_wait_is_loud_and_recovers(monkeypatch):
+    """The fused kernel's bounded waits forced to give up from the host (a
+    spin limit of 0 polls): the launch still completes; rows whose wait
+    expired are NaN, never stale; the next launch, which finds the error word
+    set, writes NaN everywhere instead of trusting the counters; zm_moe_status
+    reports the error and resets the sync words, and the launch after that
+    matches the oracle again."""
+    c = CONFIGS["c2"]
+    b = Built(c, seed=61)
+    L = b.layer()
+    x = torch.from_numpy(b.x).cuda()
+    lg = torch.from_numpy(b.logits).cuda()
+    monkeypatch.setenv("ZEROMOE_FUSED_DECODE", "1")
+    monkeypatch.setenv("ZEROMOE_SPIN_LIMIT", "0")
+    out1, ids, w = L.forward(x, lg)
+    out1 = out1.clone()
+    monkeypatch.delenv("ZEROMOE_SPIN_LIMIT")
+    out2, _, _ = L.forward(x, lg)
+    _sync()
+    err = L.status(c.S)
+    ids_h, w_h = ids.cpu().numpy(), w.cpu().numpy()
+    ref = b.oracle_forward(ids_h, w_h)
+    if err:
+        assert np.isnan(out1.cpu().numpy()).any()
+        assert np.isnan(out2.cpu().numpy()).all()
+    else:  # every first poll already saw its data: nothing expired, results stand
+        assert_close_layer(out1.cpu().numpy(), ref)
+        assert_close_layer(out2.cpu().numpy(), ref)
+    assert L.status(c.S) == 0
+    out3, _, _ = L.forward(x, lg)
+    _sync()
+    assert L.status(c.S) == 0
+    assert_close_layer(out3.cpu().numpy(), ref)
 
 
 @pytest.mark.parametrize("case", ["c2", "c3_small"])
@@ -478,3 +559,31 @@ def test_prefill_mfma_vs_gemv(case, monkeypatch):
     # slack bound): the layer bar then applies between the paths too.
     rtol = 1e-3 if c.F_shared else 1e-4
     assert_close_layer(out1.cpu().numpy(), out2.cpu().numpy(), rtol=rtol, slack=lambda: 2 * slack())
+
+
+def test_c3_full_size_vs_oracle():
+    """Config c3 at its stated size: H=4096, F=1536, 128 Q4_K experts, top-8
+    softmax, S=512, per-expert logit bias N(0,1.5) (0 to ~150 pairs per
+    expert, the heaviest buckets cut into several MFMA work items).  Router
+    ids bit-exact, weights to 1e-5, bucket arrays bit-exact, and the whole
+    layer against the oracle on every token within the layer bar."""
+    import zeromoe_amd as Z
+
+    c = CONFIGS["c3"]
+    b = Built(c, seed=51)
+    L = b.layer()
+    x = torch.from_numpy(b.x).cuda()
+    out, ids, w = L.forward(x, torch.from_numpy(b.logits).cuda())
+    _sync()
+    ids_r, w_r = b.oracle_route()
+    ids_h, w_h = ids.cpu().numpy(), w.cpu().numpy()
+    np.testing.assert_array_equal(ids_h, ids_r)
+    np.testing.assert_allclose(w_h, w_r, rtol=1e-5, atol=1e-7)
+    counts, offs, pairs, active, n_active = Z.bucket(ids, c.E)
+    rc, ro, rp = O.bucket(ids_r, c.E)
+    np.testing.assert_array_equal(counts.cpu().numpy(), rc)
+    np.testing.assert_array_equal(offs.cpu().numpy(), ro)
+    np.testing.assert_array_equal(pairs.cpu().numpy()[: len(rp)], rp)
+    assert rc.max() >= 100, rc.max()  # skewed: several work items for the heaviest experts
+    ref = b.oracle_forward(ids_h, w_h, nthreads=16)
+    assert_close_layer(out.cpu().numpy(), ref, slack=lambda: b.requant_slack(ids_h, w_h))

@@ -32,10 +32,13 @@ def test_dot_bit_exact_vs_reference_golden(name, t):
         assert f32bits(got) == f32bits(g[name + "_dot"][i]), (name, i)
 
 
-@pytest.mark.skipif(O.ref_lib() is None, reason="oracle/_ref not built (needs /root/reference)")
 @pytest.mark.parametrize("t", [O.TYPE_Q2_K, O.TYPE_Q4_K])
 def test_dot_bit_exact_vs_reference_live(t):
+    # Looked up inside the test, not at collection: a GPU-only run never maps
+    # the reference build.
     R = O.ref_lib()
+    if R is None:
+        pytest.skip("oracle/_ref not built (needs /root/reference)")
     fn = R.zmref_dot_q2_K if t == O.TYPE_Q2_K else R.zmref_dot_q4_K
     rng = np.random.default_rng(7)
     for trial in range(300):

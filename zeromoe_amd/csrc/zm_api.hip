@@ -776,6 +776,8 @@ int launch_fused(const zm_moe_layer *L, const float *x, const float *logits, int
   a.grid = uses(T_IQ4_XS) ? d->iq4 : (uses(T_IQ3_XXS) ? d->iq3 : d->grid);
   a.signs = d->signs;
   a.spin_limit = 1 << 23;
+  if (const char *sl = getenv("ZEROMOE_SPIN_LIMIT"); sl && sl[0])  // test hook: force the bounded waits to give up
+    a.spin_limit = atoi(sl);
   if (const char *tr = getenv("ZEROMOE_TRACE"); tr && tr[0] == '1') {
     DeviceState *dm = const_cast<DeviceState *>(d);
     if (dm->trace_n < (size_t)G * 8) {

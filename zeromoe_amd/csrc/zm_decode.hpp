@@ -139,6 +139,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   __shared__ int s_doff[DEC_MAX_PAIRS];  // pair -> down expert byte offset (or -1)
   __shared__ int s_nvp;
   __shared__ int s_err;
+  __shared__ uint32_t s_stale;
   __shared__ __attribute__((aligned(16))) uint8_t s_q8[DEC_LDS_Q8];
   __shared__ float4 s_stage[DEC_WAVES][256];  // per wave: router scratch, then the act transpose
   constexpr bool kIQ2 = TG == T_IQ2_XXS || TD == T_IQ2_XXS || TS == T_IQ2_XXS;
@@ -162,6 +163,12 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   ZM_TRACE(0);
   // counter set of this call (the other set is cleared at the end, for the next call)
   const uint32_t epoch = __builtin_amdgcn_readfirstlane(ld_co(&a.sync[0]));
+  // An earlier call's wait expired (error word set): its counters are in an
+  // unknown state, so none of them is trusted.  The word is read here by one
+  // thread and acted on after the first workgroup barrier (a uniform decision):
+  // every workgroup writes NaN to its output rows and leaves.  zm_moe_status
+  // reports the error and resets the sync words; calls then run normally.
+  if (tid == 0) s_stale = ld_co(&a.sync[1]);
   uint32_t *const cnt = a.sync + DEC_CNT_STRIDE * (1 + DEC_NCNT * (int)(epoch & 1u));
   uint32_t *const bcnt = a.sync + DEC_BLK_BASE + DEC_BCNT_STRIDE * DEC_MAX_ABLK * (int)(epoch & 1u);
 
@@ -230,6 +237,12 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   }
   ZM_TRACE(7);
   __syncthreads();
+  if (s_stale != 0u) {
+    const int T2e = S * H;
+    const int v0 = (int)((long)T2e * g / G), v1 = (int)((long)T2e * (g + 1) / G);
+    for (int j = v0 + tid; j < v1; j += DEC_THREADS) a.out[j] = __builtin_nanf("");
+    return;
+  }
   if (S > 1 && wave == 0) {
     // compact the routed pairs (id >= 0) in pair order: ballot + prefix count
     int n = 0;
@@ -558,7 +571,10 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     arrived = __builtin_amdgcn_readlane(group_sum_i<16>(c), 0);
   }
 
-  if (!s_err) {
+  if (s_err) {
+    // this call's wait expired: its output rows are marked, not left stale
+    for (int j = u0 + tid; j < u1; j += DEC_THREADS) bst(rout, 4 * j, __builtin_nanf(""));
+  } else {
     for (int st = 0; st < nst2; ++st) {
       bool valid;
       int s, h;
