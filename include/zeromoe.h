@@ -94,10 +94,33 @@ int zm_mul_mat_id_negative_skip_batched(void);
  *   dst : F32 [O, n_ids, S]
  * execute = 0 is a pure capability query; execute = 1 launches on `stream`.
  * Returns 1 when handled/supported, 0 when declined.
+ * Like the reference hook it allocates nothing and borrows every tensor
+ * (kquant_matmul.cu:644-646): its scratch (Q8_K rows of src1, the bucket
+ * arrays) lives in a caller-owned workspace bound to the stream with
+ * zm_mul_mat_id_set_workspace.  The query (any stream, ggml passes NULL)
+ * accepts a shape only if the smallest workspace bound on the current device
+ * holds it; an execute call uses the workspace bound to its stream and
+ * declines when there is none or it is too small.  Calls on one stream are
+ * stream-ordered; streams with workspaces of their own never share scratch.
+ * Launches only (kernels and one device-to-device copy of ids): safe under
+ * HIP-graph capture once the workspace is bound.
  * Replaces native_f32_quant_hook / zeromoe_install_f32_quant_graph_hook
  * (kernels/quant/kquant_matmul.cu:702-761, patches/ggml/0010-...:9-27). */
 int zm_mul_mat_id(const zm_tensor *src0, const zm_tensor *src1, const zm_tensor *ids, zm_tensor *dst, void *stream,
                   int execute);
+/* Workspace bytes zm_mul_mat_id needs for this shape (0: shape declined).
+ * The reference hook needs none (its FP32 kernels read src1 directly); this
+ * path stages Q8_K activations and expert buckets.  Sizing call for the
+ * workspace of zm_mul_mat_id_set_workspace. */
+size_t zm_mul_mat_id_workspace_size(const zm_tensor *src0, const zm_tensor *src1, const zm_tensor *ids,
+                                    const zm_tensor *dst);
+/* Bind a caller-owned device buffer (256-byte aligned, `bytes` long) as
+ * zm_mul_mat_id's workspace for (current device, stream); NULL unbinds.  At
+ * most 64 bindings.  The caller keeps the buffer alive and unmodified while
+ * work that uses it is queued.  The counterpart of the scratch a ggml backend
+ * context owns per stream (the reference hook's caller,
+ * patches/ggml/0010-...:57-61, passes ctx.stream()). */
+int zm_mul_mat_id_set_workspace(void *stream, void *workspace, size_t bytes);
 /* Count of executed zm_mul_mat_id launches (kquant_matmul.cu:762-764). */
 uint64_t zm_mul_mat_id_launches(void);
 

@@ -184,6 +184,156 @@ def test_iq3_xxs_custom_grid():
         lib_o.zmo_set_iq3xxs_grid(default.ctypes.data)
 
 
+def _hook_descs(W, t, I, x, ids, y):
+    import ctypes as C
+
+    from zeromoe_amd.ops import _tensor
+
+    return [C.byref(d) for d in (_tensor(t, W, I), _tensor(0, x, None), _tensor(26, ids, None), _tensor(0, y, None))]
+
+
+def test_mul_mat_id_workspace_binding_rules():
+    """The hook allocates nothing: it declines (query and execute) without a
+    workspace bound on the device/stream or with one too small, and runs once
+    one is bound; the query uses the smallest workspace bound on the device."""
+    from zeromoe_amd._lib import lib
+    from zeromoe_amd.ops import _MMID_WS
+
+    L = lib()
+    for (dev, st), _ in list(_MMID_WS.items()):  # start from no bindings
+        assert L.zm_mul_mat_id_set_workspace(st, None, 0) == 0
+    _MMID_WS.clear()
+    rng = np.random.default_rng(8)
+    E, O_, I, S = 6, 64, 1024, 5
+    W = torch.from_numpy(O.random_blocks(Q4, E * O_, I, seed=3).reshape(E, O_, -1)).cuda()
+    x = torch.from_numpy(rng.standard_normal((S, 1, I)).astype(np.float32)).cuda()
+    ids = torch.from_numpy(np.stack([rng.permutation(E)[:4] for _ in range(S)]).astype(np.int32)).cuda()
+    y = torch.full((S, 4, O_), 7.0, device="cuda")
+    d = _hook_descs(W, Q4, I, x, ids, y)
+    need = L.zm_mul_mat_id_workspace_size(*d)
+    assert need > 0
+    st = torch.cuda.current_stream().cuda_stream
+    assert L.zm_mul_mat_id(*d, None, 0) == 0  # nothing bound
+    assert L.zm_mul_mat_id(*d, st, 1) == 0
+    small = torch.empty(need - 256, dtype=torch.uint8, device="cuda")
+    assert L.zm_mul_mat_id_set_workspace(st, small.data_ptr(), small.numel()) == 0
+    assert L.zm_mul_mat_id(*d, None, 0) == 0 and L.zm_mul_mat_id(*d, st, 1) == 0
+    _sync()
+    assert (y == 7.0).all()  # a declined call launches nothing
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    assert L.zm_mul_mat_id_set_workspace(st, ws.data_ptr(), ws.numel()) == 0
+    assert L.zm_mul_mat_id(*d, None, 0) == 1
+    other = torch.cuda.Stream()
+    assert L.zm_mul_mat_id(*d, other.cuda_stream, 1) == 0  # no workspace on that stream
+    assert L.zm_mul_mat_id(*d, st, 1) == 1
+    _sync()
+    ref = O.mul_mat_id(Q4, W.cpu().numpy(), x.cpu().numpy(), ids.cpu().numpy(), nthreads=8)
+    np.testing.assert_allclose(y.cpu().numpy(), ref, rtol=1e-3, atol=1e-3 * np.abs(ref).max())
+    # the query takes the smallest binding on the device
+    assert L.zm_mul_mat_id_set_workspace(other.cuda_stream, small.data_ptr(), small.numel()) == 0
+    assert L.zm_mul_mat_id(*d, None, 0) == 0
+    assert L.zm_mul_mat_id_set_workspace(other.cuda_stream, None, 0) == 0
+    assert L.zm_mul_mat_id_set_workspace(st, None, 0) == 0
+    assert L.zm_mul_mat_id(*d, None, 0) == 0
+
+
+@pytest.mark.parametrize("case", ["decode", "prefill_mfma", "strided_ids_ne11"])
+def test_mul_mat_id_hook_graph_capture_replays_bit_exact(case):
+    """The hook recorded into a HIP graph on a stream with a bound workspace,
+    replayed several times with eager hook calls (other inputs, same
+    workspace) in between: every replay gives the eager result bit for bit."""
+    from zeromoe_amd._lib import lib
+
+    L = lib()
+    rng = np.random.default_rng(21)
+    t, E, O_, I, S, n_ids, ne11 = {"decode": (Q2, 16, 512, 2048, 1, 8, 1),
+                                   "prefill_mfma": (Q4, 8, 256, 1024, 64, 8, 1),
+                                   "strided_ids_ne11": (Q3, 12, 192, 1536, 6, 4, 4)}[case]
+    W = torch.from_numpy(O.random_blocks(t, E * O_, I, seed=5).reshape(E, O_, -1)).cuda()
+    x = torch.from_numpy(rng.standard_normal((S, ne11, I)).astype(np.float32)).cuda()
+    ids_np = np.stack([rng.permutation(E)[:n_ids] for _ in range(S)]).astype(np.int32)
+    ids_np[0, 1] = -1
+    if case == "strided_ids_ne11":  # ids with a row stride larger than n_ids
+        big = torch.from_numpy(np.pad(ids_np, ((0, 0), (0, 3)))).cuda()
+        ids = big[:, :n_ids]
+    else:
+        ids = torch.from_numpy(ids_np).cuda()
+    y = torch.empty((S, n_ids, O_), device="cuda")
+    d = _hook_descs(W, t, I, x, ids, y)
+    s = torch.cuda.Stream()
+    ws = torch.empty(L.zm_mul_mat_id_workspace_size(*d), dtype=torch.uint8, device="cuda")
+    assert L.zm_mul_mat_id_set_workspace(s.cuda_stream, ws.data_ptr(), ws.numel()) == 0
+    try:
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            assert L.zm_mul_mat_id(*d, s.cuda_stream, 1) == 1
+        s.synchronize()
+        eager = y.clone()
+        ref = O.mul_mat_id(t, W.cpu().numpy(), x.cpu().numpy(), ids_np, nthreads=8)
+        np.testing.assert_allclose(eager.cpu().numpy(), ref, rtol=1e-3, atol=1e-3 * np.abs(ref).max())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            assert L.zm_mul_mat_id(*d, s.cuda_stream, 1) == 1
+        x2 = torch.randn_like(x)
+        y2 = torch.empty_like(y)
+        d2 = _hook_descs(W, t, I, x2, ids, y2)
+        for rep in range(4):
+            y.fill_(float(rep))
+            g.replay()
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(y.cpu().numpy(), eager.cpu().numpy())
+            with torch.cuda.stream(s):  # eager use of the same workspace between replays
+                assert L.zm_mul_mat_id(*d2, s.cuda_stream, 1) == 1
+            s.synchronize()
+    finally:
+        L.zm_mul_mat_id_set_workspace(s.cuda_stream, None, 0)
+
+
+def test_mul_mat_id_two_streams_concurrent():
+    """Two streams with their own workspaces running the hook at the same
+    time on different inputs: both results are right (no shared scratch)."""
+    import zeromoe_amd as Z
+
+    rng = np.random.default_rng(4)
+    E, O_, I, S = 8, 384, 2048, 48
+    W = O.random_blocks(Q4, E * O_, I, seed=9).reshape(E, O_, -1)
+    Wd = torch.from_numpy(W).cuda()
+    xs = [rng.standard_normal((S, 1, I)).astype(np.float32) for _ in range(2)]
+    idss = [np.stack([rng.permutation(E)[:8] for _ in range(S)]).astype(np.int32) for _ in range(2)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [None, None]
+    for rep in range(3):
+        for i, s in enumerate(streams):
+            with torch.cuda.stream(s):
+                outs[i] = Z.mul_mat_id(Wd, Q4, I, torch.from_numpy(xs[i]).cuda(), torch.from_numpy(idss[i]).cuda(),
+                                       stream=s)
+        torch.cuda.synchronize()
+        for i in range(2):
+            ref = O.mul_mat_id(Q4, W, xs[i], idss[i], nthreads=8)
+            np.testing.assert_allclose(outs[i].cpu().numpy(), ref, rtol=1e-3, atol=1e-3 * np.abs(ref).max())
+
+
+def test_mul_mat_id_many_pairs_grid_stride():
+    """More than 65535 (token, slot) pairs with negative and out-of-range ids:
+    the skipped rows are strided over the launch grid (zero / NaN rows)."""
+    import zeromoe_amd as Z
+
+    rng = np.random.default_rng(6)
+    E, O_, I, S, n_ids = 4, 16, 256, 9000, 8
+    ids = rng.integers(-1, E, (S, n_ids)).astype(np.int32)
+    ids[-1, -1] = E + 3
+    W = O.random_blocks(Q4, E * O_, I, seed=2).reshape(E, O_, -1)
+    x = rng.standard_normal((S, 1, I)).astype(np.float32)
+    got = Z.mul_mat_id(torch.from_numpy(W).cuda(), Q4, I, torch.from_numpy(x).cuda(),
+                       torch.from_numpy(ids).cuda()).cpu().numpy()
+    assert np.isnan(got[-1, -1]).all()
+    neg = ids < 0
+    assert neg[S // 2:].any() and not got[neg].any()
+    ok = (ids >= 0) & (ids < E)
+    ref = O.mul_mat_id(Q4, W, x, np.where(ok, ids, -1).astype(np.int32), nthreads=8)
+    np.testing.assert_allclose(got[ok], ref[ok], rtol=1e-3, atol=1e-3 * np.abs(ref).max())
+
+
 def test_mul_mat_id_out_of_range_is_nan():
     ids = np.array([[2, 99]], np.int32)
     got, _ = _mmid_case(Q2, 512, 8, 4, np.array([[2, 1]], np.int32), 1, seed=1)

@@ -44,8 +44,6 @@ struct DeviceState {
   uint64_t *signs = nullptr;  // 128 x u64 byte masks of ksigns_iq2xs
   uint64_t *iq4 = nullptr;    // IQ4_XS value table, 16 x i8
   uint64_t *iq3 = nullptr;    // IQ3_XXS grid, 256 x u32
-  void *ws = nullptr;         // zm_mul_mat_id workspace
-  size_t ws_size = 0;
   uint64_t *trace = nullptr;  // decode-kernel phase timestamps (ZEROMOE_TRACE=1)
   size_t trace_n = 0;
 };
@@ -392,104 +390,123 @@ int zm_bucket(const int32_t *ids, int S, int K, int E, int32_t *counts, int32_t 
 
 // ---------------------------------------------------------------- mul_mat_id hook
 
-int zm_mul_mat_id(const zm_tensor *w, const zm_tensor *x, const zm_tensor *ids, zm_tensor *y, void *stream,
-                  int execute) {
-  if (!w || !x || !ids || !y) return 0;
-  if (!type_supported(w->type) || x->type != T_F32 || y->type != T_F32 || ids->type != T_I32) return 0;
+}  // extern "C"
+
+namespace {
+
+// A validated MUL_MAT_ID shape (see zm_mul_mat_id's rules) and the workspace
+// it needs: planar Q8_K rows of src1, a contiguous copy of ids, the bucket
+// arrays and the MFMA work list.
+struct MmidShape {
+  int64_t I, O, E, n_ids, S, ne11, n_pairs, nq;
+  int nb;
+  size_t ws_bytes;
+};
+
+struct MmidWs {
+  uint8_t *xq;
+  int32_t *idc, *counts, *offs, *pairs, *active, *n_active, *items, *n_items;
+};
+
+size_t mmid_carve(const MmidShape &m, uint8_t *base, MmidWs *out) {
+  Bump b{base};
+  MmidWs w{};
+  w.xq = b.take<uint8_t>((size_t)m.nq * q8_row_bytes(m.nb));
+  w.idc = b.take<int32_t>((size_t)m.n_pairs * 4);
+  w.counts = b.take<int32_t>((size_t)m.E * 4);
+  w.offs = b.take<int32_t>((size_t)(m.E + 1) * 4);
+  w.pairs = b.take<int32_t>((size_t)m.n_pairs * 4);
+  w.active = b.take<int32_t>((size_t)m.E * 4);
+  w.n_active = b.take<int32_t>(4);
+  w.items = b.take<int32_t>((size_t)mmq_max_items((int)m.n_pairs, (int)m.E) * 4);
+  w.n_items = b.take<int32_t>(4);
+  if (out) *out = w;
+  return b.off + 256;
+}
+
+// The validation rules of the reference hook (kquant_matmul.cu:705-722) plus
+// this kernel set's limits; false = decline.
+bool mmid_shape(const zm_tensor *w, const zm_tensor *x, const zm_tensor *ids, const zm_tensor *y, MmidShape *m) {
+  if (!w || !x || !ids || !y) return false;
+  if (!type_supported(w->type) || x->type != T_F32 || y->type != T_F32 || ids->type != T_I32) return false;
   const int64_t I = w->ne[0], O = w->ne[1], E = w->ne[2];
   if (I <= 0 || I % QK || I / QK > 64 || O <= 0 || O > INT32_MAX || E <= 0 || E > BUCKET_MAX_E || w->ne[3] != 1)
-    return 0;
-  if (w->nb[1] != row_bytes(w->type, I) || w->nb[2] < (size_t)O * w->nb[1]) return 0;
+    return false;
+  if (w->nb[1] != row_bytes(w->type, I) || w->nb[2] < (size_t)O * w->nb[1]) return false;
   const int64_t n_ids = ids->ne[0], S = ids->ne[1];
-  if (ids->nb[0] != 4 || n_ids <= 0 || S <= 0 || ids->ne[2] != 1 || ids->ne[3] != 1) return 0;
+  if (ids->nb[0] != 4 || n_ids <= 0 || S <= 0 || ids->ne[2] != 1 || ids->ne[3] != 1) return false;
   if (x->nb[0] != 4 || x->ne[0] != I || (x->ne[1] != 1 && x->ne[1] != n_ids) || x->ne[2] != S || x->ne[3] != 1)
-    return 0;
-  if (x->nb[1] % 16 || x->nb[2] % 16 || ((uintptr_t)x->data & 15)) return 0;  // float4 row loads
-  if (y->nb[0] != 4 || y->ne[0] != O || y->ne[1] != n_ids || y->ne[2] != S || y->ne[3] != 1) return 0;
-  if (y->nb[1] % 4 || y->nb[2] % 4 || ids->nb[1] % 4) return 0;
+    return false;
+  if (x->nb[1] % 16 || x->nb[2] % 16 || ((uintptr_t)x->data & 15)) return false;  // float4 row loads
+  if (y->nb[0] != 4 || y->ne[0] != O || y->ne[1] != n_ids || y->ne[2] != S || y->ne[3] != 1) return false;
+  if (y->nb[1] % 4 || y->nb[2] % 4 || ids->nb[1] % 4) return false;
   const int64_t n_pairs = n_ids * S;
-  if (n_pairs > (1 << 24)) return 0;
-  if (!execute) return 1;
+  if (n_pairs > (1 << 24)) return false;
+  m->I = I;
+  m->O = O;
+  m->E = E;
+  m->n_ids = n_ids;
+  m->S = S;
+  m->ne11 = x->ne[1];
+  m->n_pairs = n_pairs;
+  m->nq = m->ne11 * S;
+  m->nb = (int)(I / QK);
+  m->ws_bytes = mmid_carve(*m, nullptr, nullptr);
+  return true;
+}
 
-  hipStream_t st = (hipStream_t)stream;
-  DeviceState *d;
-  if (device_state(&d)) return 0;
-  const int nb = (int)(I / QK);
-  const int ne11 = (int)x->ne[1];
-  // workspace: q8 rows, a contiguous copy of ids, bucket arrays
-  const int64_t nq = (int64_t)ne11 * S;
-  Bump sz{nullptr};
-  sz.take<uint8_t>((size_t)nq * q8_row_bytes(nb));
-  sz.take<int32_t>((size_t)n_pairs * 4);
-  sz.take<int32_t>((size_t)E * 4);
-  sz.take<int32_t>((size_t)(E + 1) * 4);
-  sz.take<int32_t>((size_t)n_pairs * 4);
-  sz.take<int32_t>((size_t)E * 4);
-  sz.take<int32_t>(4);
-  sz.take<int32_t>((size_t)mmq_max_items((int)n_pairs, (int)E) * 4);
-  sz.take<int32_t>(4);
-  const size_t need = sz.off + 256;
-  if (d->ws_size < need) {
-    if (d->ws) (void)hipFree(d->ws);
-    d->ws = nullptr;
-    d->ws_size = 0;
-    if (hipMalloc(&d->ws, need) != hipSuccess) {
-      fail("zm_mul_mat_id: workspace allocation of %zu bytes failed", need);
-      return 0;
-    }
-    d->ws_size = need;
-  }
-  Bump b{(uint8_t *)d->ws};
-  uint8_t *xq = b.take<uint8_t>((size_t)nq * q8_row_bytes(nb));
-  int32_t *idc = b.take<int32_t>((size_t)n_pairs * 4);
-  int32_t *counts = b.take<int32_t>((size_t)E * 4);
-  int32_t *offs = b.take<int32_t>((size_t)(E + 1) * 4);
-  int32_t *pairs = b.take<int32_t>((size_t)n_pairs * 4);
-  int32_t *active = b.take<int32_t>((size_t)E * 4);
-  int32_t *n_active = b.take<int32_t>(4);
-  int32_t *items = b.take<int32_t>((size_t)mmq_max_items((int)n_pairs, (int)E) * 4);
-  int32_t *n_items = b.take<int32_t>(4);
-
+// The op on a workspace of at least m.ws_bytes (256-byte aligned); launches
+// only, stream-ordered, allocates nothing.  Returns 1 handled / 0 failed.
+int mmid_exec(const MmidShape &m, const zm_tensor *w, const zm_tensor *x, const zm_tensor *ids, zm_tensor *y,
+              hipStream_t st, uint8_t *ws, const DeviceState *d) {
+  MmidWs b;
+  mmid_carve(m, ws, &b);
+  const int nb = m.nb;
+  const int ne11 = (int)m.ne11;
+  const int64_t S = m.S, n_ids = m.n_ids, n_pairs = m.n_pairs, nq = m.nq, E = m.E, O = m.O;
   // 1. quantize src1 rows (token t, row i11) -> planar Q8_K row t*ne11 + i11
   if (x->nb[2] == (size_t)ne11 * x->nb[1]) {
-    if (launch_quant((const float *)x->data, x->nb[1] / 4, nb, (int)nq, xq, q8_row_bytes(nb), 1, st)) return 0;
+    if (launch_quant((const float *)x->data, x->nb[1] / 4, nb, (int)nq, b.xq, q8_row_bytes(nb), 1, st)) return 0;
   } else {
     for (int64_t t = 0; t < S; ++t) {
       const float *xt = (const float *)((const char *)x->data + t * x->nb[2]);
-      if (launch_quant(xt, x->nb[1] / 4, nb, ne11, xq + (size_t)t * ne11 * q8_row_bytes(nb), q8_row_bytes(nb), 1,
+      if (launch_quant(xt, x->nb[1] / 4, nb, ne11, b.xq + (size_t)t * ne11 * q8_row_bytes(nb), q8_row_bytes(nb), 1,
                        st))
         return 0;
     }
   }
   // 2. ids -> contiguous [S][n_ids] (strided copy), then bucket
   if (ids->nb[1] == (size_t)n_ids * 4) {
-    if (hipMemcpyAsync(idc, ids->data, (size_t)n_pairs * 4, hipMemcpyDeviceToDevice, st) != hipSuccess) return 0;
+    if (hipMemcpyAsync(b.idc, ids->data, (size_t)n_pairs * 4, hipMemcpyDeviceToDevice, st) != hipSuccess) return 0;
   } else {
-    if (hipMemcpy2DAsync(idc, (size_t)n_ids * 4, ids->data, ids->nb[1], (size_t)n_ids * 4, (size_t)S,
+    if (hipMemcpy2DAsync(b.idc, (size_t)n_ids * 4, ids->data, ids->nb[1], (size_t)n_ids * 4, (size_t)S,
                          hipMemcpyDeviceToDevice, st) != hipSuccess)
       return 0;
   }
-  hipLaunchKernelGGL(k_bucket, dim3(1), dim3(1024), 0, st, idc, (int)n_pairs, (int)E, counts, offs, pairs, active,
-                     n_active);
-  // 3. skipped / invalid routes
-  hipLaunchKernelGGL(k_fill_skipped, dim3((unsigned)std::min<int64_t>((O + 255) / 256, 64), (unsigned)n_pairs),
-                     dim3(256), 0, st, idc, (size_t)n_ids, (size_t)1, (int)n_ids, (int)S, (int)E, (int)O,
-                     (float *)y->data, y->nb[2] / 4, y->nb[1] / 4);
-  // 4. bucketed GEMV
+  hipLaunchKernelGGL(k_bucket, dim3(1), dim3(1024), 0, st, b.idc, (int)n_pairs, (int)E, b.counts, b.offs, b.pairs,
+                     b.active, b.n_active);
+  // 3. skipped / invalid routes (pairs over grid x and y, each <= 65535)
+  {
+    const unsigned gy = (unsigned)std::min<int64_t>(n_pairs, 65535);
+    hipLaunchKernelGGL(k_fill_skipped, dim3((unsigned)std::min<int64_t>((O + 255) / 256, 64), gy), dim3(256), 0, st,
+                       b.idc, (size_t)n_ids, (size_t)1, (int)n_ids, (int)S, (int)E, (int)O, (float *)y->data,
+                       y->nb[2] / 4, y->nb[1] / 4);
+  }
+  // 4. bucketed GEMV or MFMA
   GemvArgs a{};
   a.w0 = (const uint8_t *)w->data;
   a.w_estride = w->nb[2];
   a.w_rstride = w->nb[1];
   a.nrows = (int)O;
   a.nb = nb;
-  a.xq = xq;
+  a.xq = b.xq;
   a.xq_rstride = q8_row_bytes(nb);
   a.ne11 = ne11;
   a.K = (int)n_ids;
-  a.n_active = n_active;
-  a.active = active;
-  a.offs = offs;
-  a.pairs = pairs;
+  a.n_active = b.n_active;
+  a.active = b.active;
+  a.offs = b.offs;
+  a.pairs = b.pairs;
   a.out = (float *)y->data;
   a.out_s = y->nb[2] / 4;
   a.out_k = y->nb[1] / 4;
@@ -500,16 +517,96 @@ int zm_mul_mat_id(const zm_tensor *w, const zm_tensor *x, const zm_tensor *ids, 
     // the MFMA path addresses the activations through a 32-bit buffer offset
     const double avg = (size_t)nq * q8_row_bytes(nb) < (1ull << 31) ? (double)n_pairs / groups : 0.0;
     if (mmq_applies(w->type, avg))
-      hipLaunchKernelGGL(k_mmq_items, dim3(1), dim3(1024), 0, st, n_active, active, offs, items, n_items,
+      hipLaunchKernelGGL(k_mmq_items, dim3(1), dim3(1024), 0, st, b.n_active, b.active, b.offs, b.items, b.n_items,
                          16 * mmq_tt(w->type, false));
-    a.items = items;
-    a.n_items = n_items;
+    a.items = b.items;
+    a.n_items = b.n_items;
     a.xq_bytes = (uint32_t)((size_t)nq * q8_row_bytes(nb));
     const int rc = launch_mmq(w->type, false, a, mmq_max_items((int)n_pairs, (int)E), avg, mmq_tt(w->type, false), st);
     if (rc < 0 || (rc > 0 && launch_gemv(w->type, false, pick_np((int)n_pairs, (int)E), a, groups, st))) return 0;
   }
-  g_mmid_launches.fetch_add(1, std::memory_order_relaxed);
+  count_mmid_launch();
   return hipPeekAtLastError() == hipSuccess ? 1 : 0;
+}
+
+// Caller-owned workspaces bound to (device, stream) by zm_mul_mat_id_set_workspace.
+struct WsBinding {
+  int dev;
+  hipStream_t stream;
+  uint8_t *ptr;
+  size_t bytes;
+};
+constexpr int kMaxBindings = 64;
+WsBinding g_bind[kMaxBindings];
+int g_nbind = 0;
+std::mutex g_bind_mu;
+
+}  // namespace
+
+extern "C" {
+
+size_t zm_mul_mat_id_workspace_size(const zm_tensor *src0, const zm_tensor *src1, const zm_tensor *ids,
+                                    const zm_tensor *dst) {
+  MmidShape m;
+  return mmid_shape(src0, src1, ids, dst, &m) ? m.ws_bytes : 0;
+}
+
+int zm_mul_mat_id_set_workspace(void *stream, void *workspace, size_t bytes) {
+  int dev = 0;
+  HIP_OK(hipGetDevice(&dev));
+  if (workspace && ((uintptr_t)workspace & 255)) return fail("zm_mul_mat_id_set_workspace: workspace not 256-byte aligned");
+  std::lock_guard<std::mutex> lk(g_bind_mu);
+  for (int i = 0; i < g_nbind; ++i)
+    if (g_bind[i].dev == dev && g_bind[i].stream == (hipStream_t)stream) {
+      if (workspace) {
+        g_bind[i].ptr = (uint8_t *)workspace;
+        g_bind[i].bytes = bytes;
+      } else {
+        g_bind[i] = g_bind[--g_nbind];
+      }
+      return 0;
+    }
+  if (!workspace) return 0;
+  if (g_nbind == kMaxBindings) return fail("zm_mul_mat_id_set_workspace: more than %d bound streams", kMaxBindings);
+  g_bind[g_nbind++] = WsBinding{dev, (hipStream_t)stream, (uint8_t *)workspace, bytes};
+  return 0;
+}
+
+int zm_mul_mat_id(const zm_tensor *w, const zm_tensor *x, const zm_tensor *ids, zm_tensor *y, void *stream,
+                  int execute) {
+  MmidShape m;
+  if (!mmid_shape(w, x, ids, y, &m)) return 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  uint8_t *ws = nullptr;
+  {
+    // query: the smallest workspace bound on this device must hold the shape
+    // (ggml asks with no stream, then executes on one of its streams);
+    // execute: the workspace bound to this stream
+    std::lock_guard<std::mutex> lk(g_bind_mu);
+    size_t cap = 0;
+    bool any = false;
+    for (int i = 0; i < g_nbind; ++i) {
+      if (g_bind[i].dev != dev) continue;
+      if (!execute) {
+        cap = any ? std::min(cap, g_bind[i].bytes) : g_bind[i].bytes;
+        any = true;
+      } else if (g_bind[i].stream == (hipStream_t)stream) {
+        cap = g_bind[i].bytes;
+        ws = g_bind[i].ptr;
+        any = true;
+      }
+    }
+    if (!any || cap < m.ws_bytes) {
+      fail("zm_mul_mat_id: %s (needs %zu bytes, zm_mul_mat_id_workspace_size)",
+           any ? "bound workspace too small" : "no workspace bound for this device/stream", m.ws_bytes);
+      return 0;
+    }
+  }
+  if (!execute) return 1;
+  DeviceState *d;
+  if (device_state(&d)) return 0;
+  return mmid_exec(m, w, x, ids, y, (hipStream_t)stream, ws, d);
 }
 
 // ---------------------------------------------------------------- debug: block dots
@@ -917,7 +1014,7 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
   if (launch_quant(w.act, (size_t)F, nbF, S * K, w.aq, q8_row_bytes(nbF), 1, st)) return -1;
   // skipped routes (slot table -1) read as zero rows; router ids are always valid otherwise
   if (L->route_map)
-    hipLaunchKernelGGL(k_fill_skipped, dim3((unsigned)std::min((H + 255) / 256, 64), (unsigned)(S * K)), dim3(256), 0,
+    hipLaunchKernelGGL(k_fill_skipped, dim3((unsigned)std::min((H + 255) / 256, 64), (unsigned)std::min(S * K, 65535)), dim3(256), 0,
                      st, ids, (size_t)K, (size_t)1, K, S, NS, H, w.y, (size_t)K * H, (size_t)H);
   // down
   GemvArgs b = a;

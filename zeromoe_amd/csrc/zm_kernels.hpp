@@ -714,12 +714,14 @@ static __global__ __launch_bounds__(256) void k_combine(const float *__restrict_
 // (patches/ggml/0002...:50-54; kernels/quant/kquant_matmul.cu:660-663)
 static __global__ void k_fill_skipped(const int32_t *__restrict__ ids, size_t id_s, size_t id_k, int n_ids, int S,
                                int n_experts, int O, float *out, size_t out_s, size_t out_k) {
-  const int pair = blockIdx.y;
-  const int s = pair / n_ids, k = pair % n_ids;
-  const int e = ids[s * id_s + k * id_k];
-  if (e >= 0 && e < n_experts) return;
-  const float v = e < 0 ? 0.0f : __int_as_float(0x7fc00000);
-  for (int r = blockIdx.x * 256 + threadIdx.x; r < O; r += gridDim.x * 256) out[s * out_s + k * out_k + r] = v;
+  // pairs are strided over grid y (at most 65535 rows of workgroups)
+  for (int pair = blockIdx.y; pair < n_ids * S; pair += gridDim.y) {
+    const int s = pair / n_ids, k = pair % n_ids;
+    const int e = ids[s * id_s + k * id_k];
+    if (e >= 0 && e < n_experts) continue;
+    const float v = e < 0 ? 0.0f : __int_as_float(0x7fc00000);
+    for (int r = blockIdx.x * 256 + threadIdx.x; r < O; r += gridDim.x * 256) out[s * out_s + k * out_k + r] = v;
+  }
 }
 
 // ============================================================ fp32 router GEMV

@@ -131,10 +131,30 @@ def mul_mat_id(W: torch.Tensor, wtype: int, n_in: int, x: torch.Tensor, ids: tor
     tx = _tensor(0, x, None)
     ti = _tensor(26, ids, None)
     ty = _tensor(0, out, None)
-    ok = lib().zm_mul_mat_id(C.byref(tw), C.byref(tx), C.byref(ti), C.byref(ty), _stream(stream), 1)
+    st = _stream(stream)
+    bind_mmid_workspace(st, lib().zm_mul_mat_id_workspace_size(C.byref(tw), C.byref(tx), C.byref(ti), C.byref(ty)),
+                        x.device)
+    ok = lib().zm_mul_mat_id(C.byref(tw), C.byref(tx), C.byref(ti), C.byref(ty), st, 1)
     if ok != 1:
         raise RuntimeError(f"zm_mul_mat_id declined: {lib().zm_last_error().decode()}")
     return out
+
+
+# stream handle -> device buffer bound as zm_mul_mat_id's workspace (the role
+# of a ggml backend context's per-stream scratch)
+_MMID_WS: dict = {}
+
+
+def bind_mmid_workspace(stream: int, need: int, device) -> None:
+    """Bind (or grow) the caller-owned workspace of `stream`.  Growing happens
+    here, outside the op: a buffer freed by torch is reused only by work
+    ordered after it on the same stream."""
+    cur = _MMID_WS.get((device.index, stream))
+    if cur is not None and cur.numel() >= need:
+        return
+    buf = torch.empty(max(need, 1 << 20), dtype=torch.uint8, device=device)
+    check(lib().zm_mul_mat_id_set_workspace(stream, buf.data_ptr(), buf.numel()), "zm_mul_mat_id_set_workspace")
+    _MMID_WS[(device.index, stream)] = buf
 
 
 def mul_mat_id_supported(W, wtype, n_in, x, ids, out) -> bool:
