@@ -121,6 +121,18 @@ size_t zm_mul_mat_id_workspace_size(const zm_tensor *src0, const zm_tensor *src1
  * context owns per stream (the reference hook's caller,
  * patches/ggml/0010-...:57-61, passes ctx.stream()). */
 int zm_mul_mat_id_set_workspace(void *stream, void *workspace, size_t bytes);
+/* zm_mul_mat_id with no workspace at all, for callers that cannot allocate
+ * or bind memory (code under HIP-graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  Its scratch is a
+ * 16 MiB device array compiled into the library (one per GPU, held until the
+ * process ends); shapes that need more (zm_mul_mat_id_workspace_size) are
+ * declined with an error.  zm_init must have run on the device (it looks up
+ * the array's address); the call itself only launches.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (two streams, two
+ * threads) race and must be serialised by the caller.  Same arguments,
+ * semantics and return convention as zm_mul_mat_id. */
+int zm_mul_mat_id_static(const zm_tensor *src0, const zm_tensor *src1, const zm_tensor *ids, zm_tensor *dst,
+                         void *stream, int execute);
 /* Count of executed zm_mul_mat_id launches (kquant_matmul.cu:762-764). */
 uint64_t zm_mul_mat_id_launches(void);
 

@@ -58,6 +58,7 @@ SIGNATURES = {
     "zm_mul_mat_id_launches": (U64, []),
     "zm_mul_mat_id_workspace_size": (SZ, [C.POINTER(ZmTensor)] * 4),
     "zm_mul_mat_id_set_workspace": (I, [P, P, SZ]),
+    "zm_mul_mat_id_static": (I, [C.POINTER(ZmTensor)] * 3 + [C.POINTER(ZmTensor), P, I]),
     "zm_quantize_q8_K": (I, [P, I64, I64, P, P]),
     "zm_router": (I, [C.POINTER(ZmRouterSpec), P, P, P, P, P, I, P, P, P]),
     "zm_bucket": (I, [P, I, I, I, P, P, P, P, P, P]),

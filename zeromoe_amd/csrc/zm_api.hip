@@ -38,12 +38,20 @@ namespace {
 
 constexpr int kMaxDevices = 16;
 
+// Device-resident scratch of zm_mul_mat_id_static: one copy per GPU, held until
+// the process ends.  Host code never passes `scratch` itself to a kernel (on the
+// host the name is only a stand-in): its per-device address comes from
+// hipGetSymbolAddress at set-up (DeviceState::scratch).
+constexpr size_t kStaticScratchBytes = 16u << 20;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
 struct DeviceState {
   bool ready = false;
   uint64_t *grid = nullptr;   // IQ2_XXS grid, 256 x u64
   uint64_t *signs = nullptr;  // 128 x u64 byte masks of ksigns_iq2xs
   uint64_t *iq4 = nullptr;    // IQ4_XS value table, 16 x i8
   uint64_t *iq3 = nullptr;    // IQ3_XXS grid, 256 x u32
+  uint8_t *scratch = nullptr; // this device's address of `scratch`
   uint64_t *trace = nullptr;  // decode-kernel phase timestamps (ZEROMOE_TRACE=1)
   size_t trace_n = 0;
 };
@@ -123,10 +131,22 @@ int device_state(DeviceState **out) {
     builtin_iq3_grid(g3);
     HIP_OK(hipMalloc(&d.iq3, sizeof(g3)));
     HIP_OK(hipMemcpy(d.iq3, g3, sizeof(g3), hipMemcpyHostToDevice));
+    void *sp = nullptr;
+    HIP_OK(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)));
+    d.scratch = (uint8_t *)sp;
     d.ready = true;
   }
   *out = &d;
   return 0;
+}
+
+// The state of the current device if zm_init (or any first call) has set it
+// up; nullptr otherwise.  Allocates nothing.
+DeviceState *device_state_if_ready() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lk(g_mu);
+  return g_dev[dev].ready ? &g_dev[dev] : nullptr;
 }
 
 }  // namespace
@@ -607,6 +627,26 @@ int zm_mul_mat_id(const zm_tensor *w, const zm_tensor *x, const zm_tensor *ids, 
   DeviceState *d;
   if (device_state(&d)) return 0;
   return mmid_exec(m, w, x, ids, y, (hipStream_t)stream, ws, d);
+}
+
+int zm_mul_mat_id_static(const zm_tensor *w, const zm_tensor *x, const zm_tensor *ids, zm_tensor *dst, void *stream,
+                         int execute) {
+  MmidShape m;
+  if (!mmid_shape(w, x, ids, dst, &m)) return 0;
+  if (m.ws_bytes > kStaticScratchBytes) {
+    fail("zm_mul_mat_id_static: shape needs %zu bytes of scratch, more than the %zu-byte device array", m.ws_bytes,
+         kStaticScratchBytes);
+    return 0;
+  }
+  if (!execute) return 1;
+  DeviceState *d = device_state_if_ready();
+  if (!d) {
+    fail("zm_mul_mat_id_static: zm_init has not run on this device");
+    return 0;
+  }
+  // every scratch array is written before it is read within the call, so
+  // nothing needs clearing between calls
+  return mmid_exec(m, w, x, ids, dst, (hipStream_t)stream, d->scratch, d);
 }
 
 // ---------------------------------------------------------------- debug: block dots
