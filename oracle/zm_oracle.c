@@ -271,7 +271,9 @@ void zmo_set_iq3xxs_grid(const uint32_t grid[256]) {
 
 /* ggml quantize_row_q8_K_ref: per 256 values take the signed value of largest
  * magnitude (first one on ties), iscale = -127/max, q = min(127, round(iscale x)),
- * d = 1/iscale, bsums = sums of 16 consecutive q. */
+ * d = 1/iscale, bsums = sums of 16 consecutive q.  The reference restates the
+ * same rounding in tests/test_real_tensor_numerics.cpp:115-126 (signed max,
+ * scale |max|/127, nearest integer clamped to +-127). */
 void zmo_quantize_row_q8_K(const float *x, zmo_block_q8_K *y, int64_t k) {
   const int64_t nb = k / ZMO_QK_K;
   for (int64_t i = 0; i < nb; ++i, x += ZMO_QK_K) {
@@ -1300,33 +1302,41 @@ static float dot_iq4_xs(int n, const zmo_block_iq4_xs *x, const zmo_block_q8_K *
   return acc;
 }
 
-/* ggml_vec_dot_iq3_xxs_q8_K, scalar order: per block d = fp16(d) * d_y,
- * bsum = sum_ib (2 ls + 1) * sum grid * sign * q8, sumf += d * bsum; result
- * 0.25 * sumf.  Float order: parity unpinned (no stock copy in the reference
- * tree). */
+/* ggml_vec_dot_iq3_xxs_q8_K in the stock AVX2 order that the reference holds
+ * as source (bench/iq3k/iq3_dot_bench.c:17-37, ref()): int32 lane l (of 8)
+ * sums (2 ls + 1) * grid * sign * q8 over bytes [4l, 4l+4) of every 32-weight
+ * sub-block of a block (the even and odd sub-blocks in two accumulators, added
+ * lane-wise at the end of the block: the same integers), one fma per block and
+ * lane with d = fp16(d) * d_y, result 0.25 * hsum8.  That file needs ggml's
+ * ggml-common.h (absent here), so it is not built: the integer sums are pinned
+ * by brute force, the float order only by this restatement. */
 static float dot_iq3_xxs(int n, const zmo_block_iq3_xxs *x, const zmo_block_q8_K *y) {
   const uint32_t *grid = zmo_iq3xxs_grid();
-  float sumf = 0.f;
+  float acc[8] = {0};
   for (int i = 0; i < n / ZMO_QK_K; ++i) {
     const float d = zmo_fp16_to_fp32(x[i].d) * y[i].d;
-    int32_t bsum = 0;
+    int32_t sumi[8] = {0};
     for (int ib = 0; ib < 8; ++ib) {
       uint32_t u;
       memcpy(&u, x[i].qs + 64 + 4 * ib, 4);
-      int32_t sumi = 0;
-      for (int l = 0; l < 4; ++l) {
-        const uint8_t signs = zmo_ksigns_iq2xs((int)((u >> (7 * l)) & 127));
-        for (int j = 0; j < 8; ++j) {
-          const int g = (int)((grid[x[i].qs[8 * ib + 2 * l + (j >> 2)]] >> (8 * (j & 3))) & 0xff);
-          const int q8 = y[i].qs[32 * ib + 8 * l + j];
-          sumi += ((signs >> j) & 1) ? -g * q8 : g * q8;
+      const int32_t ls = 2 * (int32_t)(u >> 28) + 1;
+      for (int lane = 0; lane < 8; ++lane) {
+        /* bytes 4*lane .. 4*lane+3 of the sub-block: grid entry qs[8 ib + lane],
+         * sign group lane / 2 (8 signs per 7-bit index) */
+        const uint8_t signs = zmo_ksigns_iq2xs((int)((u >> (7 * (lane >> 1))) & 127));
+        const uint32_t g4 = grid[x[i].qs[8 * ib + lane]];
+        int32_t s4 = 0;
+        for (int j = 0; j < 4; ++j) {
+          const int g = (int)((g4 >> (8 * j)) & 0xff);
+          const int q8 = y[i].qs[32 * ib + 4 * lane + j];
+          s4 += ((signs >> (4 * (lane & 1) + j)) & 1) ? -g * q8 : g * q8;
         }
+        sumi[lane] += ls * s4;
       }
-      bsum += (2 * (int32_t)(u >> 28) + 1) * sumi;
     }
-    sumf += d * (float)bsum;
+    for (int l = 0; l < 8; ++l) acc[l] = fmaf(d, (float)sumi[l], acc[l]);
   }
-  return 0.25f * sumf;
+  return 0.25f * hsum8(acc);
 }
 
 /* ggml_vec_dot_iq2_xxs_q8_K, AVX2 / AVX-512BW order (patches/ggml/0009...:34-95,

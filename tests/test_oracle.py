@@ -379,6 +379,33 @@ def test_q8_K_closed_forms():
         assert np.abs(q[b]["qs"]).max() == 127
 
 
+def test_q8_K_matches_reference_rounding_restatement():
+    """The reference's own statement of Q8_K rounding
+    (tests/test_real_tensor_numerics.cpp:115-126: the signed value of largest
+    magnitude, scale |max|/127, q = nearbyint(v / scale) clamped to +-127),
+    evaluated here in float64: the oracle's d has that magnitude with the sign
+    opposite to max (iscale = -127/max), and every q equals the reference's
+    -q except where v/scale sits within float rounding of a half-integer."""
+    rng = np.random.default_rng(12)
+    for trial in range(40):
+        x = (rng.standard_normal(256 * 4) * 10.0 ** rng.uniform(-4, 4)).astype(np.float32)
+        q = O.quantize_q8_K(x)
+        for b in range(4):
+            v = x[256 * b: 256 * (b + 1)].astype(np.float64)
+            i = int(np.argmax(np.abs(v)))  # first maximal magnitude
+            mx = v[i]
+            scale = abs(mx) / 127.0
+            qr = np.clip(np.rint(v / scale), -127, 127)
+            near_half = np.abs(np.abs(v / scale - np.floor(v / scale)) - 0.5) < 1e-4
+            got = q[b]["qs"].astype(np.float64)
+            # ggml's iscale = -127/max flips the sign when max > 0
+            sgn = -1.0 if mx > 0 else 1.0
+            ok = (got == sgn * qr) | near_half
+            assert ok.all(), (trial, b, np.nonzero(~ok)[0][:5])
+            assert abs(abs(float(q[b]["d"])) - scale) <= 1e-6 * scale
+            assert np.sign(float(q[b]["d"])) == -np.sign(mx)
+
+
 # ------------------------------------------------------------------ float helpers
 
 def test_fp16_conversions_exhaustive():
