@@ -278,9 +278,12 @@ def run_unpack(torch, Z, steps, warmup, records=32):
 
 
 def cpu_baseline(seconds: float = 10.0):
-    """CPU restatement of ggml's MUL_MAT_ID layer (oracle/zm_oracle.c) on this
-    host's cores at the c2 shape, S=1: ids re-drawn every iteration over a
-    32-expert pool (218 MB of weights, beyond the LLC)."""
+    """Restatement of the reference's CPU expert path (ggml CPU MUL_MAT_ID on
+    AVX-512: serial Q8_K of x on one thread, OpenMP over the output rows of
+    gate+up and of down, one VNNI vec_dot per row; oracle/zm_oracle.c,
+    zmo_moe_forward_fast, bit-identical to the oracle) at the c2 shape, S=1,
+    on this host's cores: ids re-drawn every iteration over a 32-expert pool
+    (218 MB of weights, beyond the LLC)."""
     import numpy as np
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -294,13 +297,19 @@ def cpu_baseline(seconds: float = 10.0):
     Wd = O.random_blocks(Q3, pool * H, F, seed=3).reshape(pool, H, -1)
     rng = np.random.default_rng(0)
     x = rng.standard_normal((1, H)).astype(np.float32)
-    threads = max(1, min(16, os.cpu_count() or 1))
+    # the GPU box's CPU share is 16 threads (OMP_NUM_THREADS there); never more
+    threads = max(1, min(16, int(os.environ.get("OMP_NUM_THREADS", "16")), os.cpu_count() or 1))
     w = np.full((1, K), 1.0 / K, np.float32)
-    O.moe_forward(x, rng.permutation(pool)[:K][None].astype(np.int32), w, Q2, Q2, Q3, Wg, Wu, Wd, nthreads=threads)
+    avx = O.has_avx512()
+
+    def one():
+        ids = rng.permutation(pool)[:K][None].astype(np.int32)
+        O.moe_forward(x, ids, w, Q2, Q2, Q3, Wg, Wu, Wd, nthreads=threads, fast=True)
+
+    one()
     n, t0 = 0, time.perf_counter()
     while True:
-        ids = rng.permutation(pool)[:K][None].astype(np.int32)
-        O.moe_forward(x, ids, w, Q2, Q2, Q3, Wg, Wu, Wd, nthreads=threads)
+        one()
         n += 1
         el = time.perf_counter() - t0
         if el >= seconds and n >= 3:
@@ -308,9 +317,10 @@ def cpu_baseline(seconds: float = 10.0):
     us = el / n * 1e6
     gbs = K * expert_bytes(c) / (us * 1e-6) / 1e9
     return {"value": round(us, 1), "unit": "us/layer", "GBps": round(gbs, 2), "cores": threads, "kind": "port",
-            "sample": f"c2 layer S=1 (8 of a 32-expert pool per iteration), {n} iterations in {el:.1f} s, "
-                      f"OpenMP over output rows"}
-
+            "nproc": os.cpu_count(), "avx512_vnni": avx,
+            "sample": f"c2 layer S=1 (8 of a 32-expert pool per iteration), {n} iterations in {el:.1f} s; "
+                      f"restatement of the reference CPU path ({'AVX-512 VNNI' if avx else 'scalar, no AVX-512 on this host'} "
+                      f"Q2_K/Q3_K dots, serial Q8_K, OpenMP over output rows, {threads} threads of nproc={os.cpu_count()})"}
 
 
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "k_moe_decode_c2_hbm_traffic.txt")

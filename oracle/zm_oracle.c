@@ -1699,3 +1699,180 @@ void zmo_router_gemv(const float *W, const float *x, int H, int E, int S, float 
       logits[(size_t)s * E + e] = (float)acc;
     }
 }
+
+/* ====================================================================== *
+ * AVX-512 restatement of the reference's CPU expert path (the CPU baseline).
+ *
+ * The reference times ggml's CPU MUL_MAT_ID on AVX-512 hosts: per layer the
+ * src1 row is quantized to Q8_K on one thread (patches/ggml/0002...:18-45),
+ * threads split the output rows of the gate, up and down matrices, and each
+ * row is one ggml_vec_dot_<type>_q8_K (models/qwen/ggml_qwen_cpu_moe.cpp:49-57;
+ * 512-bit dots as in bench/q3k_q4k_dot_bench.cpp:73-125).  This restatement
+ * keeps that structure and computes every dot with VNNI (vpdpbusd) in the
+ * integer grouping of the oracle dots above, so its results are bit-identical
+ * to zmo_moe_forward (checked by tests/test_oracle.py): per block the integer
+ * lane sums of 4 consecutive bytes of each 32-weight chunk are formed exactly
+ * (vpdpbusd of the unsigned 2-bit values against the signed Q8_K bytes, times
+ * the chunk's 16-weight sub-block scale), folded to the 8 lanes of the
+ * oracle's accumulator, and added with the same fmas and the same final hsum.
+ * Types other than Q2_K / Q3_K use the oracle dots.
+ * ====================================================================== */
+
+#if defined(__x86_64__)
+#include <immintrin.h>
+
+#define ZMO_AVX512 __attribute__((target("avx512f,avx512bw,avx512vl,avx512vnni,avx512dq,fma")))
+
+/* lane l of 16 -> sub-block scale index 4k + (l >> 2) of 64-byte chunk pair k */
+ZMO_AVX512 static inline __m512i scale_index(int k) {
+  return _mm512_setr_epi32(4 * k, 4 * k, 4 * k, 4 * k, 4 * k + 1, 4 * k + 1, 4 * k + 1, 4 * k + 1, 4 * k + 2,
+                           4 * k + 2, 4 * k + 2, 4 * k + 2, 4 * k + 3, 4 * k + 3, 4 * k + 3, 4 * k + 3);
+}
+/* per 16-bit word shift: s0 for the low 32 bytes, s1 for the high 32 */
+ZMO_AVX512 static inline __m512i shift_pair(int s0, int s1) {
+  return _mm512_inserti64x4(_mm512_castsi256_si512(_mm256_set1_epi16((short)s0)), _mm256_set1_epi16((short)s1), 1);
+}
+ZMO_AVX512 static inline float finish8(__m256 acc) {
+  float a[8];
+  _mm256_storeu_ps(a, acc);
+  return hsum8(a);
+}
+
+ZMO_AVX512 static float dot_q2_K_avx512(int n, const zmo_block_q2_K *x, const zmo_block_q8_K *y) {
+  const __m512i m3 = _mm512_set1_epi8(3);
+  const __m512i sh[2] = {shift_pair(0, 2), shift_pair(4, 6)};
+  const __m512i idx[4] = {scale_index(0), scale_index(1), scale_index(2), scale_index(3)};
+  __m256 acc = _mm256_setzero_ps();
+  for (int i = 0; i < n / ZMO_QK_K; ++i) {
+    const float d = y[i].d * zmo_fp16_to_fp32(x[i].d);
+    const float dmin = -y[i].d * zmo_fp16_to_fp32(x[i].dmin);
+    const __m128i sc8 = _mm_loadu_si128((const __m128i *)x[i].scales);
+    /* mins: lane l = m[2l] * bsum[2l] + m[2l+1] * bsum[2l+1] */
+    const __m256i m16 = _mm256_cvtepu8_epi16(_mm_and_si128(_mm_srli_epi16(sc8, 4), _mm_set1_epi8(0x0F)));
+    const __m256i prod = _mm256_madd_epi16(m16, _mm256_loadu_si256((const __m256i *)y[i].bsums));
+    acc = _mm256_fmadd_ps(_mm256_set1_ps(dmin), _mm256_cvtepi32_ps(prod), acc);
+    const __m512i sc32 = _mm512_and_si512(_mm512_cvtepu8_epi32(sc8), _mm512_set1_epi32(0xF));
+    __m512i sumi = _mm512_setzero_si512();
+    for (int j = 0; j < 2; ++j) {
+      const __m512i q = _mm512_broadcast_i64x4(_mm256_loadu_si256((const __m256i *)(x[i].qs + 32 * j)));
+      for (int h = 0; h < 2; ++h) {
+        const int k = 2 * j + h;
+        const __m512i w = _mm512_and_si512(_mm512_srlv_epi16(q, sh[h]), m3);
+        const __m512i q8 = _mm512_loadu_si512((const void *)(y[i].qs + 64 * k));
+        const __m512i dp = _mm512_dpbusd_epi32(_mm512_setzero_si512(), w, q8);
+        sumi = _mm512_add_epi32(sumi, _mm512_mullo_epi32(dp, _mm512_permutexvar_epi32(idx[k], sc32)));
+      }
+    }
+    const __m256i s8 = _mm256_add_epi32(_mm512_castsi512_si256(sumi), _mm512_extracti64x4_epi64(sumi, 1));
+    acc = _mm256_fmadd_ps(_mm256_set1_ps(d), _mm256_cvtepi32_ps(s8), acc);
+  }
+  return finish8(acc);
+}
+
+ZMO_AVX512 static float dot_q3_K_avx512(int n, const zmo_block_q3_K *x, const zmo_block_q8_K *y) {
+  const __m512i m3 = _mm512_set1_epi8(3), m1 = _mm512_set1_epi8(1);
+  const __m512i sh[2] = {shift_pair(0, 2), shift_pair(4, 6)};
+  const __m512i hs[4] = {shift_pair(0, 1), shift_pair(2, 3), shift_pair(4, 5), shift_pair(6, 7)};
+  const __m512i idx[4] = {scale_index(0), scale_index(1), scale_index(2), scale_index(3)};
+  __m256 acc = _mm256_setzero_ps();
+  for (int i = 0; i < n / ZMO_QK_K; ++i) {
+    const float d = y[i].d * zmo_fp16_to_fp32(x[i].d);
+    int8_t sc[16];
+    q3_scales(x[i].scales, sc);
+    const __m512i sc32 = _mm512_cvtepi8_epi32(_mm_loadu_si128((const __m128i *)sc));
+    /* 4 * (high bit clear): bit 2k (low half) / 2k+1 (high half) of hmask[t] */
+    const __m512i nh = _mm512_broadcast_i64x4(
+        _mm256_xor_si256(_mm256_loadu_si256((const __m256i *)x[i].hmask), _mm256_set1_epi8(-1)));
+    __m512i sumi = _mm512_setzero_si512();
+    for (int j = 0; j < 2; ++j) {
+      const __m512i q = _mm512_broadcast_i64x4(_mm256_loadu_si256((const __m256i *)(x[i].qs + 32 * j)));
+      for (int h = 0; h < 2; ++h) {
+        const int k = 2 * j + h;
+        const __m512i w = _mm512_and_si512(_mm512_srlv_epi16(q, sh[h]), m3);
+        const __m512i n4 = _mm512_slli_epi16(_mm512_and_si512(_mm512_srlv_epi16(nh, hs[k]), m1), 2);
+        const __m512i q8 = _mm512_loadu_si512((const void *)(y[i].qs + 64 * k));
+        const __m512i dp = _mm512_sub_epi32(_mm512_dpbusd_epi32(_mm512_setzero_si512(), w, q8),
+                                            _mm512_dpbusd_epi32(_mm512_setzero_si512(), n4, q8));
+        sumi = _mm512_add_epi32(sumi, _mm512_mullo_epi32(dp, _mm512_permutexvar_epi32(idx[k], sc32)));
+      }
+    }
+    const __m256i s8 = _mm256_add_epi32(_mm512_castsi512_si256(sumi), _mm512_extracti64x4_epi64(sumi, 1));
+    acc = _mm256_fmadd_ps(_mm256_set1_ps(d), _mm256_cvtepi32_ps(s8), acc);
+  }
+  return finish8(acc);
+}
+
+int zmo_cpu_has_avx512(void) {
+  return __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+         __builtin_cpu_supports("avx512vl") && __builtin_cpu_supports("avx512vnni") &&
+         __builtin_cpu_supports("avx512dq");
+}
+#else
+int zmo_cpu_has_avx512(void) { return 0; }
+#endif
+
+/* vec_dot with the AVX-512 kernels where the host has them (Q2_K, Q3_K); the
+ * oracle dot otherwise.  Bit-identical either way. */
+float zmo_vec_dot_q8_K_fast(int type, int n, const void *x, const zmo_block_q8_K *y) {
+#if defined(__x86_64__)
+  static int have = -1;
+  if (have < 0) have = zmo_cpu_has_avx512();
+  if (have && type == ZMO_TYPE_Q2_K) return dot_q2_K_avx512(n, (const zmo_block_q2_K *)x, y);
+  if (have && type == ZMO_TYPE_Q3_K) return dot_q3_K_avx512(n, (const zmo_block_q3_K *)x, y);
+#endif
+  return zmo_vec_dot_q8_K(type, n, x, y);
+}
+
+/* The layer as ggml's CPU graph runs it (mul_mat_id gate, up, swiglu,
+ * mul_mat_id down, mul, sum_topk; moe_routed_ggml.hpp:166-214): per token the
+ * Q8_K of x on one thread, gate and up rows of all K routes split over the
+ * threads in one parallel region, SwiGLU and the Q8_K of every route's act on
+ * one thread, the down rows of all routes in a second region, then the
+ * k-ascending weighted sum.  Same values as zmo_moe_forward, bit for bit
+ * (no shared expert). */
+void zmo_moe_forward_fast(const zmo_moe_desc *d, const float *x, const int32_t *ids, const float *weights,
+                          float *out, int nthreads) {
+  const int H = d->H, F = d->F, K = d->K, S = d->S;
+  const size_t rg = zmo_row_size(d->type_gate, H), ru = zmo_row_size(d->type_up, H), rd = zmo_row_size(d->type_down, F);
+  const size_t eg = rg * (size_t)F, eu = ru * (size_t)F, ed = rd * (size_t)H;
+  const int nbH = H / ZMO_QK_K, nbF = F / ZMO_QK_K;
+  zmo_block_q8_K *xq = (zmo_block_q8_K *)malloc(sizeof(zmo_block_q8_K) * (size_t)nbH);
+  zmo_block_q8_K *aq = (zmo_block_q8_K *)malloc(sizeof(zmo_block_q8_K) * (size_t)nbF * (size_t)K);
+  float *g = (float *)malloc(sizeof(float) * (size_t)F * (size_t)K * 3);
+  float *u = g + (size_t)F * K, *a = u + (size_t)F * K;
+  float *y = (float *)malloc(sizeof(float) * (size_t)H * (size_t)K);
+  for (int s = 0; s < S; ++s) {
+    const int32_t *id = ids + (size_t)s * K;
+    zmo_quantize_row_q8_K(x + (size_t)s * H, xq, H);
+#pragma omp parallel for num_threads(nthreads > 0 ? nthreads : 1) schedule(static)
+    for (int r = 0; r < K * F; ++r) {
+      const int k = r / F, nrow = r % F;
+      if (id[k] < 0) continue;
+      g[r] = zmo_vec_dot_q8_K_fast(d->type_gate, H, (const char *)d->w_gate + (size_t)id[k] * eg + (size_t)nrow * rg, xq);
+      u[r] = zmo_vec_dot_q8_K_fast(d->type_up, H, (const char *)d->w_up + (size_t)id[k] * eu + (size_t)nrow * ru, xq);
+    }
+    for (int k = 0; k < K; ++k) {
+      if (id[k] < 0) continue;
+      zmo_swiglu(g + (size_t)k * F, u + (size_t)k * F, a + (size_t)k * F, F);
+      zmo_quantize_row_q8_K(a + (size_t)k * F, aq + (size_t)k * nbF, F);
+    }
+#pragma omp parallel for num_threads(nthreads > 0 ? nthreads : 1) schedule(static)
+    for (int r = 0; r < K * H; ++r) {
+      const int k = r / H, h = r % H;
+      y[r] = id[k] < 0 ? 0.0f
+                       : zmo_vec_dot_q8_K_fast(d->type_down, F,
+                                               (const char *)d->w_down + (size_t)id[k] * ed + (size_t)h * rd,
+                                               aq + (size_t)k * nbF);
+    }
+    float *o = out + (size_t)s * H;
+    for (int h = 0; h < H; ++h) {
+      float acc = weights[(size_t)s * K] * y[h];
+      for (int k = 1; k < K; ++k) acc = acc + weights[(size_t)s * K + k] * y[(size_t)k * H + h];
+      o[h] = acc;
+    }
+  }
+  free(y);
+  free(g);
+  free(aq);
+  free(xq);
+}

@@ -160,6 +160,13 @@ typedef struct {
 } zmo_moe_desc;
 void zmo_moe_forward(const zmo_moe_desc *d, const float *x, const int32_t *ids, const float *weights, float *out,
                      int nthreads);
+/* CPU baseline: the same layer with AVX-512 VNNI dots where the host has
+ * them (Q2_K, Q3_K), ggml's two-region thread structure; bit-identical to
+ * zmo_moe_forward (no shared expert). */
+int zmo_cpu_has_avx512(void);
+float zmo_vec_dot_q8_K_fast(int type, int n, const void *x, const zmo_block_q8_K *y);
+void zmo_moe_forward_fast(const zmo_moe_desc *d, const float *x, const int32_t *ids, const float *weights,
+                          float *out, int nthreads);
 
 /* Router GEMV: logits[s][e] = sum_i W[e][i] x[s][i], W [E][H] f32 (ggml [H, E]). */
 void zmo_router_gemv(const float *W, const float *x, int H, int E, int S, float *logits);

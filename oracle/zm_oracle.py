@@ -75,6 +75,10 @@ def lib():
         L.zmo_bucket.argtypes = [P, I, I, I, P, P, P]
         L.zmo_swiglu.argtypes = [P, P, P, I64]
         L.zmo_moe_forward.argtypes = [P, P, P, P, P, I]
+        L.zmo_moe_forward_fast.argtypes = [P, P, P, P, P, I]
+        L.zmo_vec_dot_q8_K_fast.restype = F
+        L.zmo_vec_dot_q8_K_fast.argtypes = [I, I, P, P]
+        L.zmo_cpu_has_avx512.restype = I
         L.zmo_router_gemv.argtypes = [P, P, I, I, I, P]
         _lib = L
     return _lib
@@ -160,6 +164,11 @@ def dequantize(t: int, w: np.ndarray, n: int) -> np.ndarray:
 def vec_dot(t: int, w_row: np.ndarray, q8_row: np.ndarray) -> float:
     n = (q8_row.size * q8_row.itemsize // 292) * QK_K
     return lib().zmo_vec_dot_q8_K(t, n, _p(np.ascontiguousarray(w_row)), _p(np.ascontiguousarray(q8_row)))
+
+
+def vec_dot_fast(t: int, w_row: np.ndarray, q8_row: np.ndarray) -> float:
+    n = (q8_row.size * q8_row.itemsize // 292) * QK_K
+    return lib().zmo_vec_dot_q8_K_fast(t, n, _p(np.ascontiguousarray(w_row)), _p(np.ascontiguousarray(q8_row)))
 
 
 def block_dots(t: int, w_row: np.ndarray, q8_row: np.ndarray):
@@ -312,9 +321,11 @@ class _MoeDesc(C.Structure):
                 ("ws_gate", C.c_void_p), ("ws_up", C.c_void_p), ("ws_down", C.c_void_p)]
 
 
-def moe_forward(x, ids, weights, tg, tu, td, Wg, Wu, Wd, shared=None, nthreads: int = 1) -> np.ndarray:
+def moe_forward(x, ids, weights, tg, tu, td, Wg, Wu, Wd, shared=None, nthreads: int = 1,
+                fast: bool = False) -> np.ndarray:
     """Routed layer: x (S,H) f32, ids/weights (S,K); Wg/Wu (E,F,rowH), Wd (E,H,rowF) uint8.
-    shared = (type, F_shared, Sg, Su, Sd) or None."""
+    shared = (type, F_shared, Sg, Su, Sd) or None.  fast: the AVX-512 CPU
+    baseline (zmo_moe_forward_fast, bit-identical, no shared expert)."""
     x = np.ascontiguousarray(x, np.float32)
     ids = np.ascontiguousarray(ids, np.int32)
     weights = np.ascontiguousarray(weights, np.float32)
@@ -327,8 +338,16 @@ def moe_forward(x, ids, weights, tg, tu, td, Wg, Wu, Wd, shared=None, nthreads: 
         d.F_shared, d.type_shared = Fs, ts
         d.ws_gate, d.ws_up, d.ws_down = _p(Sg), _p(Su), _p(Sd)
     out = np.zeros((S, H), np.float32)
-    lib().zmo_moe_forward(C.byref(d), _p(x), _p(ids), _p(weights), _p(out), nthreads)
+    if fast:
+        assert shared is None, "the CPU baseline has no shared expert"
+        lib().zmo_moe_forward_fast(C.byref(d), _p(x), _p(ids), _p(weights), _p(out), nthreads)
+    else:
+        lib().zmo_moe_forward(C.byref(d), _p(x), _p(ids), _p(weights), _p(out), nthreads)
     return out
+
+
+def has_avx512() -> bool:
+    return bool(lib().zmo_cpu_has_avx512())
 
 
 def router_gemv(W: np.ndarray, x: np.ndarray) -> np.ndarray:

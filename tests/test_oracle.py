@@ -725,3 +725,43 @@ def test_moe_unpack_inverts_pack_and_scatter_skips():
             want = planar[p][lo:hi] if e in (4, 5, 2) else np.full(parts[p], 7, np.uint8)
             np.testing.assert_array_equal(out[p][lo:hi], want)
             np.testing.assert_array_equal(out[p][hi:(e + 1) * strides[p]], 7)
+
+
+# ------------------------------------------------------------------ AVX-512 CPU baseline
+
+@pytest.mark.parametrize("t", [O.TYPE_Q2_K, O.TYPE_Q3_K])
+def test_avx512_dots_bit_identical_to_oracle(t):
+    """The CPU baseline's VNNI dots equal the oracle dots bit for bit (random
+    blocks over a wide range of scales, every hmask / scale pattern); Q2_K
+    also against the reference's golden vectors."""
+    if not O.has_avx512():
+        pytest.skip("host without AVX-512 VNNI")
+    rng = np.random.default_rng(30 + t)
+    for trial in range(200):
+        nb = int(rng.integers(1, 17))
+        w = O.random_blocks(t, 1, 256 * nb, seed=1000 + trial)[0]
+        x = (rng.standard_normal(256 * nb) * 10.0 ** rng.uniform(-3, 3)).astype(np.float32)
+        q = O.quantize_q8_K(x)
+        assert f32bits(O.vec_dot_fast(t, w, q)) == f32bits(O.vec_dot(t, w, q)), trial
+    if t == O.TYPE_Q2_K:
+        g = np.load(GOLDEN, allow_pickle=False)
+        for i, nb in enumerate(g["q2_K_nb"]):
+            w = np.ascontiguousarray(g["q2_K_w"][i][: nb * O.BLOCK_BYTES[t]])
+            q = np.ascontiguousarray(g["q2_K_q8"][i][: nb * 292]).view(O.Q8K_DTYPE)
+            assert f32bits(O.vec_dot_fast(t, w, q)) == f32bits(g["q2_K_dot"][i]), i
+
+
+def test_avx512_layer_bit_identical_to_oracle():
+    """zmo_moe_forward_fast (the CPU baseline: two parallel regions, serial
+    Q8_K) equals zmo_moe_forward on a c2-shaped layer with a skipped route."""
+    rng = np.random.default_rng(3)
+    H, F, E, K = 1024, 512, 6, 4
+    Wg = O.random_blocks(O.TYPE_Q2_K, E * F, H, seed=1).reshape(E, F, -1)
+    Wu = O.random_blocks(O.TYPE_Q2_K, E * F, H, seed=2).reshape(E, F, -1)
+    Wd = O.random_blocks(O.TYPE_Q3_K, E * H, F, seed=3).reshape(E, H, -1)
+    x = rng.standard_normal((2, H)).astype(np.float32)
+    ids = np.array([[3, 0, 5, 1], [2, -1, 4, 0]], np.int32)
+    w = rng.uniform(0.1, 0.4, (2, K)).astype(np.float32)
+    ref = O.moe_forward(x, ids, w, O.TYPE_Q2_K, O.TYPE_Q2_K, O.TYPE_Q3_K, Wg, Wu, Wd, nthreads=4)
+    got = O.moe_forward(x, ids, w, O.TYPE_Q2_K, O.TYPE_Q2_K, O.TYPE_Q3_K, Wg, Wu, Wd, nthreads=4, fast=True)
+    np.testing.assert_array_equal(f32bits(got), f32bits(ref))
