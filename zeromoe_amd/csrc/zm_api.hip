@@ -262,12 +262,13 @@ bool mmq_applies(int type, double avg_pairs) {
 // unpacking is shared by more tokens), Q2_K and dense (shared expert) rows 2
 int mmq_tt(int type, bool dense) { return type == T_Q4_K && !dense ? 4 : 2; }
 int launch_mmq(int type, bool gateup, const GemvArgs &a, int max_items, double avg_pairs, int tt, hipStream_t st);
-template <int T, int TT>
+template <int T, int TT, int NW = 4>
 void launch_mmq_t(bool gateup, dim3 grid, const GemvArgs &a, hipStream_t st) {
+  grid.x = (unsigned)((a.nrows + 16 * NW - 1) / (16 * NW));  // NW waves of 16 weight rows per workgroup
   if (gateup)
-    hipLaunchKernelGGL((k_mmq<T, true, TT>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((k_mmq<T, true, TT, NW>), grid, dim3(64 * NW), 0, st, a);
   else
-    hipLaunchKernelGGL((k_mmq<T, false, TT>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((k_mmq<T, false, TT, NW>), grid, dim3(64 * NW), 0, st, a);
 }
 // tt: 16-token tiles per work item (the tiling the item list was cut with)
 int launch_mmq(int type, bool gateup, const GemvArgs &a, int max_items, double avg_pairs, int tt, hipStream_t st) {
@@ -275,7 +276,11 @@ int launch_mmq(int type, bool gateup, const GemvArgs &a, int max_items, double a
   if ((size_t)a.nrows * a.w_rstride >= (1ull << 31) || max_items <= 0) return 1;
   const dim3 grid((unsigned)((a.nrows + 63) / 64), (unsigned)max_items);
   if (type == T_Q4_K) {
-    if (tt == 4) launch_mmq_t<T_Q4_K, 4>(gateup, grid, a, st);
+    if (tt == 8) {
+      if (getenv_flag_off("ZEROMOE_MMQ_NW8")) launch_mmq_t<T_Q4_K, 8, 4>(gateup, grid, a, st);
+      else launch_mmq_t<T_Q4_K, 8, 8>(gateup, grid, a, st);
+    }
+    else if (tt == 4) launch_mmq_t<T_Q4_K, 4>(gateup, grid, a, st);
     else launch_mmq_t<T_Q4_K, 2>(gateup, grid, a, st);
   } else if (type == T_Q5_K) {
     if (tt == 4) launch_mmq_t<T_Q5_K, 4>(gateup, grid, a, st);
@@ -1038,11 +1043,20 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
   a.grid = d->grid;
   a.signs = d->signs;
   const double avg_pairs = (double)(S * K) / std::max(1, std::min(NS, S * K));
-  const int max_items = mmq_max_items(S * K, NS);
-  const int tt = L->type_gate == T_Q4_K && L->type_down == T_Q4_K ? 4 : 2;  // tiles per routed item
-  if (mmq_applies(L->type_gate, avg_pairs) || mmq_applies(L->type_down, avg_pairs))
-    hipLaunchKernelGGL(k_mmq_items, dim3(1), dim3(1024), 0, st, w.n_active, w.active, w.offs, w.items, w.n_items,
-                       16 * tt);
+  // 16-token tiles per routed work item: Q4_K items hold up to 128 pairs, so an
+  // expert's weights are unpacked once per workgroup for most buckets
+  int tt = L->type_gate == T_Q4_K && L->type_down == T_Q4_K ? 4 : 2;
+  if (const char *v = getenv("ZEROMOE_MMQ_TT"); v && tt == 4) tt = atoi(v);  // experiment knob (4 or 8)
+  // items: at most one partial run per active expert plus the full runs
+  const int max_items = std::min(mmq_max_items(S * K, NS), (S * K + 16 * tt - 1) / (16 * tt) + std::min(NS, S * K));
+  if (mmq_applies(L->type_gate, avg_pairs) || mmq_applies(L->type_down, avg_pairs)) {
+    if (getenv_flag_off("ZEROMOE_MMQ_LPT") || NS > 1024)
+      hipLaunchKernelGGL(k_mmq_items, dim3(1), dim3(1024), 0, st, w.n_active, w.active, w.offs, w.items, w.n_items,
+                         16 * tt);
+    else
+      hipLaunchKernelGGL(k_mmq_items_lpt, dim3(1), dim3(1024), 0, st, w.n_active, w.active, w.offs, w.items,
+                         w.n_items, 16 * tt);
+  }
   a.items = w.items;
   a.n_items = w.n_items;
   a.xq_bytes = (uint32_t)((size_t)S * q8_row_bytes(nbH));

@@ -108,6 +108,51 @@ __global__ __launch_bounds__(1024) void k_mmq_items(const int32_t *__restrict__ 
   if (threadIdx.x == 0) *n_items = total;
 }
 
+// The same work items, largest first: full runs of `tok` pairs, then every
+// expert's remaining run in descending order of its 16-pair tiles, so the
+// short items fill the tail of the launch.  The order of items with the same
+// size is not fixed; no result depends on it (every item writes its own pairs).
+// Needs n_active <= 1024 and tok <= 256.
+__global__ __launch_bounds__(1024) void k_mmq_items_lpt(const int32_t *__restrict__ n_active,
+                                                        const int32_t *__restrict__ active,
+                                                        const int32_t *__restrict__ offs, int32_t *__restrict__ items,
+                                                        int32_t *__restrict__ n_items, int tok) {
+  constexpr int NK = 18;  // size classes: 1..16 tiles of a partial run, 17 = full run
+  __shared__ int hist[NK], cur[NK];
+  const int tid = threadIdx.x;
+  if (tid < NK) hist[tid] = 0;
+  __syncthreads();
+  const int na = *n_active;
+  const int tt = tok / 16;
+  int e = 0, nfull = 0, rem = 0, key = 0;
+  if (tid < na) {
+    e = active[tid];
+    const int cnt = offs[e + 1] - offs[e];
+    nfull = cnt / tok;
+    rem = cnt - nfull * tok;
+    key = (rem + 15) / 16;  // 0: no partial run
+    if (nfull) atomicAdd(&hist[NK - 1], nfull);
+    if (key) atomicAdd(&hist[key], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int k = NK - 1; k >= 1; --k) {
+      cur[k] = run;
+      run += (k == NK - 1 || k <= tt) ? hist[k] : 0;
+    }
+    *n_items = run;
+  }
+  __syncthreads();
+  if (tid < na) {
+    if (nfull) {
+      const int p = atomicAdd(&cur[NK - 1], nfull);
+      for (int q = 0; q < nfull; ++q) items[p + q] = e | ((q * tok) << 12);
+    }
+    if (key) items[atomicAdd(&cur[key], 1)] = e | ((nfull * tok) << 12);
+  }
+}
+
 // One work item (up to 16*TT pairs of one bucket) against 64 weight rows
 // (4 waves x 16 rows).  The activation block of the item is staged in LDS
 // (double buffered over the K blocks; each thread holds the next block's share
@@ -156,9 +201,10 @@ struct MmqW<T_Q6_K> {  // this lane's 4 x 8 bytes of ql, 2 x 8 bytes of qh | sca
   uint32_t d;
 };
 
-template <int T, bool GATEUP, int TT>
-__global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
+template <int T, bool GATEUP, int TT, int NW = 4>
+__global__ __launch_bounds__(64 * NW) void k_mmq(GemvArgs a) {
   constexpr int TOK = 16 * TT;  // pairs per work item
+  constexpr int NT = 64 * NW;   // threads: NW waves of 16 weight rows each
   static_assert(T == T_Q4_K || T == T_Q5_K || T == T_Q2_K || T == T_Q6_K || T == T_IQ4_XS || T == T_IQ2_XXS ||
                     T == T_IQ3_XXS,
                 "MFMA prefill types");
@@ -189,7 +235,7 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
   constexpr int BB = block_bytes(T);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
-  const int row = blockIdx.x * 64 + wave * 16 + n;  // weight row of this lane (B operand, output column)
+  const int row = blockIdx.x * (16 * NW) + wave * 16 + n;  // weight row of this lane (B operand, output column)
   const bool rv = row < a.nrows;
   const uint32_t wbytes = (uint32_t)((size_t)a.nrows * a.w_rstride);
   rsrc_t rw[NM];
@@ -210,7 +256,7 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
   }
 
   if constexpr (kGrid) {
-    for (int i = tid; i < (T == T_IQ2_XXS ? 256 : 128); i += 256) s_grid[i] = a.grid[i];
+    for (int i = tid; i < (T == T_IQ2_XXS ? 256 : 128); i += NT) s_grid[i] = a.grid[i];
     if (tid < 128) s_signs[tid] = a.signs[tid];
   }
   if (tid < TOK) {
@@ -268,24 +314,24 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
   // this thread's share of an activation block: qs chunks c = tid, tid + 256
   // (token c >> 4, 16-byte chunk c & 15), one 32-weight bsum (token tid >> 3,
   // sub-block tid & 7), and d of token tid (tid < TOK)
-  constexpr int NBSH = (TOK * 8 + 255) / 256;  // bsum dwords per thread
+  constexpr int NBSH = (TOK * 8 + NT - 1) / NT;  // bsum dwords per thread
   struct XShare {
-    uint4 q[TOK * 16 / 256];
+    uint4 q[TOK * 16 / NT];
     uint32_t bs[NBSH];
     float d;
   };
-  static_assert(TOK * 16 % 256 == 0 && TOK <= 256, "staging shares");
+  static_assert(TOK * 16 % NT == 0 && TOK <= NT, "staging shares");
   auto load_x = [&](int b, XShare &x) {
     const bool bv = b < nb;
 #pragma unroll
-    for (int r = 0; r < TOK * 16 / 256; ++r) {
-      const int c = tid + 256 * r, t = c >> 4, ch = c & 15;
+    for (int r = 0; r < TOK * 16 / NT; ++r) {
+      const int c = tid + NT * r, t = c >> 4, ch = c & 15;
       const int o = s_xoff[t];
       x.q[r] = bld16(rx, (bv && o != OOR) ? o + b * QK + 16 * ch : OOR, 0);
     }
 #pragma unroll
     for (int r = 0; r < NBSH; ++r) {
-      const int c = tid + 256 * r;
+      const int c = tid + NT * r;
       const int t = (c >> 3) & (TOK - 1), sb = c & 7;
       const int o = s_xoff[t];
       x.bs[r] = __builtin_amdgcn_raw_buffer_load_b32(rx, (bv && o != OOR && c < TOK * 8) ? o + (int)q8_bs_off(nb) + b * 32 + 4 * sb : OOR, 0, 0);
@@ -297,13 +343,13 @@ __global__ __launch_bounds__(256) void k_mmq(GemvArgs a) {
   };
   auto store_x = [&](const XShare &x, int buf) {
 #pragma unroll
-    for (int r = 0; r < TOK * 16 / 256; ++r) {
-      const int c = tid + 256 * r, t = c >> 4, ch = c & 15;
+    for (int r = 0; r < TOK * 16 / NT; ++r) {
+      const int c = tid + NT * r, t = c >> 4, ch = c & 15;
       *reinterpret_cast<uint4 *>(&s_xq[buf][t][16 * ch]) = x.q[r];
     }
 #pragma unroll
     for (int r = 0; r < NBSH; ++r) {
-      const int c = tid + 256 * r;
+      const int c = tid + NT * r;
       if (c < TOK * 8) {
         const int lo = (int)(int16_t)(x.bs[r] & 0xffffu), hi = (int)(int16_t)(x.bs[r] >> 16);
         if constexpr (K45) {
