@@ -18,8 +18,11 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -ffp-contract=off: the quantizer, router and SwiGLU are bit-reproducible
 # IQ2/K-quant arithmetic only if no multiply-add is fused behind our back.
 # -packed-fp32-ops off: packed fp32 VALU forms are avoided on this target.
+# -amdgpu-mfma-vgpr-form: MFMA results land in ordinary VGPRs, so the float
+# epilogue of the prefill tiles reads them without v_accvgpr_read copies.
 FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-shared", "-std=c++17", "-ffp-contract=off",
-         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function"]
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-mllvm", "-amdgpu-mfma-vgpr-form",
+         "-Wall", "-Wno-unused-function"]
 
 
 def build(verbose: bool = False) -> str:

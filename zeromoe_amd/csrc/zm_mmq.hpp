@@ -363,6 +363,8 @@ __global__ __launch_bounds__(64 * NW) void k_mmq(GemvArgs a) {
     if (tid < TOK) s_xd[buf][tid] = x.d;
   };
 
+  // per (matrix, token tile, output): f += d_x * (d * isum - dmin * imin), as
+  // two fmas (the tile epilogue is most of the per-tile VALU work)
   float f[NM][TT][4];
 #pragma unroll
   for (int m = 0; m < NM; ++m)
@@ -447,7 +449,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmq(GemvArgs a) {
           mn = __builtin_amdgcn_mfma_f32_16x16x4f32(bs1, mb1[m], mn, 0, 0, 0);
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            f[m][t][j] += xdj[j] * (dd[m] * (float)(dlo[j] + 8 * dhi[j] + 16 * d5[j]) - dm[m] * mn[j]);
+            f[m][t][j] = __builtin_fmaf(xdj[j], __builtin_fmaf(dd[m], (float)(dlo[j] + 8 * dhi[j] + 16 * d5[j]), -dm[m] * mn[j]), f[m][t][j]);
         }
       }
     } else if constexpr (kGrid) {
@@ -531,7 +533,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmq(GemvArgs a) {
             for (int j = 0; j < 4; ++j) isum[j] = __mul24(S0[m][c], d0[j]) + __mul24(S1[m][c], d1[j]) + isum[j];
           }
 #pragma unroll
-          for (int j = 0; j < 4; ++j) f[m][t][j] += xdj[j] * (DD[m] * (float)isum[j]);
+          for (int j = 0; j < 4; ++j) f[m][t][j] = __builtin_fmaf(xdj[j], DD[m] * (float)isum[j], f[m][t][j]);
         }
       }
     } else if constexpr (T == T_IQ4_XS) {
@@ -574,7 +576,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmq(GemvArgs a) {
           for (int j = 0; j < 4; ++j) isum[j] = __mul24(s0[c], d0[j]) + __mul24(s1[c], d1[j]) + isum[j];
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) f[m][t][j] += s_xd[buf][16 * t + 4 * g + j] * (d * (float)isum[j]);
+        for (int j = 0; j < 4; ++j) f[m][t][j] = __builtin_fmaf(s_xd[buf][16 * t + 4 * g + j], d * (float)isum[j], f[m][t][j]);
       }
     }
     } else if constexpr (T == T_Q6_K) {
@@ -625,7 +627,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmq(GemvArgs a) {
           off = __builtin_amdgcn_mfma_f32_16x16x4f32((float)s_bs[buf][16 * t + n][4 * i + g], mb[i], off, 0, 0, 0);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          f[m][t][j] += s_xd[buf][16 * t + 4 * g + j] * (d * (float)(isum[j] - 32 * (int)off[j]));
+          f[m][t][j] = __builtin_fmaf(s_xd[buf][16 * t + 4 * g + j], d * (float)(isum[j] - 32 * (int)off[j]), f[m][t][j]);
       }
     }
     } else {
@@ -676,7 +678,8 @@ __global__ __launch_bounds__(64 * NW) void k_mmq(GemvArgs a) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) mn = __builtin_amdgcn_mfma_f32_16x16x4f32(bs[i], mb[m][i], mn, 0, 0, 0);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) f[m][t][j] += xdj[j] * (dd[m] * (float)isum[j] - dm[m] * mn[j]);
+          for (int j = 0; j < 4; ++j)
+            f[m][t][j] = __builtin_fmaf(xdj[j], __builtin_fmaf(dd[m], (float)isum[j], -dm[m] * mn[j]), f[m][t][j]);
         }
       }
     }
