@@ -343,6 +343,56 @@ int launch_ggml_moe_unpack_scatter(const void *src, void *gate, void *up, void *
  * Synchronises the device.  Returns the count copied. */
 int zm_debug_trace(uint64_t *host, int n);
 
+/* ---------------------------------------------------------------- CPU lane (hot/cold split) */
+
+/* The cold branch of a layer whose experts are split between VRAM (hot) and
+ * host memory (cold): the cold experts run on the host cores while the GPU
+ * computes the hot ones.  Replaces EarlyReadyLane
+ * (models/graph/early_ready_lane.hpp:75-211) with the branch semantics of
+ * backends/ggml/moe_partial_route_ggml.hpp:21-60: a route (token s, slot k) of
+ * expert e is cold when route_map[e] >= 0 (its host slot); its weight is
+ * w * route_mask[e] (1 when route_mask is NULL).  The caller runs the hot
+ * branch itself (zm_moe_forward with the hot slot table) and the lane adds
+ * sum over cold routes (k ascending) of w' * expert(x) to its output.
+ * Weights are ggml expert tensors in host memory: gate/up [n_slots][F][row(H)],
+ * down [n_slots][H][row(F)], Q2_K, Q3_K or Q4_K. */
+typedef struct zm_cold_lane zm_cold_lane;
+typedef struct zm_cold_lane_desc {
+  int32_t H, F, n_experts, topk;
+  int32_t type_gate, type_up, type_down;
+  const void *w_gate, *w_up, *w_down; /* host memory, borrowed */
+  int32_t n_slots;                     /* host expert slots */
+  const int32_t *route_map;            /* [n_experts] expert -> host slot or -1 (copied) */
+  const float *route_mask;             /* [n_experts] or NULL (copied) */
+  int32_t max_tokens;                  /* tokens per call */
+  int32_t n_threads;                   /* host threads of the lane */
+  int32_t scalar;                      /* 1: scalar dots even on AVX-512 hosts (same bits) */
+} zm_cold_lane_desc;
+typedef struct zm_cold_lane_stats {
+  int64_t fork_ns, compute_begin_ns, compute_end_ns, merge_ns; /* steady-clock times of the last call */
+  int32_t vectorized;                                          /* AVX-512 VNNI dots in use */
+} zm_cold_lane_stats;
+/* Create (NULL on a bad descriptor or unsupported types, zm_last_error says
+ * why).  Host memory only; device buffers and the lane thread are set up on
+ * the first fork.  Replaces EarlyReadyLane::prepare (early_ready_lane.hpp:196). */
+zm_cold_lane *zm_cold_lane_create(const zm_cold_lane_desc *desc);
+void zm_cold_lane_destroy(zm_cold_lane *lane);
+/* Fork: stream-ordered copies of x [S][H], ids [S][topk] (router expert ids)
+ * and weights [S][topk] (device pointers) into the lane's pinned buffers; the
+ * lane thread starts as soon as they land, while the caller queues the hot
+ * GPU work.  The fork of early_ready_lane.hpp:3-10. */
+int zm_cold_lane_fork(zm_cold_lane *lane, const float *x, const int32_t *ids, const float *weights, int S,
+                      void *stream);
+/* Merge: waits (host) for the lane's result, uploads it on the lane's own
+ * stream and makes `stream` add it to out [S][H] (device).  The merge of
+ * early_ready_lane.hpp:7-9 / moe_block.hpp:182-184. */
+int zm_cold_lane_merge(zm_cold_lane *lane, float *out, int S, void *stream);
+/* The lane's computation on host buffers, synchronously (no device): out [S][H]
+ * = the cold branch.  For callers without a GPU stream and for tests. */
+int zm_cold_lane_compute_host(zm_cold_lane *lane, const float *x, const int32_t *ids, const float *weights, int S,
+                              float *out);
+int zm_cold_lane_get_stats(const zm_cold_lane *lane, zm_cold_lane_stats *stats);
+
 #ifdef __cplusplus
 }
 #endif

@@ -26,12 +26,12 @@ Torch is used only for device memory and the current stream.
 """
 from __future__ import annotations
 
-from .ops import (GGML_TYPES, ExpertExecutor, MoELayer, block_dots, bucket, builtin_iq2xxs_grid, builtin_iq3xxs_grid,
+from .ops import (GGML_TYPES, ColdLane, ExpertExecutor, MoELayer, block_dots, bucket, builtin_iq2xxs_grid, builtin_iq3xxs_grid,
                   builtin_iq4nl_table,                   f32_matmul,
                   glm5next_router_topk, init, moe_unpack, mul_mat_id, mul_mat_id_f32, quantize_q8_K, router, row_size,
                   scatter_accum, set_iq2xxs_grid, set_iq3xxs_grid, set_iq4nl_table, swiglu)
 
-__all__ = ["GGML_TYPES", "ExpertExecutor", "MoELayer", "block_dots", "bucket", "builtin_iq2xxs_grid", "builtin_iq3xxs_grid", "builtin_iq4nl_table",
+__all__ = ["GGML_TYPES", "ColdLane", "ExpertExecutor", "MoELayer", "block_dots", "bucket", "builtin_iq2xxs_grid", "builtin_iq3xxs_grid", "builtin_iq4nl_table",
            "f32_matmul",
            "glm5next_router_topk", "init", "moe_unpack", "mul_mat_id", "mul_mat_id_f32", "quantize_q8_K", "router", "row_size",
            "scatter_accum", "set_iq2xxs_grid", "set_iq3xxs_grid", "set_iq4nl_table", "swiglu"]

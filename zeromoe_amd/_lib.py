@@ -37,6 +37,18 @@ class ZmExpertScratch(C.Structure):
                 ("cap_sd", SZ), ("cap_si", SZ), ("device_id", I32)]
 
 
+class ZmColdLaneDesc(C.Structure):
+    _fields_ = [("H", I32), ("F", I32), ("n_experts", I32), ("topk", I32),
+                ("type_gate", I32), ("type_up", I32), ("type_down", I32),
+                ("w_gate", P), ("w_up", P), ("w_down", P), ("n_slots", I32), ("route_map", P), ("route_mask", P),
+                ("max_tokens", I32), ("n_threads", I32), ("scalar", I32)]
+
+
+class ZmColdLaneStats(C.Structure):
+    _fields_ = [("fork_ns", C.c_int64), ("compute_begin_ns", C.c_int64), ("compute_end_ns", C.c_int64),
+                ("merge_ns", C.c_int64), ("vectorized", I32)]
+
+
 _MM = (None, [P, P, P, I, I, I])
 _MMS = (None, [P, P, P, I, I, I, P])
 _XS = C.POINTER(ZmExpertScratch)
@@ -94,6 +106,12 @@ SIGNATURES = {
     "zm_expert_ffn_finish_stage2": (I, [_XS, P, I, I, P]),
     "zm_expert_bad_counts": (I, [_XS, P, I]),
     "zm_moe_forward": (I, [C.POINTER(ZmMoeLayer), P, P, I, P, P, P, P, SZ, P]),
+    "zm_cold_lane_create": (P, [C.POINTER(ZmColdLaneDesc)]),
+    "zm_cold_lane_destroy": (None, [P]),
+    "zm_cold_lane_fork": (I, [P, P, P, P, I, P]),
+    "zm_cold_lane_merge": (I, [P, P, I, P]),
+    "zm_cold_lane_compute_host": (I, [P, P, P, P, I, P]),
+    "zm_cold_lane_get_stats": (I, [P, C.POINTER(ZmColdLaneStats)]),
 }
 
 _lib = None

@@ -12,7 +12,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG_DIR)
 SRC = os.path.join(PKG_DIR, "csrc")
 OUT = os.path.join(PKG_DIR, "lib", "libzeromoe_hip.so")
-SOURCES = ("zm_api.hip", "zm_dec_a.hip", "zm_dec_b.hip", "zm_exec.hip", "zm_pack.hip")
+SOURCES = ("zm_api.hip", "zm_dec_a.hip", "zm_dec_b.hip", "zm_exec.hip", "zm_pack.hip", "zm_lane.hip")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # -ffp-contract=off: the quantizer, router and SwiGLU are bit-reproducible

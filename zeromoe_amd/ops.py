@@ -7,7 +7,7 @@ from typing import Optional
 
 import torch
 
-from ._lib import ZmExpertScratch, ZmMoeLayer, ZmRouterSpec, ZmTensor, check, lib
+from ._lib import ZmColdLaneDesc, ZmColdLaneStats, ZmExpertScratch, ZmMoeLayer, ZmRouterSpec, ZmTensor, check, lib
 
 GGML_TYPES = {"f32": 0, "q2_K": 10, "q3_K": 11, "q4_K": 12, "q5_K": 13, "q6_K": 14, "q8_K": 15, "iq2_xxs": 16, "iq3_xxs": 18, "iq4_xs": 23, "i32": 26}
 BLOCK_BYTES = {10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 15: 292, 16: 66, 18: 98, 23: 136}
@@ -447,3 +447,68 @@ def moe_unpack(src: torch.Tensor, gate: torch.Tensor, up: torch.Tensor, down: to
                                                   _stream(stream))
     if rc != 0:
         raise RuntimeError(f"launch_ggml_moe_unpack failed ({rc}): {lib().zm_last_error().decode()}")
+
+
+# ---------------------------------------------------------------- CPU lane of a hot/cold split
+
+
+class ColdLane:
+    """The cold branch of a hot/cold expert split on the host cores
+    (zm_cold_lane_*, the reference's EarlyReadyLane,
+    models/graph/early_ready_lane.hpp:75-211).  Weights are host numpy uint8
+    arrays in ggml layout: gate/up (n_slots, F, row_bytes(H)), down
+    (n_slots, H, row_bytes(F)); route_map maps router experts to host slots
+    (-1: not cold), route_mask optionally scales their weights."""
+
+    def __init__(self, H, F, n_experts, topk, type_gate, type_up, type_down, w_gate, w_up, w_down, route_map,
+                 route_mask=None, max_tokens=1, n_threads=8, scalar=False):
+        import numpy as np
+
+        self._keep = [np.ascontiguousarray(w_gate), np.ascontiguousarray(w_up), np.ascontiguousarray(w_down),
+                      np.ascontiguousarray(route_map, np.int32)]
+        if route_mask is not None:
+            self._keep.append(np.ascontiguousarray(route_mask, np.float32))
+        d = ZmColdLaneDesc()
+        d.H, d.F, d.n_experts, d.topk = H, F, n_experts, topk
+        d.type_gate, d.type_up, d.type_down = type_gate, type_up, type_down
+        d.w_gate, d.w_up, d.w_down = (a.ctypes.data for a in self._keep[:3])
+        d.n_slots = self._keep[0].shape[0]
+        d.route_map = self._keep[3].ctypes.data
+        d.route_mask = self._keep[4].ctypes.data if route_mask is not None else None
+        d.max_tokens, d.n_threads, d.scalar = max_tokens, n_threads, int(scalar)
+        self.H, self.topk = H, topk
+        self._h = lib().zm_cold_lane_create(C.byref(d))
+        if not self._h:
+            raise RuntimeError(f"zm_cold_lane_create: {lib().zm_last_error().decode()}")
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().zm_cold_lane_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def compute_host(self, x, ids, weights):
+        """The cold branch on host numpy arrays: x (S, H) f32, ids/weights (S, topk)."""
+        import numpy as np
+
+        x = np.ascontiguousarray(x, np.float32)
+        ids = np.ascontiguousarray(ids, np.int32)
+        weights = np.ascontiguousarray(weights, np.float32)
+        out = np.zeros_like(x)
+        check(lib().zm_cold_lane_compute_host(self._h, x.ctypes.data, ids.ctypes.data, weights.ctypes.data,
+                                              x.shape[0], out.ctypes.data), "zm_cold_lane_compute_host")
+        return out
+
+    def fork(self, x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, stream=None):
+        check(lib().zm_cold_lane_fork(self._h, x.data_ptr(), ids.data_ptr(), weights.data_ptr(), x.shape[0],
+                                      _stream(stream)), "zm_cold_lane_fork")
+
+    def merge(self, out: torch.Tensor, stream=None):
+        check(lib().zm_cold_lane_merge(self._h, out.data_ptr(), out.shape[0], _stream(stream)), "zm_cold_lane_merge")
+
+    def stats(self) -> dict:
+        st = ZmColdLaneStats()
+        check(lib().zm_cold_lane_get_stats(self._h, C.byref(st)), "zm_cold_lane_get_stats")
+        return {f: getattr(st, f) for f, _ in ZmColdLaneStats._fields_}
