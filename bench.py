@@ -282,8 +282,8 @@ def cpu_baseline(seconds: float = 10.0):
     AVX-512: serial Q8_K of x on one thread, OpenMP over the output rows of
     gate+up and of down, one VNNI vec_dot per row; oracle/zm_oracle.c,
     zmo_moe_forward_fast, bit-identical to the oracle) at the c2 shape, S=1,
-    on this host's cores: ids re-drawn every iteration over a 32-expert pool
-    (218 MB of weights, beyond the LLC)."""
+    on this host's cores: ids re-drawn every iteration over all 128 experts
+    of the layer (875 MB of weights, beyond any host cache)."""
     import numpy as np
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -291,7 +291,7 @@ def cpu_baseline(seconds: float = 10.0):
 
     c = CONFIGS["c2"]
     H, F, K = c["H"], c["F"], c["K"]
-    pool = 32
+    pool = c["E"]
     Wg = O.random_blocks(Q2, pool * F, H, seed=1).reshape(pool, F, -1)
     Wu = O.random_blocks(Q2, pool * F, H, seed=2).reshape(pool, F, -1)
     Wd = O.random_blocks(Q3, pool * H, F, seed=3).reshape(pool, H, -1)
@@ -318,7 +318,8 @@ def cpu_baseline(seconds: float = 10.0):
     gbs = K * expert_bytes(c) / (us * 1e-6) / 1e9
     return {"value": round(us, 1), "unit": "us/layer", "GBps": round(gbs, 2), "cores": threads, "kind": "port",
             "nproc": os.cpu_count(), "avx512_vnni": avx,
-            "sample": f"c2 layer S=1 (8 of a 32-expert pool per iteration), {n} iterations in {el:.1f} s; "
+            "sample": f"c2 layer S=1 (8 of the layer's {pool} experts per iteration, {pool * expert_bytes(c) / 1e6:.0f} MB), "
+                      f"{n} iterations in {el:.1f} s; "
                       f"restatement of the reference CPU path ({'AVX-512 VNNI' if avx else 'scalar, no AVX-512 on this host'} "
                       f"Q2_K/Q3_K dots, serial Q8_K, OpenMP over output rows, {threads} threads of nproc={os.cpu_count()})"}
 
