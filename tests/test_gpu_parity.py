@@ -737,3 +737,27 @@ def test_c3_full_size_vs_oracle():
     assert rc.max() >= 100, rc.max()  # skewed: several work items for the heaviest experts
     ref = b.oracle_forward(ids_h, w_h, nthreads=16)
     assert_close_layer(out.cpu().numpy(), ref, slack=lambda: b.requant_slack(ids_h, w_h))
+
+
+@pytest.mark.parametrize("name", ["c1", "c2"])
+def test_layer_with_ggml_quantized_weights(name):
+    """The configurations state weights quantized from seeded N(0, 0.02) by
+    ggml's quantizers: the experts a token routes to are filled that way here
+    (the oracle's restated quantizers, a portable splitmix64 + Box-Muller
+    generator) instead of random valid blocks; decode through the fused
+    kernel against the oracle."""
+    c = CONFIGS[name]
+    b = Built(c, seed=71)
+    ids_r, w_r = b.oracle_route()
+    for e in sorted(set(int(v) for v in ids_r.reshape(-1) if v >= 0)):
+        for k, (W, t, rows, n) in enumerate([(b.wg, c.tg, c.F, c.H), (b.wu, c.tg, c.F, c.H), (b.wd, c.td, c.H, c.F)]):
+            x = O.fill_normal(1000 * e + k, rows * n, 0.0, 0.02).reshape(rows, n)
+            W[e].copy_(torch.from_numpy(O.quantize(t, x)).cuda())
+    L = b.layer()
+    out, ids, w = L.forward(torch.from_numpy(b.x).cuda(), torch.from_numpy(b.logits).cuda())
+    _sync()
+    assert L.status(c.S) == 0
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_r)
+    ids_h, w_h = ids.cpu().numpy(), w.cpu().numpy()
+    ref = b.oracle_forward(ids_h, w_h)
+    assert_close_layer(out.cpu().numpy(), ref, slack=lambda: b.requant_slack(ids_h, w_h))
