@@ -12,15 +12,20 @@
 // folded into the weights: the lane multiplies its nibbles by lo and by hi
 // (products <= 105, int8), and two MFMA chains accumulate over the block:
 //   isum[t][r] = D_lo + 8 * D_hi = sum_sb sc[r][sb] * (q[r] . x[t])_sb  (int32, exact)
-//   imin[t][r] = sum_sb bsum[t][sb] * m[r][sb]           (v_mfma_f32_16x16x4f32;
-//                |terms| < 2^18, sums < 2^24: exact in fp32)
-//   f[t][r]   += d_x[t] * (d[r] * isum - dmin[r] * imin)  (ggml's vec_dot_q4_K_q8_K combine)
-// K order of a 64-weight chunk i (qs bytes 32i..32i+31): k-group g holds the
-// low nibbles (g < 2) or high nibbles (g >= 2) of bytes 16*(g & 1)..+15, i.e.
-// weights 64i + 16g .. +15, so the activation operand is the contiguous 16
-// bytes 64i + 16g of the token's row.  The weight unpacking is done once per
-// block for all MMQ_TT token tiles of the work item.
-// No dequantized weight copy is materialized.
+//   mn[t][r]   = sum_sb bsum[t][sb] * (-dmin[r] * m[r][sb])   (v_mfma_f32_16x16x4f32;
+//                -dmin * m is exact in fp32, so mn is -dmin * imin to fp32 rounding)
+//   f[t][r]   += d_x[t] * (d[r] * isum + mn)  (ggml's vec_dot_q4_K_q8_K combine)
+// Q4_K K order of a 64-weight chunk i (qs group i, bytes 32i..32i+31, holding
+// sub-block 2i in its low nibbles and 2i + 1 in its high nibbles): k-group g
+// holds bytes 8g..8g+7 of the group, low nibbles then high nibbles, i.e.
+// weights 64i + 8g .. +7 and 64i + 32 + 8g .. +7, so every qs byte is loaded
+// by one lane only; the activation operand is read in the same order (two
+// 8-byte LDS reads).  Q5_K keeps the contiguous order: k-group g holds the low
+// nibbles (g < 2) or high nibbles (g >= 2) of bytes 16*(g & 1)..+15, i.e.
+// weights 64i + 16g .. +15.  The weight unpacking is done once per block for
+// all token tiles of the work item.  No dequantized weight copy is materialized.
+// Q4_K activations reach LDS by direct buffer-to-LDS loads (no register
+// staging), token rows XOR-swizzled in 16-byte chunks by the token index.
 //
 // IQ2_XXS / IQ3_XXS (grid values up to 43 / 62 with per-8-weight signs, and a
 // (2 ls + 1) <= 31 scale per 32-weight sub-block) take the same per-sub-block
@@ -41,8 +46,8 @@
 // 32h + 16(g & 1) .. +15, i.e. weights 64c + 16g .. +15 of sub-block
 // 8h + 2j + (g & 1), each byte multiplied by that sub-block's scale; one MFMA
 // chain over the 4 chunks gives isum = sum_sb sc * (q . x)_sb exactly, the
-// mins term sum_sb m * bsum16 goes through four v_mfma_f32_16x16x4f32 (K = 16
-// sub-blocks), and f += d_x * (d * isum - dmin * imin) (ggml's vec_dot_q2_K_q8_K).  Activations are the planar Q8_K rows of the decode
+// mins term sum_sb (-dmin * m) * bsum16 goes through four v_mfma_f32_16x16x4f32
+// (K = 16 sub-blocks), and f += d_x * (d * isum + mn) (ggml's vec_dot_q2_K_q8_K).  Activations are the planar Q8_K rows of the decode
 // path (qs | bsums | d).
 //
 // Q6_K (a 6-bit value and a signed 8-bit scale per 16-weight sub-block: the
@@ -66,6 +71,36 @@ namespace zm {
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 typedef float v4f_t __attribute__((ext_vector_type(4)));
 typedef unsigned short v2u16_t __attribute__((ext_vector_type(2)));
+typedef short v2i16_t __attribute__((ext_vector_type(2)));
+typedef unsigned v4u_t __attribute__((ext_vector_type(4)));
+
+// buffer-to-LDS loads (lane L's `bytes` land at lds + bytes * L; out-of-range
+// lanes write zeros) issued as inline asm: the compiler's wait insertion does not
+// track them, so the reads of the other LDS buffer are not held behind them.
+// The caller waits for them itself (vmcnt(0)) before the barrier that publishes
+// the buffer.
+__device__ __forceinline__ v4u_t dma_rsrc(const void *p, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  return v4u_t{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is written by the asm and by nothing else here
+__device__ __forceinline__ void dma_lds16(v4u_t rs, uint32_t lds, int vo) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(vo), "s"(rs)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma_lds4(v4u_t rs, uint32_t lds, int vo) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(vo), "s"(rs)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
 
 // four packed bytes times a small factor, bytewise (every product < 256: no
 // carry crosses a byte): one packed 16-bit multiply
@@ -161,9 +196,9 @@ __global__ __launch_bounds__(1024) void k_mmq_items_lpt(const int32_t *__restric
 template <int T>
 struct MmqW;
 template <>
-struct MmqW<T_Q4_K> {  // d, dmin, scales | this lane's 4 x 16 bytes of qs
+struct MmqW<T_Q4_K> {  // d, dmin, scales | this lane's 8 bytes of each 32-byte qs group
   uint4 hdr;
-  uint4 qs[4];
+  uint2 qs[4];
 };
 template <>
 struct MmqW<T_Q5_K> {  // d, dmin, scales | this lane's 16 bytes of qh | 4 x 16 bytes of qs
@@ -202,7 +237,7 @@ struct MmqW<T_Q6_K> {  // this lane's 4 x 8 bytes of ql, 2 x 8 bytes of qh | sca
 };
 
 template <int T, bool GATEUP, int TT, int NW = 4>
-__global__ __launch_bounds__(64 * NW) void k_mmq(GemvArgs a) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_Q4_K && !GATEUP && TT <= 4 ? 4 : 1))) void k_mmq(GemvArgs a) {
   constexpr int TOK = 16 * TT;  // pairs per work item
   constexpr int NT = 64 * NW;   // threads: NW waves of 16 weight rows each
   static_assert(T == T_Q4_K || T == T_Q5_K || T == T_Q2_K || T == T_Q6_K || T == T_IQ4_XS || T == T_IQ2_XXS ||
@@ -213,9 +248,17 @@ __global__ __launch_bounds__(64 * NW) void k_mmq(GemvArgs a) {
   __shared__ uint64_t s_signs[kGrid ? 128 : 1];
   constexpr bool K45 = T == T_Q4_K || T == T_Q5_K;
   constexpr int NBS = K45 ? 8 : 16;  // bsums per block used: 32-sums (Q4_K, Q5_K) or 16-sums (Q2_K, Q6_K)
-  __shared__ __attribute__((aligned(16))) uint8_t s_xq[2][TOK][MMQ_XS];
-  __shared__ int s_bs[2][TOK][NBS];
-  __shared__ float s_xd[2][TOK];
+  // Q4_K: the activation blocks reach LDS by direct buffer-to-LDS loads (no
+  // register staging); a token's row is 256 bytes with its 16-byte chunks
+  // XOR-swizzled by the token index (chunk c of token t at c ^ (t & 15)), so the
+  // 16 tokens of an MFMA A operand read 16 different bank groups; the raw int16
+  // 16-sums are kept and added pairwise when read
+  constexpr bool kDma = T == T_Q4_K;
+  constexpr int NXB = 2;  // activation buffers
+  __shared__ __attribute__((aligned(16))) uint8_t s_xq[NXB][TOK][kDma ? QK : MMQ_XS];
+  __shared__ int s_bs[2][TOK][kDma ? 1 : NBS];
+  __shared__ __attribute__((aligned(16))) int16_t s_bs16[kDma ? NXB : 1][kDma ? TOK : 1][16];
+  __shared__ __attribute__((aligned(16))) float s_xd[NXB][TOK];
   __shared__ int s_xoff[TOK];      // byte offset of each pair's activation row (OOR: none)
   __shared__ int s_pair[TOK];
   int e, pc, p1;
@@ -242,6 +285,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmq(GemvArgs a) {
   rw[0] = make_rsrc(a.w0 + (size_t)e * a.w_estride, wbytes);
   if constexpr (GATEUP) rw[1] = make_rsrc(a.w1 + (size_t)e * a.w_estride, wbytes);
   const rsrc_t rx = make_rsrc(a.xq, a.xq_bytes);
+  const v4u_t rxd = dma_rsrc(a.xq, a.xq_bytes);
   const int vrow = rv ? row * (int)a.w_rstride : OOR;
   const int Kp = a.dense_S > 0 ? 1 : a.K;
   const int nb = a.nb;
@@ -276,7 +320,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmq(GemvArgs a) {
       if constexpr (T == T_Q4_K) {
         w[m].hdr = bld16(rw[m], vo, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) w[m].qs[i] = bld16(rw[m], vo + 16 + 32 * i + 16 * (g & 1), 0);
+        for (int i = 0; i < 4; ++i) w[m].qs[i] = bld8(rw[m], vo + 16 + 32 * i + 8 * g, 0);
       } else if constexpr (T == T_Q5_K) {
         w[m].hdr = bld16(rw[m], vo, 0);
         w[m].qh = bld16(rw[m], vo + 16 + 16 * (g & 1), 0);
@@ -363,7 +407,38 @@ __global__ __launch_bounds__(64 * NW) void k_mmq(GemvArgs a) {
     if (tid < TOK) s_xd[buf][tid] = x.d;
   };
 
-  // per (matrix, token tile, output): f += d_x * (d * isum - dmin * imin), as
+  // direct loads of block b's activations into buffer buf (Q4_K): the qs of
+  // TOK tokens (1 KB = 4 tokens per wave instruction), their 16 bsums (32 B per
+  // token) and d; out-of-range lanes write zeros
+  auto dma_x = [&](int b, int buf) {
+    if constexpr (kDma) {
+      const bool bv = b < nb;
+      constexpr int QI = TOK / 4 / NW;  // qs instructions per wave
+      static_assert(TOK % (4 * NW) == 0, "qs instructions per wave");
+#pragma unroll
+      for (int i = 0; i < QI; ++i) {
+        const int t0 = 4 * (QI * wave + i);
+        const int t = t0 + (lane >> 4), c = (lane & 15) ^ (t & 15);
+        const int o = s_xoff[t];
+        dma_lds16(rxd, lds_addr(&s_xq[buf][t0][0]), (bv && o != OOR) ? o + b * QK + 16 * c : OOR);
+      }
+      for (int i = wave; 32 * i < TOK; i += NW) {  // bsums: 2 lanes per token
+        const int t = 32 * i + (lane >> 1);
+        if (t >= TOK) break;  // lanes past the tile write nothing
+        const int o = s_xoff[t];
+        dma_lds16(rxd, lds_addr(&s_bs16[buf][32 * i][0]),
+                  (bv && o != OOR) ? o + (int)q8_bs_off(nb) + b * 32 + 16 * (lane & 1) : OOR);
+      }
+      for (int i = wave; 64 * i < TOK; i += NW) {  // d: one float per token
+        const int t = 64 * i + lane;
+        if (t >= TOK) break;
+        const int o = s_xoff[t];
+        dma_lds4(rxd, lds_addr(&s_xd[buf][64 * i]), (bv && o != OOR) ? o + (int)q8_d_off(nb) + 4 * b : OOR);
+      }
+    }
+  };
+
+  // per (matrix, token tile, output): f += d_x * (d * isum + mn), as
   // two fmas (the tile epilogue is most of the per-tile VALU work)
   float f[NM][TT][4];
 #pragma unroll
@@ -373,16 +448,9 @@ __global__ __launch_bounds__(64 * NW) void k_mmq(GemvArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) f[m][t][j] = 0.f;
 
-  WBlk wcur[NM], wnxt[NM];
   XShare xs;
-  load_w(0, wcur);
-  load_x(0, xs);
-  store_x(xs, 0);
-  load_x(1, xs);
-  __syncthreads();
-  for (int b = 0; b < nb; ++b) {
-    const int buf = b & 1;
-    load_w(b + 1, wnxt);
+  // block b of the K loop from the weights in wcur and activation buffer b & 1
+  auto step = [&](int b, int buf, const WBlk(&wcur)[NM]) {
     if constexpr (K45) {
       // both matrices' operands first, then one pass over the token tiles: the
       // activation operand (and the bsums of the min product) is read from LDS
@@ -400,26 +468,46 @@ __global__ __launch_bounds__(64 * NW) void k_mmq(GemvArgs a) {
         dd[m] = h2f((uint16_t)(wcur[m].hdr.x & 0xffffu));
         dm[m] = h2f((uint16_t)(wcur[m].hdr.x >> 16));
         // B operand of the min product: m[row][sb] for sb = g and g + 4
-        mb0[m] = (float)((mn_lo >> (8 * g)) & 0xffu);
-        mb1[m] = (float)((mn_hi >> (8 * g)) & 0xffu);
+        // with -dmin folded in (exact: an f16 times a 6-bit integer), so the
+        // product comes out as the whole min term
+        mb0[m] = -dm[m] * (float)((mn_lo >> (8 * g)) & 0xffu);
+        mb1[m] = -dm[m] * (float)((mn_hi >> (8 * g)) & 0xffu);
         // scale-folded weights of the 4 chunks: lane's sub-block 2i + (g >> 1),
         // sc = 8 * hi + lo; Q5_K: the fifth bit (bit 2i + (g >> 1) of the lane's
         // qh bytes) is a third chain with the whole scale, isum = D_lo + 8 D_hi + 16 D_5
+        if constexpr (kDma) {
+          // chunk i = qs group i (sub-blocks 2i, 2i + 1): the lane's 8 bytes
+          // 8g .. 8g + 7 give 8 weights of each sub-block, low nibbles then
+          // high nibbles (the activation operand is read in the same order)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t scw = i < 2 ? sc_lo : sc_hi;
-          const uint32_t sc = (scw >> (16 * (i & 1) + hs)) & 0xffu;
-          const uint32_t lo = sc & 7u, hi = sc >> 3;
-          const uint4 q = wcur[m].qs[i];
-          const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t scw = (i < 2 ? sc_lo : sc_hi) >> (16 * (i & 1));
+            const uint32_t s0 = scw & 0xffu, s1 = (scw >> 8) & 0xffu;
+            const uint2 q = wcur[m].qs[i];
+            const uint32_t n0 = q.x & 0x0f0f0f0fu, n1 = q.y & 0x0f0f0f0fu;
+            const uint32_t n2 = (q.x >> 4) & 0x0f0f0f0fu, n3 = (q.y >> 4) & 0x0f0f0f0fu;
+            bl[m][i] = v4i_t{(int)mul_bytes(n0, s0 & 7u), (int)mul_bytes(n1, s0 & 7u), (int)mul_bytes(n2, s1 & 7u),
+                             (int)mul_bytes(n3, s1 & 7u)};
+            bh[m][i] = v4i_t{(int)mul_bytes(n0, s0 >> 3), (int)mul_bytes(n1, s0 >> 3), (int)mul_bytes(n2, s1 >> 3),
+                             (int)mul_bytes(n3, s1 >> 3)};
+          }
+        } else {
 #pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const uint32_t nib = (qw[c] >> ns) & 0x0f0f0f0fu;
-            bl[m][i][c] = (int)mul_bytes(nib, lo);
-            bh[m][i][c] = (int)mul_bytes(nib, hi);
-            if constexpr (T == T_Q5_K) {
-              const uint32_t hq[4] = {wcur[m].qh.x, wcur[m].qh.y, wcur[m].qh.z, wcur[m].qh.w};
-              b5[m][i][c] = (int)mul_bytes((hq[c] >> (2 * i + (g >> 1))) & 0x01010101u, sc);
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t scw = i < 2 ? sc_lo : sc_hi;
+            const uint32_t sc = (scw >> (16 * (i & 1) + hs)) & 0xffu;
+            const uint32_t lo = sc & 7u, hi = sc >> 3;
+            const uint4 q = wcur[m].qs[i];
+            const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              const uint32_t nib = (qw[c] >> ns) & 0x0f0f0f0fu;
+              bl[m][i][c] = (int)mul_bytes(nib, lo);
+              bh[m][i][c] = (int)mul_bytes(nib, hi);
+              if constexpr (T == T_Q5_K) {
+                const uint32_t hq[4] = {wcur[m].qh.x, wcur[m].qh.y, wcur[m].qh.z, wcur[m].qh.w};
+                b5[m][i][c] = (int)mul_bytes((hq[c] >> (2 * i + (g >> 1))) & 0x01010101u, sc);
+              }
             }
           }
         }
@@ -429,9 +517,26 @@ __global__ __launch_bounds__(64 * NW) void k_mmq(GemvArgs a) {
         if (t >= nt) continue;
         const uint8_t *xr = &s_xq[buf][16 * t + n][0];
         v4i_t xa[4];
+        float bs0, bs1;
+        if constexpr (kDma) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xa[i] = *reinterpret_cast<const v4i_t *>(xr + 64 * i + 16 * g);
-        const float bs0 = (float)s_bs[buf][16 * t + n][g], bs1 = (float)s_bs[buf][16 * t + n][g + 4];
+          for (int i = 0; i < 4; ++i) {
+            // activations 64i + 8g .. +7 and 64i + 32 + 8g .. +7 (logical 16-byte
+            // chunks 4i + g/2 and 4i + 2 + g/2, half g & 1)
+            const uint2 lo8 = *reinterpret_cast<const uint2 *>(xr + 16 * ((4 * i + (g >> 1)) ^ n) + 8 * (g & 1));
+            const uint2 hi8 = *reinterpret_cast<const uint2 *>(xr + 16 * ((4 * i + 2 + (g >> 1)) ^ n) + 8 * (g & 1));
+            xa[i] = v4i_t{(int)lo8.x, (int)lo8.y, (int)hi8.x, (int)hi8.y};
+          }
+          // 32-sums of sub-blocks g and g + 4: pairs of the raw 16-sums
+          const int *bw = reinterpret_cast<const int *>(&s_bs16[buf][16 * t + n][0]);
+          bs0 = (float)__builtin_amdgcn_sdot2(__builtin_bit_cast(v2i16_t, bw[g]), v2i16_t{1, 1}, 0, false);
+          bs1 = (float)__builtin_amdgcn_sdot2(__builtin_bit_cast(v2i16_t, bw[g + 4]), v2i16_t{1, 1}, 0, false);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xa[i] = *reinterpret_cast<const v4i_t *>(xr + 64 * i + 16 * g);
+          bs0 = (float)s_bs[buf][16 * t + n][g];
+          bs1 = (float)s_bs[buf][16 * t + n][g + 4];
+        }
         float xdj[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) xdj[j] = s_xd[buf][16 * t + 4 * g + j];
@@ -449,7 +554,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmq(GemvArgs a) {
           mn = __builtin_amdgcn_mfma_f32_16x16x4f32(bs1, mb1[m], mn, 0, 0, 0);
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            f[m][t][j] = __builtin_fmaf(xdj[j], __builtin_fmaf(dd[m], (float)(dlo[j] + 8 * dhi[j] + 16 * d5[j]), -dm[m] * mn[j]), f[m][t][j]);
+            f[m][t][j] = __builtin_fmaf(xdj[j], __builtin_fmaf(dd[m], (float)(dlo[j] + 8 * dhi[j] + 16 * d5[j]), mn[j]), f[m][t][j]);
         }
       }
     } else if constexpr (kGrid) {
@@ -642,7 +747,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmq(GemvArgs a) {
         const uint32_t scb[4] = {wcur[m].sc.x, wcur[m].sc.y, wcur[m].sc.z, wcur[m].sc.w};
         // B operand of the min product: m[row][sb] for sb = 4i + g
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mb[m][i] = (float)((scb[i] >> (8 * g + 4)) & 15u);
+        for (int i = 0; i < 4; ++i) mb[m][i] = -dm[m] * (float)((scb[i] >> (8 * g + 4)) & 15u);  // -dmin folded in (exact)
         // scale-folded weights of the 4 chunks c = 2h + jp: plane j = 2jp + (g >> 1),
         // sub-block 8h + 2j + (g & 1)
 #pragma unroll
@@ -679,17 +784,52 @@ __global__ __launch_bounds__(64 * NW) void k_mmq(GemvArgs a) {
           for (int i = 0; i < 4; ++i) mn = __builtin_amdgcn_mfma_f32_16x16x4f32(bs[i], mb[m][i], mn, 0, 0, 0);
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            f[m][t][j] = __builtin_fmaf(xdj[j], __builtin_fmaf(dd[m], (float)isum[j], -dm[m] * mn[j]), f[m][t][j]);
+            f[m][t][j] = __builtin_fmaf(xdj[j], __builtin_fmaf(dd[m], (float)isum[j], mn[j]), f[m][t][j]);
         }
       }
     }
-    // block b+1 into the other buffer (its readers finished at the last barrier),
-    // then request block b+2
-    store_x(xs, buf ^ 1);
-    load_x(b + 2, xs);
-#pragma unroll
-    for (int m = 0; m < NM; ++m) wcur[m] = wnxt[m];
+  };
+  if constexpr (kDma) {
+    // one block ahead; the loop is unrolled by two so the two weight register
+    // sets and activation buffers alternate without copies. Each step issues
+    // block b + 1's activations and weights and waits for all of it at its end.
+    WBlk w0[NM], w1[NM];
+    load_w(0, w0);
+    dma_x(0, 0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the direct loads have landed
     __syncthreads();
+    for (int b = 0;; b += 2) {
+      dma_x(b + 1, 1);  // buffer 1's readers finished at the last barrier
+      load_w(b + 1, w1);
+      step(b, 0, w0);
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      __syncthreads();
+      if (b + 1 >= nb) break;
+      dma_x(b + 2, 0);
+      load_w(b + 2, w0);
+      step(b + 1, 1, w1);
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      __syncthreads();
+      if (b + 2 >= nb) break;
+    }
+  } else {
+    WBlk wcur[NM], wnxt[NM];
+    load_w(0, wcur);
+    load_x(0, xs);
+    store_x(xs, 0);
+    load_x(1, xs);
+    __syncthreads();
+    for (int b = 0; b < nb; ++b) {
+      load_w(b + 1, wnxt);
+      step(b, b & 1, wcur);
+      // block b+1 into the other buffer (its readers finished at the last
+      // barrier), then request block b+2
+      store_x(xs, (b & 1) ^ 1);
+      load_x(b + 2, xs);
+#pragma unroll
+      for (int m = 0; m < NM; ++m) wcur[m] = wnxt[m];
+      __syncthreads();
+    }
   }
   // lane holds (pair pc + 16t + 4g + j, row): store out[tok][k][row]
   if (rv) {
