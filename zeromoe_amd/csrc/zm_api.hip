@@ -754,7 +754,8 @@ struct LayerWs {
   float *y_s;
   float *f_act;
   uint32_t *f_sync;
-  int32_t *items, *n_items;
+  int32_t *items, *n_items;    // MFMA work items of the gate/up launch
+  int32_t *items2, *n_items2;  // and of the down launch when its tiling differs
 };
 
 size_t layer_ws(const zm_moe_layer *L, int S, uint8_t *base, LayerWs *w) {
@@ -773,6 +774,8 @@ size_t layer_ws(const zm_moe_layer *L, int S, uint8_t *base, LayerWs *w) {
   t.n_active = b.take<int32_t>(4);
   t.items = b.take<int32_t>((size_t)mmq_max_items(S * K, NS) * 4);
   t.n_items = b.take<int32_t>(4);
+  t.items2 = b.take<int32_t>((size_t)mmq_max_items(S * K, NS) * 4);
+  t.n_items2 = b.take<int32_t>(4);
   t.act = b.take<float>((size_t)S * K * F * 4);
   t.aq = b.take<uint8_t>((size_t)S * K * q8_row_bytes(nbF));
   t.y = b.take<float>((size_t)S * K * H * 4);
@@ -1043,25 +1046,36 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
   a.grid = d->grid;
   a.signs = d->signs;
   const double avg_pairs = (double)(S * K) / std::max(1, std::min(NS, S * K));
-  // 16-token tiles per routed work item: Q4_K items hold up to 128 pairs, so an
-  // expert's weights are unpacked once per workgroup for most buckets
-  int tt = L->type_gate == T_Q4_K && L->type_down == T_Q4_K ? 4 : 2;
-  if (const char *v = getenv("ZEROMOE_MMQ_TT"); v && tt == 4) tt = atoi(v);  // experiment knob (4 or 8)
+  // 16-token tiles per routed work item, per projection: Q4_K items hold 64
+  // pairs (the weight unpacking is shared by four tiles), other types 32; gate/up
+  // and down take separate item lists when their tilings differ
+  int tt_g = mmq_tt(L->type_gate, false), tt_d = mmq_tt(L->type_down, false);
+  if (const char *v = getenv("ZEROMOE_MMQ_TT"); v) {  // experiment knob (4 or 8) for Q4_K
+    if (tt_g == 4) tt_g = atoi(v);
+    if (tt_d == 4) tt_d = atoi(v);
+  }
   // items: at most one partial run per active expert plus the full runs
-  const int max_items = std::min(mmq_max_items(S * K, NS), (S * K + 16 * tt - 1) / (16 * tt) + std::min(NS, S * K));
-  if (mmq_applies(L->type_gate, avg_pairs) || mmq_applies(L->type_down, avg_pairs)) {
+  auto max_items_for = [&](int tt) {
+    return std::min(mmq_max_items(S * K, NS), (S * K + 16 * tt - 1) / (16 * tt) + std::min(NS, S * K));
+  };
+  auto cut_items = [&](int tt, int32_t *items, int32_t *n_items) {
     if (getenv_flag_off("ZEROMOE_MMQ_LPT") || NS > 1024)
-      hipLaunchKernelGGL(k_mmq_items, dim3(1), dim3(1024), 0, st, w.n_active, w.active, w.offs, w.items, w.n_items,
+      hipLaunchKernelGGL(k_mmq_items, dim3(1), dim3(1024), 0, st, w.n_active, w.active, w.offs, items, n_items,
                          16 * tt);
     else
-      hipLaunchKernelGGL(k_mmq_items_lpt, dim3(1), dim3(1024), 0, st, w.n_active, w.active, w.offs, w.items,
-                         w.n_items, 16 * tt);
-  }
+      hipLaunchKernelGGL(k_mmq_items_lpt, dim3(1), dim3(1024), 0, st, w.n_active, w.active, w.offs, items, n_items,
+                         16 * tt);
+  };
+  const bool mmq_g = mmq_applies(L->type_gate, avg_pairs), mmq_d = mmq_applies(L->type_down, avg_pairs);
+  const bool split_items = mmq_g && mmq_d && tt_d != tt_g;
+  if (!mmq_g && mmq_d) tt_g = tt_d;  // one list, cut for the down launch
+  if (mmq_g || mmq_d) cut_items(tt_g, w.items, w.n_items);
+  if (split_items) cut_items(tt_d, w.items2, w.n_items2);
   a.items = w.items;
   a.n_items = w.n_items;
   a.xq_bytes = (uint32_t)((size_t)S * q8_row_bytes(nbH));
   {
-    const int rc = launch_mmq(L->type_gate, true, a, max_items, avg_pairs, tt, st);
+    const int rc = launch_mmq(L->type_gate, true, a, max_items_for(tt_g), avg_pairs, tt_g, st);
     if (rc < 0 || (rc > 0 && launch_gemv(L->type_gate, true, np, a, groups, st))) return -1;
   }
   // act -> Q8_K
@@ -1085,8 +1099,14 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
   b.out = w.y;
   b.out_s = (size_t)K * H;
   b.out_k = H;
+  if (split_items) {
+    b.items = w.items2;
+    b.n_items = w.n_items2;
+  } else {
+    tt_d = tt_g;
+  }
   {
-    const int rc = launch_mmq(L->type_down, false, b, max_items, avg_pairs, tt, st);
+    const int rc = launch_mmq(L->type_down, false, b, max_items_for(tt_d), avg_pairs, tt_d, st);
     if (rc < 0 || (rc > 0 && launch_gemv(L->type_down, false, np, b, groups, st))) return -1;
   }
   // shared expert (dense over all tokens)
