@@ -48,6 +48,8 @@ CONFIGS["iq4xs"] = dict(CONFIGS["c2"], tg=IQ4X, td=IQ4X)
 CONFIGS["c3_iq4xs"] = dict(CONFIGS["c3"], tg=IQ4X, td=IQ4X)
 CONFIGS["iq3xxs"] = dict(CONFIGS["c2"], tg=IQ3X, td=IQ3X)
 CONFIGS["c3_iq2xxs"] = dict(CONFIGS["c3"], tg=IQ2, td=IQ2)
+CONFIGS["c3_q5k"] = dict(CONFIGS["c3"], tg=Q5, td=Q5)
+CONFIGS["c3_iq3xxs"] = dict(CONFIGS["c3"], tg=IQ3X, td=IQ3X)
 WORKLOAD = {
     "c1": "decode S=1, H=2048 F=768 E=128 top-8 softmax, Q4_K",
     "c2": "decode S=1, H=4096 F=1536 E=128 top-8 softmax, gate/up Q2_K, down Q3_K",
@@ -58,6 +60,8 @@ WORKLOAD = {
     "c3_iq2xxs": "prefill S=512 at c3's shape and routing with IQ2_XXS gate/up/down (stand-in grid)",
     "iq3xxs": "decode S=1 at c2's shape with IQ3_XXS gate/up/down (stand-in grid)",
     "c3_iq4xs": "prefill S=512 at c3's shape and routing with IQ4_XS gate/up/down",
+    "c3_q5k": "prefill S=512 at c3's shape and routing with Q5_K gate/up/down",
+    "c3_iq3xxs": "prefill S=512 at c3's shape and routing with IQ3_XXS gate/up/down (stand-in grid)",
     "c3_q6k": "prefill S=512 at c3's shape and routing with a Q6_K down projection (mixed-type layer)",
     "q4k_q6k": "decode S=1 at c2's shape with Q4_K gate/up and a Q6_K down projection (mixed-type layer)",
     "c5_s64": "full block S=64, H=7168 F=2048, 256 routed Q2_K (96 resident slots) + shared Q4_K, sigmoid 8 groups/top-4",
@@ -513,7 +517,7 @@ def main():
     traffic = committed_traffic()
     extras = {}
     for name in [n for n in args.extras.split(",") if n]:
-        st = max(10, args.steps // 4) if name in ("c3", "c5_s64", "c3_q6k", "c3_iq4xs", "c3_iq2xxs") else args.steps
+        st = max(10, args.steps // 4) if name in ("c3", "c5_s64", "c3_q6k", "c3_iq4xs", "c3_iq2xxs", "c3_q5k", "c3_iq3xxs") else args.steps
         r = run_config(torch, Z, name, st, max(3, args.warmup // 2), reps(name), use_graph=not args.eager)
         extras[name] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}
         extras[name]["workload"] = WORKLOAD[name]

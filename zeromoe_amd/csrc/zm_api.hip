@@ -258,9 +258,10 @@ bool mmq_applies(int type, double avg_pairs) {
           (type == T_Q2_K && avg_pairs >= 2.0)) &&
          !getenv_flag_off("ZEROMOE_MMQ");
 }
-// 16-token tiles per work item: routed Q4_K buckets take 4 (the weight
-// unpacking is shared by more tokens), Q2_K and dense (shared expert) rows 2
-int mmq_tt(int type, bool dense) { return type == T_Q4_K && !dense ? 4 : 2; }
+// 16-token tiles per work item: routed buckets take 4 (the weight unpacking is
+// shared by 64 pairs); Q2_K (small buckets of resident slots), Q5_K (its three
+// MFMA chains leave one wave per SIMD at 4 tiles) and dense shared-expert rows 2
+int mmq_tt(int type, bool dense) { return type != T_Q2_K && type != T_Q5_K && !dense ? 4 : 2; }
 int launch_mmq(int type, bool gateup, const GemvArgs &a, int max_items, double avg_pairs, int tt, hipStream_t st);
 template <int T, int TT, int NW = 4>
 void launch_mmq_t(bool gateup, dim3 grid, const GemvArgs &a, hipStream_t st) {
@@ -1046,9 +1047,8 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
   a.grid = d->grid;
   a.signs = d->signs;
   const double avg_pairs = (double)(S * K) / std::max(1, std::min(NS, S * K));
-  // 16-token tiles per routed work item, per projection: Q4_K items hold 64
-  // pairs (the weight unpacking is shared by four tiles), other types 32; gate/up
-  // and down take separate item lists when their tilings differ
+  // 16-token tiles per routed work item, per projection (mmq_tt); gate/up and
+  // down take separate item lists when their tilings differ
   int tt_g = mmq_tt(L->type_gate, false), tt_d = mmq_tt(L->type_down, false);
   if (const char *v = getenv("ZEROMOE_MMQ_TT"); v) {  // experiment knob (4 or 8) for Q4_K
     if (tt_g == 4) tt_g = atoi(v);
