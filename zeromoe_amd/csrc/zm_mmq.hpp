@@ -24,8 +24,8 @@
 // nibbles (g < 2) or high nibbles (g >= 2) of bytes 16*(g & 1)..+15, i.e.
 // weights 64i + 16g .. +15.  The weight unpacking is done once per block for
 // all token tiles of the work item.  No dequantized weight copy is materialized.
-// Q4_K activations reach LDS by direct buffer-to-LDS loads (no register
-// staging), token rows XOR-swizzled in 16-byte chunks by the token index.
+// Activations reach LDS by direct buffer-to-LDS loads (no register staging),
+// token rows XOR-swizzled in 16-byte chunks by the token index.
 //
 // IQ2_XXS / IQ3_XXS (grid values up to 43 / 62 with per-8-weight signs, and a
 // (2 ls + 1) <= 31 scale per 32-weight sub-block) take the same per-sub-block
@@ -111,7 +111,6 @@ __device__ __forceinline__ uint32_t mul_bytes(uint32_t packed, uint32_t f) {
 }
 
 constexpr int MMQ_TOK = 32;            // pairs per work item of the 2-tile kernels (item count bound)
-constexpr int MMQ_XS = QK + 16;        // LDS stride of one token's qs (bank spread)
 
 
 // Work items: every active expert's bucket cut into runs of `tok` pairs,
@@ -247,18 +246,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
   __shared__ uint64_t s_grid[kGrid ? (T == T_IQ2_XXS ? 256 : 128) : 1];  // IQ3_XXS: 256 x u32
   __shared__ uint64_t s_signs[kGrid ? 128 : 1];
   constexpr bool K45 = T == T_Q4_K || T == T_Q5_K;
-  constexpr int NBS = K45 ? 8 : 16;  // bsums per block used: 32-sums (Q4_K, Q5_K) or 16-sums (Q2_K, Q6_K)
-  // Q4_K: the activation blocks reach LDS by direct buffer-to-LDS loads (no
-  // register staging); a token's row is 256 bytes with its 16-byte chunks
-  // XOR-swizzled by the token index (chunk c of token t at c ^ (t & 15)), so the
-  // 16 tokens of an MFMA A operand read 16 different bank groups; the raw int16
-  // 16-sums are kept and added pairwise when read
-  constexpr bool kDma = T == T_Q4_K;
-  constexpr int NXB = 2;  // activation buffers
-  __shared__ __attribute__((aligned(16))) uint8_t s_xq[NXB][TOK][kDma ? QK : MMQ_XS];
-  __shared__ int s_bs[2][TOK][kDma ? 1 : NBS];
-  __shared__ __attribute__((aligned(16))) int16_t s_bs16[kDma ? NXB : 1][kDma ? TOK : 1][16];
-  __shared__ __attribute__((aligned(16))) float s_xd[NXB][TOK];
+  // The activation blocks reach LDS by direct buffer-to-LDS loads (no register
+  // staging); a token's row is 256 bytes with its 16-byte chunks XOR-swizzled
+  // by the token index (chunk c of token t at c ^ (t & 15)), so the 16 tokens
+  // of an MFMA A operand read 16 different bank groups; the raw int16 16-sums
+  // are kept (and added pairwise where 32-sums are used)
+  __shared__ __attribute__((aligned(16))) uint8_t s_xq[2][TOK][QK];
+  __shared__ __attribute__((aligned(16))) int16_t s_bs16[2][TOK][16];
+  __shared__ __attribute__((aligned(16))) float s_xd[2][TOK];
   __shared__ int s_xoff[TOK];      // byte offset of each pair's activation row (OOR: none)
   __shared__ int s_pair[TOK];
   int e, pc, p1;
@@ -284,7 +279,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
   rsrc_t rw[NM];
   rw[0] = make_rsrc(a.w0 + (size_t)e * a.w_estride, wbytes);
   if constexpr (GATEUP) rw[1] = make_rsrc(a.w1 + (size_t)e * a.w_estride, wbytes);
-  const rsrc_t rx = make_rsrc(a.xq, a.xq_bytes);
   const v4u_t rxd = dma_rsrc(a.xq, a.xq_bytes);
   const int vrow = rv ? row * (int)a.w_rstride : OOR;
   const int Kp = a.dense_S > 0 ? 1 : a.K;
@@ -355,63 +349,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
       }
     }
   };
-  // this thread's share of an activation block: qs chunks c = tid, tid + 256
-  // (token c >> 4, 16-byte chunk c & 15), one 32-weight bsum (token tid >> 3,
-  // sub-block tid & 7), and d of token tid (tid < TOK)
-  constexpr int NBSH = (TOK * 8 + NT - 1) / NT;  // bsum dwords per thread
-  struct XShare {
-    uint4 q[TOK * 16 / NT];
-    uint32_t bs[NBSH];
-    float d;
-  };
-  static_assert(TOK * 16 % NT == 0 && TOK <= NT, "staging shares");
-  auto load_x = [&](int b, XShare &x) {
-    const bool bv = b < nb;
-#pragma unroll
-    for (int r = 0; r < TOK * 16 / NT; ++r) {
-      const int c = tid + NT * r, t = c >> 4, ch = c & 15;
-      const int o = s_xoff[t];
-      x.q[r] = bld16(rx, (bv && o != OOR) ? o + b * QK + 16 * ch : OOR, 0);
-    }
-#pragma unroll
-    for (int r = 0; r < NBSH; ++r) {
-      const int c = tid + NT * r;
-      const int t = (c >> 3) & (TOK - 1), sb = c & 7;
-      const int o = s_xoff[t];
-      x.bs[r] = __builtin_amdgcn_raw_buffer_load_b32(rx, (bv && o != OOR && c < TOK * 8) ? o + (int)q8_bs_off(nb) + b * 32 + 4 * sb : OOR, 0, 0);
-    }
-    {
-      const int o = s_xoff[tid & (TOK - 1)];
-      x.d = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, (bv && o != OOR && tid < TOK) ? o + (int)q8_d_off(nb) + 4 * b : OOR, 0, 0));
-    }
-  };
-  auto store_x = [&](const XShare &x, int buf) {
-#pragma unroll
-    for (int r = 0; r < TOK * 16 / NT; ++r) {
-      const int c = tid + NT * r, t = c >> 4, ch = c & 15;
-      *reinterpret_cast<uint4 *>(&s_xq[buf][t][16 * ch]) = x.q[r];
-    }
-#pragma unroll
-    for (int r = 0; r < NBSH; ++r) {
-      const int c = tid + NT * r;
-      if (c < TOK * 8) {
-        const int lo = (int)(int16_t)(x.bs[r] & 0xffffu), hi = (int)(int16_t)(x.bs[r] >> 16);
-        if constexpr (K45) {
-          s_bs[buf][c >> 3][c & 7] = lo + hi;
-        } else {
-          s_bs[buf][c >> 3][2 * (c & 7)] = lo;
-          s_bs[buf][c >> 3][2 * (c & 7) + 1] = hi;
-        }
-      }
-    }
-    if (tid < TOK) s_xd[buf][tid] = x.d;
-  };
-
-  // direct loads of block b's activations into buffer buf (Q4_K): the qs of
+  // direct loads of block b's activations into buffer buf: the qs of
   // TOK tokens (1 KB = 4 tokens per wave instruction), their 16 bsums (32 B per
   // token) and d; out-of-range lanes write zeros
   auto dma_x = [&](int b, int buf) {
-    if constexpr (kDma) {
+    {
       const bool bv = b < nb;
       constexpr int QI = TOK / 4 / NW;  // qs instructions per wave
       static_assert(TOK % (4 * NW) == 0, "qs instructions per wave");
@@ -438,6 +380,20 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
     }
   };
 
+  // reads of the staged activations: logical 16-byte chunk c (or its 8-byte
+  // half h) of token tok, and its raw 16-sum j / 32-sum j (16-sums 2j, 2j + 1)
+  auto xq16 = [&](int buf, int tok, int c) {
+    return *reinterpret_cast<const v4i_t *>(&s_xq[buf][tok][16 * (c ^ (tok & 15))]);
+  };
+  auto xq8 = [&](int buf, int tok, int c, int h) {
+    return *reinterpret_cast<const uint2 *>(&s_xq[buf][tok][16 * (c ^ (tok & 15)) + 8 * h]);
+  };
+  auto bsum16 = [&](int buf, int tok, int j) { return (int)s_bs16[buf][tok][j]; };
+  auto bsum32 = [&](int buf, int tok, int j) {
+    const int w = reinterpret_cast<const int *>(&s_bs16[buf][tok][0])[j];
+    return __builtin_amdgcn_sdot2(__builtin_bit_cast(v2i16_t, w), v2i16_t{1, 1}, 0, false);
+  };
+
   // per (matrix, token tile, output): f += d_x * (d * isum + mn), as
   // two fmas (the tile epilogue is most of the per-tile VALU work)
   float f[NM][TT][4];
@@ -448,7 +404,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
 #pragma unroll
       for (int j = 0; j < 4; ++j) f[m][t][j] = 0.f;
 
-  XShare xs;
   // block b of the K loop from the weights in wcur and activation buffer b & 1
   auto step = [&](int b, int buf, const WBlk(&wcur)[NM]) {
     if constexpr (K45) {
@@ -475,7 +430,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
         // scale-folded weights of the 4 chunks: lane's sub-block 2i + (g >> 1),
         // sc = 8 * hi + lo; Q5_K: the fifth bit (bit 2i + (g >> 1) of the lane's
         // qh bytes) is a third chain with the whole scale, isum = D_lo + 8 D_hi + 16 D_5
-        if constexpr (kDma) {
+        if constexpr (T == T_Q4_K) {
           // chunk i = qs group i (sub-blocks 2i, 2i + 1): the lane's 8 bytes
           // 8g .. 8g + 7 give 8 weights of each sub-block, low nibbles then
           // high nibbles (the activation operand is read in the same order)
@@ -515,28 +470,23 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
         if (t >= nt) continue;
-        const uint8_t *xr = &s_xq[buf][16 * t + n][0];
+        const int tok = 16 * t + n;
         v4i_t xa[4];
-        float bs0, bs1;
-        if constexpr (kDma) {
+        if constexpr (T == T_Q4_K) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             // activations 64i + 8g .. +7 and 64i + 32 + 8g .. +7 (logical 16-byte
             // chunks 4i + g/2 and 4i + 2 + g/2, half g & 1)
-            const uint2 lo8 = *reinterpret_cast<const uint2 *>(xr + 16 * ((4 * i + (g >> 1)) ^ n) + 8 * (g & 1));
-            const uint2 hi8 = *reinterpret_cast<const uint2 *>(xr + 16 * ((4 * i + 2 + (g >> 1)) ^ n) + 8 * (g & 1));
+            const uint2 lo8 = xq8(buf, tok, 4 * i + (g >> 1), g & 1);
+            const uint2 hi8 = xq8(buf, tok, 4 * i + 2 + (g >> 1), g & 1);
             xa[i] = v4i_t{(int)lo8.x, (int)lo8.y, (int)hi8.x, (int)hi8.y};
           }
-          // 32-sums of sub-blocks g and g + 4: pairs of the raw 16-sums
-          const int *bw = reinterpret_cast<const int *>(&s_bs16[buf][16 * t + n][0]);
-          bs0 = (float)__builtin_amdgcn_sdot2(__builtin_bit_cast(v2i16_t, bw[g]), v2i16_t{1, 1}, 0, false);
-          bs1 = (float)__builtin_amdgcn_sdot2(__builtin_bit_cast(v2i16_t, bw[g + 4]), v2i16_t{1, 1}, 0, false);
         } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) xa[i] = *reinterpret_cast<const v4i_t *>(xr + 64 * i + 16 * g);
-          bs0 = (float)s_bs[buf][16 * t + n][g];
-          bs1 = (float)s_bs[buf][16 * t + n][g + 4];
+          for (int i = 0; i < 4; ++i) xa[i] = xq16(buf, tok, 4 * i + g);
         }
+        // 32-sums of sub-blocks g and g + 4
+        const float bs0 = (float)bsum32(buf, tok, g), bs1 = (float)bsum32(buf, tok, g + 4);
         float xdj[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) xdj[j] = s_xd[buf][16 * t + 4 * g + j];
@@ -619,10 +569,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
         if (t >= nt) continue;
-        const uint8_t *xr = &s_xq[buf][16 * t + n][0];
+        const int tok = 16 * t + n;
         v4i_t xa[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) xa[c] = *reinterpret_cast<const v4i_t *>(xr + 64 * c + 16 * g);
+        for (int c = 0; c < 4; ++c) xa[c] = xq16(buf, tok, 4 * c + g);
         float xdj[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) xdj[j] = s_xd[buf][16 * t + 4 * g + j];
@@ -669,11 +619,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
         if (t >= nt) continue;
-        const uint8_t *xr = &s_xq[buf][16 * t + n][0];
+        const int tok = 16 * t + n;
         int isum[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          const v4i_t xa = *reinterpret_cast<const v4i_t *>(xr + 64 * c + 16 * g);
+          const v4i_t xa = xq16(buf, tok, 4 * c + g);
           const v4i_t z = {0, 0, 0, 0};
           const v4i_t d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, b0[c], z, 0, 0, 0);
           const v4i_t d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, b1[c], z, 0, 0, 0);
@@ -715,11 +665,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
         if (t >= nt) continue;
-        const uint8_t *xr = &s_xq[buf][16 * t + n][0];
+        const int tok = 16 * t + n;
         int isum[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int p = 0; p < 8; ++p) {
-          const long xa = *reinterpret_cast<const long *>(xr + 32 * p + 8 * g);
+          const long xa = __builtin_bit_cast(long, xq8(buf, tok, 2 * p + (g >> 1), g & 1));
           const v4i_t z = {0, 0, 0, 0};
           const v4i_t d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa, b0[p], z, 0, 0, 0);
           const v4i_t d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa, b1[p], z, 0, 0, 0);
@@ -729,7 +679,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
         v4f_t off = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          off = __builtin_amdgcn_mfma_f32_16x16x4f32((float)s_bs[buf][16 * t + n][4 * i + g], mb[i], off, 0, 0, 0);
+          off = __builtin_amdgcn_mfma_f32_16x16x4f32((float)bsum16(buf, tok, 4 * i + g), mb[i], off, 0, 0, 0);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           f[m][t][j] = __builtin_fmaf(s_xd[buf][16 * t + 4 * g + j], d * (float)(isum[j] - 32 * (int)off[j]), f[m][t][j]);
@@ -765,13 +715,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
         if (t >= nt) continue;
-        const uint8_t *xr = &s_xq[buf][16 * t + n][0];
+        const int tok = 16 * t + n;
         v4i_t xa[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) xa[c] = *reinterpret_cast<const v4i_t *>(xr + 64 * c + 16 * g);
+        for (int c = 0; c < 4; ++c) xa[c] = xq16(buf, tok, 4 * c + g);
         float bs[4], xdj[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) bs[i] = (float)s_bs[buf][16 * t + n][4 * i + g];
+        for (int i = 0; i < 4; ++i) bs[i] = (float)bsum16(buf, tok, 4 * i + g);
 #pragma unroll
         for (int j = 0; j < 4; ++j) xdj[j] = s_xd[buf][16 * t + 4 * g + j];
 #pragma unroll
@@ -789,15 +739,27 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
       }
     }
   };
-  if constexpr (kDma) {
-    // one block ahead; the loop is unrolled by two so the two weight register
-    // sets and activation buffers alternate without copies. Each step issues
-    // block b + 1's activations and weights and waits for all of it at its end.
-    WBlk w0[NM], w1[NM];
-    load_w(0, w0);
-    dma_x(0, 0);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the direct loads have landed
-    __syncthreads();
+  // one block ahead: each step issues block b + 1's activations and weights and
+  // waits for all of it at its end.  The loop is unrolled by two, so the two
+  // weight register sets and activation buffers alternate without copies;
+  // IQ2_XXS keeps the rolled loop with a register copy (its unrolled loop
+  // measured 10% slower).
+  WBlk w0[NM], w1[NM];
+  load_w(0, w0);
+  dma_x(0, 0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the direct loads have landed
+  __syncthreads();
+  if constexpr (T == T_IQ2_XXS) {
+    for (int b = 0; b < nb; ++b) {
+      dma_x(b + 1, (b + 1) & 1);  // that buffer's readers finished at the last barrier
+      load_w(b + 1, w1);
+      step(b, b & 1, w0);
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      __syncthreads();
+#pragma unroll
+      for (int m = 0; m < NM; ++m) w0[m] = w1[m];
+    }
+  } else {
     for (int b = 0;; b += 2) {
       dma_x(b + 1, 1);  // buffer 1's readers finished at the last barrier
       load_w(b + 1, w1);
@@ -811,24 +773,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
       __builtin_amdgcn_s_waitcnt(0x0F70);
       __syncthreads();
       if (b + 2 >= nb) break;
-    }
-  } else {
-    WBlk wcur[NM], wnxt[NM];
-    load_w(0, wcur);
-    load_x(0, xs);
-    store_x(xs, 0);
-    load_x(1, xs);
-    __syncthreads();
-    for (int b = 0; b < nb; ++b) {
-      load_w(b + 1, wnxt);
-      step(b, b & 1, wcur);
-      // block b+1 into the other buffer (its readers finished at the last
-      // barrier), then request block b+2
-      store_x(xs, (b & 1) ^ 1);
-      load_x(b + 2, xs);
-#pragma unroll
-      for (int m = 0; m < NM; ++m) wcur[m] = wnxt[m];
-      __syncthreads();
     }
   }
   // lane holds (pair pc + 16t + 4g + j, row): store out[tok][k][row]
