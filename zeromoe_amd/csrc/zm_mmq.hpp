@@ -28,9 +28,10 @@
 // token rows XOR-swizzled in 16-byte chunks by the token index.
 //
 // IQ2_XXS / IQ3_XXS (grid values up to 43 / 62 with per-8-weight signs, and a
-// (2 ls + 1) <= 31 scale per 32-weight sub-block) take the same per-sub-block
-// route as IQ4_XS: signed grid bytes from the LDS-staged grid and sign masks,
-// two half-masked MFMAs per chunk, scales per lane.
+// (2 ls + 1) <= 31 scale per 32-weight sub-block) dot each sub-block on its own
+// v_mfma_i32_16x16x32_i8 (K = the sub-block; lane group g holds its 8-weight
+// group g): signed grid bytes from the LDS-staged grid and sign masks, scales
+// per lane on the integer results.
 //
 // IQ4_XS (a 16-entry value table, up to |127|, and a 6-bit signed scale per
 // 32-weight sub-block) dots each 64-weight chunk as its two sub-blocks on
@@ -508,84 +509,62 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
         }
       }
     } else if constexpr (kGrid) {
-      v4i_t B0[NM][4], B1[NM][4];
-      int S0[NM][4], S1[NM][4];
+      // one v_mfma_i32_16x16x32_i8 per 32-weight sub-block (K = the sub-block):
+      // lane group g holds 8-weight group l = g of every sub-block, grid values
+      // with their signs applied (conditional byte negate); the scale (2 ls + 1)
+      // multiplies the sub-block's integer dot per lane, the 1/8 (IQ2_XXS) or
+      // 1/4 (IQ3_XXS) is folded into d
+      long B[NM][8];
+      int S[NM][8];
       float DD[NM];
 #pragma unroll
-    for (int m = 0; m < NM; ++m) {
-      // chunk c = sub-blocks 2c (lane groups 0-1) and 2c + 1 (groups 2-3); group
-      // g holds weights 16(g & 1) .. +15 of its sub-block = the two 8-weight
-      // groups l = 2(g & 1), 2(g & 1) + 1: grid values with their signs applied
-      // (conditional byte negate), the other sub-block's half of B zeroed;
-      // scales (2 ls + 1) per lane afterwards, the 1/8 (IQ2_XXS) or 1/4
-      // (IQ3_XXS) folded into d
-      constexpr float kf = T == T_IQ2_XXS ? 0.125f : 0.25f;
-      DD[m] = kf * h2f((uint16_t)(wcur[m].d & 0xffffu));
-      const uint32_t keep0 = g < 2 ? 0xffffffffu : 0u;
-      const int hl = g & 1;
+      for (int m = 0; m < NM; ++m) {
+        constexpr float kf = T == T_IQ2_XXS ? 0.125f : 0.25f;
+        DD[m] = kf * h2f((uint16_t)(wcur[m].d & 0xffffu));
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int ib = 2 * c + (g >> 1);
-        uint32_t v[4];
-        if constexpr (T == T_IQ2_XXS) {
-          // sub-block ib: words 2ib (grid indices), 2ib + 1 (signs, scale)
-          const uint32_t aux0 = u4_get(wcur[m].q[ib >> 1], 2 * (ib & 1)), aux1 = u4_get(wcur[m].q[ib >> 1], 2 * (ib & 1) + 1);
-#pragma unroll
-          for (int li = 0; li < 2; ++li) {
-            const int l = 2 * hl + li;
-            const uint64_t gg = s_grid[(aux0 >> (8 * l)) & 0xffu];
-            const uint64_t mm = s_signs[(aux1 >> (7 * l)) & 127u];
-            const uint32_t glo = (uint32_t)gg, ghi = (uint32_t)(gg >> 32), mlo = (uint32_t)mm, mhi = (uint32_t)(mm >> 32);
-            v[2 * li] = (glo ^ mlo) + (mlo & 0x01010101u);
-            v[2 * li + 1] = (ghi ^ mhi) + (mhi & 0x01010101u);
+        for (int sb = 0; sb < 8; ++sb) {
+          uint32_t glo, ghi, aux;
+          if constexpr (T == T_IQ2_XXS) {
+            // sub-block sb: words 2sb (grid indices), 2sb + 1 (signs, scale)
+            const uint32_t aux0 = u4_get(wcur[m].q[sb >> 1], 2 * (sb & 1));
+            aux = u4_get(wcur[m].q[sb >> 1], 2 * (sb & 1) + 1);
+            const uint64_t gg = s_grid[(aux0 >> (8 * g)) & 0xffu];
+            glo = (uint32_t)gg;
+            ghi = (uint32_t)(gg >> 32);
+          } else {
+            // sub-block sb: grid-index bytes 8sb + 2g, +1 (two 4-value entries), word sb
+            const uint32_t iw = u4_get(wcur[m].gi[sb >> 1], 2 * (sb & 1) + (g >> 1));
+            aux = u4_get(wcur[m].sas[sb >> 2], sb & 3);
+            const uint32_t *g3 = reinterpret_cast<const uint32_t *>(s_grid);
+            glo = g3[(iw >> (16 * (g & 1))) & 0xffu];
+            ghi = g3[(iw >> (16 * (g & 1) + 8)) & 0xffu];
           }
-          const uint32_t a0 = u4_get(wcur[m].q[c], 1), a1 = u4_get(wcur[m].q[c], 3);  // sub-blocks 2c, 2c + 1
-          S0[m][c] = 2 * (int)(a0 >> 28) + 1;
-          S1[m][c] = 2 * (int)(a1 >> 28) + 1;
-        } else {
-          // sub-block ib: grid-index bytes 8ib .. +7 (two per 8-weight group), word ib
-          const uint32_t iw = u4_get(wcur[m].gi[ib >> 1], 2 * (ib & 1) + hl);
-          const uint32_t aux = u4_get(wcur[m].sas[ib >> 2], ib & 3);
-          const uint32_t *g3 = reinterpret_cast<const uint32_t *>(s_grid);
-#pragma unroll
-          for (int li = 0; li < 2; ++li) {
-            const int l = 2 * hl + li;
-            const uint32_t g1 = g3[(iw >> (16 * li)) & 0xffu], g2 = g3[(iw >> (16 * li + 8)) & 0xffu];
-            const uint64_t mm = s_signs[(aux >> (7 * l)) & 127u];
-            const uint32_t mlo = (uint32_t)mm, mhi = (uint32_t)(mm >> 32);
-            v[2 * li] = (g1 ^ mlo) + (mlo & 0x01010101u);
-            v[2 * li + 1] = (g2 ^ mhi) + (mhi & 0x01010101u);
-          }
-          S0[m][c] = 2 * (int)(u4_get(wcur[m].sas[c >> 1], 2 * (c & 1)) >> 28) + 1;
-          S1[m][c] = 2 * (int)(u4_get(wcur[m].sas[c >> 1], 2 * (c & 1) + 1) >> 28) + 1;
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          B0[m][c][k] = (int)(v[k] & keep0);
-          B1[m][c][k] = (int)(v[k] & ~keep0);
+          const uint64_t mm = s_signs[(aux >> (7 * g)) & 127u];
+          const uint32_t mlo = (uint32_t)mm, mhi = (uint32_t)(mm >> 32);
+          const uint32_t v0 = (glo ^ mlo) + (mlo & 0x01010101u), v1 = (ghi ^ mhi) + (mhi & 0x01010101u);
+          B[m][sb] = (long)(((uint64_t)v1 << 32) | v0);
+          S[m][sb] = 2 * (int)(aux >> 28) + 1;
         }
       }
-    }
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
         if (t >= nt) continue;
         const int tok = 16 * t + n;
-        v4i_t xa[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) xa[c] = xq16(buf, tok, 4 * c + g);
         float xdj[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) xdj[j] = s_xd[buf][16 * t + 4 * g + j];
+        long xa[8];
+#pragma unroll
+        for (int sb = 0; sb < 8; ++sb) xa[sb] = __builtin_bit_cast(long, xq8(buf, tok, 2 * sb + (g >> 1), g & 1));
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
           int isum[4] = {0, 0, 0, 0};
 #pragma unroll
-          for (int c = 0; c < 4; ++c) {
+          for (int sb = 0; sb < 8; ++sb) {
             const v4i_t z = {0, 0, 0, 0};
-            const v4i_t d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[c], B0[m][c], z, 0, 0, 0);
-            const v4i_t d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[c], B1[m][c], z, 0, 0, 0);
+            const v4i_t d = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa[sb], B[m][sb], z, 0, 0, 0);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) isum[j] = __mul24(S0[m][c], d0[j]) + __mul24(S1[m][c], d1[j]) + isum[j];
+            for (int j = 0; j < 4; ++j) isum[j] = __mul24(S[m][sb], d[j]) + isum[j];
           }
 #pragma unroll
           for (int j = 0; j < 4; ++j) f[m][t][j] = __builtin_fmaf(xdj[j], DD[m] * (float)isum[j], f[m][t][j]);
@@ -741,39 +720,25 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
   };
   // one block ahead: each step issues block b + 1's activations and weights and
   // waits for all of it at its end.  The loop is unrolled by two, so the two
-  // weight register sets and activation buffers alternate without copies;
-  // IQ2_XXS keeps the rolled loop with a register copy (its unrolled loop
-  // measured 10% slower).
+  // weight register sets and activation buffers alternate without copies.
   WBlk w0[NM], w1[NM];
   load_w(0, w0);
   dma_x(0, 0);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the direct loads have landed
   __syncthreads();
-  if constexpr (T == T_IQ2_XXS) {
-    for (int b = 0; b < nb; ++b) {
-      dma_x(b + 1, (b + 1) & 1);  // that buffer's readers finished at the last barrier
-      load_w(b + 1, w1);
-      step(b, b & 1, w0);
-      __builtin_amdgcn_s_waitcnt(0x0F70);
-      __syncthreads();
-#pragma unroll
-      for (int m = 0; m < NM; ++m) w0[m] = w1[m];
-    }
-  } else {
-    for (int b = 0;; b += 2) {
-      dma_x(b + 1, 1);  // buffer 1's readers finished at the last barrier
-      load_w(b + 1, w1);
-      step(b, 0, w0);
-      __builtin_amdgcn_s_waitcnt(0x0F70);
-      __syncthreads();
-      if (b + 1 >= nb) break;
-      dma_x(b + 2, 0);
-      load_w(b + 2, w0);
-      step(b + 1, 1, w1);
-      __builtin_amdgcn_s_waitcnt(0x0F70);
-      __syncthreads();
-      if (b + 2 >= nb) break;
-    }
+  for (int b = 0;; b += 2) {
+    dma_x(b + 1, 1);  // buffer 1's readers finished at the last barrier
+    load_w(b + 1, w1);
+    step(b, 0, w0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    if (b + 1 >= nb) break;
+    dma_x(b + 2, 0);
+    load_w(b + 2, w0);
+    step(b + 1, 1, w1);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    if (b + 2 >= nb) break;
   }
   // lane holds (pair pc + 16t + 4g + j, row): store out[tok][k][row]
   if (rv) {
