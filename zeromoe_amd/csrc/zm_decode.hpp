@@ -146,8 +146,11 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   constexpr bool kIQ4 = TG == T_IQ4_XS || TD == T_IQ4_XS || TS == T_IQ4_XS;
   constexpr bool kIQ3 = TG == T_IQ3_XXS || TD == T_IQ3_XXS || TS == T_IQ3_XXS;
   static_assert((int)kIQ2 + (int)kIQ3 + (int)kIQ4 <= 1, "one lookup table per layer");
-  __shared__ uint64_t s_grid[kIQ2 ? 256 : (kIQ3 ? 128 : (kIQ4 ? 2 : 1))];
-  __shared__ uint64_t s_signs[kIQ2 || kIQ3 ? 128 : 1];
+  // the lookup tables first in LDS (largest alignment first): their addresses
+  // fit the 16-bit offset field of the LDS reads, so an index becomes an
+  // address in one or two instructions
+  __shared__ __attribute__((aligned(kIQ2 || kIQ3 ? 4096 : 8))) uint64_t s_grid[kIQ2 ? 256 : (kIQ3 ? 128 : (kIQ4 ? 2 : 1))];
+  __shared__ __attribute__((aligned(kIQ2 || kIQ3 ? 2048 : 8))) uint64_t s_signs[kIQ2 || kIQ3 ? 128 : 1];
   static_assert(IS == 0 || TS != 0, "shared iterations need a shared type");
   static_assert(L1 == 16 || L1 == 32, "lanes per routed gate/up row");
   constexpr int L2 = 32;  // lanes per down row (2 rows per wave step)

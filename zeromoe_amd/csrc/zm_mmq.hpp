@@ -244,8 +244,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
                     T == T_IQ3_XXS,
                 "MFMA prefill types");
   constexpr bool kGrid = T == T_IQ2_XXS || T == T_IQ3_XXS;
-  __shared__ uint64_t s_grid[kGrid ? (T == T_IQ2_XXS ? 256 : 128) : 1];  // IQ3_XXS: 256 x u32
-  __shared__ uint64_t s_signs[kGrid ? 128 : 1];
+  // the lookup tables first in LDS (largest alignment first), so their
+  // addresses fold into the LDS reads' offset field
+  __shared__ __attribute__((aligned(kGrid ? 4096 : 8))) uint64_t s_grid[kGrid ? (T == T_IQ2_XXS ? 256 : 128) : 1];  // IQ3_XXS: 256 x u32
+  __shared__ __attribute__((aligned(kGrid ? 2048 : 8))) uint64_t s_signs[kGrid ? 128 : 1];
   constexpr bool K45 = T == T_Q4_K || T == T_Q5_K;
   // The activation blocks reach LDS by direct buffer-to-LDS loads (no register
   // staging); a token's row is 256 bytes with its 16-byte chunks XOR-swizzled
