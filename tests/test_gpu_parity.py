@@ -479,10 +479,11 @@ LAYER_CASES = {
     "q5k_q6k_S1": (CONFIGS["c2"], dict(tg=Q5, td=Q6)),
     # both projections on the MFMA path: mixed types with one tiling (64-pair
     # runs), and with different tilings, so gate/up and down run from separate
-    # work-item lists (Q5_K takes 32-pair runs)
+    # work-item lists (Q2_K takes 32-pair runs)
     "q4k_q6k_mmq": (CONFIGS["c3"], dict(tg=Q4, td=Q6, S=256, H=1024, F=512, E=16)),
     "q4k_q5k_mmq": (CONFIGS["c3"], dict(tg=Q4, td=Q5, S=256, H=1024, F=512, E=16)),
-    "q5k_q6k_mmq": (CONFIGS["c3"], dict(tg=Q5, td=Q6, S=256, H=1024, F=512, E=16)),
+    "q5k_q2k_mmq": (CONFIGS["c3"], dict(tg=Q5, td=Q2, S=256, H=1024, F=512, E=16)),
+    "q2k_q6k_mmq": (CONFIGS["c3"], dict(tg=Q2, td=Q6, S=256, H=1024, F=512, E=16)),
     "iq2xxs_mmq": (CONFIGS["c3"], dict(tg=IQ2, td=IQ2, S=256, H=1024, F=512, E=16)),
     "iq3xxs_iq4xs_mmq": (CONFIGS["c3"], dict(tg=IQ3, td=IQ4, S=256, H=1024, F=512, E=16)),
     "q5k_q5k_S64": (CONFIGS["c3"], dict(tg=Q5, td=Q5, S=64, H=1024, F=512)),

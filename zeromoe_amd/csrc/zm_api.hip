@@ -259,9 +259,9 @@ bool mmq_applies(int type, double avg_pairs) {
          !getenv_flag_off("ZEROMOE_MMQ");
 }
 // 16-token tiles per work item: routed buckets take 4 (the weight unpacking is
-// shared by 64 pairs); Q2_K (small buckets of resident slots), Q5_K (its three
-// MFMA chains leave one wave per SIMD at 4 tiles) and dense shared-expert rows 2
-int mmq_tt(int type, bool dense) { return type != T_Q2_K && type != T_Q5_K && !dense ? 4 : 2; }
+// shared by 64 pairs); Q2_K (small buckets of resident slots) and dense
+// shared-expert rows 2
+int mmq_tt(int type, bool dense) { return type != T_Q2_K && !dense ? 4 : 2; }
 int launch_mmq(int type, bool gateup, const GemvArgs &a, int max_items, double avg_pairs, int tt, hipStream_t st);
 template <int T, int TT, int NW = 4>
 void launch_mmq_t(bool gateup, dim3 grid, const GemvArgs &a, hipStream_t st) {

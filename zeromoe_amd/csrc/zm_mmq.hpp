@@ -15,15 +15,14 @@
 //   mn[t][r]   = sum_sb bsum[t][sb] * (-dmin[r] * m[r][sb])   (v_mfma_f32_16x16x4f32;
 //                -dmin * m is exact in fp32, so mn is -dmin * imin to fp32 rounding)
 //   f[t][r]   += d_x[t] * (d[r] * isum + mn)  (ggml's vec_dot_q4_K_q8_K combine)
-// Q4_K K order of a 64-weight chunk i (qs group i, bytes 32i..32i+31, holding
-// sub-block 2i in its low nibbles and 2i + 1 in its high nibbles): k-group g
-// holds bytes 8g..8g+7 of the group, low nibbles then high nibbles, i.e.
-// weights 64i + 8g .. +7 and 64i + 32 + 8g .. +7, so every qs byte is loaded
-// by one lane only; the activation operand is read in the same order (two
-// 8-byte LDS reads).  Q5_K keeps the contiguous order: k-group g holds the low
-// nibbles (g < 2) or high nibbles (g >= 2) of bytes 16*(g & 1)..+15, i.e.
-// weights 64i + 16g .. +15.  The weight unpacking is done once per block for
-// all token tiles of the work item.  No dequantized weight copy is materialized.
+// Q4_K / Q5_K K order of a 64-weight chunk i (qs group i, bytes 32i..32i+31,
+// holding sub-block 2i in its low nibbles and 2i + 1 in its high nibbles):
+// k-group g holds bytes 8g..8g+7 of the group, low nibbles then high nibbles,
+// i.e. weights 64i + 8g .. +7 and 64i + 32 + 8g .. +7, so every qs byte is
+// loaded by one lane only (Q5_K: the fifth bits are bits 2i, 2i + 1 of the
+// lane's qh bytes 8g..8g+7); the activation operand is read in the same order
+// (two 8-byte LDS reads).  The weight unpacking is done once per block for all
+// token tiles of the work item.  No dequantized weight copy is materialized.
 // Activations reach LDS by direct buffer-to-LDS loads (no register staging),
 // token rows XOR-swizzled in 16-byte chunks by the token index.
 //
@@ -201,10 +200,10 @@ struct MmqW<T_Q4_K> {  // d, dmin, scales | this lane's 8 bytes of each 32-byte 
   uint2 qs[4];
 };
 template <>
-struct MmqW<T_Q5_K> {  // d, dmin, scales | this lane's 16 bytes of qh | 4 x 16 bytes of qs
+struct MmqW<T_Q5_K> {  // d, dmin, scales | this lane's 8 bytes of qh and of each 32-byte qs group
   uint4 hdr;
-  uint4 qh;
-  uint4 qs[4];
+  uint2 qh;
+  uint2 qs[4];
 };
 template <>
 struct MmqW<T_Q2_K> {  // scales | this lane's 2 x 16 bytes of qs | d, dmin
@@ -320,9 +319,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
         for (int i = 0; i < 4; ++i) w[m].qs[i] = bld8(rw[m], vo + 16 + 32 * i + 8 * g, 0);
       } else if constexpr (T == T_Q5_K) {
         w[m].hdr = bld16(rw[m], vo, 0);
-        w[m].qh = bld16(rw[m], vo + 16 + 16 * (g & 1), 0);
+        w[m].qh = bld8(rw[m], vo + 16 + 8 * g, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) w[m].qs[i] = bld16(rw[m], vo + 48 + 32 * i + 16 * (g & 1), 0);
+        for (int i = 0; i < 4; ++i) w[m].qs[i] = bld8(rw[m], vo + 48 + 32 * i + 8 * g, 0);
       } else if constexpr (T == T_IQ2_XXS) {
         w[m].d = bld2(rw[m], vo, 0);
 #pragma unroll
@@ -416,7 +415,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
       constexpr int N5 = T == T_Q5_K ? 4 : 1;
       v4i_t bl[NM][4], bh[NM][4], b5[NM][N5];
       float dd[NM], dm[NM], mb0[NM], mb1[NM];
-      const int hs = 8 * (g >> 1), ns = 4 * (g >> 1);
 #pragma unroll
       for (int m = 0; m < NM; ++m) {
         const uint32_t u0 = wcur[m].hdr.y, u1 = wcur[m].hdr.z, u2 = wcur[m].hdr.w;
@@ -433,10 +431,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
         // scale-folded weights of the 4 chunks: lane's sub-block 2i + (g >> 1),
         // sc = 8 * hi + lo; Q5_K: the fifth bit (bit 2i + (g >> 1) of the lane's
         // qh bytes) is a third chain with the whole scale, isum = D_lo + 8 D_hi + 16 D_5
-        if constexpr (T == T_Q4_K) {
+        {
           // chunk i = qs group i (sub-blocks 2i, 2i + 1): the lane's 8 bytes
           // 8g .. 8g + 7 give 8 weights of each sub-block, low nibbles then
-          // high nibbles (the activation operand is read in the same order)
+          // high nibbles (the activation operand is read in the same order);
+          // Q5_K: their fifth bits are bits 2i, 2i + 1 of the lane's 8 qh bytes
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const uint32_t scw = (i < 2 ? sc_lo : sc_hi) >> (16 * (i & 1));
@@ -448,24 +447,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
                              (int)mul_bytes(n3, s1 & 7u)};
             bh[m][i] = v4i_t{(int)mul_bytes(n0, s0 >> 3), (int)mul_bytes(n1, s0 >> 3), (int)mul_bytes(n2, s1 >> 3),
                              (int)mul_bytes(n3, s1 >> 3)};
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint32_t scw = i < 2 ? sc_lo : sc_hi;
-            const uint32_t sc = (scw >> (16 * (i & 1) + hs)) & 0xffu;
-            const uint32_t lo = sc & 7u, hi = sc >> 3;
-            const uint4 q = wcur[m].qs[i];
-            const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              const uint32_t nib = (qw[c] >> ns) & 0x0f0f0f0fu;
-              bl[m][i][c] = (int)mul_bytes(nib, lo);
-              bh[m][i][c] = (int)mul_bytes(nib, hi);
-              if constexpr (T == T_Q5_K) {
-                const uint32_t hq[4] = {wcur[m].qh.x, wcur[m].qh.y, wcur[m].qh.z, wcur[m].qh.w};
-                b5[m][i][c] = (int)mul_bytes((hq[c] >> (2 * i + (g >> 1))) & 0x01010101u, sc);
-              }
+            if constexpr (T == T_Q5_K) {
+              const uint2 h = wcur[m].qh;
+              b5[m][i] = v4i_t{(int)mul_bytes((h.x >> (2 * i)) & 0x01010101u, s0),
+                               (int)mul_bytes((h.y >> (2 * i)) & 0x01010101u, s0),
+                               (int)mul_bytes((h.x >> (2 * i + 1)) & 0x01010101u, s1),
+                               (int)mul_bytes((h.y >> (2 * i + 1)) & 0x01010101u, s1)};
             }
           }
         }
@@ -475,18 +462,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
         if (t >= nt) continue;
         const int tok = 16 * t + n;
         v4i_t xa[4];
-        if constexpr (T == T_Q4_K) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            // activations 64i + 8g .. +7 and 64i + 32 + 8g .. +7 (logical 16-byte
-            // chunks 4i + g/2 and 4i + 2 + g/2, half g & 1)
-            const uint2 lo8 = xq8(buf, tok, 4 * i + (g >> 1), g & 1);
-            const uint2 hi8 = xq8(buf, tok, 4 * i + 2 + (g >> 1), g & 1);
-            xa[i] = v4i_t{(int)lo8.x, (int)lo8.y, (int)hi8.x, (int)hi8.y};
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) xa[i] = xq16(buf, tok, 4 * i + g);
+        for (int i = 0; i < 4; ++i) {
+          // activations 64i + 8g .. +7 and 64i + 32 + 8g .. +7 (logical 16-byte
+          // chunks 4i + g/2 and 4i + 2 + g/2, half g & 1)
+          const uint2 lo8 = xq8(buf, tok, 4 * i + (g >> 1), g & 1);
+          const uint2 hi8 = xq8(buf, tok, 4 * i + 2 + (g >> 1), g & 1);
+          xa[i] = v4i_t{(int)lo8.x, (int)lo8.y, (int)hi8.x, (int)hi8.y};
         }
         // 32-sums of sub-blocks g and g + 4
         const float bs0 = (float)bsum32(buf, tok, g), bs1 = (float)bsum32(buf, tok, g + 4);
