@@ -8,12 +8,13 @@
 //       redundant, but no grid-wide barrier precedes the first weight request.
 //       Each wave then requests the weights of its first down rows (P2), so
 //       they stream while gate/up computes and while the workgroups wait.
-//   P1  the (pair, row) space of gate/up rows is cut into one contiguous range
-//       per workgroup; waves stream batches of rows (double-buffered) and store
-//       the SwiGLU output; the workgroup then counts itself in one of 16
-//       arrival counters.
-//       and adds its row count to the counter of every 256-row act block its
-//       range touches.
+//   P1  the shared expert's gate/up rows (which need no routing) and then the
+//       routed (pair, row) rows are each cut into one contiguous range per
+//       workgroup; the shared range starts as soon as x is quantized, while
+//       the routing waves finish.  Waves stream batches of rows
+//       (double-buffered) and store the SwiGLU output; the workgroup then
+//       counts itself in one of 16 arrival counters and adds its row counts to
+//       the counter of every 256-row act block its ranges touch.
 //   P2  down rows (token s, row h): each wave takes act blocks of the
 //       workgroup's tokens as soon as their counters reach 256 rows,
 //       quantizes them into LDS (Q8_K), and after the last one the workgroup
@@ -138,6 +139,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   __shared__ int s_gtok[DEC_MAX_PAIRS];  // compact index -> token
   __shared__ int s_doff[DEC_MAX_PAIRS];  // pair -> down expert byte offset (or -1)
   __shared__ int s_nvp;
+  __shared__ int s_xq_done;  // waves done quantizing x (shared-expert rows start on it)
   __shared__ int s_err;
   __shared__ uint32_t s_stale;
   __shared__ __attribute__((aligned(16))) uint8_t s_q8[DEC_LDS_Q8];
@@ -164,6 +166,14 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   const size_t q8Fs = a.Fs > 0 ? q8l_row_bytes(a.nbFs) : 0;
   uint64_t trace_t[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   ZM_TRACE(0);
+  if constexpr (TS != 0) {
+    // the x-quantization counter starts at zero before any wave counts itself:
+    // an LDS store and a plain barrier (no memory fence, so no wave waits for
+    // its global loads here)
+    if (tid == 0) s_xq_done = 0;
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+  }
   // counter set of this call (the other set is cleared at the end, for the next call)
   const uint32_t epoch = __builtin_amdgcn_readfirstlane(ld_co(&a.sync[0]));
   // An earlier call's wait expired (error word set): its counters are in an
@@ -239,6 +249,98 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     }
   }
   ZM_TRACE(7);
+  // P1 rows: L lanes per row (L1 for routed rows, 64 for shared rows), 64/L
+  // rows per wave step; lane li = lane % L takes unit li of the row (one
+  // super-block, or half of one for Q4_K).  Steps go through two register
+  // buffers: step st+1 is in flight while step st computes.  act holds the S *
+  // Fs shared rows (token, row n) first, then the routed rows (route c, row n).
+  const int Tsh = S * a.Fs;
+  const rsrc_t ract = make_rsrc(a.act, (uint32_t)(S * K * F + Tsh) * 4u);
+  const float invF = 1.0f / (float)F, invFs = a.Fs > 0 ? 1.0f / (float)a.Fs : 0.f;
+  auto stream_rows = [&](auto ttag, int r0, int r1) {
+    // rows [r0, r1) of the kind's own row space; routed rows sit after the
+    // S * Fs shared rows in act
+    constexpr int TT = decltype(ttag)::value;
+    constexpr bool SH = decltype(ttag)::shared;
+    constexpr int LL = decltype(ttag)::lanes;
+    constexpr int R1 = 64 / LL;
+    const int li1 = lane % LL, rg1 = lane / LL;
+    constexpr int UP = unit_per_block<TT>();
+    constexpr int BT = block_bytes(TT);
+    const int U1 = a.nbH * UP;
+    const rsrc_t rgt = SH ? make_rsrc(a.sg, a.sg_bytes) : make_rsrc(a.wg, a.wg_bytes);
+    const rsrc_t rut = SH ? make_rsrc(a.su, a.sg_bytes) : make_rsrc(a.wu, a.wg_bytes);
+    const bool uok = li1 < U1;
+    const int blk = min(li1 / UP, a.nbH - 1), part = li1 % UP;
+    const int nst_all = (r1 - r0 + R1 - 1) / R1;
+    const int nst = nst_all > wave ? (nst_all - wave + DEC_WAVES - 1) / DEC_WAVES : 0;
+    // step st -> this lane's (valid, row j, token, weight-row byte offset)
+    auto row1 = [&](int st, bool &valid, int &j, int &tok, int &roff) {
+      j = r0 + R1 * (wave + DEC_WAVES * st) + rg1;
+      valid = st < nst && j < r1;
+      j = valid ? j : r0;
+      int q, n;
+      if constexpr (SH) {
+        divmod24(j, a.Fs, invFs, q, n);
+        tok = q;
+        roff = (int)__umul24((uint32_t)n, (uint32_t)a.sg_rstride);
+      } else {
+        divmod24(j, F, invF, q, n);
+        tok = s_gtok[q];
+        roff = s_goff[q] + (int)__umul24((uint32_t)n, (uint32_t)a.g_rstride);
+      }
+    };
+    // a step's row (valid, j, token) is worked out once, when its loads are issued
+    struct RowInfo {
+      bool valid;
+      int j, tok;
+    };
+    auto issue = [&](int st, Unit<TT> (&bw)[2], RowInfo &ri) {
+      int roff;
+      row1(st, ri.valid, ri.j, ri.tok, roff);
+      const int vo = (ri.valid && uok) ? roff + blk * BT : OOR;
+      load_unit<TT>(rgt, vo, part, bw[0]);
+      load_unit<TT>(rut, vo, part, bw[1]);
+    };
+    auto compute = [&](const Unit<TT> (&bw)[2], const RowInfo &ri) {
+      const bool valid = ri.valid;
+      const int j = ri.j, tok = ri.tok;
+      float o[2];
+      unit_dots<TT, 2>(bw, part, xblk(s_q8 + (size_t)tok * q8x, a.nbH, blk), s_grid, s_signs, o);
+      const float ag = group_sum<LL>(o[0]), au = group_sum<LL>(o[1]);
+      bst_co(ract, (li1 == 0 && valid) ? 4 * (SH ? j : Tsh + j) : OOR, silu_f32(ag) * au);
+    };
+    // sched_barrier keeps every load of a step ahead of the math that waits
+    // on the previous one (vmcnt is in order: an interleaved wait drains the
+    // queue); steps past the end load and store nothing
+    Unit<TT> A[2], B[2];
+    RowInfo ra, rb;
+    if (nst > 0) issue(0, A, ra);
+    for (int st = 0; st < nst; st += 2) {
+      issue(st + 1, B, rb);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(A, ra);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(st + 2, A, ra);
+      __builtin_amdgcn_sched_barrier(0);
+      if (st + 1 < nst) compute(B, rb);  // an odd step count leaves B empty: no dots on zeros
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // shared-expert rows need no routing: every wave starts its share of this
+  // workgroup's shared rows once all of x is quantized (the waves that had
+  // quantization work count themselves in LDS), so they stream while the
+  // routing waves finish
+  const int sh0 = (int)((long)Tsh * g / G), sh1 = (int)((long)Tsh * (g + 1) / G);
+  if constexpr (TS != 0) {
+    const int nqw = min(DEC_WAVES, (nxb + 3) / 4);  // waves with x-quantization work
+    if (wi < nqw) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's x blocks are in LDS
+      if (lane == 0) atomicAdd(&s_xq_done, 1);
+    }
+    while (__atomic_load_n(&s_xq_done, __ATOMIC_RELAXED) < nqw) __builtin_amdgcn_s_sleep(1);
+    stream_rows(RowsTag<TS, true, 64>{}, sh0, sh1);
+  }
   __syncthreads();
   if (s_stale != 0u) {
     const int T2e = S * H;
@@ -281,7 +383,6 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   ZM_TRACE(1);
   const int nvp = s_nvp;
   const int T1r = nvp * F;
-  const int T1 = T1r + S * a.Fs;
 
   // ---------------------------------------------------------------- P2 set-up: down rows
   // 16 lanes per down row, 4 rows per wave step; step st of this wave covers
@@ -335,96 +436,24 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   load_step2(0, c2r, c2s);
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---------------------------------------------------------------- P1: gate/up rows
-  // Rows [t0, t1) of this workgroup: routed rows (route c, row n) first, then
-  // the shared expert's rows (token, row n).  L lanes per row (L1 for routed
-  // rows, 64 for shared rows), 64/L rows per wave step; lane li = lane % L
-  // takes unit li of the row (one super-block,
-  // or half of one for Q4_K).  Steps go through two register buffers: step
-  // st+1 is in flight while step st computes.
-  const int t0 = (int)((long)T1 * g / G), t1 = (int)((long)T1 * (g + 1) / G);
-  const rsrc_t ract = make_rsrc(a.act, (uint32_t)T1 * 4u);
-  {
-    const float invF = 1.0f / (float)F, invFs = a.Fs > 0 ? 1.0f / (float)a.Fs : 0.f;
-    auto stream_rows = [&](auto ttag, int r0, int r1) {
-      constexpr int TT = decltype(ttag)::value;
-      constexpr bool SH = decltype(ttag)::shared;
-      constexpr int LL = decltype(ttag)::lanes;
-      constexpr int R1 = 64 / LL;
-      const int li1 = lane % LL, rg1 = lane / LL;
-      constexpr int UP = unit_per_block<TT>();
-      constexpr int BT = block_bytes(TT);
-      const int U1 = a.nbH * UP;
-      const rsrc_t rgt = SH ? make_rsrc(a.sg, a.sg_bytes) : make_rsrc(a.wg, a.wg_bytes);
-      const rsrc_t rut = SH ? make_rsrc(a.su, a.sg_bytes) : make_rsrc(a.wu, a.wg_bytes);
-      const bool uok = li1 < U1;
-      const int blk = min(li1 / UP, a.nbH - 1), part = li1 % UP;
-      const int nst_all = (r1 - r0 + R1 - 1) / R1;
-      const int nst = nst_all > wave ? (nst_all - wave + DEC_WAVES - 1) / DEC_WAVES : 0;
-      // step st -> this lane's (valid, row j, token, weight-row byte offset)
-      auto row1 = [&](int st, bool &valid, int &j, int &tok, int &roff) {
-        j = r0 + R1 * (wave + DEC_WAVES * st) + rg1;
-        valid = st < nst && j < r1;
-        j = valid ? j : r0;
-        int q, n;
-        if constexpr (SH) {
-          divmod24(j - T1r, a.Fs, invFs, q, n);
-          tok = q;
-          roff = (int)__umul24((uint32_t)n, (uint32_t)a.sg_rstride);
-        } else {
-          divmod24(j, F, invF, q, n);
-          tok = s_gtok[q];
-          roff = s_goff[q] + (int)__umul24((uint32_t)n, (uint32_t)a.g_rstride);
-        }
-      };
-      // a step's row (valid, j, token) is worked out once, when its loads are issued
-      struct RowInfo {
-        bool valid;
-        int j, tok;
-      };
-      auto issue = [&](int st, Unit<TT> (&bw)[2], RowInfo &ri) {
-        int roff;
-        row1(st, ri.valid, ri.j, ri.tok, roff);
-        const int vo = (ri.valid && uok) ? roff + blk * BT : OOR;
-        load_unit<TT>(rgt, vo, part, bw[0]);
-        load_unit<TT>(rut, vo, part, bw[1]);
-      };
-      auto compute = [&](const Unit<TT> (&bw)[2], const RowInfo &ri) {
-        const bool valid = ri.valid;
-        const int j = ri.j, tok = ri.tok;
-        float o[2];
-        unit_dots<TT, 2>(bw, part, xblk(s_q8 + (size_t)tok * q8x, a.nbH, blk), s_grid, s_signs, o);
-        const float ag = group_sum<LL>(o[0]), au = group_sum<LL>(o[1]);
-        bst_co(ract, (li1 == 0 && valid) ? 4 * j : OOR, silu_f32(ag) * au);
-      };
-      // sched_barrier keeps every load of a step ahead of the math that waits
-      // on the previous one (vmcnt is in order: an interleaved wait drains the
-      // queue); steps past the end load and store nothing
-      Unit<TT> A[2], B[2];
-      RowInfo ra, rb;
-      if (nst > 0) issue(0, A, ra);
-      for (int st = 0; st < nst; st += 2) {
-        issue(st + 1, B, rb);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(A, ra);
-        __builtin_amdgcn_sched_barrier(0);
-        issue(st + 2, A, ra);
-        __builtin_amdgcn_sched_barrier(0);
-        if (st + 1 < nst) compute(B, rb);  // an odd step count leaves B empty: no dots on zeros
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    };
-    stream_rows(RowsTag<TG, false, L1>{}, t0, min(t1, T1r));
-    if constexpr (TS != 0) stream_rows(RowsTag<TS, true, 64>{}, max(t0, T1r), t1);
-  }
+  // ---------------------------------------------------------------- P1: routed gate/up rows
+  // rows [t0, t1) of the routed row space (route c, row n); the shared rows
+  // were streamed before the routing barrier
+  const int t0 = (int)((long)T1r * g / G), t1 = (int)((long)T1r * (g + 1) / G);
+  stream_rows(RowsTag<TG, false, L1>{}, t0, t1);
   stores_done();
   __syncthreads();
   ZM_TRACE(2);
   // arrival (for the epoch) and rows per act block: row j belongs to block j / 256
   if (tid == 0) atomicAdd(&cnt[DEC_CNT_STRIDE * (g % DEC_NCNT)], 1u);
-  if (t1 > t0 && tid >= 1 && tid <= ((t1 - 1) >> 8) - (t0 >> 8) + 1) {
-    const int b = (t0 >> 8) + tid - 1;
-    atomicAdd(&bcnt[DEC_BCNT_STRIDE * b], (uint32_t)(min(t1, (b + 1) << 8) - max(t0, b << 8)));
+  {
+    // act rows stored: the routed range [Tsh + t0, Tsh + t1) (threads 1..) and
+    // the shared range [sh0, sh1) (threads 65..)
+    const int r0 = tid < 64 ? Tsh + t0 : sh0, r1 = tid < 64 ? Tsh + t1 : sh1, i = (tid & 63) - 1;
+    if (r1 > r0 && tid < 128 && i >= 0 && i <= ((r1 - 1) >> 8) - (r0 >> 8)) {
+      const int b = (r0 >> 8) + i;
+      atomicAdd(&bcnt[DEC_BCNT_STRIDE * b], (uint32_t)(min(r1, (b + 1) << 8) - max(r0, b << 8)));
+    }
   }
   // Clear the other counter set for the next call: its last users were the
   // previous call's workgroups, all finished.  Issued here by wave 0, behind
@@ -456,12 +485,12 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
         blk = r - k * a.nbF;
         nb = a.nbF;
         const int c = s_cidx[s * K + k];
-        aoff = c < 0 ? OOR : (c * F + blk * QK) * 4;
+        aoff = c < 0 ? OOR : (Tsh + c * F + blk * QK) * 4;
         row = s_q8 + (size_t)ts * tok_bytes + (size_t)k * q8F;
       } else {
         blk = r - K * a.nbF;
         nb = a.nbFs;
-        aoff = (T1r + s * a.Fs + blk * QK) * 4;
+        aoff = (s * a.Fs + blk * QK) * 4;
         row = s_q8 + (size_t)ts * tok_bytes + (size_t)K * q8F;
       }
     };
@@ -473,7 +502,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     // is bounded: on expiry the error word is set and the kernel still drains.
     constexpr int QR = 3;
     const int kq = lane >> 4;
-    const int T1b = T1r >> 8;
+    const int Tshb = Tsh >> 8;  // act blocks of the shared rows (Fs is a multiple of 256)
     for (int base = wave * 4; base < nb_all; base += DEC_WAVES * 4 * QR) {
       // act offsets of this round's blocks (wave-uniform), worked out before
       // the wait: the divisions and slot-table reads are ~2 us of scalar code
@@ -509,9 +538,9 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
           if (r < K * a.nbF) {
             const int k = r / a.nbF;
             const int c = s_cidx[s * K + k];
-            bid = c < 0 ? -1 : c * a.nbF + (r - k * a.nbF);
+            bid = c < 0 ? -1 : Tshb + c * a.nbF + (r - k * a.nbF);
           } else {
-            bid = T1b + s * a.nbFs + (r - K * a.nbF);
+            bid = s * a.nbFs + (r - K * a.nbF);
           }
         }
         int spins = 0;
