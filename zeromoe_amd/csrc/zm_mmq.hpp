@@ -406,8 +406,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
 #pragma unroll
       for (int j = 0; j < 4; ++j) f[m][t][j] = 0.f;
 
-  // block b of the K loop from the weights in wcur and activation buffer b & 1
-  auto step = [&](int b, int buf, const WBlk(&wcur)[NM]) {
+  // one block of the K loop from the weights in wcur and activation buffer buf
+  auto step = [&](int buf, const WBlk(&wcur)[NM]) {
     if constexpr (K45) {
       // both matrices' operands first, then one pass over the token tiles: the
       // activation operand (and the bsums of the min product) is read from LDS
@@ -713,13 +713,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
   for (int b = 0;; b += 2) {
     dma_x(b + 1, 1);  // buffer 1's readers finished at the last barrier
     load_w(b + 1, w1);
-    step(b, 0, w0);
+    step(0, w0);
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
     if (b + 1 >= nb) break;
     dma_x(b + 2, 0);
     load_w(b + 2, w0);
-    step(b + 1, 1, w1);
+    step(1, w1);
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
     if (b + 2 >= nb) break;
