@@ -485,6 +485,9 @@ LAYER_CASES = {
     "q5k_q2k_mmq": (CONFIGS["c3"], dict(tg=Q5, td=Q2, S=256, H=1024, F=512, E=16)),
     "q2k_q6k_mmq": (CONFIGS["c3"], dict(tg=Q2, td=Q6, S=256, H=1024, F=512, E=16)),
     "iq2xxs_mmq": (CONFIGS["c3"], dict(tg=IQ2, td=IQ2, S=256, H=1024, F=512, E=16)),
+    # odd K-block counts (H = 5, F = 3 super-blocks) through the two-way unrolled K loop
+    "q4k_mmq_odd_nb": (CONFIGS["c3"], dict(S=256, H=1280, F=768, E=16)),
+    "iq3xxs_q6k_mmq_odd_nb": (CONFIGS["c3"], dict(tg=IQ3, td=Q6, S=256, H=1280, F=768, E=16)),
     "iq3xxs_iq4xs_mmq": (CONFIGS["c3"], dict(tg=IQ3, td=IQ4, S=256, H=1024, F=512, E=16)),
     "q5k_q5k_S64": (CONFIGS["c3"], dict(tg=Q5, td=Q5, S=64, H=1024, F=512)),
     "q4k_iq4xs_S1": (CONFIGS["c2"], dict(tg=Q4, td=IQ4)),
@@ -687,6 +690,9 @@ PREFILL_CASES = {
     "q5k_q6k_mmq": (CONFIGS["c3"], dict(tg=Q5, td=Q6, S=256, H=1024, F=512, E=16)),
     "iq4xs_mmq": (CONFIGS["c3"], dict(tg=IQ4, td=IQ4, S=256, H=1024, F=512, E=16)),
     "iq2xxs_mmq": (CONFIGS["c3"], dict(tg=IQ2, td=IQ2, S=256, H=1024, F=512, E=16)),
+    # odd K-block counts (H = 5, F = 3 super-blocks) through the two-way unrolled K loop
+    "q4k_mmq_odd_nb": (CONFIGS["c3"], dict(S=256, H=1280, F=768, E=16)),
+    "iq3xxs_q6k_mmq_odd_nb": (CONFIGS["c3"], dict(tg=IQ3, td=Q6, S=256, H=1280, F=768, E=16)),
     "iq3xxs_mmq": (CONFIGS["c3"], dict(tg=IQ3, td=IQ3, S=256, H=1024, F=512, E=16)),
 }
 
