@@ -157,17 +157,21 @@ static uint64_t splitmix64(uint64_t *s) {
   return z ^ (z >> 31);
 }
 
-/* Portable seeded normals: splitmix64 uniforms + Box-Muller (both outputs). */
+/* Portable seeded normals: splitmix64 uniforms + Box-Muller (both outputs).
+ * splitmix64's state after c calls is seed + c * gamma, so pair p (outputs
+ * 2p, 2p+1) starts from seed + 2p * gamma: the pairs are independent and are
+ * filled in parallel, with the same values as the sequential recurrence. */
 void zmo_fill_normal(uint64_t seed, float mean, float sd, float *out, int64_t n) {
-  uint64_t s = seed;
-  int64_t i = 0;
-  while (i < n) {
+  const int64_t pairs = (n + 1) / 2;
+#pragma omp parallel for schedule(static) if (pairs > 65536)
+  for (int64_t p = 0; p < pairs; ++p) {
+    uint64_t s = seed + (uint64_t)(2 * p) * 0x9e3779b97f4a7c15ull;
     const double u1 = ((splitmix64(&s) >> 11) + 1.0) * (1.0 / 9007199254740993.0);
     const double u2 = (splitmix64(&s) >> 11) * (1.0 / 9007199254740992.0);
     const double r = sqrt(-2.0 * log(u1));
     const double t = 6.283185307179586476925286766559 * u2;
-    out[i++] = (float)(mean + sd * r * cos(t));
-    if (i < n) out[i++] = (float)(mean + sd * r * sin(t));
+    out[2 * p] = (float)(mean + sd * r * cos(t));
+    if (2 * p + 1 < n) out[2 * p + 1] = (float)(mean + sd * r * sin(t));
   }
 }
 
@@ -706,27 +710,41 @@ void zmo_quantize_row_q6_K(const float *x, zmo_block_q6_K *y, int64_t k) {
  * an odd count the smallest-magnitude weight keeps a positive sign) and the
  * nearest grid vector to |x|/scale; per 32-weight sub-block a 4-bit scale
  * ls with value d*(0.5+ls)*0.25; block d in fp16. */
-static int nearest_grid(const float *a, float inv, const uint64_t *grid, float *err_out) {
+/* gt: the grid as floats, transposed: gt[256 * j + g] = byte j of grid[g].
+ * The squared error of every grid point is summed j = 0..7 in order; the
+ * points are scanned 8 at a time (8 independent sums, one vector lane each),
+ * the first minimum wins. */
+__attribute__((optimize("O3"))) static int nearest_grid(const float *a, float inv, const float *gt, float *err_out) {
+  float s[8];
+  for (int j = 0; j < 8; ++j) s[j] = a[j] * inv;
   int best = 0;
   float be = 3.4e38f;
-  for (int g = 0; g < 256; ++g) {
-    float e = 0;
+  for (int g0 = 0; g0 < 256; g0 += 8) {
+    float e[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int j = 0; j < 8; ++j) {
-      const float v = (float)((grid[g] >> (8 * j)) & 0xff);
-      const float dd = a[j] * inv - v;
-      e += dd * dd;
+      const float *row = gt + 256 * j + g0;
+      for (int q = 0; q < 8; ++q) {
+        const float dd = s[j] - row[q];
+        e[q] += dd * dd;
+      }
     }
-    if (e < be) {
-      be = e;
-      best = g;
-    }
+    for (int q = 0; q < 8; ++q)
+      if (e[q] < be) {
+        be = e[q];
+        best = g0 + q;
+      }
   }
   if (err_out) *err_out = be;
   return best;
 }
 
 void zmo_quantize_row_iq2_xxs(const float *x, zmo_block_iq2_xxs *y, int64_t k) {
-  const uint64_t *grid = zmo_iq2xxs_grid();
+  float grid[256 * 8];
+  {
+    const uint64_t *g64 = zmo_iq2xxs_grid();
+    for (int g = 0; g < 256; ++g)
+      for (int j = 0; j < 8; ++j) grid[256 * j + g] = (float)((g64[g] >> (8 * j)) & 0xff);
+  }
   const int64_t nb = k / ZMO_QK_K;
   for (int64_t i = 0; i < nb; ++i, x += ZMO_QK_K) {
     float sub_scale[8];

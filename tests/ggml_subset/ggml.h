@@ -6,7 +6,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-enum ggml_type { GGML_TYPE_F32 = 0, GGML_TYPE_Q4_K = 12, GGML_TYPE_I32 = 26 };
+enum ggml_type { GGML_TYPE_F32 = 0, GGML_TYPE_Q2_K = 10, GGML_TYPE_Q3_K = 11, GGML_TYPE_Q4_K = 12, GGML_TYPE_I32 = 26 };
 
 struct ggml_tensor {
   enum ggml_type type;

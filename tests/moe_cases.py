@@ -222,22 +222,39 @@ class Built:
         return slack
 
 
-def assert_close_layer(got: np.ndarray, ref: np.ndarray, rtol: float = 1e-3, slack=None):
+# (label, per-token-norm max error, element-wise max relative error, elements
+# counted) of every checked layer output, printed at the end of a pytest run
+LAYER_ERRORS: list = []
+
+
+def assert_close_layer(got: np.ndarray, ref: np.ndarray, rtol: float = 1e-3, slack=None, label: str = ""):
     """Layer-output tolerance: per token, max |got - ref| <= rtol * max |ref|
     (the 1e-3 max relative error of the north star, taken against the token's
     output scale so isolated near-zero outputs do not dominate).  `slack`
     (a callable returning a per-token bound, see Built.requant_slack) is
     consulted only for tokens over the tolerance: their excess must be
-    explained by activation re-quantization ties."""
+    explained by activation re-quantization ties.
+
+    Reported beside it (not asserted): the element-wise max relative error
+    |got - ref| / |ref| over the elements with |ref| >= 1e-2 * max |ref| of
+    their token, the reading of "max relative error" that excludes outputs
+    near zero, where a relative error is dominated by cancellation."""
     assert got.shape == ref.shape
     assert np.isfinite(got).all()
+    g64, r64 = got.astype(np.float64), ref.astype(np.float64)
+    scale = np.abs(r64).max(axis=-1, keepdims=True)
+    big = np.abs(r64) >= 1e-2 * scale
+    elem = float((np.abs(g64 - r64)[big] / np.abs(r64)[big]).max()) if big.any() else 0.0
+    tok = float((np.abs(g64 - r64).max(axis=-1) / np.maximum(scale[..., 0], 1e-30)).max())
+    LAYER_ERRORS.append((label, tok, elem, int(big.sum())))
     bound = None
     for s in range(ref.shape[0]):
-        scale = float(np.abs(ref[s]).max())
+        scale_s = float(np.abs(ref[s]).max())
         err = float(np.abs(got[s] - ref[s]).max())
-        if err <= rtol * max(scale, 1e-30):
+        if err <= rtol * max(scale_s, 1e-30):
             continue
-        assert slack is not None, (s, err, scale)
+        assert slack is not None, (s, err, scale_s)
         if bound is None:
             bound = slack()
-        assert err <= rtol * scale + bound[s], (s, err, scale, float(bound[s]))
+        assert err <= rtol * scale_s + bound[s], (s, err, scale_s, float(bound[s]))
+    return tok, elem

@@ -6,6 +6,9 @@ to the cold routes (ids' = cold_map[ids], w' = w * cold_mask[ids],
 backends/ggml/moe_partial_route_ggml.hpp:21-35) bit for bit, with the AVX-512
 and the scalar dots.  GPU test: fork -> hot layer on the GPU -> merge equals
 the oracle's whole layer, and the lane's CPU work overlaps the GPU's."""
+import threading
+import time
+
 import numpy as np
 import pytest
 
@@ -120,12 +123,22 @@ def test_cold_lane_fork_hot_merge_on_gpu():
         lane.fork(x, ids_g, w_g)
         hot_layer.forward(x, lg, out=out)
         hot_only = out.clone()
-        torch.cuda._sleep(100_000_000)  # keep the stream busy well past the lane's CPU work
+        torch.cuda._sleep(100_000_000)  # keep the stream busy after the fork
         busy = torch.cuda.Event()
         busy.record()
+        # host time at which the stream drained, seen by a poller started now
+        drained = []
+
+        def poll():
+            while not busy.query():
+                time.sleep(20e-6)
+            drained.append(time.monotonic_ns())
+
+        poller = threading.Thread(target=poll)
+        poller.start()
         lane.merge(out)
-        still_busy = not busy.query()
         torch.cuda.synchronize()
+        poller.join()
         assert hot_layer.status(S) == 0
         ids_h, w_h = ids_g.cpu().numpy(), w_g.cpu().numpy()
         assert (cmap[ids_h] >= 0).any() and (hmap[ids_h] >= 0).any()
@@ -144,5 +157,7 @@ def test_cold_lane_fork_hot_merge_on_gpu():
         assert_close_layer(hot_only.cpu().numpy(), ref_hot)
         st = lane.stats()
         assert st["fork_ns"] <= st["compute_begin_ns"] <= st["compute_end_ns"] <= st["merge_ns"]
-        assert still_busy, "the lane's result was ready only after the GPU stream drained"
+        # the lane starts on the fork's event, not after the GPU work: its CPU
+        # work began while the stream was still busy (same monotonic clock)
+        assert st["compute_begin_ns"] < drained[0], "the lane started only after the GPU stream drained"
         lane.close()

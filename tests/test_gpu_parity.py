@@ -519,7 +519,7 @@ def test_moe_layer_vs_oracle(case):
     np.testing.assert_allclose(w.cpu().numpy(), w_r, rtol=1e-5, atol=1e-7)
     ids_h, w_h = ids.cpu().numpy(), w.cpu().numpy()
     ref = b.oracle_forward(ids_h, w_h)
-    assert_close_layer(out.cpu().numpy(), ref, slack=lambda: b.requant_slack(ids_h, w_h))
+    assert_close_layer(out.cpu().numpy(), ref, slack=lambda: b.requant_slack(ids_h, w_h), label=f"layer {case}")
 
 
 def test_moe_layer_repeatable_and_stream_ordered():
@@ -619,32 +619,29 @@ def test_fused_decode_varying_routes(case, monkeypatch):
 
 def test_fused_decode_expired_wait_is_loud_and_recovers(monkeypatch):
     """The fused kernel's bounded waits forced to give up from the host (a
-    spin limit of 0 polls): the launch still completes; rows whose wait
-    expired are NaN, never stale; the next launch, which finds the error word
-    set, writes NaN everywhere instead of trusting the counters; zm_moe_status
-    reports the error and resets the sync words, and the launch after that
-    matches the oracle again."""
+    negative spin limit: every act-block wait expires on its first poll): the
+    launch still completes and its rows are NaN, never stale; the next launch,
+    which finds the error word set, writes NaN everywhere instead of trusting
+    the counters; zm_moe_status reports the error and resets the sync words,
+    and the launch after that matches the oracle again."""
     c = CONFIGS["c2"]
     b = Built(c, seed=61)
     L = b.layer()
     x = torch.from_numpy(b.x).cuda()
     lg = torch.from_numpy(b.logits).cuda()
     monkeypatch.setenv("ZEROMOE_FUSED_DECODE", "1")
-    monkeypatch.setenv("ZEROMOE_SPIN_LIMIT", "0")
+    monkeypatch.setenv("ZEROMOE_SPIN_LIMIT", "-1")
     out1, ids, w = L.forward(x, lg)
     out1 = out1.clone()
     monkeypatch.delenv("ZEROMOE_SPIN_LIMIT")
     out2, _, _ = L.forward(x, lg)
     _sync()
     err = L.status(c.S)
+    assert err != 0, "the forced give-up did not set the error word"
+    assert np.isnan(out1.cpu().numpy()).all()  # every workgroup waited for act blocks
+    assert np.isnan(out2.cpu().numpy()).all()  # stale counters are never trusted
     ids_h, w_h = ids.cpu().numpy(), w.cpu().numpy()
     ref = b.oracle_forward(ids_h, w_h)
-    if err:
-        assert np.isnan(out1.cpu().numpy()).any()
-        assert np.isnan(out2.cpu().numpy()).all()
-    else:  # every first poll already saw its data: nothing expired, results stand
-        assert_close_layer(out1.cpu().numpy(), ref)
-        assert_close_layer(out2.cpu().numpy(), ref)
     assert L.status(c.S) == 0
     out3, _, _ = L.forward(x, lg)
     _sync()
@@ -751,28 +748,41 @@ def test_c3_full_size_vs_oracle():
     np.testing.assert_array_equal(pairs.cpu().numpy()[: len(rp)], rp)
     assert rc.max() >= 100, rc.max()  # skewed: several work items for the heaviest experts
     ref = b.oracle_forward(ids_h, w_h, nthreads=16)
-    assert_close_layer(out.cpu().numpy(), ref, slack=lambda: b.requant_slack(ids_h, w_h))
+    assert_close_layer(out.cpu().numpy(), ref, slack=lambda: b.requant_slack(ids_h, w_h), label="c3 full size")
 
 
-@pytest.mark.parametrize("name", ["c1", "c2"])
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4", "c5"])
 def test_layer_with_ggml_quantized_weights(name):
     """The configurations state weights quantized from seeded N(0, 0.02) by
-    ggml's quantizers: the experts a token routes to are filled that way here
-    (the oracle's restated quantizers, a portable splitmix64 + Box-Muller
-    generator) instead of random valid blocks; decode through the fused
-    kernel against the oracle."""
+    ggml's quantizers: every expert the batch routes to (and c5's shared
+    expert) is filled that way here -- the oracle's restated quantizers on a
+    portable splitmix64 + Box-Muller generator (seed 1000 * expert + matrix,
+    the reference seeds its weights per tensor, tests/test_option_b_compact_ggml.cpp:90)
+    instead of random valid blocks.  c1/c2/c4/c5 decode through the fused
+    kernel, c3 (S=512) through the MFMA prefill; ids bit-exact and the layer
+    against the oracle.  IQ2_XXS (c4) has no importance matrix argument in
+    the restated quantizer, which is the uniform-importance case."""
     c = CONFIGS[name]
     b = Built(c, seed=71)
     ids_r, w_r = b.oracle_route()
-    for e in sorted(set(int(v) for v in ids_r.reshape(-1) if v >= 0)):
-        for k, (W, t, rows, n) in enumerate([(b.wg, c.tg, c.F, c.H), (b.wu, c.tg, c.F, c.H), (b.wd, c.td, c.H, c.F)]):
+    mats = lambda: [(b.wg, c.tg, c.F, c.H), (b.wu, c.tg, c.F, c.H), (b.wd, c.td, c.H, c.F)]
+    used = sorted(set(int(v) for v in ids_r.reshape(-1) if v >= 0))
+    print(f"{name}: quantizing {len(used)} experts", flush=True)
+    for e in used:
+        for k, (W, t, rows, n) in enumerate(mats()):
             x = O.fill_normal(1000 * e + k, rows * n, 0.0, 0.02).reshape(rows, n)
             W[e].copy_(torch.from_numpy(O.quantize(t, x)).cuda())
+    if c.F_shared:
+        for k, (W, rows, n) in enumerate([(b.sg, c.F_shared, c.H), (b.su, c.F_shared, c.H), (b.sd, c.H, c.F_shared)]):
+            x = O.fill_normal(999_000 + k, rows * n, 0.0, 0.02).reshape(rows, n)
+            W.copy_(torch.from_numpy(O.quantize(c.t_shared, x).reshape(W.shape)).cuda())
     L = b.layer()
-    out, ids, w = L.forward(torch.from_numpy(b.x).cuda(), torch.from_numpy(b.logits).cuda())
+    lg = None if c.router_gemv else torch.from_numpy(b.logits).cuda()
+    out, ids, w = L.forward(torch.from_numpy(b.x).cuda(), lg)
     _sync()
     assert L.status(c.S) == 0
     np.testing.assert_array_equal(ids.cpu().numpy(), ids_r)
     ids_h, w_h = ids.cpu().numpy(), w.cpu().numpy()
-    ref = b.oracle_forward(ids_h, w_h)
-    assert_close_layer(out.cpu().numpy(), ref, slack=lambda: b.requant_slack(ids_h, w_h))
+    ref = b.oracle_forward(ids_h, w_h, nthreads=16)
+    assert_close_layer(out.cpu().numpy(), ref, slack=lambda: b.requant_slack(ids_h, w_h),
+                       label=f"{name} ggml-quantized weights")

@@ -578,6 +578,95 @@ def test_quantizer_round_trip(t, tol):
     assert rel < tol, rel
 
 
+def _f16_bytes(v):
+    return np.frombuffer(np.float16(v).tobytes(), np.uint8)
+
+
+def _q2_K_block(d, dmin, sc, m, q):
+    """GGUF block_q2_K from its fields (scales: low nibble sc, high nibble m;
+    q of weight l at bits 2j of qs[32*(l // 128) + l % 32], j = (l % 128) // 32)."""
+    b = np.zeros(84, np.uint8)
+    b[0:16] = (sc & 15) | ((m & 15) << 4)
+    for l in range(256):
+        half, r = divmod(l, 128)
+        j, ll = divmod(r, 32)
+        b[16 + 32 * half + ll] |= (q[l] & 3) << (2 * j)
+    b[80:82], b[82:84] = _f16_bytes(d), _f16_bytes(dmin)
+    return b
+
+
+def _q3_K_block(d, sc, q):
+    """GGUF block_q3_K: q in [-4, 3] (low 2 bits in qs as for Q2_K, hmask bit
+    l // 32 of byte l % 32 set when q >= 0), 6-bit scales sc (value sc - 32)."""
+    b = np.zeros(110, np.uint8)
+    u = q + 4
+    for l in range(256):
+        half, r = divmod(l, 128)
+        j, ll = divmod(r, 32)
+        b[32 + 32 * half + ll] |= (u[l] & 3) << (2 * j)
+        if u[l] & 4:
+            b[ll] |= 1 << (l // 32)
+    for j in range(16):
+        b[96 + (j % 8)] |= (sc[j] & 15) << (4 * (j // 8))
+        b[96 + 8 + j % 4] |= (sc[j] >> 4) << (2 * (j // 4))
+    b[108:110] = _f16_bytes(d)
+    return b
+
+
+def _q4_K_block(d, dmin, sc, m, q):
+    """GGUF block_q4_K: 6-bit (sc, m) packed as get_scale_min_k4 reads them,
+    sub-blocks 2i / 2i+1 in the low / high nibbles of qs[32i .. 32i+31]."""
+    b = np.zeros(144, np.uint8)
+    b[0:2], b[2:4] = _f16_bytes(d), _f16_bytes(dmin)
+    for j in range(8):
+        if j < 4:
+            b[4 + j] = sc[j]
+            b[8 + j] = m[j]
+        else:
+            b[12 + j - 4] = (sc[j] & 15) | ((m[j] & 15) << 4)
+            b[4 + j - 4] |= (sc[j] >> 4) << 6
+            b[8 + j - 4] |= (m[j] >> 4) << 6
+    for i in range(4):
+        b[16 + 32 * i:48 + 32 * i] = q[64 * i:64 * i + 32] | (q[64 * i + 32:64 * i + 64] << 4)
+    return b
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q2_K, O.TYPE_Q3_K, O.TYPE_Q4_K])
+def test_quantizer_reproduces_representable_blocks(t):
+    """A block built from chosen fields is exactly representable; quantizing its
+    dequantized values must give back the identical values.  Each sub-block
+    holds both ends of its quant range and the largest scale and min sit at the
+    top of their field (Q3_K: the largest-magnitude scale is -32 and every
+    sub-block holds q = -4, the value the quantizer maps to the scale), so the
+    optimal scales are unique: a wrong scale search, rounding or packing in the
+    restated ggml quantizers fails here."""
+    rng = np.random.default_rng(100 + t)
+    for _ in range(60):
+        d, dmin = (float(np.float16(rng.uniform(1e-4, 1e-3))) for _ in range(2))
+        if t == O.TYPE_Q2_K:
+            sc, m = rng.integers(1, 16, 16), rng.integers(0, 16, 16)
+            sc[rng.integers(16)] = 15
+            m[rng.integers(16)] = 15
+            q = rng.integers(0, 4, 256)
+            q[0::16], q[1::16] = 0, 3
+            blk = _q2_K_block(d, dmin, sc, m, q)
+        elif t == O.TYPE_Q3_K:
+            v = rng.integers(1, 32, 16) * rng.choice([-1, 1], 16)
+            v[rng.integers(16)] = -32
+            q = rng.integers(-4, 4, 256)
+            q[0::16] = -4
+            blk = _q3_K_block(d, v + 32, q)
+        else:
+            sc, m = rng.integers(1, 64, 8), rng.integers(0, 64, 8)
+            sc[rng.integers(8)] = 63
+            m[rng.integers(8)] = 63
+            q = rng.integers(0, 16, 256)
+            q[0::32], q[1::32] = 0, 15
+            blk = _q4_K_block(d, dmin, sc, m, q)
+        x = O.dequantize(t, blk[None, :], 256)
+        np.testing.assert_array_equal(O.dequantize(t, O.quantize(t, x), 256), x)
+
+
 # ------------------------------------------------------------------ FP32-activation path restatements
 
 

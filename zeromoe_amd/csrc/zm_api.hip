@@ -922,7 +922,9 @@ int launch_fused(const zm_moe_layer *L, const float *x, const float *logits, int
   a.grid = uses(T_IQ4_XS) ? d->iq4 : (uses(T_IQ3_XXS) ? d->iq3 : d->grid);
   a.signs = d->signs;
   a.spin_limit = 1 << 23;
-  if (const char *sl = getenv("ZEROMOE_SPIN_LIMIT"); sl && sl[0])  // test hook: force the bounded waits to give up
+  // test hook: force the bounded waits to give up (a negative limit expires
+  // every act-block wait on its first poll, whatever the counters show)
+  if (const char *sl = getenv("ZEROMOE_SPIN_LIMIT"); sl && sl[0])
     a.spin_limit = atoi(sl);
   if (const char *tr = getenv("ZEROMOE_TRACE"); tr && tr[0] == '1') {
     DeviceState *dm = const_cast<DeviceState *>(d);
@@ -1050,10 +1052,6 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
   // 16-token tiles per routed work item, per projection (mmq_tt); gate/up and
   // down take separate item lists when their tilings differ
   int tt_g = mmq_tt(L->type_gate, false), tt_d = mmq_tt(L->type_down, false);
-  if (const char *v = getenv("ZEROMOE_MMQ_TT"); v) {  // experiment knob (4 or 8) for Q4_K
-    if (tt_g == 4) tt_g = atoi(v);
-    if (tt_d == 4) tt_d = atoi(v);
-  }
   // items: at most one partial run per active expert plus the full runs
   auto max_items_for = [&](int tt) {
     return std::min(mmq_max_items(S * K, NS), (S * K + 16 * tt - 1) / (16 * tt) + std::min(NS, S * K));

@@ -99,6 +99,17 @@ __device__ __forceinline__ void stores_done() {
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt and lgkmcnt left at their maxima
 }
 __device__ __forceinline__ void after_wait() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup"); }
+// LDS hand-over between the waves of a workgroup: this wave's LDS accesses
+// complete (release, LDS only: no wait for its global loads), then lane 0 adds
+// v to the counter; the waiter spins on the counter and acquires
+__device__ __forceinline__ void lds_signal(int *c, int v) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  if (__lane_id() == 0) __hip_atomic_fetch_add(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_wait(int *c, int v) {
+  while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < v) __builtin_amdgcn_s_sleep(1);
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 // one f32 through a buffer resource with sc1 (coherent past the L2); an
 // out-of-range offset drops the store
 __device__ __forceinline__ void bst_co(rsrc_t r, int vo, float v) {
@@ -148,6 +159,9 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   constexpr bool kIQ4 = TG == T_IQ4_XS || TD == T_IQ4_XS || TS == T_IQ4_XS;
   constexpr bool kIQ3 = TG == T_IQ3_XXS || TD == T_IQ3_XXS || TS == T_IQ3_XXS;
   static_assert((int)kIQ2 + (int)kIQ3 + (int)kIQ4 <= 1, "one lookup table per layer");
+  // the shared rows start before the table-filling waves (the routing waves
+  // among them) are counted, so a shared expert never reads a lookup table
+  static_assert(TS != T_IQ2_XXS && TS != T_IQ3_XXS && TS != T_IQ4_XS, "shared expert type without a lookup table");
   // the lookup tables first in LDS (largest alignment first): their addresses
   // fit the 16-bit offset field of the LDS reads, so an index becomes an
   // address in one or two instructions
@@ -334,11 +348,8 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   const int sh0 = (int)((long)Tsh * g / G), sh1 = (int)((long)Tsh * (g + 1) / G);
   if constexpr (TS != 0) {
     const int nqw = min(DEC_WAVES, (nxb + 3) / 4);  // waves with x-quantization work
-    if (wi < nqw) {
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's x blocks are in LDS
-      if (lane == 0) atomicAdd(&s_xq_done, 1);
-    }
-    while (__atomic_load_n(&s_xq_done, __ATOMIC_RELAXED) < nqw) __builtin_amdgcn_s_sleep(1);
+    if (wi < nqw) lds_signal(&s_xq_done, 1);  // this wave's x blocks are in LDS
+    lds_wait(&s_xq_done, nqw);
     stream_rows(RowsTag<TS, true, 64>{}, sh0, sh1);
   }
   __syncthreads();
@@ -546,7 +557,8 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
         int spins = 0;
         while (true) {
           const bool ready = bid < 0 || ld_co(&bcnt[DEC_BCNT_STRIDE * bid]) >= (uint32_t)QK;
-          if (__ballot(!ready) == 0ull) break;
+          // a negative limit (a host-forced give-up) expires on the first poll
+          if (__ballot(!ready) == 0ull && a.spin_limit >= 0) break;
           __builtin_amdgcn_s_sleep(1);
           if (++spins > a.spin_limit) {
             if (lane == 0) {

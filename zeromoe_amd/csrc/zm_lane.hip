@@ -479,7 +479,12 @@ struct zm_cold_lane {
   float *h_x = nullptr, *h_w = nullptr, *h_out = nullptr;
   int32_t *h_ids = nullptr;
   float *d_cold = nullptr;
-  hipEvent_t forked = nullptr, uploaded = nullptr;
+  // forked: the fork's copies landed; uploaded: a merge's upload of h_out
+  // finished (h_out may be rewritten); added: a merge's add finished (d_cold
+  // may be rewritten)
+  hipEvent_t forked = nullptr, uploaded = nullptr, added = nullptr;
+  bool merged_once = false;
+  int forked_S = 0;
   hipStream_t side = nullptr;
   // the lane thread
   std::thread worker;
@@ -556,6 +561,8 @@ struct zm_cold_lane {
       }
       int st = 0;
       if (hipEventSynchronize(forked) != hipSuccess) st = -1;
+      // the previous merge's upload still reads h_out until its event completes
+      if (merged_once && hipEventSynchronize(uploaded) != hipSuccess) st = -1;
       stats.compute_begin_ns = now_ns();
       if (!st) compute(h_x, h_ids, h_w, S, h_out);
       stats.compute_end_ns = now_ns();
@@ -580,6 +587,7 @@ struct zm_cold_lane {
     HIP_OK(hipMalloc((void **)&d_cold, T * d.H * sizeof(float)));
     HIP_OK(hipEventCreateWithFlags(&forked, hipEventDisableTiming));
     HIP_OK(hipEventCreateWithFlags(&uploaded, hipEventDisableTiming));
+    HIP_OK(hipEventCreateWithFlags(&added, hipEventDisableTiming));
     HIP_OK(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
     worker = std::thread([this] { loop(); });
     hip_ready = true;
@@ -601,6 +609,7 @@ struct zm_cold_lane {
       (void)hipStreamDestroy(side);
       (void)hipEventDestroy(forked);
       (void)hipEventDestroy(uploaded);
+      (void)hipEventDestroy(added);
       (void)hipFree(d_cold);
       (void)hipHostFree(h_x);
       (void)hipHostFree(h_out);
@@ -681,6 +690,7 @@ int zm_cold_lane_fork(zm_cold_lane *L, const float *x, const int32_t *ids, const
   {
     std::lock_guard<std::mutex> lk(L->mu);
     L->pending_S = S;
+    L->forked_S = S;
   }
   L->cv.notify_all();
   return 0;
@@ -698,14 +708,20 @@ int zm_cold_lane_merge(zm_cold_lane *L, float *out, int S, void *stream) {
   }
   L->stats.merge_ns = now_ns();
   if (st_code) return fail("zm_cold_lane_merge: the fork's copies failed");
+  if (S != L->forked_S) return fail("zm_cold_lane_merge: S differs from the forked call's");
   hipStream_t st = (hipStream_t)stream;
-  // upload on the lane's side stream, then the caller's stream waits and adds
+  // upload on the lane's side stream, then the caller's stream waits and adds;
+  // the upload first waits for the previous merge's add, which read d_cold on
+  // the caller's stream of that call
   const size_t n = (size_t)S * L->d.H;
+  if (L->merged_once) HIP_OK(hipStreamWaitEvent(L->side, L->added, 0));
   HIP_OK(hipMemcpyAsync(L->d_cold, L->h_out, n * sizeof(float), hipMemcpyHostToDevice, L->side));
   HIP_OK(hipEventRecord(L->uploaded, L->side));
   HIP_OK(hipStreamWaitEvent(st, L->uploaded, 0));
   hipLaunchKernelGGL(k_lane_add, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, out, L->d_cold, (int)n);
   HIP_OK(hipGetLastError());
+  HIP_OK(hipEventRecord(L->added, st));
+  L->merged_once = true;
   return 0;
 }
 

@@ -13,6 +13,8 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <map>
+#include <mutex>
 
 #include "ggml.h"
 #include "zeromoe.h"
@@ -36,21 +38,46 @@ zm_tensor as_zm(const ggml_tensor *t) {
 
 bool zeromoe_hip_hook(const ggml_tensor *w, const ggml_tensor *x, const ggml_tensor *ids, ggml_tensor *y,
                       void *stream, bool execute) {
-  if (!w || !x || !ids || !y) return false;  // MUL_MAT_ID only; plain MUL_MAT stays with ggml
-  const zm_tensor zw = as_zm(w), zx = as_zm(x), zi = as_zm(ids);
+  if (!w || !x || !y) return false;
+  const zm_tensor zw = as_zm(w), zx = as_zm(x);
   zm_tensor zy = as_zm(y);
+  if (!ids) {
+    // plain MUL_MAT (dense and shared FFNs): the reference hook's ids == NULL
+    // branches, FP32 activations (kquant_matmul.cu:740-755); no workspace
+    return zm_mul_mat_id_f32(&zw, &zx, nullptr, &zy, stream, execute ? 1 : 0) == 1;
+  }
+  const zm_tensor zi = as_zm(ids);
   return zm_mul_mat_id(&zw, &zx, &zi, &zy, stream, execute ? 1 : 0) == 1;
 }
+
+// workspaces bound by zeromoe_bind_hook_workspace, one per stream
+std::mutex g_ws_mu;
+std::map<void *, void *> g_ws;
 
 }  // namespace
 
 // Set-up, once per stream ggml executes on (the backend context's stream),
 // before the first graph compute: one device buffer of `bytes` bound as the
-// hook's workspace.  The hook itself never allocates.
+// hook's workspace.  The hook itself never allocates.  Binding a stream again
+// (a larger graph) replaces its buffer; the old one is freed once the stream
+// has drained.  Until some workspace is bound on the device, the hook's
+// capability query declines every MUL_MAT_ID shape (it answers for the
+// smallest bound workspace), so bind before ggml's supports_op pass.
 extern "C" bool zeromoe_bind_hook_workspace(void *stream, size_t bytes) {
   void *p = nullptr;
   if (hipMalloc(&p, bytes) != hipSuccess) return false;
-  return zm_mul_mat_id_set_workspace(stream, p, bytes) == 0;
+  if (zm_mul_mat_id_set_workspace(stream, p, bytes) != 0) {
+    (void)hipFree(p);
+    return false;
+  }
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  void *&slot = g_ws[stream];
+  if (slot) {
+    (void)hipStreamSynchronize((hipStream_t)stream);
+    (void)hipFree(slot);
+  }
+  slot = p;
+  return true;
 }
 
 // Workspace bytes one MUL_MAT_ID node needs (the largest over a graph's nodes
@@ -73,7 +100,8 @@ extern "C" uint64_t zeromoe_f32_quant_graph_launches() { return zm_mul_mat_id_la
 extern "C" int ggml_cpu_mul_mat_id_negative_skip(void) { return zm_mul_mat_id_negative_skip(); }
 extern "C" int ggml_cuda_mul_mat_id_negative_skip_batched(void) { return zm_mul_mat_id_negative_skip_batched(); }
 
-// For tests of this adapter: the hook as registered.
+// For tests of this adapter: the hook as registered (MUL_MAT_ID, and plain
+// MUL_MAT with ids == NULL).
 extern "C" bool zeromoe_hook_for_test(const ggml_tensor *w, const ggml_tensor *x, const ggml_tensor *ids,
                                       ggml_tensor *y, void *stream, bool execute) {
   return zeromoe_hip_hook(w, x, ids, y, stream, execute);

@@ -157,8 +157,16 @@ def bind_mmid_workspace(stream: int, need: int, device) -> None:
     _MMID_WS[(device.index, stream)] = buf
 
 
-def mul_mat_id_supported(W, wtype, n_in, x, ids, out) -> bool:
+def mul_mat_id_supported(W, wtype, n_in, x, ids, out, stream=None) -> bool:
+    """The hook's capability query (execute = 0).  The library answers it for
+    the smallest workspace bound on the device, so the shape's workspace is
+    bound to `stream` first (as mul_mat_id would); a shape the library
+    declines has a workspace size of 0 and is answered False."""
     tw, tx, ti, ty = _tensor(wtype, W, n_in), _tensor(0, x, None), _tensor(26, ids, None), _tensor(0, out, None)
+    need = lib().zm_mul_mat_id_workspace_size(C.byref(tw), C.byref(tx), C.byref(ti), C.byref(ty))
+    if need == 0:
+        return False
+    bind_mmid_workspace(_stream(stream), need, x.device)
     return lib().zm_mul_mat_id(C.byref(tw), C.byref(tx), C.byref(ti), C.byref(ty), None, 0) == 1
 
 
