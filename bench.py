@@ -355,18 +355,19 @@ def _read_counters(d):
     return out
 
 
-def pmc_summary(fetch_dir, write_dir, out_path, command):
-    """Per-launch HBM traffic of the decode kernel from FETCH_SIZE / WRITE_SIZE
-    (KiB per dispatch), each scaled by what the counter reads for the copy probe."""
-    lines = [f"# HBM traffic per launch: decode kernel, c2 (bench.py --profile c2)", f"# command: {command}"]
+def pmc_summary(fetch_dir, write_dir, out_path, command, label="c2", pattern="k_moe_decode"):
+    """Per-launch HBM traffic of one kernel (name containing `pattern`) from
+    FETCH_SIZE / WRITE_SIZE (KiB per dispatch), each scaled by what the counter
+    reads for the copy probe."""
+    lines = [f"# HBM traffic per launch: {pattern}, {label} (bench.py --profile {label})", f"# command: {command}"]
     tot = 0.0
     for ctr, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
         vals = _read_counters(d)
-        dec = [v for (k, c), vs in vals.items() if c == ctr and "k_moe_decode" in k for v in vs]
+        dec = [v for (k, c), vs in vals.items() if c == ctr and pattern in k for v in vs]
         cp = [v for (k, c), vs in vals.items() if c == ctr and "copy" in k.lower() for v in vs]
         cp = [v for v in cp if v >= 0.9 * max(cp, default=0.0)]  # the 1 GiB probe, not smaller copies
         if not dec or not cp:
-            raise SystemExit(f"pmc_summary: no {ctr} samples for the decode kernel or the copy probe in {d}")
+            raise SystemExit(f"pmc_summary: no {ctr} samples for {pattern} or the copy probe in {d}")
         probe = sum(cp) / len(cp)
         factor = (COPY_PROBE_BYTES / 1024) / probe
         kib = sum(dec) / len(dec)
@@ -381,11 +382,12 @@ def pmc_summary(fetch_dir, write_dir, out_path, command):
     print("\n".join(lines))
 
 
-def mfma_summary(d, out_path, command, pattern="k_mmq", peak_ops=5.0e15):
-    """int8 MFMA utilisation of the prefill kernels from one rocprofv3 --pmc run:
-    per kernel, the mean per dispatch of each counter, the int8 MFMA ops
-    (SQ_INSTS_VALU_MFMA_MOPS_I8 counts units of 512 ops) and their rate over
-    the dispatch's duration against the dense int8 peak."""
+def mfma_summary(d, out_path, command, pattern="k_mmq", label="c3", peak_ops=5.0e15):
+    """Counters of the kernels whose name contains `pattern` from one rocprofv3
+    --pmc run: per kernel, the mean per dispatch of each counter and, when
+    SQ_INSTS_VALU_MFMA_MOPS_I8 was collected, the int8 MFMA ops (it counts
+    units of 512 ops) and their rate over the dispatch's duration against the
+    dense int8 peak."""
     import csv
     import glob
     import re
@@ -402,7 +404,8 @@ def mfma_summary(d, out_path, command, pattern="k_mmq", peak_ops=5.0e15):
                 e["_dur"][r["Dispatch_Id"]] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9
     if not per:
         raise SystemExit(f"mfma_summary: no {pattern} dispatches under {d}")
-    lines = ["# int8 MFMA utilisation of the prefill kernels (c3, bench.py --profile c3)", f"# command: {command}"]
+    lines = [f"# counters per dispatch of the {pattern} kernels ({label}, bench.py --profile {label})",
+             f"# command: {command}"]
     for name, e in sorted(per.items()):
         durs = list(e.pop("_dur").values())
         dur = sum(durs) / len(durs)
@@ -471,15 +474,17 @@ def main():
     ap.add_argument("--mfma-summary", nargs=2, metavar=("DIR", "OUT"),
                     help="int8 MFMA utilisation of the prefill kernels from a rocprofv3 --pmc run of --profile c3")
     ap.add_argument("--command", default="", help="command line recorded in a summary")
+    ap.add_argument("--label", default="", help="configuration named in a --pmc-summary / --mfma-summary")
+    ap.add_argument("--pattern", default="", help="kernel-name pattern of a --pmc-summary / --mfma-summary")
     args = ap.parse_args()
     if args.pmc_summary:
-        pmc_summary(*args.pmc_summary, args.command)
+        pmc_summary(*args.pmc_summary, args.command, args.label or "c2", args.pattern or "k_moe_decode")
         return
     if args.stats_summary:
         stats_summary(*args.stats_summary, args.command)
         return
     if args.mfma_summary:
-        mfma_summary(*args.mfma_summary, args.command)
+        mfma_summary(*args.mfma_summary, args.command, args.pattern or "k_mmq", args.label or "c3")
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the expert axis would "
