@@ -424,8 +424,8 @@ __device__ __forceinline__ void unit_ints(const Unit<T> (&w)[NW], int part, cons
           const uint32_t g1 = g3[(iw >> (16 * (l & 1))) & 0xffu], g2 = g3[(iw >> (16 * (l & 1) + 8)) & 0xffu];
           const uint64_t m = lds_signs[(aux >> (7 * l)) & 127u];
           const uint32_t mlo = (uint32_t)m, mhi = (uint32_t)(m >> 32);
-          s = dot4((g1 ^ mlo) + (mlo & 0x01010101u), xs[2 * l], s);
-          s = dot4((g2 ^ mhi) + (mhi & 0x01010101u), xs[2 * l + 1], s);
+          s = dot4(sign_bytes(g1, mlo), xs[2 * l], s);
+          s = dot4(sign_bytes(g2, mhi), xs[2 * l + 1], s);
         }
         isum = mad24(2 * (int)(aux >> 28) + 1, s, isum);
       }
@@ -511,8 +511,8 @@ __device__ __forceinline__ void unit_ints(const Unit<T> (&w)[NW], int part, cons
           const uint32_t glo = (uint32_t)g, ghi = (uint32_t)(g >> 32);
           const uint32_t mlo = (uint32_t)m, mhi = (uint32_t)(m >> 32);
           // conditional byte negate: (g ^ m) + (m & 1) per byte (no carries: 8 <= g <= 255)
-          s = dot4((glo ^ mlo) + (mlo & 0x01010101u), xs[2 * l], s);
-          s = dot4((ghi ^ mhi) + (mhi & 0x01010101u), xs[2 * l + 1], s);
+          s = dot4(sign_bytes(glo, mlo), xs[2 * l], s);
+          s = dot4(sign_bytes(ghi, mhi), xs[2 * l + 1], s);
         }
         isum[n] = mad24(2 * (int)(aux1 >> 28) + 1, s, isum[n]);
       }

@@ -84,6 +84,15 @@ __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
+// bytes of g negated where the byte of the sign mask m is 0xff: (g ^ m) +
+// (m & 1) per byte, carry-free for bytes 1..255, as one v_xad_u32 (the
+// compiler emits xor + add) after the and
+__device__ __forceinline__ uint32_t sign_bytes(uint32_t g, uint32_t m) {
+  uint32_t r;
+  asm("v_xad_u32 %0, %1, %2, %3" : "=v"(r) : "v"(g), "v"(m), "v"(m & 0x01010101u));
+  return r;
+}
+
 // byte k (0..11) of three little-endian dwords
 __device__ __forceinline__ uint32_t byte_of3(uint32_t s0, uint32_t s1, uint32_t s2, int k) {
   const uint32_t w = k < 4 ? s0 : (k < 8 ? s1 : s2);
@@ -577,8 +586,8 @@ __device__ __forceinline__ QInt quarter_int(const WSlice &w, int q, const Q8Slic
         const uint64_t m = lds_signs[(aux >> (7 * l)) & 127u];
         const uint32_t mlo = (uint32_t)m, mhi = (uint32_t)(m >> 32);
         const int qi = 2 * (4 * sb + l);  // dword index inside the 64 activations
-        dsum = dot4((g1 ^ mlo) + (mlo & 0x01010101u), u4_get(a.q[qi >> 2], qi & 3), dsum);
-        dsum = dot4((g2 ^ mhi) + (mhi & 0x01010101u), u4_get(a.q[(qi + 1) >> 2], (qi + 1) & 3), dsum);
+        dsum = dot4(sign_bytes(g1, mlo), u4_get(a.q[qi >> 2], qi & 3), dsum);
+        dsum = dot4(sign_bytes(g2, mhi), u4_get(a.q[(qi + 1) >> 2], (qi + 1) & 3), dsum);
       }
       r.isum += (2 * (int)(aux >> 28) + 1) * dsum;
     }
@@ -627,8 +636,8 @@ __device__ __forceinline__ QInt quarter_int(const WSlice &w, int q, const Q8Slic
         const uint32_t glo = (uint32_t)g, ghi = (uint32_t)(g >> 32);
         const uint32_t mlo = (uint32_t)m, mhi = (uint32_t)(m >> 32);
         // conditional byte negate: (g ^ m) + (m & 1) per byte (no carries: 8 <= g <= 255)
-        const uint32_t vlo = (glo ^ mlo) + (mlo & 0x01010101u);
-        const uint32_t vhi = (ghi ^ mhi) + (mhi & 0x01010101u);
+        const uint32_t vlo = sign_bytes(glo, mlo);
+        const uint32_t vhi = sign_bytes(ghi, mhi);
         const int qi = 2 * (4 * sb + l);  // dword index inside the 64 activations
         dsum = dot4(vlo, u4_get(a.q[qi >> 2], qi & 3), dsum);
         dsum = dot4(vhi, u4_get(a.q[(qi + 1) >> 2], (qi + 1) & 3), dsum);

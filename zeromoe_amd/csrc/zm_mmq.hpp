@@ -525,7 +525,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_
           }
           const uint64_t mm = s_signs[(aux >> (7 * g)) & 127u];
           const uint32_t mlo = (uint32_t)mm, mhi = (uint32_t)(mm >> 32);
-          const uint32_t v0 = (glo ^ mlo) + (mlo & 0x01010101u), v1 = (ghi ^ mhi) + (mhi & 0x01010101u);
+          const uint32_t v0 = sign_bytes(glo, mlo), v1 = sign_bytes(ghi, mhi);
           B[m][sb] = (long)(((uint64_t)v1 << 32) | v0);
           S[m][sb] = 2 * (int)(aux >> 28) + 1;
         }
