@@ -1152,7 +1152,10 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
     }
     ys = w.y_s;
   }
-  hipLaunchKernelGGL(k_combine, dim3((H + 255) / 256, S), dim3(256), 0, st, w.y, wts, ys, H, K, out);
+  if ((uintptr_t)out & 15)
+    hipLaunchKernelGGL(k_combine1, dim3((H + 255) / 256, S), dim3(256), 0, st, w.y, wts, ys, H, K, out);
+  else
+    hipLaunchKernelGGL(k_combine, dim3((H + 1023) / 1024, S), dim3(256), 0, st, w.y, wts, ys, H, K, out);
   HIP_OK(hipGetLastError());
   return 0;
 }

@@ -488,6 +488,11 @@ static __global__ __launch_bounds__(256) void k_router(RouterArgs a, int S) {
 // per-wave counts, so the order is exactly the sequential one.
 constexpr int BUCKET_MAX_E = 512;
 
+// Every thread reads its pairs' expert ids once (pair c * 1024 + tid for chunk
+// c, up to BUCKET_CH chunks held in registers; larger inputs re-read ids per
+// chunk), so the count, scan and ranking passes wait for memory only once.
+constexpr int BUCKET_CH = 8;
+
 static __global__ __launch_bounds__(1024) void k_bucket(const int32_t *__restrict__ ids, int n_pairs, int E,
                                                  int32_t *__restrict__ counts, int32_t *__restrict__ offs,
                                                  int32_t *__restrict__ pairs, int32_t *__restrict__ active,
@@ -496,11 +501,27 @@ static __global__ __launch_bounds__(1024) void k_bucket(const int32_t *__restric
   __shared__ int base[BUCKET_MAX_E];
   __shared__ int wcnt[16][BUCKET_MAX_E];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int nch = (n_pairs + 1023) / 1024;
+  int eid[BUCKET_CH];
+#pragma unroll
+  for (int c = 0; c < BUCKET_CH; ++c) {
+    const int i = c * 1024 + tid;
+    const int e = i < n_pairs ? ids[i] : -1;
+    eid[c] = e >= 0 && e < E ? e : -1;
+  }
   for (int e = tid; e < E; e += 1024) cnt[e] = 0;
   __syncthreads();
-  for (int i = tid; i < n_pairs; i += 1024) {
-    const int e = ids[i];
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  for (int c = 0; c < nch; ++c) {
+    const int i = c * 1024 + tid;
+    int e = -1;
+    if (c < BUCKET_CH) {
+#pragma unroll
+      for (int q = 0; q < BUCKET_CH; ++q) e = q == c ? eid[q] : e;
+    } else if (i < n_pairs) {
+      e = ids[i];
+      e = e >= 0 && e < E ? e : -1;
+    }
+    if (e >= 0) atomicAdd(&cnt[e], 1);
   }
   __syncthreads();
   if (w == 0) {
@@ -541,24 +562,31 @@ static __global__ __launch_bounds__(1024) void k_bucket(const int32_t *__restric
       *n_active = inz;
     }
   }
-  __syncthreads();
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int c0 = 0; c0 < n_pairs; c0 += 1024) {
+  const int nbits = E > 1 ? 32 - __builtin_clz((unsigned)(E - 1)) : 1;  // bits of an expert id
+  for (int c = 0; c < nch; ++c) {
     for (int e = lane; e < E; e += 64) wcnt[w][e] = 0;
-    const int i = c0 + tid;
-    const int e = i < n_pairs ? ids[i] : -1;
-    const bool valid = e >= 0 && e < E;
-    __syncthreads();
-    uint64_t remaining = __ballot(valid);
-    int rank = 0;
-    while (remaining) {
-      const int leader = __builtin_ctzll(remaining);
-      const int v = __builtin_amdgcn_readlane(e, leader);
-      const uint64_t m = __ballot(valid && e == v);
-      if (valid && e == v) rank = __builtin_popcountll(m & lt_mask);
-      if (lane == leader) wcnt[w][v] = __builtin_popcountll(m);
-      remaining &= ~m;
+    const int i = c * 1024 + tid;
+    int e = -1;
+    if (c < BUCKET_CH) {
+#pragma unroll
+      for (int q = 0; q < BUCKET_CH; ++q) e = q == c ? eid[q] : e;
+    } else if (i < n_pairs) {
+      e = ids[i];
+      e = e >= 0 && e < E ? e : -1;
     }
+    const bool valid = e >= 0;
+    __syncthreads();  // (first chunk: also the scan's base[] before it is read)
+    // rank among the earlier lanes of this wave with the same expert: the
+    // lanes holding the same id are the intersection, over the id's bits, of
+    // one ballot per bit (or its complement), so no loop over distinct ids
+    uint64_t m = __ballot(valid);
+    for (int j = 0; j < nbits; ++j) {
+      const uint64_t bj = __ballot(valid && ((e >> j) & 1));
+      m &= ((e >> j) & 1) ? bj : ~bj;
+    }
+    const int rank = __builtin_popcountll(m & lt_mask);
+    if (valid && rank == 0) wcnt[w][e] = __builtin_popcountll(m);
     __syncthreads();
     if (valid) {
       int r = base[e] + rank;
@@ -571,7 +599,7 @@ static __global__ __launch_bounds__(1024) void k_bucket(const int32_t *__restric
       for (int w2 = 0; w2 < 16; ++w2) add += wcnt[w2][e2];
       base[e2] += add;
     }
-    __syncthreads();
+    __syncthreads();  // wcnt is cleared, and base read, by the next chunk
   }
 }
 
@@ -697,9 +725,10 @@ static __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
 // ============================================================ combine
 // ggml_mul(down, weights) then sum_topk (moe_routed_ggml.hpp:198-214):
 // out = ((w0*y0 + w1*y1) + w2*y2) + ...   (+ shared, moe_block.hpp:201-202)
-static __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, const float *__restrict__ w,
-                                                 const float *__restrict__ shared, int H, int K,
-                                                 float *__restrict__ out) {
+// one output per thread: for an output buffer that is not 16-byte aligned
+static __global__ __launch_bounds__(256) void k_combine1(const float *__restrict__ y, const float *__restrict__ w,
+                                                  const float *__restrict__ shared, int H, int K,
+                                                  float *__restrict__ out) {
   const int s = blockIdx.y;
   const int h = blockIdx.x * 256 + threadIdx.x;
   if (h >= H) return;
@@ -708,6 +737,53 @@ static __global__ __launch_bounds__(256) void k_combine(const float *__restrict_
   for (int k = 1; k < K; ++k) acc = acc + w[(size_t)s * K + k] * ys[(size_t)k * H + h];
   if (shared) acc = acc + shared[(size_t)s * H + h];
   out[(size_t)s * H + h] = acc;
+}
+
+static __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, const float *__restrict__ w,
+                                                 const float *__restrict__ shared, int H, int K,
+                                                 float *__restrict__ out) {
+  // four consecutive outputs per thread (H is a multiple of 256): float4 loads
+  // of every route's row, the same k-ascending sum per element
+  const int s = blockIdx.y;
+  const int h = 4 * (blockIdx.x * 256 + threadIdx.x);
+  if (h >= H) return;
+  const float *ys = y + (size_t)s * K * H;
+  const float *ws = w + (size_t)s * K;
+  float4 yk[8];
+  const int K0 = K < 8 ? K : 8;
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (k < K0) yk[k] = *reinterpret_cast<const float4 *>(ys + (size_t)k * H + h);
+  float4 acc;
+  acc.x = ws[0] * yk[0].x;
+  acc.y = ws[0] * yk[0].y;
+  acc.z = ws[0] * yk[0].z;
+  acc.w = ws[0] * yk[0].w;
+#pragma unroll
+  for (int k = 1; k < 8; ++k)
+    if (k < K0) {
+      const float wk = ws[k];
+      acc.x = acc.x + wk * yk[k].x;
+      acc.y = acc.y + wk * yk[k].y;
+      acc.z = acc.z + wk * yk[k].z;
+      acc.w = acc.w + wk * yk[k].w;
+    }
+  for (int k = 8; k < K; ++k) {
+    const float wk = ws[k];
+    const float4 v = *reinterpret_cast<const float4 *>(ys + (size_t)k * H + h);
+    acc.x = acc.x + wk * v.x;
+    acc.y = acc.y + wk * v.y;
+    acc.z = acc.z + wk * v.z;
+    acc.w = acc.w + wk * v.w;
+  }
+  if (shared) {
+    const float4 v = *reinterpret_cast<const float4 *>(shared + (size_t)s * H + h);
+    acc.x = acc.x + v.x;
+    acc.y = acc.y + v.y;
+    acc.z = acc.z + v.z;
+    acc.w = acc.w + v.w;
+  }
+  *reinterpret_cast<float4 *>(out + (size_t)s * H + h) = acc;
 }
 
 // zero (negative id) or NaN (id >= n_experts) rows of routes the GEMV skips
