@@ -54,6 +54,7 @@ struct DeviceState {
   uint8_t *scratch = nullptr; // this device's address of `scratch`
   uint64_t *trace = nullptr;  // decode-kernel phase timestamps (ZEROMOE_TRACE=1)
   size_t trace_n = 0;
+  int n_cu = 0;               // compute units
 };
 DeviceState g_dev[kMaxDevices];
 std::mutex g_mu;
@@ -110,6 +111,7 @@ int device_state(DeviceState **out) {
   std::lock_guard<std::mutex> lk(g_mu);
   DeviceState &d = g_dev[dev];
   if (!d.ready) {
+    HIP_OK(hipDeviceGetAttribute(&d.n_cu, hipDeviceAttributeMultiprocessorCount, dev));
     uint64_t grid[256], signs[128];
     builtin_grid(grid);
     for (int i = 0; i < 128; ++i) {
@@ -262,7 +264,8 @@ bool mmq_applies(int type, double avg_pairs) {
 // shared by 64 pairs); Q2_K (small buckets of resident slots) and dense
 // shared-expert rows 2
 int mmq_tt(int type, bool dense) { return type != T_Q2_K && !dense ? 4 : 2; }
-int launch_mmq(int type, bool gateup, const GemvArgs &a, int max_items, double avg_pairs, int tt, hipStream_t st);
+int launch_mmq(int type, bool gateup, const GemvArgs &a, int max_items, double avg_pairs, int tt, hipStream_t st,
+               int nw = 4);
 template <int T, int TT, int NW = 4>
 void launch_mmq_t(bool gateup, dim3 grid, const GemvArgs &a, hipStream_t st) {
   grid.x = (unsigned)((a.nrows + 16 * NW - 1) / (16 * NW));  // NW waves of 16 weight rows per workgroup
@@ -271,8 +274,11 @@ void launch_mmq_t(bool gateup, dim3 grid, const GemvArgs &a, hipStream_t st) {
   else
     hipLaunchKernelGGL((k_mmq<T, false, TT, NW>), grid, dim3(64 * NW), 0, st, a);
 }
-// tt: 16-token tiles per work item (the tiling the item list was cut with)
-int launch_mmq(int type, bool gateup, const GemvArgs &a, int max_items, double avg_pairs, int tt, hipStream_t st) {
+// tt: 16-token tiles per work item (the tiling the item list was cut with);
+// nw: waves (16 weight rows each) per workgroup -- 1 for a Q4_K matrix whose
+// 64-row tiles alone would leave most CUs idle (a dense shared expert)
+int launch_mmq(int type, bool gateup, const GemvArgs &a, int max_items, double avg_pairs, int tt, hipStream_t st,
+               int nw) {
   if (!mmq_applies(type, avg_pairs)) return 1;
   if ((size_t)a.nrows * a.w_rstride >= (1ull << 31) || max_items <= 0) return 1;
   const dim3 grid((unsigned)((a.nrows + 63) / 64), (unsigned)max_items);
@@ -282,6 +288,7 @@ int launch_mmq(int type, bool gateup, const GemvArgs &a, int max_items, double a
       else launch_mmq_t<T_Q4_K, 8, 8>(gateup, grid, a, st);
     }
     else if (tt == 4) launch_mmq_t<T_Q4_K, 4>(gateup, grid, a, st);
+    else if (nw == 1) launch_mmq_t<T_Q4_K, 2, 1>(gateup, grid, a, st);
     else launch_mmq_t<T_Q4_K, 2>(gateup, grid, a, st);
   } else if (type == T_Q5_K) {
     if (tt == 4) launch_mmq_t<T_Q5_K, 4>(gateup, grid, a, st);
@@ -1131,7 +1138,11 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
     c.signs = d->signs;
     const int nps = S >= 4 ? 4 : (S >= 2 ? 2 : 1);
     {
-      const int rc = launch_mmq(L->type_shared, true, c, (S + 31) / 32, (double)S, 2, st);
+      // 64-row tiles of the shared expert's F rows times (S / 32) items: a
+      // one-wave workgroup per 16 rows when that leaves CUs idle
+      const int cus = d->n_cu > 0 ? d->n_cu : 256;
+      const int nw = (long)((Fs + 63) / 64) * ((S + 31) / 32) < cus ? 1 : 4;
+      const int rc = launch_mmq(L->type_shared, true, c, (S + 31) / 32, (double)S, 2, st, nw);
       if (rc < 0 || (rc > 0 && launch_gemv(L->type_shared, true, nps, c, 1, st))) return -1;
     }
     if (launch_quant(w.act_s, (size_t)Fs, nbS, S, w.aq_s, q8_row_bytes(nbS), 1, st)) return -1;
