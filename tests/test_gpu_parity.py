@@ -649,15 +649,19 @@ def test_fused_decode_expired_wait_is_loud_and_recovers(monkeypatch):
     assert_close_layer(out3.cpu().numpy(), ref)
 
 
-@pytest.mark.parametrize("case", ["c2", "c3_small"])
+@pytest.mark.parametrize("case", ["c2", "c3_small", "c5_S64_small"])
 def test_hip_graph_replay_matches_eager(case):
     """The layer recorded into a HIP graph and replayed several times, with eager
-    work in between, gives the eager result bit for bit on every replay."""
-    c = CONFIGS["c2"] if case == "c2" else reduced(CONFIGS["c3"], S=32, H=1024, F=512)
+    work in between, gives the eager result bit for bit on every replay.  c5 at
+    S=64 runs its dense shared expert on the library's side stream (forked
+    after x is quantized, joined before the combine): the fork and join are
+    recorded into the graph too."""
+    c = {"c2": CONFIGS["c2"], "c3_small": reduced(CONFIGS["c3"], S=32, H=1024, F=512),
+         "c5_S64_small": reduced(CONFIGS["c5"], S=64, H=2048, F=1024, F_shared=1024)}[case]
     b = Built(c, seed=31)
     L = b.layer()
     x = torch.from_numpy(b.x).cuda()
-    lg = torch.from_numpy(b.logits).cuda()
+    lg = None if c.router_gemv else torch.from_numpy(b.logits).cuda()
     out = torch.empty((c.S, c.H), device="cuda")
     ids = torch.empty((c.S, c.K), dtype=torch.int32, device="cuda")
     w = torch.empty((c.S, c.K), device="cuda")

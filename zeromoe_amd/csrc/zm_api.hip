@@ -55,6 +55,13 @@ struct DeviceState {
   uint64_t *trace = nullptr;  // decode-kernel phase timestamps (ZEROMOE_TRACE=1)
   size_t trace_n = 0;
   int n_cu = 0;               // compute units
+  // a dense shared expert runs beside the routed kernels of a multi-kernel
+  // layer: forked from the caller's stream after x is quantized, joined
+  // before the combine (default priority; the fork/join records into a HIP
+  // graph like any other stream work)
+  hipStream_t side = nullptr;
+  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+  std::mutex *fork_mu = nullptr;  // the events are per device: one fork at a time
 };
 DeviceState g_dev[kMaxDevices];
 std::mutex g_mu;
@@ -112,6 +119,10 @@ int device_state(DeviceState **out) {
   DeviceState &d = g_dev[dev];
   if (!d.ready) {
     HIP_OK(hipDeviceGetAttribute(&d.n_cu, hipDeviceAttributeMultiprocessorCount, dev));
+    HIP_OK(hipStreamCreateWithFlags(&d.side, hipStreamNonBlocking));
+    HIP_OK(hipEventCreateWithFlags(&d.ev_fork, hipEventDisableTiming));
+    HIP_OK(hipEventCreateWithFlags(&d.ev_join, hipEventDisableTiming));
+    d.fork_mu = new std::mutex();
     uint64_t grid[256], signs[128];
     builtin_grid(grid);
     for (int i = 0; i < 128; ++i) {
@@ -1030,6 +1041,64 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
     return -1;
   // activations -> Q8_K, buckets
   if (launch_quant(x, (size_t)H, nbH, S, w.xq, q8_row_bytes(nbH), 1, st)) return -1;
+  // shared expert (dense over all tokens) on the side stream: it needs only
+  // the Q8_K rows of x, and its gate/up, act quantization and down overlap
+  // the router-dependent kernels; the combine waits for it
+  auto launch_shared = [&](hipStream_t ss) -> int {
+    const int Fs = L->F_shared, nbS = Fs / QK;
+    GemvArgs c{};
+    c.w0 = (const uint8_t *)L->ws_gate;
+    c.w1 = (const uint8_t *)L->ws_up;
+    c.w_rstride = row_bytes(L->type_shared, H);
+    c.w_estride = 0;
+    c.nrows = Fs;
+    c.nb = nbH;
+    c.xq = w.xq;
+    c.xq_rstride = q8_row_bytes(nbH);
+    c.xq_bytes = (uint32_t)((size_t)S * q8_row_bytes(nbH));
+    c.ne11 = 1;
+    c.K = 1;
+    c.dense_S = S;
+    c.out = w.act_s;
+    c.out_s = Fs;
+    c.out_k = 0;
+    c.grid = d->grid;
+    c.signs = d->signs;
+    const int nps = S >= 4 ? 4 : (S >= 2 ? 2 : 1);
+    {
+      // 64-row tiles of the shared expert's F rows times (S / 32) items: a
+      // one-wave workgroup per 16 rows when that leaves CUs idle
+      const int cus = d->n_cu > 0 ? d->n_cu : 256;
+      const int nw = (long)((Fs + 63) / 64) * ((S + 31) / 32) < cus ? 1 : 4;
+      const int rc = launch_mmq(L->type_shared, true, c, (S + 31) / 32, (double)S, 2, ss, nw);
+      if (rc < 0 || (rc > 0 && launch_gemv(L->type_shared, true, nps, c, 1, ss))) return -1;
+    }
+    if (launch_quant(w.act_s, (size_t)Fs, nbS, S, w.aq_s, q8_row_bytes(nbS), 1, ss)) return -1;
+    GemvArgs e2 = c;
+    e2.w0 = (const uint8_t *)L->ws_down;
+    e2.w1 = nullptr;
+    e2.w_rstride = row_bytes(L->type_shared, Fs);
+    e2.nrows = H;
+    e2.nb = nbS;
+    e2.xq = w.aq_s;
+    e2.xq_rstride = q8_row_bytes(nbS);
+    e2.xq_bytes = (uint32_t)((size_t)S * q8_row_bytes(nbS));
+    e2.out = w.y_s;
+    e2.out_s = H;
+    {
+      const int rc = launch_mmq(L->type_shared, false, e2, (S + 31) / 32, (double)S, 2, ss);
+      if (rc < 0 || (rc > 0 && launch_gemv(L->type_shared, false, nps, e2, 1, ss))) return -1;
+    }
+    return 0;
+  };
+  std::unique_lock<std::mutex> fork_lk;
+  if (L->F_shared > 0) {
+    fork_lk = std::unique_lock<std::mutex>(*d->fork_mu);
+    HIP_OK(hipEventRecord(d->ev_fork, st));
+    HIP_OK(hipStreamWaitEvent(d->side, d->ev_fork, 0));
+    if (launch_shared(d->side)) return -1;
+    HIP_OK(hipEventRecord(d->ev_join, d->side));
+  }
   hipLaunchKernelGGL(k_bucket, dim3(1), dim3(1024), 0, st, ids, S * K, NS, w.counts, w.offs, w.pairs, w.active,
                      w.n_active);
   // gate/up + SwiGLU
@@ -1114,55 +1183,8 @@ int zm_moe_forward(const zm_moe_layer *L, const float *x, const float *logits, i
     const int rc = launch_mmq(L->type_down, false, b, max_items_for(tt_d), avg_pairs, tt_d, st);
     if (rc < 0 || (rc > 0 && launch_gemv(L->type_down, false, np, b, groups, st))) return -1;
   }
-  // shared expert (dense over all tokens)
-  const float *ys = nullptr;
-  if (L->F_shared > 0) {
-    const int Fs = L->F_shared, nbS = Fs / QK;
-    GemvArgs c{};
-    c.w0 = (const uint8_t *)L->ws_gate;
-    c.w1 = (const uint8_t *)L->ws_up;
-    c.w_rstride = row_bytes(L->type_shared, H);
-    c.w_estride = 0;
-    c.nrows = Fs;
-    c.nb = nbH;
-    c.xq = w.xq;
-    c.xq_rstride = q8_row_bytes(nbH);
-    c.xq_bytes = (uint32_t)((size_t)S * q8_row_bytes(nbH));
-    c.ne11 = 1;
-    c.K = 1;
-    c.dense_S = S;
-    c.out = w.act_s;
-    c.out_s = Fs;
-    c.out_k = 0;
-    c.grid = d->grid;
-    c.signs = d->signs;
-    const int nps = S >= 4 ? 4 : (S >= 2 ? 2 : 1);
-    {
-      // 64-row tiles of the shared expert's F rows times (S / 32) items: a
-      // one-wave workgroup per 16 rows when that leaves CUs idle
-      const int cus = d->n_cu > 0 ? d->n_cu : 256;
-      const int nw = (long)((Fs + 63) / 64) * ((S + 31) / 32) < cus ? 1 : 4;
-      const int rc = launch_mmq(L->type_shared, true, c, (S + 31) / 32, (double)S, 2, st, nw);
-      if (rc < 0 || (rc > 0 && launch_gemv(L->type_shared, true, nps, c, 1, st))) return -1;
-    }
-    if (launch_quant(w.act_s, (size_t)Fs, nbS, S, w.aq_s, q8_row_bytes(nbS), 1, st)) return -1;
-    GemvArgs e2 = c;
-    e2.w0 = (const uint8_t *)L->ws_down;
-    e2.w1 = nullptr;
-    e2.w_rstride = row_bytes(L->type_shared, Fs);
-    e2.nrows = H;
-    e2.nb = nbS;
-    e2.xq = w.aq_s;
-    e2.xq_rstride = q8_row_bytes(nbS);
-    e2.xq_bytes = (uint32_t)((size_t)S * q8_row_bytes(nbS));
-    e2.out = w.y_s;
-    e2.out_s = H;
-    {
-      const int rc = launch_mmq(L->type_shared, false, e2, (S + 31) / 32, (double)S, 2, st);
-      if (rc < 0 || (rc > 0 && launch_gemv(L->type_shared, false, nps, e2, 1, st))) return -1;
-    }
-    ys = w.y_s;
-  }
+  if (L->F_shared > 0) HIP_OK(hipStreamWaitEvent(st, d->ev_join, 0));  // the shared expert's y_s
+  const float *ys = L->F_shared > 0 ? w.y_s : nullptr;
   if ((uintptr_t)out & 15)
     hipLaunchKernelGGL(k_combine1, dim3((H + 255) / 256, S), dim3(256), 0, st, w.y, wts, ys, H, K, out);
   else
