@@ -883,11 +883,17 @@ int launch_fused(const zm_moe_layer *L, const float *x, const float *logits, int
     return 1;
   if (L->type_up != L->type_gate) return 1;
   const int u1 = nbH * units_per_block(L->type_gate);
-  const int l1 = u1 <= 16 ? 16 : (u1 <= 32 ? 32 : 0);
   if (Fs && nbH * units_per_block(L->type_shared) > 64) return 1;
   const int ir = (K * nbF * units_per_block(L->type_down) + 31) / 32;
   const int is = Fs ? (nbFs * units_per_block(L->type_shared) + 31) / 32 : 0;
-  DecFn fn = find_decode(L->type_gate, L->type_down, Fs ? L->type_shared : 0, l1, ir, is);
+  // lanes per routed gate/up row: 16 or 32, or 16 + 4 for rows of 20 units
+  // where the kernel has that layout
+  DecFn fn = nullptr;
+  if (u1 == 20) fn = find_decode(L->type_gate, L->type_down, Fs ? L->type_shared : 0, 20, ir, is);
+  if (!fn) {
+    const int l1 = u1 <= 16 ? 16 : (u1 <= 32 ? 32 : 0);
+    fn = find_decode(L->type_gate, L->type_down, Fs ? L->type_shared : 0, l1, ir, is);
+  }
   if (!fn) return 1;
   int G = 0;
   if (decode_grid(fn, &G)) return -1;

@@ -168,7 +168,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   __shared__ __attribute__((aligned(kIQ2 || kIQ3 ? 4096 : 8))) uint64_t s_grid[kIQ2 ? 256 : (kIQ3 ? 128 : (kIQ4 ? 2 : 1))];
   __shared__ __attribute__((aligned(kIQ2 || kIQ3 ? 2048 : 8))) uint64_t s_signs[kIQ2 || kIQ3 ? 128 : 1];
   static_assert(IS == 0 || TS != 0, "shared iterations need a shared type");
-  static_assert(L1 == 16 || L1 == 32, "lanes per routed gate/up row");
+  static_assert(L1 == 16 || L1 == 32 || L1 == 20, "lanes per routed gate/up row");
   constexpr int L2 = 32;  // lanes per down row (2 rows per wave step)
   constexpr int NS = IS > 0 ? IS : 1;
 
@@ -277,8 +277,14 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     constexpr int TT = decltype(ttag)::value;
     constexpr bool SH = decltype(ttag)::shared;
     constexpr int LL = decltype(ttag)::lanes;
-    constexpr int R1 = 64 / LL;
-    const int li1 = lane % LL, rg1 = lane / LL;
+    // LL = 20: rows of 20 units (IQ2_XXS at H = 5120) as 16 + 4 lanes, three
+    // rows per step: main lanes 16r .. 16r + 15 take units 0..15 of row r,
+    // tail lanes 48 + 4r .. +3 units 16..19 (lanes 60..63 idle), so 60 of
+    // 64 lanes work where 32-lane rows would leave 12 of every 32 idle
+    constexpr bool TAIL = LL == 20;
+    constexpr int R1 = TAIL ? 3 : 64 / LL;
+    const int li1 = TAIL ? (lane < 48 ? (lane & 15) : 16 + (lane & 3)) : lane % LL;
+    const int rg1 = TAIL ? (lane < 48 ? (lane >> 4) : ((lane - 48) >> 2)) : lane / LL;
     constexpr int UP = unit_per_block<TT>();
     constexpr int BT = block_bytes(TT);
     const int U1 = a.nbH * UP;
@@ -291,7 +297,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     // step st -> this lane's (valid, row j, token, weight-row byte offset)
     auto row1 = [&](int st, bool &valid, int &j, int &tok, int &roff) {
       j = r0 + R1 * (wave + DEC_WAVES * st) + rg1;
-      valid = st < nst && j < r1;
+      valid = st < nst && j < r1 && rg1 < R1;
       j = valid ? j : r0;
       int q, n;
       if constexpr (SH) {
@@ -321,7 +327,24 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
       const int j = ri.j, tok = ri.tok;
       float o[2];
       unit_dots<TT, 2>(bw, part, xblk(s_q8 + (size_t)tok * q8x, a.nbH, blk), s_grid, s_signs, o);
-      const float ag = group_sum<LL>(o[0]), au = group_sum<LL>(o[1]);
+      float ag, au;
+      if constexpr (TAIL) {
+        // row r = main 16-sum (lanes 16r..) + tail 4-sum (lanes 48 + 4r..),
+        // read out by the row's writer lane
+        const float g16 = group_sum<16>(o[0]), u16 = group_sum<16>(o[1]);
+        const float g4 = group_sum<4>(o[0]), u4 = group_sum<4>(o[1]);
+        float tg[3], tu[3];
+#pragma unroll
+        for (int rr = 0; rr < 3; ++rr) {
+          tg[rr] = readlane_f(g16, 16 * rr) + readlane_f(g4, 48 + 4 * rr);
+          tu[rr] = readlane_f(u16, 16 * rr) + readlane_f(u4, 48 + 4 * rr);
+        }
+        ag = rg1 == 0 ? tg[0] : (rg1 == 1 ? tg[1] : tg[2]);
+        au = rg1 == 0 ? tu[0] : (rg1 == 1 ? tu[1] : tu[2]);
+      } else {
+        ag = group_sum<LL>(o[0]);
+        au = group_sum<LL>(o[1]);
+      }
       bst_co(ract, (li1 == 0 && valid) ? 4 * (SH ? j : Tsh + j) : OOR, silu_f32(ag) * au);
     };
     // sched_barrier keeps every load of a step ahead of the math that waits
@@ -697,6 +720,8 @@ DecFn dec_pick2(int ir, int is) {
 // 64); IR / IS: 32-lane iterations over the routed / shared units of a down row
 template <int TG, int TD, int TS>
 DecFn dec_pick(int l1, int ir, int is) {
+  if constexpr (TG == T_IQ2_XXS)
+    if (l1 == 20) return dec_pick2<TG, TD, TS, 20>(ir, is);
   if (l1 == 16) return dec_pick2<TG, TD, TS, 16>(ir, is);
   if (l1 == 32) return dec_pick2<TG, TD, TS, 32>(ir, is);
   return nullptr;

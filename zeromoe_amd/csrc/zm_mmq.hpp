@@ -236,7 +236,7 @@ struct MmqW<T_Q6_K> {  // this lane's 4 x 8 bytes of ql, 2 x 8 bytes of qh | sca
 };
 
 template <int T, bool GATEUP, int TT, int NW = 4>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_Q4_K && !GATEUP && TT <= 4 ? 4 : 1))) void k_mmq(GemvArgs a) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(T == T_Q4_K && !GATEUP && TT <= 4 && NW == 4 ? 4 : 1))) void k_mmq(GemvArgs a) {
   constexpr int TOK = 16 * TT;  // pairs per work item
   constexpr int NT = 64 * NW;   // threads: NW waves of 16 weight rows each
   static_assert(T == T_Q4_K || T == T_Q5_K || T == T_Q2_K || T == T_Q6_K || T == T_IQ4_XS || T == T_IQ2_XXS ||
