@@ -21,6 +21,23 @@
 
 namespace zm {
 
+#ifndef ZM_IQ2S
+#define ZM_IQ2S 0
+#endif
+
+// ggml's ksigns/keven_signs entry for 7 sign bits s7: byte k is 0xff where
+// bit k of (s7 | parity(s7) << 7) is set.  Each nibble is spread to one bit
+// per byte by a multiply (x + x<<7 + x<<14 + x<<21, no carries for x < 64:
+// bits above 3 fall outside bits 0, 8, 16, 24), and a byte permute turns
+// selector 12 / 13 into 0x00 / 0xff.
+__device__ __forceinline__ uint64_t iq2_sign_mask(uint32_t s7) {
+  const uint32_t lo = __umul24(s7 & 15u, 0x00204081u);
+  const uint32_t hi = __umul24((s7 >> 4) | ((uint32_t)__builtin_popcount(s7) << 3), 0x00204081u);
+  const uint32_t ml = __builtin_amdgcn_perm(0u, 0u, (lo & 0x01010101u) | 0x0c0c0c0cu);
+  const uint32_t mh = __builtin_amdgcn_perm(0u, 0u, (hi & 0x01010101u) | 0x0c0c0c0cu);
+  return (uint64_t)ml | ((uint64_t)mh << 32);
+}
+
 template <int T>
 __host__ __device__ constexpr int unit_per_block() {
   return T == T_Q4_K || T == T_Q5_K || T == T_Q6_K || T == T_IQ4_XS || T == T_IQ3_XXS ? 2 : 1;
@@ -496,25 +513,46 @@ __device__ __forceinline__ void unit_ints(const Unit<T> (&w)[NW], int part, cons
     int isum[NW];
 #pragma unroll
     for (int n = 0; n < NW; ++n) isum[n] = 0;
+    // all table reads of a batch of sub-blocks (two for a single weight row)
+    // are issued before the first dot that uses them
+    constexpr int IBB = NW == 1 ? 2 : 1;
 #pragma unroll
-    for (int ib = 0; ib < 8; ++ib) {
-      const uint4 x0 = x.q[2 * ib], x1 = x.q[2 * ib + 1];
-      const uint32_t xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    for (int ib0 = 0; ib0 < 8; ib0 += IBB) {
+      uint64_t g[IBB][NW][4], m[IBB][NW][4];
 #pragma unroll
-      for (int n = 0; n < NW; ++n) {
-        const uint32_t aux0 = u4c(w[n].q[ib >> 1], 2 * (ib & 1)), aux1 = u4c(w[n].q[ib >> 1], 2 * (ib & 1) + 1);
-        int s = 0;
+      for (int bb = 0; bb < IBB; ++bb)
 #pragma unroll
-        for (int l = 0; l < 4; ++l) {
-          const uint64_t g = lds_grid[(aux0 >> (8 * l)) & 0xffu];
-          const uint64_t m = lds_signs[(aux1 >> (7 * l)) & 127u];
-          const uint32_t glo = (uint32_t)g, ghi = (uint32_t)(g >> 32);
-          const uint32_t mlo = (uint32_t)m, mhi = (uint32_t)(m >> 32);
-          // conditional byte negate: (g ^ m) + (m & 1) per byte (no carries: 8 <= g <= 255)
-          s = dot4(sign_bytes(glo, mlo), xs[2 * l], s);
-          s = dot4(sign_bytes(ghi, mhi), xs[2 * l + 1], s);
+        for (int n = 0; n < NW; ++n) {
+          const int ib = ib0 + bb;
+          const uint32_t aux0 = u4c(w[n].q[ib >> 1], 2 * (ib & 1)), aux1 = u4c(w[n].q[ib >> 1], 2 * (ib & 1) + 1);
+#pragma unroll
+          for (int l = 0; l < 4; ++l) {
+            g[bb][n][l] = lds_grid[(aux0 >> (8 * l)) & 0xffu];
+#if ZM_IQ2S == 1
+            m[bb][n][l] = iq2_sign_mask((aux1 >> (7 * l)) & 127u);
+#else
+            m[bb][n][l] = lds_signs[(aux1 >> (7 * l)) & 127u];
+#endif
+          }
         }
-        isum[n] = mad24(2 * (int)(aux1 >> 28) + 1, s, isum[n]);
+#pragma unroll
+      for (int bb = 0; bb < IBB; ++bb) {
+        const int ib = ib0 + bb;
+        const uint4 x0 = x.q[2 * ib], x1 = x.q[2 * ib + 1];
+        const uint32_t xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int n = 0; n < NW; ++n) {
+          const uint32_t aux1 = u4c(w[n].q[ib >> 1], 2 * (ib & 1) + 1);
+          int sacc = 0;
+#pragma unroll
+          for (int l = 0; l < 4; ++l) {
+            // conditional byte negate: (g ^ m) + (m & 1) per byte (no carries: 8 <= g <= 255)
+            const uint64_t gv = g[bb][n][l], mv = m[bb][n][l];
+            sacc = dot4(sign_bytes((uint32_t)gv, (uint32_t)mv), xs[2 * l], sacc);
+            sacc = dot4(sign_bytes((uint32_t)(gv >> 32), (uint32_t)(mv >> 32)), xs[2 * l + 1], sacc);
+          }
+          isum[n] = mad24(2 * (int)(aux1 >> 28) + 1, sacc, isum[n]);
+        }
       }
     }
 #pragma unroll
