@@ -188,25 +188,56 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
   }
-  // counter set of this call (the other set is cleared at the end, for the next call)
-  const uint32_t epoch = __builtin_amdgcn_readfirstlane(ld_co(&a.sync[0]));
-  // An earlier call's wait expired (error word set): its counters are in an
-  // unknown state, so none of them is trusted.  The word is read here by one
-  // thread and acted on after the first workgroup barrier (a uniform decision):
-  // every workgroup writes NaN to its output rows and leaves.  zm_moe_status
-  // reports the error and resets the sync words; calls then run normally.
-  if (tid == 0) s_stale = ld_co(&a.sync[1]);
-  uint32_t *const cnt = a.sync + DEC_CNT_STRIDE * (1 + DEC_NCNT * (int)(epoch & 1u));
-  uint32_t *const bcnt = a.sync + DEC_BLK_BASE + DEC_BCNT_STRIDE * DEC_MAX_ABLK * (int)(epoch & 1u);
+  // The epoch word selects this call's counter set (the other set is cleared
+  // at the end, for the next call).  An earlier call's wait expired (error
+  // word set): its counters are in an unknown state, so none of them is
+  // trusted.  The error word is read by one thread and acted on after the
+  // first workgroup barrier (a uniform decision): every workgroup writes NaN
+  // to its output rows and leaves.  zm_moe_status reports the error and resets
+  // the sync words; calls then run normally.  Both words are requested here
+  // and consumed later, so no wave waits for them before its first loads.
+  const uint32_t epoch_v = ld_co(&a.sync[0]);
+  uint32_t stale_v = 0;
+  if (tid == 0) stale_v = ld_co(&a.sync[1]);
 
   // ---------------------------------------------------------------- P0: route, quantize x
-  // Wave w < S routes token w (its loads go out first); the other waves
-  // quantize x (16 lanes per block, 4 blocks per wave and round), then the
-  // routing waves join them.
+  // Wave w < S routes token w; the other waves quantize x (16 lanes per
+  // block, 4 blocks per wave and round), each loading its next group of blocks
+  // while it quantizes one.  With S = DEC_WAVES every wave routes, then
+  // quantizes.  The lookup tables are loaded up front by the non-routing
+  // threads (thread index rotated past the routing waves) and stored to LDS
+  // after routing, so their latency overlaps the router's.
   if (tid == 0) s_err = 0;
   const int nxb = S * a.nbH;
   const int l16 = lane & 15;
-  const int wi = wave >= S ? wave - S : wave + DEC_WAVES - S;  // x-quant worker index
+  const int nwk = S < DEC_WAVES ? DEC_WAVES - S : DEC_WAVES;  // x-quant workers
+  const int wi = wave >= S ? wave - S : (S < DEC_WAVES ? nwk + wave : wave);  // worker index (>= nwk: none)
+  const int jt = (tid - 64 * S) & (DEC_THREADS - 1);
+  uint64_t tab_g = 0, tab_s = 0;
+  if constexpr (kIQ2) {
+    if (jt < 256) tab_g = a.grid[jt];
+    if (jt < 128) tab_s = a.signs[jt];
+  } else if constexpr (kIQ3) {  // a.grid: the IQ3_XXS grid (256 x u32)
+    if (jt < 128) tab_g = a.grid[jt];
+    if (jt < 128) tab_s = a.signs[jt];
+  } else if constexpr (kIQ4) {  // a.grid: the IQ4_XS value table
+    if (jt < 2) tab_g = a.grid[jt];
+  }
+  auto xload = [&](int grp, float4 (&v)[4]) {
+    const int bb = grp * 4 + (lane >> 4);
+    if (grp * 4 < nxb && bb < nxb) {
+      const int s = bb / a.nbH, b = bb % a.nbH;
+      const float4 *src = reinterpret_cast<const float4 *>(a.x + (size_t)s * H + (size_t)b * QK + 16 * l16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = src[i];
+    }
+  };
+  float4 xcur[4] = {};
+  // with more groups than workers the first group is requested before the
+  // router's loads; with one group or less per worker it is requested after
+  // them (at c2's shape an early x load delays the routing wave)
+  const bool xearly = (nxb + 3) / 4 > nwk;
+  if (xearly && wave >= S) xload(wi, xcur);
   if (wave < S) {
     const WaveRoute r = route_token<8>(a.r, wave, reinterpret_cast<float *>(s_stage[wave]));
     if (lane < K) {
@@ -236,30 +267,35 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     }
   }
   if constexpr (kIQ2) {
-    for (int i = tid; i < 256; i += DEC_THREADS) s_grid[i] = a.grid[i];
-    for (int i = tid; i < 128; i += DEC_THREADS) s_signs[i] = a.signs[i];
-  } else if constexpr (kIQ3) {  // a.grid: the IQ3_XXS grid (256 x u32)
-    for (int i = tid; i < 128; i += DEC_THREADS) s_grid[i] = a.grid[i];
-    for (int i = tid; i < 128; i += DEC_THREADS) s_signs[i] = a.signs[i];
-  } else if constexpr (kIQ4) {  // a.grid: the IQ4_XS value table
-    if (tid < 2) s_grid[tid] = a.grid[tid];
+    if (jt < 256) s_grid[jt] = tab_g;
+    if (jt < 128) s_signs[jt] = tab_s;
+  } else if constexpr (kIQ3) {
+    if (jt < 128) s_grid[jt] = tab_g;
+    if (jt < 128) s_signs[jt] = tab_s;
+  } else if constexpr (kIQ4) {
+    if (jt < 2) s_grid[jt] = tab_g;
   }
   ZM_TRACE(6);
-  for (int grp = wi; grp * 4 < nxb; grp += DEC_WAVES) {
-    const int bb = grp * 4 + (lane >> 4);
-    if (bb < nxb) {
-      const int s = bb / a.nbH, b = bb % a.nbH;
-      const float4 *src = reinterpret_cast<const float4 *>(a.x + (size_t)s * H + (size_t)b * QK + 16 * l16);
-      float xv[16];
+  if (wi < nwk) {
+    if (!xearly || wave < S) xload(wi, xcur);
+    for (int grp = wi; grp * 4 < nxb; grp += nwk) {
+      float4 xnext[4] = {};
+      xload(grp + nwk, xnext);
+      const int bb = grp * 4 + (lane >> 4);
+      if (bb < nxb) {
+        const int s = bb / a.nbH, b = bb % a.nbH;
+        float xv[16];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float4 f = src[i];
-        xv[4 * i] = f.x;
-        xv[4 * i + 1] = f.y;
-        xv[4 * i + 2] = f.z;
-        xv[4 * i + 3] = f.w;
+        for (int i = 0; i < 4; ++i) {
+          xv[4 * i] = xcur[i].x;
+          xv[4 * i + 1] = xcur[i].y;
+          xv[4 * i + 2] = xcur[i].z;
+          xv[4 * i + 3] = xcur[i].w;
+        }
+        store_q8_16l(s_q8 + (size_t)s * q8x, a.nbH, b, quant_block16(xv, l16), l16);
       }
-      store_q8_16l(s_q8 + (size_t)s * q8x, a.nbH, b, quant_block16(xv, l16), l16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xcur[i] = xnext[i];
     }
   }
   ZM_TRACE(7);
@@ -370,11 +406,12 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   // routing waves finish
   const int sh0 = (int)((long)Tsh * g / G), sh1 = (int)((long)Tsh * (g + 1) / G);
   if constexpr (TS != 0) {
-    const int nqw = min(DEC_WAVES, (nxb + 3) / 4);  // waves with x-quantization work
+    const int nqw = min(nwk, (nxb + 3) / 4);  // waves with x-quantization work
     if (wi < nqw) lds_signal(&s_xq_done, 1);  // this wave's x blocks are in LDS
     lds_wait(&s_xq_done, nqw);
     stream_rows(RowsTag<TS, true, 64>{}, sh0, sh1);
   }
+  if (tid == 0) s_stale = stale_v;
   __syncthreads();
   if (s_stale != 0u) {
     const int T2e = S * H;
@@ -478,6 +515,9 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   stores_done();
   __syncthreads();
   ZM_TRACE(2);
+  const uint32_t epoch = __builtin_amdgcn_readfirstlane(epoch_v);
+  uint32_t *const cnt = a.sync + DEC_CNT_STRIDE * (1 + DEC_NCNT * (int)(epoch & 1u));
+  uint32_t *const bcnt = a.sync + DEC_BLK_BASE + DEC_BCNT_STRIDE * DEC_MAX_ABLK * (int)(epoch & 1u);
   // arrival (for the epoch) and rows per act block: row j belongs to block j / 256
   if (tid == 0) atomicAdd(&cnt[DEC_CNT_STRIDE * (g % DEC_NCNT)], 1u);
   {
