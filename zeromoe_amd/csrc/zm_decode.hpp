@@ -167,6 +167,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   // address in one or two instructions
   __shared__ __attribute__((aligned(kIQ2 || kIQ3 ? 4096 : 8))) uint64_t s_grid[kIQ2 ? 256 : (kIQ3 ? 128 : (kIQ4 ? 2 : 1))];
   __shared__ __attribute__((aligned(kIQ2 || kIQ3 ? 2048 : 8))) uint64_t s_signs[kIQ2 || kIQ3 ? 128 : 1];
+  __shared__ int s_step;  // next dynamically assigned routed gate/up step
   static_assert(IS == 0 || TS != 0, "shared iterations need a shared type");
   static_assert(L1 == 16 || L1 == 32 || L1 == 20, "lanes per routed gate/up row");
   constexpr int L2 = 32;  // lanes per down row (2 rows per wave step)
@@ -180,6 +181,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   const size_t q8Fs = a.Fs > 0 ? q8l_row_bytes(a.nbFs) : 0;
   uint64_t trace_t[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   ZM_TRACE(0);
+  if (tid == 0) s_step = 0;  // published by the first workgroup barrier
   if constexpr (TS != 0) {
     // the x-quantization counter starts at zero before any wave counts itself:
     // an LDS store and a plain barrier (no memory fence, so no wave waits for
@@ -329,11 +331,24 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     const bool uok = li1 < U1;
     const int blk = min(li1 / UP, a.nbH - 1), part = li1 % UP;
     const int nst_all = (r1 - r0 + R1 - 1) / R1;
-    const int nst = nst_all > wave ? (nst_all - wave + DEC_WAVES - 1) / DEC_WAVES : 0;
-    // step st -> this lane's (valid, row j, token, weight-row byte offset)
-    auto row1 = [&](int st, bool &valid, int &j, int &tok, int &roff) {
-      j = r0 + R1 * (wave + DEC_WAVES * st) + rg1;
-      valid = st < nst && j < r1 && rg1 < R1;
+    // Wave w starts with step w.  With many steps per wave (routed rows only)
+    // the further steps come from an LDS counter when the wave issues its
+    // loads: with a fixed stride the two waves of a SIMD drift apart (the
+    // older one is issued first) and the late one finishes alone, without a
+    // second wave to hide its latency (c4: first and last wave of a workgroup
+    // 11 us apart, 3 us with the counter).  With few steps per wave the fixed
+    // stride is kept (c5 was 0.9 us slower with the counter).
+    const bool dyn = !SH && nst_all >= 6 * DEC_WAVES;
+    auto grab = [&](int kprev) {
+      if (!dyn) return kprev + DEC_WAVES;
+      int v = 0;
+      if (lane == 0) v = __hip_atomic_fetch_add(&s_step, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      return DEC_WAVES + __builtin_amdgcn_readfirstlane(v);
+    };
+    // step k -> this lane's (valid, row j, token, weight-row byte offset)
+    auto row1 = [&](int k, bool &valid, int &j, int &tok, int &roff) {
+      j = r0 + R1 * k + rg1;
+      valid = k < nst_all && j < r1 && rg1 < R1;
       j = valid ? j : r0;
       int q, n;
       if constexpr (SH) {
@@ -388,15 +403,19 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     // queue); steps past the end load and store nothing
     Unit<TT> A[2], B[2];
     RowInfo ra, rb;
-    if (nst > 0) issue(0, A, ra);
-    for (int st = 0; st < nst; st += 2) {
-      issue(st + 1, B, rb);
+    int ka = wave;
+    if (ka < nst_all) issue(ka, A, ra);
+    while (ka < nst_all) {
+      const int kb = grab(ka);
+      issue(kb, B, rb);
       __builtin_amdgcn_sched_barrier(0);
       compute(A, ra);
       __builtin_amdgcn_sched_barrier(0);
-      issue(st + 2, A, ra);
+      if (kb >= nst_all) break;  // B empty: no dots on zeros
+      ka = grab(kb);
+      issue(ka, A, ra);
       __builtin_amdgcn_sched_barrier(0);
-      if (st + 1 < nst) compute(B, rb);  // an odd step count leaves B empty: no dots on zeros
+      compute(B, rb);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
