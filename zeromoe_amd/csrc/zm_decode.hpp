@@ -6,8 +6,10 @@
 // Grid: as many 512-thread workgroups as the device holds at once.
 //   P0  every workgroup routes all tokens and quantizes x into LDS --
 //       redundant, but no grid-wide barrier precedes the first weight request.
-//       Each wave then requests the weights of its first down rows (P2), so
-//       they stream while gate/up computes and while the workgroups wait.
+//       With a shared expert each wave then requests the weights of its first
+//       down rows (P2); without one it requests them when its workgroup's
+//       gate/up rows are done, so they stream while the workgroups wait for
+//       the act rows and take no bandwidth from the gate/up rows.
 //   P1  the shared expert's gate/up rows (which need no routing) and then the
 //       routed (pair, row) rows are each cut into one contiguous range per
 //       workgroup; the shared range starts as soon as x is quantized, while
@@ -523,8 +525,17 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   };
   Unit<TD> c2r[IR];
   Unit<TS ? TS : TD> c2s[NS];
-  load_step2(0, c2r, c2s);
-  __builtin_amdgcn_sched_barrier(0);
+  // The first down step is requested before the gate/up rows when the layer
+  // has a shared expert (c5: its down rows then stream during the routing),
+  // else once this workgroup's gate/up rows are done: requested first, the
+  // down weights took HBM bandwidth from the gate/up rows every workgroup
+  // waits for (c2: first gate/up data 8.4 -> 5.2 us after the start, layer
+  // 25.9 -> 25.1 us; c5 0.8 us slower).
+  constexpr bool kLateDown = TS == 0;
+  if constexpr (!kLateDown) {
+    load_step2(0, c2r, c2s);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   // ---------------------------------------------------------------- P1: routed gate/up rows
   // rows [t0, t1) of the routed row space (route c, row n); the shared rows
@@ -532,6 +543,10 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   const int t0 = (int)((long)T1r * g / G), t1 = (int)((long)T1r * (g + 1) / G);
   stream_rows(RowsTag<TG, false, L1>{}, t0, t1);
   stores_done();
+  if constexpr (kLateDown) {  // after the act stores are acknowledged (stores_done waits for every load)
+    load_step2(0, c2r, c2s);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   __syncthreads();
   ZM_TRACE(2);
   const uint32_t epoch = __builtin_amdgcn_readfirstlane(epoch_v);
