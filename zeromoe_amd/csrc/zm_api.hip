@@ -832,7 +832,7 @@ int check_layer(const zm_moe_layer *L) {
   return 0;
 }
 int units_per_block(int t) {
-  return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_IQ4_XS || t == T_IQ3_XXS ? 2 : 1;
+  return t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_IQ4_XS || t == T_IQ3_XXS ? 2 : 1;
 }
 
 DecFn find_decode(int tg, int td, int ts, int l1, int ir, int is) {

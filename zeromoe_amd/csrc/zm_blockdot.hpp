@@ -40,7 +40,7 @@ __device__ __forceinline__ uint64_t iq2_sign_mask(uint32_t s7) {
 
 template <int T>
 __host__ __device__ constexpr int unit_per_block() {
-  return T == T_Q4_K || T == T_Q5_K || T == T_Q6_K || T == T_IQ4_XS || T == T_IQ3_XXS ? 2 : 1;
+  return T == T_Q3_K || T == T_Q4_K || T == T_Q5_K || T == T_Q6_K || T == T_IQ4_XS || T == T_IQ3_XXS ? 2 : 1;
 }
 
 // types with a whole-block unit (the fused decode kernel's dot)
@@ -59,9 +59,9 @@ struct Unit<T_Q2_K> {  // scales[16] | qs[64] | d, dmin
   uint32_t dd;
 };
 template <>
-struct Unit<T_Q3_K> {  // hmask[32] | qs[64] | scales[12] | d
+struct Unit<T_Q3_K> {  // half h: all of hmask[32] | qs[32h, +32) | scales[12] | d
   uint4 hm[2];
-  uint4 q[4];
+  uint4 q[2];
   uint32_t sc[3];
   uint32_t d;
 };
@@ -135,34 +135,28 @@ __device__ __forceinline__ void load_unit(rsrc_t r, int vo, int part, Unit<T> &u
     u.dd = bld4(r, vo + 80, 0);
   } else if constexpr (T == T_Q3_K) {
     // 110-byte blocks start 2 bytes off a dword every other block, and 16-byte
-    // loads that are not dword aligned stream ~35% slower: load dword-aligned
-    // and shift the 27 dwords of hmask | qs | scales into place
+    // loads that are not dword aligned stream ~35% slower: each region (hmask,
+    // the half's qs, scales) is loaded dword-aligned with one dword more and
+    // shifted into place
     const int sh = vo & 3, base = vo - sh;
-    uint32_t w[28];
+    auto region8 = [&](int off, uint4 &a, uint4 &b) {  // 8 dwords at vo + off
+      const uint4 v0 = bld16(r, base + off, 0), v1 = bld16(r, base + off + 16, 0);
+      const uint32_t v2 = bld4(r, sh ? base + off + 32 : OOR, 0);  // inside the block when shifted
+      const uint32_t w[9] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, v2};
+      uint32_t o[8];
 #pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      const uint4 v = bld16(r, base + 16 * i, 0);
-      w[4 * i] = v.x;
-      w[4 * i + 1] = v.y;
-      w[4 * i + 2] = v.z;
-      w[4 * i + 3] = v.w;
-    }
-    const auto s = __builtin_amdgcn_raw_buffer_load_b96(r, base + 96, 0, 0);
-    w[24] = s[0];
-    w[25] = s[1];
-    w[26] = s[2];
-    w[27] = bld4(r, sh ? base + 108 : OOR, 0);  // only needed (and inside the block) when shifted
+      for (int k = 0; k < 8; ++k) o[k] = __builtin_amdgcn_alignbyte(w[k + 1], w[k], (uint32_t)sh);
+      a = make_uint4(o[0], o[1], o[2], o[3]);
+      b = make_uint4(o[4], o[5], o[6], o[7]);
+    };
+    region8(0, u.hm[0], u.hm[1]);
+    region8(32 + 32 * part, u.q[0], u.q[1]);
+    const auto sv = __builtin_amdgcn_raw_buffer_load_b96(r, base + 96, 0, 0);
+    const uint32_t s3 = bld4(r, sh ? base + 108 : OOR, 0);
+    u.sc[0] = __builtin_amdgcn_alignbyte(sv[1], sv[0], (uint32_t)sh);
+    u.sc[1] = __builtin_amdgcn_alignbyte(sv[2], sv[1], (uint32_t)sh);
+    u.sc[2] = __builtin_amdgcn_alignbyte(s3, sv[2], (uint32_t)sh);
     u.d = bld2(r, vo + 108, 0);
-    uint32_t o[27];
-#pragma unroll
-    for (int k = 0; k < 27; ++k) o[k] = __builtin_amdgcn_alignbyte(w[k + 1], w[k], (uint32_t)sh);
-    u.hm[0] = make_uint4(o[0], o[1], o[2], o[3]);
-    u.hm[1] = make_uint4(o[4], o[5], o[6], o[7]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) u.q[i] = make_uint4(o[8 + 4 * i], o[9 + 4 * i], o[10 + 4 * i], o[11 + 4 * i]);
-    u.sc[0] = o[24];
-    u.sc[1] = o[25];
-    u.sc[2] = o[26];
   } else if constexpr (T == T_Q4_K) {
     u.hdr = bld16(r, vo, 0);
 #pragma unroll
@@ -303,13 +297,26 @@ __device__ __forceinline__ void unit_ints(const Unit<T> (&w)[NW], int part, cons
       s4[n][2] = (((a0 >> 4) & 0x0f0f0f0fu) | (((a2 >> 4) & 0x03030303u) << 4)) ^ 0x20202020u;
       s4[n][3] = (((a1 >> 4) & 0x0f0f0f0fu) | (((a2 >> 6) & 0x03030303u) << 4)) ^ 0x20202020u;
     }
-    const uint4 b0 = x.bs[0], b1 = x.bs[1];
-    const uint32_t bsw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    // half h = part: sub-blocks 8h .. 8h + 7, hmask bits 4h + j (moved down to j)
+    const int h = part;
+    const uint4 bh = x.bs[h];
+    const uint32_t bsw[4] = {bh.x, bh.y, bh.z, bh.w};
+    uint4 hmh[NW][2];
+    uint32_t sh4[NW][2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int n = 0; n < NW; ++n) {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const uint4 m = w[n].hm[kk];
+        const uint32_t c = 4u * (uint32_t)h;
+        hmh[n][kk] = make_uint4(m.x >> c, m.y >> c, m.z >> c, m.w >> c);
+      }
+      sh4[n][0] = h ? s4[n][2] : s4[n][0];
+      sh4[n][1] = h ? s4[n][3] : s4[n][1];
+    }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int t = j < 3 ? 2 * j + 2 : 6, sft = t - (4 * h + j);
+        const int t = j < 3 ? 2 * j + 2 : 6, sft = t - j;
         auto val = [&](uint32_t b, uint32_t m) {
           const uint32_t pl = j < 3 ? (b & (0x03030303u << (2 * j))) : ((b >> 2) & 0x30303030u);
           const uint32_t hs = sft >= 0 ? (m << sft) : (m >> -sft);
@@ -318,17 +325,17 @@ __device__ __forceinline__ void unit_ints(const Unit<T> (&w)[NW], int part, cons
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           const uint4 xv = x.q[8 * h + 2 * j + kk];
-          const int sb = 8 * h + 2 * j + kk;
+          const int sb = 2 * j + kk;  // sub-block 8h + sb
           const int bs = (int)(int16_t)(bsw[sb >> 1] >> (16 * (sb & 1)));
 #pragma unroll
           for (int n = 0; n < NW; ++n) {
-            const uint4 q = w[n].q[2 * h + kk];
-            const uint4 hm = w[n].hm[kk];
+            const uint4 q = w[n].q[kk];
+            const uint4 hm = hmh[n][kk];
             int sq = dot4(val(q.x, hm.x), xv.x, 0);
             sq = dot4(val(q.y, hm.y), xv.y, sq);
             sq = dot4(val(q.z, hm.z), xv.z, sq);
             sq = dot4(val(q.w, hm.w), xv.w, sq);
-            const int sc = __builtin_amdgcn_sbfe((int)s4[n][sb >> 2], 8 * (sb & 3), 6);
+            const int sc = __builtin_amdgcn_sbfe((int)sh4[n][sb >> 2], 8 * (sb & 3), 6);
             accq[n][j] = mad24(sc, sq, accq[n][j]);
             soff[n] = mad24(sc, bs, soff[n]);
           }
