@@ -884,7 +884,8 @@ int launch_fused(const zm_moe_layer *L, const float *x, const float *logits, int
   if (L->type_up != L->type_gate) return 1;
   const int u1 = nbH * units_per_block(L->type_gate);
   if (Fs && nbH * units_per_block(L->type_shared) > 64) return 1;
-  const int ir = (K * nbF * units_per_block(L->type_down) + 31) / 32;
+  // down rows: IQ2_XXS in half blocks (the decode kernel's H2)
+  const int ir = (K * nbF * (L->type_down == T_IQ2_XXS ? 2 : units_per_block(L->type_down)) + 31) / 32;
   const int is = Fs ? (nbFs * units_per_block(L->type_shared) + 31) / 32 : 0;
   // lanes per routed gate/up row: 16 or 32, or 16 + 4 for rows of 20 units
   // where the kernel has that layout

@@ -21,23 +21,6 @@
 
 namespace zm {
 
-#ifndef ZM_IQ2S
-#define ZM_IQ2S 0
-#endif
-
-// ggml's ksigns/keven_signs entry for 7 sign bits s7: byte k is 0xff where
-// bit k of (s7 | parity(s7) << 7) is set.  Each nibble is spread to one bit
-// per byte by a multiply (x + x<<7 + x<<14 + x<<21, no carries for x < 64:
-// bits above 3 fall outside bits 0, 8, 16, 24), and a byte permute turns
-// selector 12 / 13 into 0x00 / 0xff.
-__device__ __forceinline__ uint64_t iq2_sign_mask(uint32_t s7) {
-  const uint32_t lo = __umul24(s7 & 15u, 0x00204081u);
-  const uint32_t hi = __umul24((s7 >> 4) | ((uint32_t)__builtin_popcount(s7) << 3), 0x00204081u);
-  const uint32_t ml = __builtin_amdgcn_perm(0u, 0u, (lo & 0x01010101u) | 0x0c0c0c0cu);
-  const uint32_t mh = __builtin_amdgcn_perm(0u, 0u, (hi & 0x01010101u) | 0x0c0c0c0cu);
-  return (uint64_t)ml | ((uint64_t)mh << 32);
-}
-
 template <int T>
 __host__ __device__ constexpr int unit_per_block() {
   return T == T_Q3_K || T == T_Q4_K || T == T_Q5_K || T == T_Q6_K || T == T_IQ4_XS || T == T_IQ3_XXS ? 2 : 1;
@@ -187,6 +170,15 @@ __device__ __forceinline__ void load_unit(rsrc_t r, int vo, int part, Unit<T> &u
   }
 }
 
+// half `part` of an IQ2_XXS block (d, sub-blocks 4 part .. 4 part + 3) into q[0..1]
+__device__ __forceinline__ void load_unit_half(rsrc_t r, int vo, int part, Unit<T_IQ2_XXS> &u) {
+  u.d = bld2(r, vo, 0);
+  u.q[0] = bld16(r, vo + 2 + 32 * part, 0);
+  u.q[1] = bld16(r, vo + 18 + 32 * part, 0);
+  u.q[2] = make_uint4(0u, 0u, 0u, 0u);
+  u.q[3] = make_uint4(0u, 0u, 0u, 0u);
+}
+
 __device__ __forceinline__ uint32_t u4c(const uint4 &v, int i) {
   return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
@@ -230,7 +222,9 @@ __device__ __forceinline__ XBlk xblk_planar(const uint8_t *row, int nb, int blk)
 // Integer parts of weight unit w[n] against activation block x, as ggml's
 // per-block sums: Q2_K/Q4_K isum = sum sc*dot, imin = sum m*bsum; Q3_K isum
 // with q3 = q2 - 4*(bit clear), imin = 0; IQ2_XXS isum = sum (2ls+1)*dot.
-template <int T, int NW>
+// HALF (IQ2_XXS only): w holds half `part` of the block (sub-blocks 4 part ..
+// 4 part + 3 in q[0..1]), as the down rows of the fused decode kernel use it
+template <int T, int NW, bool HALF = false>
 __device__ __forceinline__ void unit_ints(const Unit<T> (&w)[NW], int part, const XBlk &x, const uint64_t *lds_grid,
                                           const uint64_t *lds_signs, int (&ri)[NW], int (&rm)[NW]) {
   if constexpr (T == T_Q2_K) {
@@ -523,8 +517,10 @@ __device__ __forceinline__ void unit_ints(const Unit<T> (&w)[NW], int part, cons
     // all table reads of a batch of sub-blocks (two for a single weight row)
     // are issued before the first dot that uses them
     constexpr int IBB = NW == 1 ? 2 : 1;
+    constexpr int NSB = HALF ? 4 : 8;      // sub-blocks in the unit
+    const int xb = HALF ? 4 * part : 0;    // first sub-block of the unit in the block
 #pragma unroll
-    for (int ib0 = 0; ib0 < 8; ib0 += IBB) {
+    for (int ib0 = 0; ib0 < NSB; ib0 += IBB) {
       uint64_t g[IBB][NW][4], m[IBB][NW][4];
 #pragma unroll
       for (int bb = 0; bb < IBB; ++bb)
@@ -535,17 +531,13 @@ __device__ __forceinline__ void unit_ints(const Unit<T> (&w)[NW], int part, cons
 #pragma unroll
           for (int l = 0; l < 4; ++l) {
             g[bb][n][l] = lds_grid[(aux0 >> (8 * l)) & 0xffu];
-#if ZM_IQ2S == 1
-            m[bb][n][l] = iq2_sign_mask((aux1 >> (7 * l)) & 127u);
-#else
             m[bb][n][l] = lds_signs[(aux1 >> (7 * l)) & 127u];
-#endif
           }
         }
 #pragma unroll
       for (int bb = 0; bb < IBB; ++bb) {
         const int ib = ib0 + bb;
-        const uint4 x0 = x.q[2 * ib], x1 = x.q[2 * ib + 1];
+        const uint4 x0 = x.q[2 * (xb + ib)], x1 = x.q[2 * (xb + ib) + 1];
         const uint32_t xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
         for (int n = 0; n < NW; ++n) {
@@ -593,11 +585,12 @@ __device__ __forceinline__ float unit_float(const Unit<T> &w, float xd, int isum
 }
 
 // out[n] = float contribution of weight unit w[n] against activation block x
-template <int T, int NW>
+template <int T, int NW, bool HALF = false>
 __device__ __forceinline__ void unit_dots(const Unit<T> (&w)[NW], int part, const XBlk &x, const uint64_t *lds_grid,
                                           const uint64_t *lds_signs, float (&out)[NW]) {
+  static_assert(!HALF || T == T_IQ2_XXS, "half units: IQ2_XXS only");
   int ri[NW], rm[NW];
-  unit_ints<T, NW>(w, part, x, lds_grid, lds_signs, ri, rm);
+  unit_ints<T, NW, HALF>(w, part, x, lds_grid, lds_signs, ri, rm);
 #pragma unroll
   for (int n = 0; n < NW; ++n) out[n] = unit_float<T>(w[n], x.d, ri[n], rm[n]);
 }

@@ -488,7 +488,11 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   const int nst2_all = (u1 - u0 + (64 / L2) - 1) / (64 / L2);
   const int nst2 = nst2_all > wave ? (nst2_all - wave + DEC_WAVES - 1) / DEC_WAVES : 0;
   const float invH = 1.0f / (float)H;
-  constexpr int UPD = unit_per_block<TD>();
+  // IQ2_XXS down rows in half blocks: c4's 8 x 6 blocks per row split into 96
+  // units over 32 lanes (three full iterations instead of two with half the
+  // lanes idle in the second)
+  constexpr bool H2 = TD == T_IQ2_XXS;
+  constexpr int UPD = H2 ? 2 : unit_per_block<TD>();
   constexpr int UPS = TS ? unit_per_block<TS>() : 1;
   constexpr int BD = block_bytes(TD);
   constexpr int BSD = TS ? block_bytes(TS) : 1;
@@ -511,8 +515,12 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
       const int k = u / URb, rem = u - k * URb;
       const int eoff = s_doff[s * K + min(k, K - 1)];
       const bool ok = valid && u < URd && eoff >= 0;
-      load_unit<TD>(rd, ok ? eoff + (int)__umul24((uint32_t)h, (uint32_t)a.d_rstride) + (rem / UPD) * BD : OOR,
-                    rem % UPD, wr[it]);
+      if constexpr (H2)
+        load_unit_half(rd, ok ? eoff + (int)__umul24((uint32_t)h, (uint32_t)a.d_rstride) + (rem / UPD) * BD : OOR,
+                       rem % UPD, wr[it]);
+      else
+        load_unit<TD>(rd, ok ? eoff + (int)__umul24((uint32_t)h, (uint32_t)a.d_rstride) + (rem / UPD) * BD : OOR,
+                      rem % UPD, wr[it]);
     }
     if constexpr (IS > 0) {
 #pragma unroll
@@ -729,7 +737,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
         const float wk = u < URd ? s_w[s * K + k] : 0.0f;
         float o[1];
         const Unit<TD> one[1] = {c2r[it]};
-        unit_dots<TD, 1>(one, rem % UPD, xblk(tb + (size_t)k * q8F, a.nbF, min(rem / UPD, a.nbF - 1)), s_grid,
+        unit_dots<TD, 1, H2>(one, rem % UPD, xblk(tb + (size_t)k * q8F, a.nbF, min(rem / UPD, a.nbF - 1)), s_grid,
                          s_signs, o);
         acc += wk * o[0];
       }
