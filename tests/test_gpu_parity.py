@@ -544,6 +544,7 @@ FUSED_CASES = {
     "c1": (CONFIGS["c1"], {}),
     "c2": (CONFIGS["c2"], {}),
     "c2_S8": (CONFIGS["c2"], dict(S=8)),
+    "c2_S3": (CONFIGS["c2"], dict(S=3)),  # x quantized by 5 workers, first groups requested before routing
     "c4": (CONFIGS["c4"], {}),
     "c5": (CONFIGS["c5"], {}),
     "c5_S2": (CONFIGS["c5"], dict(S=2)),
@@ -553,6 +554,7 @@ FUSED_CASES = {
     "iq4xs": (CONFIGS["c2"], dict(tg=IQ4, td=IQ4)),
     "iq4xs_S3": (CONFIGS["c2"], dict(tg=IQ4, td=IQ4, S=3)),
     "iq3xxs": (CONFIGS["c2"], dict(tg=IQ3, td=IQ3)),
+    "iq2xxs_S2": (CONFIGS["c2"], dict(tg=IQ2, td=IQ2, S=2)),  # 16 lanes per gate/up row, half-block down units
     "c5_selbias_mask": (CONFIGS["c5"], dict(sel_bias_sd=0.3, route_mask=True)),
     "c5_S3_selbias_mask": (CONFIGS["c5"], dict(S=3, sel_bias_sd=0.3, route_mask=True)),
 }
