@@ -478,11 +478,12 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   const int T1r = nvp * F;
 
   // ---------------------------------------------------------------- P2 set-up: down rows
-  // 16 lanes per down row, 4 rows per wave step; step st of this wave covers
-  // rows u0 + 4*(wave + DEC_WAVES*st) + (lane >> 4).  Lane li = lane & 15 takes
-  // units li + 16*it of the row: IR routed iterations over K*nbF*upb(TD) units
-  // (route, block, part), IS shared iterations over nbFs*upb(TS) units.  The
-  // first step of every wave is requested now, before any gate/up work.
+  // L2 = 32 lanes per down row, 2 rows per wave step; step st of this wave
+  // covers rows u0 + 2*(wave + DEC_WAVES*st) + lane / 32.  Lane li = lane % 32
+  // takes units li + 32*it of the row: IR routed iterations over K*nbF*UPD
+  // units (route, block, part), IS shared iterations over nbFs*UPS units.  The
+  // first step of every wave is requested below (before or after the gate/up
+  // rows, see kLateDown).
   const int li2 = lane % L2, rg2 = lane / L2;
   const int T2 = S * H;
   const int u0 = (int)((long)T2 * g / G), u1 = (int)((long)T2 * (g + 1) / G);
