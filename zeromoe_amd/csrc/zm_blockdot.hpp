@@ -1,7 +1,8 @@
 // zm_blockdot.hpp -- whole-super-block int8 dots for the fused decode kernel.
 //
 // One lane holds one "unit" of a weight row in registers: a whole super-block
-// (Q2_K, Q3_K, IQ2_XXS) or half of one (Q4_K, Q5_K, Q6_K), and reads the matching Q8_K
+// (Q2_K, IQ2_XXS) or half of one (Q3_K, Q4_K, Q5_K, Q6_K, IQ3_XXS, IQ4_XS; the
+// IQ2_XXS half is used for down rows), and reads the matching Q8_K
 // block of the activation row from LDS (planar layout: qs | bsums | d).  A
 // unit's integer dot is the ggml per-block integer sum (kquant layouts of
 // /root/reference/kernels/quant/kquant_matmul.cu:35-200, iq2_matmul.cu:27-91);
