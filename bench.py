@@ -454,6 +454,59 @@ def committed_traffic():
     return None
 
 
+TRACE_SLOTS = [(0, "workgroup start"), (6, "routing wave done (tables stored)"), (7, "wave 0 past x quantization"),
+               (1, "routed (routing barrier)"), (2, "gate/up rows done (workgroup)"), (3, "hand-off counted"),
+               (4, "act quantized in LDS"), (5, "down rows done")]
+
+
+def trace_summary(torch, Z, name, out_path, command, launches=40):
+    """Phase trace of the fused decode kernel (ZEROMOE_TRACE=1: eight s_memrealtime
+    stamps per workgroup, 100 MHz): percentiles over workgroups and launches, in us
+    from the first workgroup's start of each launch."""
+    import ctypes
+
+    import numpy as np
+
+    from zeromoe_amd import _lib
+
+    os.environ["ZEROMOE_TRACE"] = "1"
+    c = CONFIGS[name]
+    S, H, E = c["S"], c["H"], c["E"]
+    layers = build_layers(torch, Z, c, 4, seed=1234)
+    xs = torch.randn((S, H), device="cuda")
+    out = torch.empty((S, H), device="cuda")
+    use_logits = not c.get("router_gemv")
+    runs = []
+    for it in range(launches + 8):
+        lg = torch.randn((S, E), device="cuda") if use_logits else None
+        layers[it % 4].forward(xs, lg, out=out)
+        torch.cuda.synchronize()
+        buf = (ctypes.c_uint64 * (4096 * 8))()
+        n = _lib.lib().zm_debug_trace(buf, 4096 * 8)
+        t = np.frombuffer(buf, dtype=np.uint64, count=n).reshape(-1, 8).astype(np.int64)
+        t = t[t[:, 0] > 0]
+        if it >= 8:
+            runs.append((t - t[:, 0].min()) / 100.0)
+    os.environ.pop("ZEROMOE_TRACE")
+    status = [L.status(S) for L in layers]
+    R = np.stack(runs)
+    lines = [f"# phase trace of the fused decode kernel, {name} ({WORKLOAD[name]})",
+             f"# command: {command}",
+             f"# {R.shape[0]} launches x {R.shape[1]} workgroups; us from the first workgroup's start; status {status}",
+             f"{'phase':36s} {'p10':>7s} {'p50':>7s} {'p90':>7s} {'max':>7s}"]
+    for sl, label in TRACE_SLOTS:
+        v = R[:, :, sl].ravel()
+        lines.append(f"{label:36s} {np.percentile(v, 10):7.2f} {np.percentile(v, 50):7.2f} "
+                     f"{np.percentile(v, 90):7.2f} {v.max():7.2f}")
+    d = (R[:, :, 2] - R[:, :, 1]).ravel()
+    lines.append(f"{'gate/up duration (done - routed)':36s} {np.percentile(d, 10):7.2f} {np.percentile(d, 50):7.2f} "
+                 f"{np.percentile(d, 90):7.2f} {d.max():7.2f}")
+    text = "\n".join(lines) + "\n"
+    with open(out_path, "w") as f:
+        f.write(text)
+    print(text, end="")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -473,6 +526,8 @@ def main():
     ap.add_argument("--stats-summary", nargs=2, metavar=("DIR", "OUT"), help="summarize a rocprofv3 --stats run")
     ap.add_argument("--mfma-summary", nargs=2, metavar=("DIR", "OUT"),
                     help="int8 MFMA utilisation of the prefill kernels from a rocprofv3 --pmc run of --profile c3")
+    ap.add_argument("--trace", nargs=2, metavar=("CFG", "OUT"),
+                    help="phase trace of CFG's fused decode kernel (percentiles over workgroups) into OUT")
     ap.add_argument("--command", default="", help="command line recorded in a summary")
     ap.add_argument("--label", default="", help="configuration named in a --pmc-summary / --mfma-summary")
     ap.add_argument("--pattern", default="", help="kernel-name pattern of a --pmc-summary / --mfma-summary")
@@ -505,6 +560,9 @@ def main():
         per = NS * expert_bytes(c)
         return max(2, min(16, int(1.2e9 // per) + 2))
 
+    if args.trace:
+        trace_summary(torch, Z, args.trace[0], args.trace[1], args.command)
+        return
     if args.profile == "unpack":
         r = run_unpack(torch, Z, args.steps, args.warmup)
         print(json.dumps({"profile": "unpack", "us": round(r["us"], 2), "GBps": round(r["GBps"], 1)}))
