@@ -454,7 +454,7 @@ def committed_traffic():
     return None
 
 
-TRACE_SLOTS = [(0, "workgroup start"), (6, "routing wave done (tables stored)"), (7, "wave 0 past x quantization"),
+TRACE_SLOTS = [(0, "workgroup start"), (6, "routing wave done (tables stored)"), (7, "first x-quant worker done"),
                (1, "routed (routing barrier)"), (2, "gate/up rows done (workgroup)"), (3, "hand-off counted"),
                (4, "act quantized in LDS"), (5, "down rows done")]
 

@@ -229,9 +229,8 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   }
   auto xload = [&](int grp, float4 (&v)[4]) {
     const int bb = grp * 4 + (lane >> 4);
-    if (grp * 4 < nxb && bb < nxb) {
-      const int s = bb / a.nbH, b = bb % a.nbH;
-      const float4 *src = reinterpret_cast<const float4 *>(a.x + (size_t)s * H + (size_t)b * QK + 16 * l16);
+    if (grp * 4 < nxb && bb < nxb) {  // x rows are contiguous (H = nbH * QK): block bb at bb * QK
+      const float4 *src = reinterpret_cast<const float4 *>(a.x + (size_t)bb * QK + 16 * l16);
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] = src[i];
     }
@@ -253,22 +252,24 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
         a.r.weights[wave * K + lane] = r.w;
       }
     }
-    if (S == 1) {
-      // one token: its routing wave compacts the routed pairs itself (see
-      // below), which saves a workgroup barrier
+    if (S == 1 || !a.r.route_map) {
+      // one token, or no slot table (every route valid, so token w's pairs
+      // are compact indices wK .. wK + K - 1): each routing wave compacts its
+      // own pairs (see below), which saves a workgroup barrier
       const bool ok = lane < K && r.id >= 0;
       const unsigned long long m = __ballot(ok);
-      const int c = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+      const int c = wave * K + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+      const int p = wave * K + lane;
       if (lane < K) {
-        s_cidx[lane] = ok ? c : -1;
-        s_doff[lane] = ok ? r.id * (int)a.d_estride : -1;
+        s_cidx[p] = ok ? c : -1;
+        s_doff[p] = ok ? r.id * (int)a.d_estride : -1;
       }
       if (ok) {
-        s_vp[c] = lane;
+        s_vp[c] = p;
         s_goff[c] = r.id * (int)a.g_estride;
-        s_gtok[c] = 0;
+        s_gtok[c] = wave;
       }
-      if (lane == 0) s_nvp = __popcll(m);
+      if (tid == 0) s_nvp = S == 1 ? __popcll(m) : S * K;
     }
   }
   if constexpr (kIQ2) {
@@ -283,12 +284,14 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   ZM_TRACE(6);
   if (wi < nwk) {
     if (!xearly || wave < S) xload(wi, xcur);
+    // this lane's block (token s, block b) of each group, stepped by the
+    // 4 * nwk blocks between a worker's groups (one division, up front)
+    const int bb0 = wi * 4 + (lane >> 4), ds = 4 * nwk / a.nbH, db = 4 * nwk % a.nbH;
+    int s = bb0 / a.nbH, b = bb0 % a.nbH;
     for (int grp = wi; grp * 4 < nxb; grp += nwk) {
       float4 xnext[4] = {};
       xload(grp + nwk, xnext);
-      const int bb = grp * 4 + (lane >> 4);
-      if (bb < nxb) {
-        const int s = bb / a.nbH, b = bb % a.nbH;
+      if (s < S) {
         float xv[16];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -298,6 +301,12 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
           xv[4 * i + 3] = xcur[i].w;
         }
         store_q8_16l(s_q8 + (size_t)s * q8x, a.nbH, b, quant_block16(xv, l16), l16);
+      }
+      s += ds;
+      b += db;
+      if (b >= a.nbH) {
+        b -= a.nbH;
+        ++s;
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) xcur[i] = xnext[i];
@@ -309,7 +318,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   // super-block, or half of one for Q4_K).  Steps go through two register
   // buffers: step st+1 is in flight while step st computes.  act holds the S *
   // Fs shared rows (token, row n) first, then the routed rows (route c, row n).
-  const int Tsh = S * a.Fs;
+  const int Tsh = TS != 0 ? S * a.Fs : 0;  // Fs = 0 exactly when there is no shared expert
   const rsrc_t ract = make_rsrc(a.act, (uint32_t)(S * K * F + Tsh) * 4u);
   const float invF = 1.0f / (float)F, invFs = a.Fs > 0 ? 1.0f / (float)a.Fs : 0.f;
   auto stream_rows = [&](auto ttag, int r0, int r1) {
@@ -441,7 +450,8 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     for (int j = v0 + tid; j < v1; j += DEC_THREADS) a.out[j] = __builtin_nanf("");
     return;
   }
-  if (S > 1 && wave == 0) {
+  const bool compact = S > 1 && a.r.route_map;
+  if (compact && wave == 0) {
     // compact the routed pairs (id >= 0) in pair order: ballot + prefix count
     int n = 0;
     for (int p0 = 0; p0 < S * K; p0 += 64) {
@@ -472,7 +482,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     }
     if (lane == 0) s_nvp = n;
   }
-  if (S > 1) __syncthreads();
+  if (compact) __syncthreads();
   ZM_TRACE(1);
   const int nvp = s_nvp;
   const int T1r = nvp * F;
@@ -781,10 +791,13 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     }
     if (ok && lane == 0 && !s_err) st_co(&a.sync[0], epoch + 1u);
   }
+  // slot 7 from the first x-quantization worker (the one with the most
+  // groups), the others from thread 0
   if (a.trace && tid == 0) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) a.trace[(size_t)g * 8 + i] = trace_t[i];
+    for (int i = 0; i < 7; ++i) a.trace[(size_t)g * 8 + i] = trace_t[i];
   }
+  if (a.trace && tid == 64 * (S < DEC_WAVES ? S : 0)) a.trace[(size_t)g * 8 + 7] = trace_t[7];
 }
 
 #undef ZM_TRACE

@@ -148,6 +148,28 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
   return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
 }
+// max / min of v and v of the DPP partner lane in one VALU instruction (the
+// DPP modifier on the max itself).  For canonical v (the output of an earlier
+// max or min) this is fmaxf / fminf of the two; the compiler would put a
+// canonicalizing max between a DPP move and fmaxf.  s_nop 1: the two wait
+// states a DPP read needs after a VALU write of its source.
+#define ZM_DPP_MINMAX(NAME, OP)                                                                          \
+  template <int CTRL>                                                                                   \
+  __device__ __forceinline__ float NAME(float v) {                                                      \
+    float r;                                                                                            \
+    if constexpr (CTRL == DPP_XOR1)                                                                     \
+      asm("s_nop 1\n\t" OP " %0, %1, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf" : "=v"(r) : "v"(v)); \
+    else if constexpr (CTRL == DPP_XOR2)                                                                \
+      asm("s_nop 1\n\t" OP " %0, %1, %1 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf" : "=v"(r) : "v"(v)); \
+    else if constexpr (CTRL == DPP_HALF_MIRROR)                                                         \
+      asm("s_nop 1\n\t" OP " %0, %1, %1 row_half_mirror row_mask:0xf bank_mask:0xf" : "=v"(r) : "v"(v));     \
+    else                                                                                                \
+      asm("s_nop 1\n\t" OP " %0, %1, %1 row_mirror row_mask:0xf bank_mask:0xf" : "=v"(r) : "v"(v));          \
+    return r;                                                                                           \
+  }
+ZM_DPP_MINMAX(dpp_max_f, "v_max_f32_dpp")
+ZM_DPP_MINMAX(dpp_min_f, "v_min_f32_dpp")
+#undef ZM_DPP_MINMAX
 __device__ __forceinline__ float readlane_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }

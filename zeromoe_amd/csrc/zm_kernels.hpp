@@ -39,14 +39,14 @@ __device__ __forceinline__ Q8Out16 quant_block16(const float (&x)[16], int l16) 
     hi = fmaxf(hi, x[j]);
     lo = fminf(lo, x[j]);
   }
-  hi = fmaxf(hi, dpp_f<DPP_XOR1>(hi));
-  lo = fminf(lo, dpp_f<DPP_XOR1>(lo));
-  hi = fmaxf(hi, dpp_f<DPP_XOR2>(hi));
-  lo = fminf(lo, dpp_f<DPP_XOR2>(lo));
-  hi = fmaxf(hi, dpp_f<DPP_HALF_MIRROR>(hi));
-  lo = fminf(lo, dpp_f<DPP_HALF_MIRROR>(lo));
-  hi = fmaxf(hi, dpp_f<DPP_MIRROR>(hi));
-  lo = fminf(lo, dpp_f<DPP_MIRROR>(lo));
+  hi = dpp_max_f<DPP_XOR1>(hi);
+  lo = dpp_min_f<DPP_XOR1>(lo);
+  hi = dpp_max_f<DPP_XOR2>(hi);
+  lo = dpp_min_f<DPP_XOR2>(lo);
+  hi = dpp_max_f<DPP_HALF_MIRROR>(hi);
+  lo = dpp_min_f<DPP_HALF_MIRROR>(lo);
+  hi = dpp_max_f<DPP_MIRROR>(hi);
+  lo = dpp_min_f<DPP_MIRROR>(lo);
   const float amax = fmaxf(hi, -lo);
   Q8Out16 o;
   if (!(amax > 0.0f)) {  // all zero (or no finite/infinite value at all)
