@@ -351,8 +351,14 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     // 11 us apart, 3 us with the counter).  With few steps per wave the fixed
     // stride is kept (c5 was 0.9 us slower with the counter).
     const bool dyn = !SH && nst_all >= 6 * DEC_WAVES;
+    // The shared rows (streamed before the routing barrier) go to the
+    // x-quantization workers only: a routing wave that took one would request
+    // it after routing and hold up the barrier by a full load round trip (c5:
+    // routing done 5.2 us, barrier 7.4 us).
+    const int kw = SH ? (wi < nwk ? wi : nst_all) : wave;
+    const int kstride = SH ? nwk : DEC_WAVES;
     auto grab = [&](int kprev) {
-      if (!dyn) return kprev + DEC_WAVES;
+      if (!dyn) return kprev + kstride;
       int v = 0;
       if (lane == 0) v = __hip_atomic_fetch_add(&s_step, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       return DEC_WAVES + __builtin_amdgcn_readfirstlane(v);
@@ -415,7 +421,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     // queue); steps past the end load and store nothing
     Unit<TT> A[2], B[2];
     RowInfo ra, rb;
-    int ka = wave;
+    int ka = kw;
     if (ka < nst_all) issue(ka, A, ra);
     while (ka < nst_all) {
       const int kb = grab(ka);
