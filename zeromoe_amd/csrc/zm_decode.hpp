@@ -498,8 +498,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   // covers rows u0 + 2*(wave + DEC_WAVES*st) + lane / 32.  Lane li = lane % 32
   // takes units li + 32*it of the row: IR routed iterations over K*nbF*UPD
   // units (route, block, part), IS shared iterations over nbFs*UPS units.  The
-  // first step of every wave is requested below (before or after the gate/up
-  // rows, see kLateDown).
+  // first step of every wave is requested after the gate/up rows (below).
   const int li2 = lane % L2, rg2 = lane / L2;
   const int T2 = S * H;
   const int u0 = (int)((long)T2 * g / G), u1 = (int)((long)T2 * (g + 1) / G);
@@ -551,28 +550,21 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   };
   Unit<TD> c2r[IR];
   Unit<TS ? TS : TD> c2s[NS];
-  // The first down step is requested before the gate/up rows when the layer
-  // has a shared expert (c5: its down rows then stream during the routing),
-  // else once this workgroup's gate/up rows are done: requested first, the
-  // down weights took HBM bandwidth from the gate/up rows every workgroup
-  // waits for (c2: first gate/up data 8.4 -> 5.2 us after the start, layer
-  // 25.9 -> 25.1 us; c5 0.8 us slower).
-  constexpr bool kLateDown = TS == 0;
-  if constexpr (!kLateDown) {
-    load_step2(0, c2r, c2s);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-
   // ---------------------------------------------------------------- P1: routed gate/up rows
   // rows [t0, t1) of the routed row space (route c, row n); the shared rows
   // were streamed before the routing barrier
   const int t0 = (int)((long)T1r * g / G), t1 = (int)((long)T1r * (g + 1) / G);
   stream_rows(RowsTag<TG, false, L1>{}, t0, t1);
   stores_done();
-  if constexpr (kLateDown) {  // after the act stores are acknowledged (stores_done waits for every load)
-    load_step2(0, c2r, c2s);
-    __builtin_amdgcn_sched_barrier(0);
-  }
+  // The first down step is requested once this workgroup's act stores are
+  // acknowledged (stores_done waits for every load and store of the wave), so
+  // the down weights stream while the workgroups wait for the act rows.
+  // Requested before the gate/up rows they took HBM bandwidth from the rows
+  // every workgroup waits for: c2 first gate/up data 8.4 -> 5.2 us after the
+  // start, layer 25.9 -> 25.1 us; with a shared expert (c5) 31.4 -> 31.0 us
+  // since its shared rows no longer hold up the routing barrier.
+  load_step2(0, c2r, c2s);
+  __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
   ZM_TRACE(2);
   const uint32_t epoch = __builtin_amdgcn_readfirstlane(epoch_v);
