@@ -585,6 +585,71 @@ __device__ __forceinline__ float unit_float(const Unit<T> &w, float xd, int isum
   }
 }
 
+// A Q3_K half-block unit expanded before its activation is known (the decode
+// kernel's first down step, while the workgroup waits for the act rows): the
+// 32 plane words of unit_ints' Q3_K branch (plane j's two value bits in
+// place, its high bit moved next to them), the half's 6-bit scales as bytes
+// and d.  q3_exp_dot then needs only the v_dot4s and the scale multiply-adds,
+// with the same integer sums, so its result is the unit_dots result bit for bit.
+struct Q3Exp {
+  uint32_t v[32];  // [plane j][sub-block kk][word]
+  uint32_t sh4[2];
+  uint32_t d;
+};
+__device__ __forceinline__ void q3_expand(const Unit<T_Q3_K> &w, int part, Q3Exp &e) {
+  const uint32_t a0 = w.sc[0], a1 = w.sc[1], a2 = w.sc[2];
+  const int h = part;
+  e.sh4[0] = h ? ((((a0 >> 4) & 0x0f0f0f0fu) | (((a2 >> 4) & 0x03030303u) << 4)) ^ 0x20202020u)
+               : (((a0 & 0x0f0f0f0fu) | ((a2 & 0x03030303u) << 4)) ^ 0x20202020u);
+  e.sh4[1] = h ? ((((a1 >> 4) & 0x0f0f0f0fu) | (((a2 >> 6) & 0x03030303u) << 4)) ^ 0x20202020u)
+               : (((a1 & 0x0f0f0f0fu) | (((a2 >> 2) & 0x03030303u) << 4)) ^ 0x20202020u);
+  e.d = w.d;
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    const uint4 m = w.hm[kk];
+    const uint32_t c = 4u * (uint32_t)h;
+    const uint32_t hm[4] = {m.x >> c, m.y >> c, m.z >> c, m.w >> c};
+    const uint32_t q[4] = {w.q[kk].x, w.q[kk].y, w.q[kk].z, w.q[kk].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = j < 3 ? 2 * j + 2 : 6, sft = t - j;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t pl = j < 3 ? (q[i] & (0x03030303u << (2 * j))) : ((q[i] >> 2) & 0x30303030u);
+        const uint32_t hs = sft >= 0 ? (hm[i] << sft) : (hm[i] >> -sft);
+        e.v[8 * j + 4 * kk + i] = pl | (hs & (0x01010101u << t));
+      }
+    }
+  }
+}
+struct NoExp {};  // the expansion slot of other down types (never dotted)
+__device__ __forceinline__ float q3_exp_dot(const NoExp &, int, const XBlk &) { return 0.0f; }
+__device__ __forceinline__ float q3_exp_dot(const Q3Exp &e, int part, const XBlk &x) {
+  const int h = part;
+  const uint4 bh = x.bs[h];
+  const uint32_t bsw[4] = {bh.x, bh.y, bh.z, bh.w};
+  int accq[4] = {0, 0, 0, 0}, soff = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const uint4 xv = x.q[8 * h + 2 * j + kk];
+      const int sb = 2 * j + kk;
+      const int bs = (int)(int16_t)(bsw[sb >> 1] >> (16 * (sb & 1)));
+      const uint32_t *v = e.v + 8 * j + 4 * kk;
+      int sq = dot4(v[0], xv.x, 0);
+      sq = dot4(v[1], xv.y, sq);
+      sq = dot4(v[2], xv.z, sq);
+      sq = dot4(v[3], xv.w, sq);
+      const int sc = __builtin_amdgcn_sbfe((int)e.sh4[sb >> 2], 8 * (sb & 3), 6);
+      accq[j] = mad24(sc, sq, accq[j]);
+      soff = mad24(sc, bs, soff);
+    }
+  }
+  const int isum = accq[0] + (accq[1] >> 2) + ((accq[2] + accq[3]) >> 4) - 4 * soff;
+  return (x.d * h2f((uint16_t)(e.d & 0xffffu))) * (float)isum;
+}
+
 // out[n] = float contribution of weight unit w[n] against activation block x
 template <int T, int NW, bool HALF = false>
 __device__ __forceinline__ void unit_dots(const Unit<T> (&w)[NW], int part, const XBlk &x, const uint64_t *lds_grid,

@@ -550,6 +550,25 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   };
   Unit<TD> c2r[IR];
   Unit<TS ? TS : TD> c2s[NS];
+  // Q3_K down units of the first step are expanded while the workgroup waits
+  // for the act rows (their loads have landed by then), so that only the
+  // v_dot4s and scale multiply-adds of that step follow the wait
+  constexpr bool kExp = TD == T_Q3_K;
+#ifndef ZM_NE
+#define ZM_NE 2
+#endif
+  constexpr int NE = IR < ZM_NE ? IR : ZM_NE;  // units expanded (the rest stay raw: register budget)
+  std::conditional_t<kExp, Q3Exp, NoExp> ex[NE];
+  auto expand_step0 = [&]() {
+    if constexpr (kExp) {
+#pragma unroll
+      for (int it = 0; it < NE; ++it) {
+        const int u = li2 + L2 * it;
+        const int rem = u - (u / URb) * URb;
+        q3_expand(c2r[it], rem % UPD, ex[it]);
+      }
+    }
+  };
   // ---------------------------------------------------------------- P1: routed gate/up rows
   // rows [t0, t1) of the routed row space (route c, row n); the shared rows
   // were streamed before the routing barrier
@@ -626,8 +645,9 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     // l holds floats 4l..4l+3 of block k), transposes each round through this
     // wave's LDS stage to 16 lanes per block and runs quant_block16.  The wait
     // is bounded: on expiry the error word is set and the kernel still drains.
-    constexpr int QR = 3;
+    constexpr int QR = kExp ? 2 : 3;  // 2 with the expanded Q3_K units in registers (c2's 48 blocks in one round)
     const int kq = lane >> 4;
+    bool expanded = false;  // wave-uniform
     const int Tshb = Tsh >> 8;  // act blocks of the shared rows (Fs is a multiple of 256)
     for (int base = wave * 4; base < nb_all; base += DEC_WAVES * 4 * QR) {
       // act offsets of this round's blocks (wave-uniform), worked out before
@@ -670,8 +690,15 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
           }
         }
         int spins = 0;
+        // the first poll is requested before the first-step expansion, whose
+        // VALU work then overlaps the poll's round trip
+        uint32_t pv = bid < 0 ? (uint32_t)QK : ld_co(&bcnt[DEC_BCNT_STRIDE * bid]);
+        if (!expanded) {
+          expand_step0();
+          expanded = true;
+        }
         while (true) {
-          const bool ready = bid < 0 || ld_co(&bcnt[DEC_BCNT_STRIDE * bid]) >= (uint32_t)QK;
+          const bool ready = bid < 0 || pv >= (uint32_t)QK;
           // a negative limit (a host-forced give-up) expires on the first poll
           if (__ballot(!ready) == 0ull && a.spin_limit >= 0) break;
           __builtin_amdgcn_s_sleep(1);
@@ -682,6 +709,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
             }
             break;
           }
+          pv = bid < 0 ? (uint32_t)QK : ld_co(&bcnt[DEC_BCNT_STRIDE * bid]);
         }
         after_wait();
       }
@@ -718,6 +746,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
                        quant_block16(xv16, l16), l16);
       }
     }
+    if (!expanded) expand_step0();  // a wave without act blocks to fetch
   }
   __syncthreads();
   ZM_TRACE(4);
@@ -734,7 +763,11 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     // this call's wait expired: its output rows are marked, not left stale
     for (int j = u0 + tid; j < u1; j += DEC_THREADS) bst(rout, 4 * j, __builtin_nanf(""));
   } else {
-    for (int st = 0; st < nst2; ++st) {
+    // one down step; FIRST (the first step of a Q3_K layer) dots the units
+    // expanded during the act wait, so the raw units are dead until the next
+    // step's loads
+    auto down_step = [&](int st, auto first_tag) {
+      constexpr bool FIRST = decltype(first_tag)::value;
       bool valid;
       int s, h;
       row2(st, valid, s, h);
@@ -746,9 +779,13 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
         const int k = min(u / URb, K - 1), rem = u - (u / URb) * URb;
         const float wk = u < URd ? s_w[s * K + k] : 0.0f;
         float o[1];
-        const Unit<TD> one[1] = {c2r[it]};
-        unit_dots<TD, 1, H2>(one, rem % UPD, xblk(tb + (size_t)k * q8F, a.nbF, min(rem / UPD, a.nbF - 1)), s_grid,
-                         s_signs, o);
+        const XBlk xb = xblk(tb + (size_t)k * q8F, a.nbF, min(rem / UPD, a.nbF - 1));
+        if (kExp && FIRST && it < NE) {  // (it is a constant after unrolling)
+          o[0] = q3_exp_dot(ex[it < NE ? it : 0], rem % UPD, xb);
+        } else {
+          const Unit<TD> one[1] = {c2r[it]};
+          unit_dots<TD, 1, H2>(one, rem % UPD, xb, s_grid, s_signs, o);
+        }
         acc += wk * o[0];
       }
       if constexpr (IS > 0) {
@@ -767,6 +804,12 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
       __builtin_amdgcn_sched_barrier(0);
       if (st + 1 < nst2) load_step2(st + 1, c2r, c2s);  // (the unpacking of a unit costs VALU even when out of range)
       __builtin_amdgcn_sched_barrier(0);
+    };
+    if constexpr (kExp) {
+      if (nst2 > 0) down_step(0, std::true_type{});
+      for (int st = 1; st < nst2; ++st) down_step(st, std::false_type{});
+    } else {
+      for (int st = 0; st < nst2; ++st) down_step(st, std::false_type{});
     }
   }
   ZM_TRACE(5);
