@@ -589,7 +589,7 @@ __device__ __forceinline__ float unit_float(const Unit<T> &w, float xd, int isum
 // kernel's first down step, while the workgroup waits for the act rows): the
 // 32 plane words of unit_ints' Q3_K branch (plane j's two value bits in
 // place, its high bit moved next to them), the half's 6-bit scales as bytes
-// and d.  q3_exp_dot then needs only the v_dot4s and the scale multiply-adds,
+// and d.  exp_dot then needs only the v_dot4s and the scale multiply-adds,
 // with the same integer sums, so its result is the unit_dots result bit for bit.
 struct Q3Exp {
   uint32_t v[32];  // [plane j][sub-block kk][word]
@@ -622,9 +622,53 @@ __device__ __forceinline__ void q3_expand(const Unit<T_Q3_K> &w, int part, Q3Exp
     }
   }
 }
+// The same for an IQ2_XXS half-block unit (sub-blocks 4 part .. 4 part + 3):
+// the signed grid bytes of its 128 weights (table reads and sign application
+// done), the four 4-bit scales as bytes and d.
+struct IQ2Exp {
+  uint32_t v[32];  // [sub-block][word]
+  uint32_t ls;     // byte ib: 2 ls + 1 of sub-block ib
+  uint32_t d;
+};
+__device__ __forceinline__ void iq2_expand(const Unit<T_IQ2_XXS> &w, const uint64_t *lds_grid,
+                                           const uint64_t *lds_signs, IQ2Exp &e) {
+  e.d = w.d;
+  uint32_t ls = 0;
+#pragma unroll
+  for (int ib = 0; ib < 4; ++ib) {
+    const uint32_t aux0 = u4c(w.q[ib >> 1], 2 * (ib & 1)), aux1 = u4c(w.q[ib >> 1], 2 * (ib & 1) + 1);
+    uint64_t g[4], m[4];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      g[l] = lds_grid[(aux0 >> (8 * l)) & 0xffu];
+      m[l] = lds_signs[(aux1 >> (7 * l)) & 127u];
+    }
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      e.v[8 * ib + 2 * l] = sign_bytes((uint32_t)g[l], (uint32_t)m[l]);
+      e.v[8 * ib + 2 * l + 1] = sign_bytes((uint32_t)(g[l] >> 32), (uint32_t)(m[l] >> 32));
+    }
+    ls |= (2u * (aux1 >> 28) + 1u) << (8 * ib);
+  }
+  e.ls = ls;
+}
+__device__ __forceinline__ float iq2_exp_dot(const IQ2Exp &e, int part, const XBlk &x) {
+  int isum = 0;
+#pragma unroll
+  for (int ib = 0; ib < 4; ++ib) {
+    const uint4 x0 = x.q[2 * (4 * part + ib)], x1 = x.q[2 * (4 * part + ib) + 1];
+    const uint32_t xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    int sacc = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) sacc = dot4(e.v[8 * ib + q], xs[q], sacc);
+    isum = mad24((int)((e.ls >> (8 * ib)) & 0xffu), sacc, isum);
+  }
+  return 0.125f * ((x.d * h2f((uint16_t)(e.d & 0xffffu))) * (float)isum);
+}
 struct NoExp {};  // the expansion slot of other down types (never dotted)
-__device__ __forceinline__ float q3_exp_dot(const NoExp &, int, const XBlk &) { return 0.0f; }
-__device__ __forceinline__ float q3_exp_dot(const Q3Exp &e, int part, const XBlk &x) {
+__device__ __forceinline__ float exp_dot(const NoExp &, int, const XBlk &) { return 0.0f; }
+__device__ __forceinline__ float exp_dot(const IQ2Exp &e, int part, const XBlk &x) { return iq2_exp_dot(e, part, x); }
+__device__ __forceinline__ float exp_dot(const Q3Exp &e, int part, const XBlk &x) {
   const int h = part;
   const uint4 bh = x.bs[h];
   const uint32_t bsw[4] = {bh.x, bh.y, bh.z, bh.w};

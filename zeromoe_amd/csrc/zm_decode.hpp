@@ -550,22 +550,26 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   };
   Unit<TD> c2r[IR];
   Unit<TS ? TS : TD> c2s[NS];
-  // Q3_K down units of the first step are expanded while the workgroup waits
-  // for the act rows (their loads have landed by then), so that only the
-  // v_dot4s and scale multiply-adds of that step follow the wait
-  constexpr bool kExp = TD == T_Q3_K;
+  // Q3_K and IQ2_XXS down units of the first step are expanded while the
+  // workgroup waits for the act rows (their loads have landed by then), so
+  // that only the v_dot4s and scale multiply-adds of that step follow the wait
+  constexpr bool kExpQ3 = TD == T_Q3_K, kExpIQ2 = TD == T_IQ2_XXS;
+  constexpr bool kExp = kExpQ3 || kExpIQ2;
 #ifndef ZM_NE
 #define ZM_NE 2
 #endif
   constexpr int NE = IR < ZM_NE ? IR : ZM_NE;  // units expanded (the rest stay raw: register budget)
-  std::conditional_t<kExp, Q3Exp, NoExp> ex[NE];
+  std::conditional_t<kExpQ3, Q3Exp, std::conditional_t<kExpIQ2, IQ2Exp, NoExp>> ex[NE];
   auto expand_step0 = [&]() {
     if constexpr (kExp) {
 #pragma unroll
       for (int it = 0; it < NE; ++it) {
         const int u = li2 + L2 * it;
         const int rem = u - (u / URb) * URb;
-        q3_expand(c2r[it], rem % UPD, ex[it]);
+        if constexpr (kExpQ3)
+          q3_expand(c2r[it], rem % UPD, ex[it]);
+        else
+          iq2_expand(c2r[it], s_grid, s_signs, ex[it]);
       }
     }
   };
@@ -645,7 +649,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     // l holds floats 4l..4l+3 of block k), transposes each round through this
     // wave's LDS stage to 16 lanes per block and runs quant_block16.  The wait
     // is bounded: on expiry the error word is set and the kernel still drains.
-    constexpr int QR = kExp ? 2 : 3;  // 2 with the expanded Q3_K units in registers (c2's 48 blocks in one round)
+    constexpr int QR = kExp ? 2 : 3;  // 2 with expanded units in registers (c2: its 48 blocks in one round)
     const int kq = lane >> 4;
     bool expanded = false;  // wave-uniform
     const int Tshb = Tsh >> 8;  // act blocks of the shared rows (Fs is a multiple of 256)
@@ -781,7 +785,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
         float o[1];
         const XBlk xb = xblk(tb + (size_t)k * q8F, a.nbF, min(rem / UPD, a.nbF - 1));
         if (kExp && FIRST && it < NE) {  // (it is a constant after unrolling)
-          o[0] = q3_exp_dot(ex[it < NE ? it : 0], rem % UPD, xb);
+          o[0] = exp_dot(ex[it < NE ? it : 0], rem % UPD, xb);
         } else {
           const Unit<TD> one[1] = {c2r[it]};
           unit_dots<TD, 1, H2>(one, rem % UPD, xb, s_grid, s_signs, o);
