@@ -665,9 +665,62 @@ __device__ __forceinline__ float iq2_exp_dot(const IQ2Exp &e, int part, const XB
   }
   return 0.125f * ((x.d * h2f((uint16_t)(e.d & 0xffffu))) * (float)isum);
 }
+// The same for a Q4_K half-block unit (sub-blocks 4 part .. 4 part + 3): its
+// nibbles as bytes, the half's scale and min bytes and (d, dmin).
+struct Q4Exp {
+  uint32_t v[32];  // [qs group g][16-byte chunk mm][low nibbles 0..3, high nibbles 4..7]
+  uint32_t scv, mv, dd;
+};
+__device__ __forceinline__ void q4_expand(const Unit<T_Q4_K> &w, int part, Q4Exp &e) {
+  const uint32_t u0 = w.hdr.y, u1 = w.hdr.z, u2 = w.hdr.w;
+  e.scv = part == 0 ? (u0 & 0x3f3f3f3fu) : ((u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4));
+  e.mv = part == 0 ? (u1 & 0x3f3f3f3fu) : (((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4));
+  e.dd = w.hdr.x;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {  // c = 2 g + mm
+    const uint4 qv = w.q[c];
+    const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      e.v[8 * c + i] = q[i] & 0x0f0f0f0fu;
+      e.v[8 * c + 4 + i] = (q[i] >> 4) & 0x0f0f0f0fu;
+    }
+  }
+}
+__device__ __forceinline__ float q4_exp_dot(const Q4Exp &e, int part, const XBlk &x) {
+  const uint4 b = x.bs[part];
+  int isum = 0, imin = 0;
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const int i = 2 * part + g;
+    int slo = 0, shi = 0;
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) {
+      const uint32_t *v = e.v + 8 * (2 * g + mm);
+      const uint4 xl = x.q[4 * i + mm], xh = x.q[4 * i + 2 + mm];
+      slo = dot4(v[0], xl.x, slo);
+      slo = dot4(v[1], xl.y, slo);
+      slo = dot4(v[2], xl.z, slo);
+      slo = dot4(v[3], xl.w, slo);
+      shi = dot4(v[4], xh.x, shi);
+      shi = dot4(v[5], xh.y, shi);
+      shi = dot4(v[6], xh.z, shi);
+      shi = dot4(v[7], xh.w, shi);
+    }
+    isum = mad24((int)((e.scv >> (16 * g)) & 0xffu), slo, isum);
+    isum = mad24((int)((e.scv >> (16 * g + 8)) & 0xffu), shi, isum);
+  }
+  imin = sdot2(__builtin_amdgcn_perm(0u, e.mv, 0x0c000c00u), b.x, imin);
+  imin = sdot2(__builtin_amdgcn_perm(0u, e.mv, 0x0c010c01u), b.y, imin);
+  imin = sdot2(__builtin_amdgcn_perm(0u, e.mv, 0x0c020c02u), b.z, imin);
+  imin = sdot2(__builtin_amdgcn_perm(0u, e.mv, 0x0c030c03u), b.w, imin);
+  const float d = h2f((uint16_t)(e.dd & 0xffffu)), dmin = h2f((uint16_t)(e.dd >> 16));
+  return (x.d * d) * (float)isum - (x.d * dmin) * (float)imin;
+}
 struct NoExp {};  // the expansion slot of other down types (never dotted)
 __device__ __forceinline__ float exp_dot(const NoExp &, int, const XBlk &) { return 0.0f; }
 __device__ __forceinline__ float exp_dot(const IQ2Exp &e, int part, const XBlk &x) { return iq2_exp_dot(e, part, x); }
+__device__ __forceinline__ float exp_dot(const Q4Exp &e, int part, const XBlk &x) { return q4_exp_dot(e, part, x); }
 __device__ __forceinline__ float exp_dot(const Q3Exp &e, int part, const XBlk &x) {
   const int h = part;
   const uint4 bh = x.bs[h];

@@ -550,16 +550,17 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   };
   Unit<TD> c2r[IR];
   Unit<TS ? TS : TD> c2s[NS];
-  // Q3_K and IQ2_XXS down units of the first step are expanded while the
+  // Q3_K, Q4_K and IQ2_XXS down units of the first step are expanded while the
   // workgroup waits for the act rows (their loads have landed by then), so
   // that only the v_dot4s and scale multiply-adds of that step follow the wait
-  constexpr bool kExpQ3 = TD == T_Q3_K, kExpIQ2 = TD == T_IQ2_XXS;
-  constexpr bool kExp = kExpQ3 || kExpIQ2;
+  constexpr bool kExpQ3 = TD == T_Q3_K, kExpIQ2 = TD == T_IQ2_XXS, kExpQ4 = TD == T_Q4_K;
+  constexpr bool kExp = kExpQ3 || kExpIQ2 || kExpQ4;
 #ifndef ZM_NE
 #define ZM_NE 2
 #endif
   constexpr int NE = IR < ZM_NE ? IR : ZM_NE;  // units expanded (the rest stay raw: register budget)
-  std::conditional_t<kExpQ3, Q3Exp, std::conditional_t<kExpIQ2, IQ2Exp, NoExp>> ex[NE];
+  std::conditional_t<kExpQ3, Q3Exp, std::conditional_t<kExpIQ2, IQ2Exp, std::conditional_t<kExpQ4, Q4Exp, NoExp>>>
+      ex[NE];
   auto expand_step0 = [&]() {
     if constexpr (kExp) {
 #pragma unroll
@@ -568,6 +569,8 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
         const int rem = u - (u / URb) * URb;
         if constexpr (kExpQ3)
           q3_expand(c2r[it], rem % UPD, ex[it]);
+        else if constexpr (kExpQ4)
+          q4_expand(c2r[it], rem % UPD, ex[it]);
         else
           iq2_expand(c2r[it], s_grid, s_signs, ex[it]);
       }
