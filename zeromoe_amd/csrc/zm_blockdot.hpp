@@ -717,10 +717,56 @@ __device__ __forceinline__ float q4_exp_dot(const Q4Exp &e, int part, const XBlk
   const float d = h2f((uint16_t)(e.dd & 0xffffu)), dmin = h2f((uint16_t)(e.dd >> 16));
   return (x.d * d) * (float)isum - (x.d * dmin) * (float)imin;
 }
+// The same for a Q6_K half-block unit: its 6-bit values (without the -32) as
+// bytes, the half's 8 signed scale bytes and d.
+struct Q6Exp {
+  uint32_t v[32];  // [sub-block 2 g + kk][word d]
+  uint32_t sc[2];
+  uint32_t d;
+};
+__device__ __forceinline__ void q6_expand(const Unit<T_Q6_K> &w, Q6Exp &e) {
+  e.sc[0] = w.sc[0];
+  e.sc[1] = w.sc[1];
+  e.d = w.d;
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const uint32_t q = w.ql[8 * (g & 1) + 4 * kk + d];
+        const uint32_t lo = g < 2 ? (q & 0x0f0f0f0fu) : ((q >> 4) & 0x0f0f0f0fu);
+        const uint32_t hb = ((w.qh[4 * kk + d] >> (2 * g)) & 0x03030303u) << 4;
+        e.v[4 * (2 * g + kk) + d] = lo | hb;
+      }
+}
+__device__ __forceinline__ float q6_exp_dot(const Q6Exp &e, int part, const XBlk &x) {
+  const uint4 b0 = x.bs[0], b1 = x.bs[1];
+  const uint32_t bs[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+  int isum = 0, soff = 0;
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int c = 8 * part + 2 * g + kk;
+      const uint4 xv = x.q[c];
+      const uint32_t *v = e.v + 4 * (2 * g + kk);
+      int sq = dot4(v[0], xv.x, 0);
+      sq = dot4(v[1], xv.y, sq);
+      sq = dot4(v[2], xv.z, sq);
+      sq = dot4(v[3], xv.w, sq);
+      const int sl = 2 * g + kk;
+      const int sc = (int)(int8_t)(e.sc[sl >> 2] >> (8 * (sl & 3)));
+      isum = mad24(sc, sq, isum);
+      soff = mad24(sc, (int)(int16_t)(bs[c >> 1] >> (16 * (c & 1))), soff);
+    }
+  return (x.d * h2f((uint16_t)(e.d & 0xffffu))) * (float)(isum - 32 * soff);
+}
 struct NoExp {};  // the expansion slot of other down types (never dotted)
 __device__ __forceinline__ float exp_dot(const NoExp &, int, const XBlk &) { return 0.0f; }
 __device__ __forceinline__ float exp_dot(const IQ2Exp &e, int part, const XBlk &x) { return iq2_exp_dot(e, part, x); }
 __device__ __forceinline__ float exp_dot(const Q4Exp &e, int part, const XBlk &x) { return q4_exp_dot(e, part, x); }
+__device__ __forceinline__ float exp_dot(const Q6Exp &e, int part, const XBlk &x) { return q6_exp_dot(e, part, x); }
 __device__ __forceinline__ float exp_dot(const Q3Exp &e, int part, const XBlk &x) {
   const int h = part;
   const uint4 bh = x.bs[h];

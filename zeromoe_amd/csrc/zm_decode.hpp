@@ -550,16 +550,20 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   };
   Unit<TD> c2r[IR];
   Unit<TS ? TS : TD> c2s[NS];
-  // Q3_K, Q4_K and IQ2_XXS down units of the first step are expanded while the
+  // Q3_K, Q4_K, Q6_K and IQ2_XXS down units of the first step are expanded while the
   // workgroup waits for the act rows (their loads have landed by then), so
   // that only the v_dot4s and scale multiply-adds of that step follow the wait
-  constexpr bool kExpQ3 = TD == T_Q3_K, kExpIQ2 = TD == T_IQ2_XXS, kExpQ4 = TD == T_Q4_K;
-  constexpr bool kExp = kExpQ3 || kExpIQ2 || kExpQ4;
+  constexpr bool kExpQ3 = TD == T_Q3_K, kExpIQ2 = TD == T_IQ2_XXS, kExpQ4 = TD == T_Q4_K, kExpQ6 = TD == T_Q6_K;
+  constexpr bool kExp = kExpQ3 || kExpIQ2 || kExpQ4 || kExpQ6;
 #ifndef ZM_NE
 #define ZM_NE 2
 #endif
-  constexpr int NE = IR < ZM_NE ? IR : ZM_NE;  // units expanded (the rest stay raw: register budget)
-  std::conditional_t<kExpQ3, Q3Exp, std::conditional_t<kExpIQ2, IQ2Exp, std::conditional_t<kExpQ4, Q4Exp, NoExp>>>
+  // units expanded (the rest stay raw: register budget; Q6_K's larger raw
+  // units leave room for one of three)
+  constexpr int NE = kExpQ6 && IR >= 3 ? 1 : (IR < ZM_NE ? IR : ZM_NE);
+  std::conditional_t<kExpQ3, Q3Exp,
+                     std::conditional_t<kExpIQ2, IQ2Exp,
+                                        std::conditional_t<kExpQ4, Q4Exp, std::conditional_t<kExpQ6, Q6Exp, NoExp>>>>
       ex[NE];
   auto expand_step0 = [&]() {
     if constexpr (kExp) {
@@ -571,6 +575,8 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
           q3_expand(c2r[it], rem % UPD, ex[it]);
         else if constexpr (kExpQ4)
           q4_expand(c2r[it], rem % UPD, ex[it]);
+        else if constexpr (kExpQ6)
+          q6_expand(c2r[it], ex[it]);
         else
           iq2_expand(c2r[it], s_grid, s_signs, ex[it]);
       }
