@@ -762,11 +762,53 @@ __device__ __forceinline__ float q6_exp_dot(const Q6Exp &e, int part, const XBlk
     }
   return (x.d * h2f((uint16_t)(e.d & 0xffffu))) * (float)(isum - 32 * soff);
 }
+// The same for an IQ3_XXS half-block unit: signed grid bytes of its 128
+// weights, the four scales (2 ls + 1) as bytes and d.
+struct IQ3Exp {
+  uint32_t v[32];  // [sub-block i][word]
+  uint32_t ls;
+  uint32_t d;
+};
+__device__ __forceinline__ void iq3_expand(const Unit<T_IQ3_XXS> &w, const uint64_t *lds_grid,
+                                           const uint64_t *lds_signs, IQ3Exp &e) {
+  const uint32_t *g3 = reinterpret_cast<const uint32_t *>(lds_grid);
+  e.d = w.d;
+  uint32_t ls = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t aux = u4c(w.sas, i);
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      const uint32_t iw = w.gi[2 * i + (l >> 1)];
+      const uint32_t g1 = g3[(iw >> (16 * (l & 1))) & 0xffu], g2 = g3[(iw >> (16 * (l & 1) + 8)) & 0xffu];
+      const uint64_t m = lds_signs[(aux >> (7 * l)) & 127u];
+      e.v[8 * i + 2 * l] = sign_bytes(g1, (uint32_t)m);
+      e.v[8 * i + 2 * l + 1] = sign_bytes(g2, (uint32_t)(m >> 32));
+    }
+    ls |= (2u * (aux >> 28) + 1u) << (8 * i);
+  }
+  e.ls = ls;
+}
+__device__ __forceinline__ float iq3_exp_dot(const IQ3Exp &e, int part, const XBlk &x) {
+  int isum = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ib = 4 * part + i;
+    const uint4 xa = x.q[2 * ib], xb = x.q[2 * ib + 1];
+    const uint32_t xs[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    int sacc = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) sacc = dot4(e.v[8 * i + q], xs[q], sacc);
+    isum = mad24((int)((e.ls >> (8 * i)) & 0xffu), sacc, isum);
+  }
+  return 0.25f * ((x.d * h2f((uint16_t)(e.d & 0xffffu))) * (float)isum);
+}
 struct NoExp {};  // the expansion slot of other down types (never dotted)
 __device__ __forceinline__ float exp_dot(const NoExp &, int, const XBlk &) { return 0.0f; }
 __device__ __forceinline__ float exp_dot(const IQ2Exp &e, int part, const XBlk &x) { return iq2_exp_dot(e, part, x); }
 __device__ __forceinline__ float exp_dot(const Q4Exp &e, int part, const XBlk &x) { return q4_exp_dot(e, part, x); }
 __device__ __forceinline__ float exp_dot(const Q6Exp &e, int part, const XBlk &x) { return q6_exp_dot(e, part, x); }
+__device__ __forceinline__ float exp_dot(const IQ3Exp &e, int part, const XBlk &x) { return iq3_exp_dot(e, part, x); }
 __device__ __forceinline__ float exp_dot(const Q3Exp &e, int part, const XBlk &x) {
   const int h = part;
   const uint4 bh = x.bs[h];
