@@ -803,12 +803,52 @@ __device__ __forceinline__ float iq3_exp_dot(const IQ3Exp &e, int part, const XB
   }
   return 0.25f * ((x.d * h2f((uint16_t)(e.d & 0xffffu))) * (float)isum);
 }
+// The same for an IQ4_XS half-block unit: its table values as bytes, the four
+// sub-block scales (signed) as bytes and d.
+struct IQ4Exp {
+  uint32_t v[32];  // [sub-block i][low nibbles 0..3, high nibbles 4..7]
+  uint32_t sc;
+  uint32_t d;
+};
+__device__ __forceinline__ void iq4_expand(const Unit<T_IQ4_XS> &w, int part, const uint64_t *lds_grid, IQ4Exp &e) {
+  const uint32_t t0 = (uint32_t)lds_grid[0], t1 = (uint32_t)(lds_grid[0] >> 32);
+  const uint32_t t2 = (uint32_t)lds_grid[1], t3 = (uint32_t)(lds_grid[1] >> 32);
+  e.d = w.hdr.x;
+  uint32_t sc = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint4 qv = w.q[i];
+    const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      e.v[8 * i + k] = lut16(q[k] & 0x0f0f0f0fu, t0, t1, t2, t3);
+      e.v[8 * i + 4 + k] = lut16((q[k] >> 4) & 0x0f0f0f0fu, t0, t1, t2, t3);
+    }
+    sc |= ((uint32_t)iq4_scale(w.hdr.x, w.hdr.y, 4 * part + i) & 0xffu) << (8 * i);
+  }
+  e.sc = sc;
+}
+__device__ __forceinline__ float iq4_exp_dot(const IQ4Exp &e, int part, const XBlk &x) {
+  int isum = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ib = 4 * part + i;
+    const uint4 xl = x.q[2 * ib], xh = x.q[2 * ib + 1];
+    const uint32_t xs[8] = {xl.x, xl.y, xl.z, xl.w, xh.x, xh.y, xh.z, xh.w};
+    int sacc = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) sacc = dot4(e.v[8 * i + q], xs[q], sacc);
+    isum = mad24(__builtin_amdgcn_sbfe((int)e.sc, 8 * i, 8), sacc, isum);
+  }
+  return (x.d * h2f((uint16_t)(e.d & 0xffffu))) * (float)isum;
+}
 struct NoExp {};  // the expansion slot of other down types (never dotted)
 __device__ __forceinline__ float exp_dot(const NoExp &, int, const XBlk &) { return 0.0f; }
 __device__ __forceinline__ float exp_dot(const IQ2Exp &e, int part, const XBlk &x) { return iq2_exp_dot(e, part, x); }
 __device__ __forceinline__ float exp_dot(const Q4Exp &e, int part, const XBlk &x) { return q4_exp_dot(e, part, x); }
 __device__ __forceinline__ float exp_dot(const Q6Exp &e, int part, const XBlk &x) { return q6_exp_dot(e, part, x); }
 __device__ __forceinline__ float exp_dot(const IQ3Exp &e, int part, const XBlk &x) { return iq3_exp_dot(e, part, x); }
+__device__ __forceinline__ float exp_dot(const IQ4Exp &e, int part, const XBlk &x) { return iq4_exp_dot(e, part, x); }
 __device__ __forceinline__ float exp_dot(const Q3Exp &e, int part, const XBlk &x) {
   const int h = part;
   const uint4 bh = x.bs[h];

@@ -550,23 +550,24 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   };
   Unit<TD> c2r[IR];
   Unit<TS ? TS : TD> c2s[NS];
-  // Q3_K, Q4_K, Q6_K, IQ2_XXS and IQ3_XXS down units of the first step are
-  // expanded while the workgroup waits for the act rows (their loads have
-  // landed by then), so that only the v_dot4s and scale multiply-adds of that
-  // step follow the wait
+  // Q3_K, Q4_K, Q6_K, IQ2_XXS, IQ3_XXS and IQ4_XS down units of the first
+  // step are expanded while the workgroup waits for the act rows (their
+  // loads have landed by then), so that only the v_dot4s and scale
+  // multiply-adds of that step follow the wait
   constexpr bool kExpQ3 = TD == T_Q3_K, kExpIQ2 = TD == T_IQ2_XXS, kExpQ4 = TD == T_Q4_K, kExpQ6 = TD == T_Q6_K;
-  constexpr bool kExpIQ3 = TD == T_IQ3_XXS;
-  constexpr bool kExp = kExpQ3 || kExpIQ2 || kExpQ4 || kExpQ6 || kExpIQ3;
+  constexpr bool kExpIQ3 = TD == T_IQ3_XXS, kExpIQ4 = TD == T_IQ4_XS;
+  constexpr bool kExp = kExpQ3 || kExpIQ2 || kExpQ4 || kExpQ6 || kExpIQ3 || kExpIQ4;
 #ifndef ZM_NE
 #define ZM_NE 2
 #endif
   // units expanded (the rest stay raw: register budget; Q6_K's larger raw
-  // units leave room for one of three)
-  constexpr int NE = kExpQ6 && IR >= 3 ? 1 : (IR < ZM_NE ? IR : ZM_NE);
+  // units leave room for one of three, IQ4_XS's kernel for one)
+  constexpr int NE = (kExpQ6 && IR >= 3) || kExpIQ4 ? 1 : (IR < ZM_NE ? IR : ZM_NE);
   std::conditional_t<kExpQ3, Q3Exp,
                      std::conditional_t<kExpIQ2, IQ2Exp,
                                         std::conditional_t<kExpQ4, Q4Exp, std::conditional_t<kExpQ6, Q6Exp,
-                                                           std::conditional_t<kExpIQ3, IQ3Exp, NoExp>>>>>
+                                                           std::conditional_t<kExpIQ3, IQ3Exp,
+                                                                              std::conditional_t<kExpIQ4, IQ4Exp, NoExp>>>>>>
       ex[NE];
   auto expand_step0 = [&]() {
     if constexpr (kExp) {
@@ -582,6 +583,8 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
           q6_expand(c2r[it], ex[it]);
         else if constexpr (kExpIQ3)
           iq3_expand(c2r[it], s_grid, s_signs, ex[it]);
+        else if constexpr (kExpIQ4)
+          iq4_expand(c2r[it], rem % UPD, s_grid, ex[it]);
         else
           iq2_expand(c2r[it], s_grid, s_signs, ex[it]);
       }
