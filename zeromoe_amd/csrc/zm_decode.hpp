@@ -557,12 +557,9 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
   constexpr bool kExpQ3 = TD == T_Q3_K, kExpIQ2 = TD == T_IQ2_XXS, kExpQ4 = TD == T_Q4_K, kExpQ6 = TD == T_Q6_K;
   constexpr bool kExpIQ3 = TD == T_IQ3_XXS, kExpIQ4 = TD == T_IQ4_XS;
   constexpr bool kExp = kExpQ3 || kExpIQ2 || kExpQ4 || kExpQ6 || kExpIQ3 || kExpIQ4;
-#ifndef ZM_NE
-#define ZM_NE 2
-#endif
   // units expanded (the rest stay raw: register budget; Q6_K's larger raw
   // units leave room for one of three, IQ4_XS's kernel for one)
-  constexpr int NE = (kExpQ6 && IR >= 3) || kExpIQ4 ? 1 : (IR < ZM_NE ? IR : ZM_NE);
+  constexpr int NE = (kExpQ6 && IR >= 3) || kExpIQ4 ? 1 : (IR < 2 ? IR : 2);
   std::conditional_t<kExpQ3, Q3Exp,
                      std::conditional_t<kExpIQ2, IQ2Exp,
                                         std::conditional_t<kExpQ4, Q4Exp, std::conditional_t<kExpQ6, Q6Exp,
@@ -784,9 +781,9 @@ __global__ __launch_bounds__(DEC_THREADS) void k_moe_decode(DecodeArgs a) {
     // this call's wait expired: its output rows are marked, not left stale
     for (int j = u0 + tid; j < u1; j += DEC_THREADS) bst(rout, 4 * j, __builtin_nanf(""));
   } else {
-    // one down step; FIRST (the first step of a Q3_K layer) dots the units
-    // expanded during the act wait, so the raw units are dead until the next
-    // step's loads
+    // one down step; FIRST (the first step of a layer with an expanded down
+    // type) dots the units expanded during the act wait, so the raw units are
+    // dead until the next step's loads
     auto down_step = [&](int st, auto first_tag) {
       constexpr bool FIRST = decltype(first_tag)::value;
       bool valid;
